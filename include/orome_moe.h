@@ -1,0 +1,274 @@
+/*
+ * orome_moe.h -- C ABI of the MI355X (gfx950) MoE feed-forward library.
+ *
+ * Drop-in boundary for Orome's MoE hot path.  The types keep the C subset of
+ * the reference's interfaces (inference/include/orome.h) with the Metal
+ * handles replaced by HIP device pointers; the functions replace the
+ * reference's GGUF loader, weight-format layer, GPU context and the MoE
+ * encoder (encode_experts_gguf).  Every declaration names the reference
+ * interface it replaces as path:line relative to the reference repository.
+ *
+ * Conventions
+ *   - Return codes: OROME_OK (0) or a negative OROME_E* code; a message is
+ *     printed to stderr with the tag "[hip]" and kept for orome_last_error().
+ *     The reference returns NULL/false and prints "[tag] ..."
+ *     (inference/src/metal.m:44-56, inference/src/gguf.m:274-308).
+ *   - All device pointers are HBM addresses from this library's allocator
+ *     (or any hipMalloc'd memory on the context's device).
+ *   - A context owns one HIP stream; forward calls are asynchronous on it and
+ *     orome_hip_sync() waits.  A context is not thread-safe (the reference is
+ *     single-threaded too: inference/src/metal.m:51).
+ */
+#ifndef OROME_MOE_H
+#define OROME_MOE_H
+
+#include <stdbool.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+#pragma GCC visibility push(default)
+
+/* inference/include/orome.h:29 -- upper bound on active experts per token. */
+#define OROME_MAX_ACTIVE 16
+
+enum {
+    OROME_OK = 0,
+    OROME_EINVAL = -1,      /* bad argument or shape */
+    OROME_EUNSUPPORTED = -2,/* format / shape not handled by a kernel */
+    OROME_EHIP = -3,        /* HIP runtime error */
+    OROME_ENOMEM = -4,      /* allocation failed */
+    OROME_ENOTFOUND = -5,   /* missing tensor or file */
+    OROME_EFORMAT = -6,     /* malformed GGUF */
+};
+
+/* inference/include/orome.h:40-43 */
+typedef enum { FFN_MOE, FFN_DENSE } FFNType;
+
+/* MoE-path subset of ModelConfig (inference/include/orome.h:49-98); field
+ * names and meanings are the reference's. */
+typedef struct {
+    char name[64];
+    int hidden_dim;           /* H, e.g. 2048 */
+    int num_layers;
+    float rms_norm_eps;       /* e.g. 1e-6 */
+    FFNType ffn_type;
+    int num_experts;          /* E, e.g. 256 */
+    int num_experts_per_tok;  /* K, e.g. 8 */
+    int moe_intermediate;     /* M, e.g. 512 */
+    int shared_intermediate;  /* S, e.g. 512; 0 = no shared expert */
+} ModelConfig;
+
+/* inference/include/orome.h:227-235 (same values, same order). */
+typedef enum {
+    QFMT_GGUF_Q4_K,
+    QFMT_GGUF_Q5_K,
+    QFMT_GGUF_Q6_K,
+    QFMT_GGUF_Q8_0,
+    QFMT_F16,
+    QFMT_BF16,
+    QFMT_F32,
+} QuantFormat;
+
+/* inference/include/orome.h:239-246.  `buffer` is the device base of the
+ * uploaded GGUF data (it was an id<MTLBuffer>); `offset` is the same GGUF byte
+ * offset (data_offset + tensor offset, relative to the file start).  The
+ * reference's `pipeline` is dropped: `format` selects the kernel. */
+typedef struct {
+    void *buffer;
+    size_t offset;
+    QuantFormat format;
+    uint32_t out_dim;
+    uint32_t in_dim;
+} TensorRef;
+
+/* inference/include/orome.h:249-254 */
+typedef struct {
+    size_t offset;
+    size_t expert_stride;
+    QuantFormat format;
+} ExpertProjRef;
+
+/* inference/include/orome.h:256-259 */
+typedef struct {
+    void *buffer;
+    ExpertProjRef gate, up, down;
+} ExpertLayerRef;
+
+/* MoE subset of LayerTensorCache (inference/include/orome.h:264-279), plus
+ * `routing_bias`: an optional fp32 [E] bias added to the router logits
+ * before top-k (synthetic skewed-routing workloads; a zeroed ref = none). */
+typedef struct {
+    TensorRef post_norm;           /* F32 [H]; truncated to bf16 when applied */
+    TensorRef routing_gate;        /* F32 [E x H] */
+    TensorRef shared_gate;         /* Q4_K/Q8_0 [S x H] */
+    TensorRef shared_up;           /* Q4_K/Q8_0 [S x H] */
+    TensorRef shared_down;         /* Q4_K/Q6_K/Q8_0 [H x S] */
+    TensorRef shared_expert_gate;  /* F32 [1 x H] */
+    TensorRef routing_bias;        /* F32 [E] or empty */
+} LayerTensorCache;
+
+/* ------------------------------------------------------------------ GGUF */
+
+/* inference/include/orome.h:415-421 */
+typedef struct GGUFTensorInfo {
+    char *name;
+    uint32_t n_dims;
+    uint64_t dims[4];
+    uint32_t type;    /* ggml type id */
+    uint64_t offset;  /* relative to the data section */
+} GGUFTensorInfo;
+
+/* MoE subset of GGUFFile (inference/include/orome.h:423-437). */
+typedef struct GGUFFile {
+    int fd;                 /* -1 for an in-memory image */
+    void *mmap_base;        /* start of the image */
+    size_t file_size;
+    size_t data_offset;     /* absolute offset of the tensor data section */
+    GGUFTensorInfo *tensors;
+    uint64_t num_tensors;
+    uint32_t alignment;
+    char arch[32];
+    FFNType ffn_type;
+    int num_layers, hidden_dim, num_experts, num_experts_per_tok, moe_intermediate;
+    float rms_norm_eps;
+    void *index;            /* private name index */
+    bool owns_map;
+} GGUFFile;
+
+/* inference/src/gguf.m:273-518 (mmap + parse; v2/v3; alignment rule 511-512) */
+GGUFFile *gguf_open(const char *path);
+/* Same parser over an image already in host memory (not copied; must outlive
+ * the GGUFFile).  No counterpart in the reference (it only maps files). */
+GGUFFile *gguf_open_memory(const void *data, size_t size);
+/* inference/src/gguf.m:520-531 */
+void gguf_close(GGUFFile *gf);
+/* inference/src/gguf.m:533-537 */
+GGUFTensorInfo *gguf_find_tensor(GGUFFile *gf, const char *name);
+/* inference/src/gguf.m:540-550 */
+size_t gguf_tensor_size(const GGUFTensorInfo *ti);
+/* inference/src/gguf.m:552-575 */
+const char *ggml_type_name(uint32_t type);
+/* inference/src/format.m:326-337.  Unknown types are an error here
+ * (OROME_EUNSUPPORTED) instead of the reference's silent Q4_K fallback. */
+int format_from_ggml_type(uint32_t ggml_type, QuantFormat *out);
+/* ModelConfig fields read from GGUF metadata and tensor shapes
+ * (inference/src/main.m:443-633, shared_intermediate at 576-588). */
+int model_config_from_gguf(const GGUFFile *gf, ModelConfig *cfg);
+
+/* ---------------------------------------------------------- HIP context */
+
+/* Replaces MetalCtx + metal_setup/metal_free (inference/include/orome.h:125-221,
+ * inference/src/metal.m:41-256, 321-328): binds a device, creates the stream,
+ * and sizes the scratch arena for up to `max_tokens` tokens per call. */
+typedef struct orome_hip_ctx orome_hip_ctx;
+orome_hip_ctx *orome_hip_create(const ModelConfig *cfg, int max_tokens, int device);
+void orome_hip_destroy(orome_hip_ctx *ctx);
+int orome_hip_sync(orome_hip_ctx *ctx);
+void *orome_hip_get_stream(orome_hip_ctx *ctx);   /* hipStream_t */
+const char *orome_last_error(void);
+
+/* Kernel path for orome_moe_forward: AUTO picks GEMV for T <= 8 tokens and
+ * the MFMA grouped GEMM above that. */
+enum { OROME_PATH_AUTO = 0, OROME_PATH_GEMV = 1, OROME_PATH_MFMA = 2 };
+int orome_hip_set_path(orome_hip_ctx *ctx, int path);
+
+/* Device memory plumbing on the context's device. */
+void *orome_hip_malloc(orome_hip_ctx *ctx, size_t bytes);
+int orome_hip_free(orome_hip_ctx *ctx, void *p);
+int orome_hip_htod(orome_hip_ctx *ctx, void *dst, const void *src, size_t bytes);
+int orome_hip_dtoh(orome_hip_ctx *ctx, void *dst, const void *src, size_t bytes);
+
+/* -------------------------------------------------- weight format layer */
+
+/* inference/include/orome.h:262-265 (FormatProvider).  model_buf is the HBM
+ * copy of the GGUF image from data_offset on; device addresses are
+ * model_buf + (gguf offset - data_offset). */
+typedef struct {
+    GGUFFile *gguf;
+    void *model_buf;      /* device base, already shifted so that
+                             model_buf + gguf_offset addresses the tensor */
+    void *alloc_base;     /* the allocation itself */
+    size_t model_bytes;
+    orome_hip_ctx *ctx;
+} FormatProvider;
+
+/* inference/src/format.m:343-363: the reference wraps the mmap without a copy
+ * (unified memory); here the data section is copied unchanged into one HBM
+ * allocation, so the same GGUF bytes feed the kernels. */
+FormatProvider *format_provider_open_gguf(GGUFFile *gf, orome_hip_ctx *ctx);
+/* inference/src/format.m:365-369 */
+void format_provider_close(FormatProvider *fp);
+/* inference/src/format.m:374-409.  A missing tensor leaves a zeroed ref. */
+ExpertLayerRef format_resolve_expert_layer(FormatProvider *fp, int layer_idx,
+                                           uint32_t num_experts);
+/* MoE part of build_tensor_cache_gguf (inference/src/format.m:458-590,
+ * MoE refs 495-509).  Returns cfg->num_layers entries; free with
+ * free_tensor_cache(). */
+LayerTensorCache *build_tensor_cache_gguf(FormatProvider *fp, const ModelConfig *cfg);
+void free_tensor_cache(LayerTensorCache *cache);
+
+/* ------------------------------------------------------------ MoE block */
+
+/* One MoE feed-forward block for T tokens, on the context stream.
+ * Replaces the routing matvec (inference/src/engine.m:656-685) plus
+ * encode_experts_gguf (inference/src/engine.m:158-340):
+ *   logits = [W_r x ; w_sg x]   (fp32, fixed reduction order)
+ *   idx, w = top-K of logits (+routing_bias), renormalised softmax
+ *   h_out  = (h_in + sum_k w_k E_idx_k(x)) + sigmoid(w_sg x) * S(x)
+ * x_dev: fp32 [T x H] normalised input.  h_in_dev: fp32 [T x H] residual or
+ * NULL (zero).  h_out_dev may alias h_in_dev.  K <= OROME_MAX_ACTIVE. */
+int orome_moe_forward(orome_hip_ctx *ctx, const ModelConfig *cfg, const ExpertLayerRef *elr,
+                      const LayerTensorCache *lt, const float *x_dev, const float *h_in_dev,
+                      float *h_out_dev, int T, int K);
+
+/* RMSNorm (post_norm, bf16-truncated weights) then the MoE block with the
+ * residual add, in place on h_dev [T x H]: h = h + MoE(RMSNorm(h)).
+ * The reference fuses the same norm into the previous combine
+ * (inference/src/shaders.metal:90-149, 1079-1135; inference/src/engine.m:627-653). */
+int orome_moe_layer_forward(orome_hip_ctx *ctx, const ModelConfig *cfg,
+                            const ExpertLayerRef *elr, const LayerTensorCache *lt, float *h_dev,
+                            int T, int K);
+
+/* n_layers consecutive orome_moe_layer_forward calls (the per-layer loop of
+ * engine_step restricted to the FFN blocks, inference/src/engine.m:481-694). */
+int orome_moe_stack_forward(orome_hip_ctx *ctx, const ModelConfig *cfg,
+                            const ExpertLayerRef *elrs, const LayerTensorCache *lts, int n_layers,
+                            float *h_dev, int T, int K);
+
+/* Parity hooks: copy the intermediates of the most recent forward to host
+ * memory (synchronises the stream).  Any pointer may be NULL.
+ *   logits  [T x (E+1)]  router logits, slot E = shared-gate logit
+ *   idx     [T x K]      expert indices, descending logit per token
+ *   w       [T x K]      renormalised weights
+ *   offsets [E+1]        dispatch run starts, pairs[offsets[e]..offsets[e+1])
+ *   pairs   [T x K]      expert-sorted pair ids p = t*K + k (stable in p) */
+int orome_moe_debug_outputs(orome_hip_ctx *ctx, float *logits, int32_t *idx, float *w,
+                            uint32_t *offsets, uint32_t *pairs);
+
+/* Top-k routing alone on given logits [T x (E+1)] (device), for teacher-forced
+ * parity of the selection (restates inference/src/shaders.metal:1141-1234).
+ * Outputs are device pointers; bias_dev may be NULL. */
+int orome_moe_topk(orome_hip_ctx *ctx, const float *logits_dev, const float *bias_dev, int T,
+                   int E, int K, int32_t *idx_dev, float *w_dev);
+
+/* Scalar dequant of `rows` rows of `in_dim` weights to fp32 on the GPU
+ * (format_decode_row_f32, inference/src/format.m:176-218; bit-exact). */
+int orome_dequant_rows(orome_hip_ctx *ctx, QuantFormat fmt, const void *src_dev, uint32_t rows,
+                       uint32_t in_dim, float *out_dev);
+
+/* The fp16 weight tiles that the MFMA path feeds to the matrix cores:
+ * fp16(dequant(w)) rounded to nearest even, [rows x in_dim]. */
+int orome_dequant_rows_f16(orome_hip_ctx *ctx, QuantFormat fmt, const void *src_dev,
+                           uint32_t rows, uint32_t in_dim, uint16_t *out_dev);
+
+/* Library version string. */
+const char *orome_version(void);
+
+#pragma GCC visibility pop
+#ifdef __cplusplus
+}
+#endif
+#endif /* OROME_MOE_H */

@@ -1,0 +1,162 @@
+/*
+ * dev_common.h -- gfx950 device helpers shared by the MoE kernels:
+ * wave64 reductions, fp16 packing, and the Q4_K / Q6_K / Q8_0 block
+ * decoders used by the GEMV (decode) and MFMA (prefill) kernels.
+ *
+ * Quant layouts (byte offsets inside one super-block / block):
+ *   Q4_K 144 B / 256 w: d f16 @0, dmin f16 @2, 12 packed 6-bit scale/min
+ *        bytes @4, 128 nibble bytes @16; weight (g*64 + l) is the low nibble
+ *        and (g*64 + 32 + l) the high nibble of qs[g*32 + l].  Scale/min
+ *        unpack follows inference/src/format.m:41-64 (reference layout).
+ *   Q6_K 210 B / 256 w: ql @0 (128), qh @128 (64), int8 scales @192 (16),
+ *        d f16 @208; inference/src/format.m:144-174.
+ *   Q8_0 34 B / 32 w: d f16 @0, 32 int8 @2; inference/src/format.m:66-79.
+ */
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef float f4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u2 __attribute__((ext_vector_type(2)));
+
+#define DEV static __device__ __forceinline__
+
+DEV h2 as_h2(uint32_t v) { return __builtin_bit_cast(h2, v); }
+DEV uint32_t as_u32(h2 v) { return __builtin_bit_cast(uint32_t, v); }
+
+DEV float f16_bits_to_f32(uint32_t bits16) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)(bits16 & 0xFFFFu));
+}
+
+/* Canonical wave64 sum: xor butterfly 32,16,8,4,2,1 (every lane ends with
+ * the total).  The order is part of the router/norm bit-exact contract. */
+DEV float wave_sum_canon(float v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v = v + __shfl_xor(v, off, 64);
+    return v;
+}
+
+/* Sum over aligned groups of `width` lanes (width a power of two <= 64). */
+template <int WIDTH>
+DEV float group_sum(float v) {
+#pragma unroll
+    for (int off = WIDTH / 2; off >= 1; off >>= 1) v = v + __shfl_xor(v, off, 64);
+    return v;
+}
+
+DEV float silu_f(float g) { return g / (1.0f + __expf(-g)); }
+DEV float sigmoid_f(float s) { return 1.0f / (1.0f + expf(-s)); }
+
+/* --------------------------------------------------------------- Q4_K */
+
+/* 6-bit scale/min byte i (0..11) of the packed region, given its three dwords */
+DEV uint32_t q4k_sbyte(uint32_t s0, uint32_t s1, uint32_t s2, int i) {
+    uint32_t w = i < 4 ? s0 : (i < 8 ? s1 : s2);
+    return (w >> ((i & 3) * 8)) & 0xFFu;
+}
+
+/* Scales/mins of sub-blocks 2g and 2g+1 (inference/src/format.m:41-64),
+ * as integers. hdr = first 16 bytes of the super-block. */
+DEV void q4k_scale_min(u4 hdr, int g, uint32_t &sl, uint32_t &sh, uint32_t &ml, uint32_t &mh) {
+    uint32_t s0 = hdr.y, s1 = hdr.z, s2 = hdr.w;
+    if (g < 2) {
+        int b = 2 * g;
+        sl = q4k_sbyte(s0, s1, s2, b) & 63u;
+        sh = q4k_sbyte(s0, s1, s2, b + 1) & 63u;
+        ml = q4k_sbyte(s0, s1, s2, b + 4) & 63u;
+        mh = q4k_sbyte(s0, s1, s2, b + 5) & 63u;
+    } else {
+        int b = 2 * (g - 2);
+        uint32_t sp = q4k_sbyte(s0, s1, s2, 8 + g - 2), mp = q4k_sbyte(s0, s1, s2, 10 + g - 2);
+        sl = (sp & 0xFu) | ((q4k_sbyte(s0, s1, s2, b) >> 6) << 4);
+        sh = (sp >> 4) | ((q4k_sbyte(s0, s1, s2, b + 1) >> 6) << 4);
+        ml = (mp & 0xFu) | ((q4k_sbyte(s0, s1, s2, b + 4) >> 6) << 4);
+        mh = (mp >> 4) | ((q4k_sbyte(s0, s1, s2, b + 5) >> 6) << 4);
+    }
+}
+
+/* Per-chunk affine terms for a Q4_K 16-byte quant chunk in group g:
+ * weight = a * q - b (exact products; one rounding at the subtract). */
+struct Q4Affine {
+    float a_lo, a_hi, b_lo, b_hi;
+};
+DEV Q4Affine q4k_affine(u4 hdr, int g) {
+    uint32_t sl, sh, ml, mh;
+    q4k_scale_min(hdr, g, sl, sh, ml, mh);
+    float d = f16_bits_to_f32(hdr.x), dm = f16_bits_to_f32(hdr.x >> 16);
+    Q4Affine r;
+    r.a_lo = d * (float)sl;
+    r.a_hi = d * (float)sh;
+    r.b_lo = dm * (float)ml;
+    r.b_hi = dm * (float)mh;
+    return r;
+}
+
+/* Exact fp16 pairs of 4-bit quants: for a dword of 4 quant bytes (positions
+ * l..l+3), lo01 = (q_lo[l], q_lo[l+1]), lo23 = (q_lo[l+2], q_lo[l+3]) and
+ * the same for the high nibbles.  0x64XX as fp16 is 1024 + XX. */
+DEV void q4_nibbles_h2(uint32_t w, h2 &lo01, h2 &lo23, h2 &hi01, h2 &hi23) {
+    const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
+    const h2 bias = {(_Float16)1024.0f, (_Float16)1024.0f};
+    lo01 = as_h2(__builtin_amdgcn_perm(0x64646464u, lo, 0x05010400u)) - bias;
+    lo23 = as_h2(__builtin_amdgcn_perm(0x64646464u, lo, 0x05030402u)) - bias;
+    hi01 = as_h2(__builtin_amdgcn_perm(0x64646464u, hi, 0x05010400u)) - bias;
+    hi23 = as_h2(__builtin_amdgcn_perm(0x64646464u, hi, 0x05030402u)) - bias;
+}
+
+/* --------------------------------------------------------------- Q6_K */
+
+/* Six-bit quants minus 32 as exact fp16 pairs: inputs are 4 ql bytes
+ * (nibble select by `shift` 0/4) and 4 qh bytes (2-bit field at qshift). */
+DEV void q6_h2(uint32_t ql, uint32_t qh, int shift, int qshift, h2 &p01, h2 &p23) {
+    uint32_t v = ((ql >> shift) & 0x0F0F0F0Fu) | (((qh >> qshift) & 0x03030303u) << 4);
+    const h2 bias = {(_Float16)1056.0f, (_Float16)1056.0f};  /* 1024 + 32 */
+    p01 = as_h2(__builtin_amdgcn_perm(0x64646464u, v, 0x05010400u)) - bias;
+    p23 = as_h2(__builtin_amdgcn_perm(0x64646464u, v, 0x05030402u)) - bias;
+}
+
+/* Signed int8 quants as exact fp16 pairs (flip the sign bit, bias 1152). */
+DEV void q8_h2(uint32_t w, h2 &p01, h2 &p23) {
+    uint32_t v = w ^ 0x80808080u;
+    const h2 bias = {(_Float16)1152.0f, (_Float16)1152.0f};
+    p01 = as_h2(__builtin_amdgcn_perm(0x64646464u, v, 0x05010400u)) - bias;
+    p23 = as_h2(__builtin_amdgcn_perm(0x64646464u, v, 0x05030402u)) - bias;
+}
+
+/* Loads that only need 2-byte alignment (Q6_K and Q8_0 blocks are 210 and
+ * 34 bytes long): aligned dword loads realigned with v_alignbyte.  They read
+ * up to 4 bytes past the last byte asked for; uploads carry tail padding. */
+typedef const __attribute__((address_space(1))) uint32_t *gp32;
+DEV gp32 gptr32(const uint8_t *p) { return (gp32)(uintptr_t)p; }
+DEV uint32_t ld_u32_a2(const uint8_t *p) {
+    uintptr_t a = (uintptr_t)p;
+    gp32 q = gptr32((const uint8_t *)(a & ~(uintptr_t)3));
+    uint32_t s = (uint32_t)(a & 3);
+    return __builtin_amdgcn_alignbyte(q[1], q[0], s);
+}
+DEV u2 ld_u32x2_a2(const uint8_t *p) {
+    uintptr_t a = (uintptr_t)p;
+    gp32 q = gptr32((const uint8_t *)(a & ~(uintptr_t)3));
+    uint32_t s = (uint32_t)(a & 3);
+    uint32_t w0 = q[0], w1 = q[1], w2 = q[2];
+    return u2{__builtin_amdgcn_alignbyte(w1, w0, s), __builtin_amdgcn_alignbyte(w2, w1, s)};
+}
+DEV u4 ld_u32x4_a2(const uint8_t *p) {
+    uintptr_t a = (uintptr_t)p;
+    gp32 q = gptr32((const uint8_t *)(a & ~(uintptr_t)3));
+    uint32_t s = (uint32_t)(a & 3);
+    uint32_t w0 = q[0], w1 = q[1], w2 = q[2], w3 = q[3], w4 = q[4];
+    return u4{__builtin_amdgcn_alignbyte(w1, w0, s), __builtin_amdgcn_alignbyte(w2, w1, s),
+              __builtin_amdgcn_alignbyte(w3, w2, s), __builtin_amdgcn_alignbyte(w4, w3, s)};
+}
+DEV u4 ld_u4(const uint8_t *p) {
+    typedef const __attribute__((address_space(1))) u4 *gp4;
+    return *(gp4)(uintptr_t)p;
+}
+
+/* ------------------------------------------------------------ dots */
+DEV float dot2(h2 a, h2 b, float c) { return __builtin_amdgcn_fdot2(a, b, c, false); }

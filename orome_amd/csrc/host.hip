@@ -1,0 +1,366 @@
+/*
+ * host.hip -- C ABI: context, device memory, and the MoE forward driver.
+ *
+ * Replaces the reference's Metal context (inference/src/metal.m:41-256) and
+ * the encoding of the MoE stages (inference/src/engine.m:158-340, routing at
+ * 656-685).  All work of one call is queued on the context's stream in
+ * order; there are no host synchronisations inside a forward.
+ */
+#include <hip/hip_runtime.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include "kernels.h"
+#include "orome_internal.h"
+#include "orome_moe.h"
+
+static thread_local char g_err[512];
+
+extern "C" int orome_fail(int code, const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof g_err, fmt, ap);
+    va_end(ap);
+    fprintf(stderr, "[hip] %s\n", g_err);
+    return code;
+}
+
+extern "C" const char *orome_last_error(void) { return g_err; }
+extern "C" const char *orome_version(void) { return "orome-mi355x 0.1 (gfx950)"; }
+
+#define HIP_OK(expr, code)                                                                  \
+    do {                                                                                    \
+        hipError_t e_ = (expr);                                                             \
+        if (e_ != hipSuccess)                                                               \
+            return orome_fail(code, "%s failed: %s", #expr, hipGetErrorString(e_));         \
+    } while (0)
+
+struct orome_hip_ctx {
+    int device;
+    hipStream_t stream;
+    ModelConfig cfg;
+    int tmax, kmax, path;
+    /* scratch */
+    float *logits, *w, *sgl, *y, *ysh, *xnorm;
+    int32_t *idx;
+    uint32_t *offsets, *pairs, *pos, *list, *counter, *tiles;
+    _Float16 *x16, *act, *act_sh;
+    void *arena;
+    size_t arena_bytes;
+    int last_T, last_K;
+};
+
+static int set_dev(orome_hip_ctx *c) {
+    HIP_OK(hipSetDevice(c->device), OROME_EHIP);
+    return OROME_OK;
+}
+
+extern "C" orome_hip_ctx *orome_hip_create(const ModelConfig *cfg, int max_tokens, int device) {
+    if (!cfg || max_tokens < 1 || cfg->hidden_dim <= 0 || cfg->num_experts <= 0 ||
+        cfg->moe_intermediate <= 0) {
+        orome_fail(OROME_EINVAL, "orome_hip_create: invalid config or max_tokens");
+        return NULL;
+    }
+    int ndev = 0;
+    if (hipGetDeviceCount(&ndev) != hipSuccess || device < 0 || device >= ndev) {
+        orome_fail(OROME_EHIP, "orome_hip_create: no HIP device %d (count %d)", device, ndev);
+        return NULL;
+    }
+    orome_hip_ctx *c = (orome_hip_ctx *)calloc(1, sizeof *c);
+    c->device = device;
+    c->cfg = *cfg;
+    c->tmax = max_tokens;
+    c->kmax = OROME_MAX_ACTIVE;
+    if (hipSetDevice(device) != hipSuccess || hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess) {
+        orome_fail(OROME_EHIP, "orome_hip_create: stream creation failed");
+        free(c);
+        return NULL;
+    }
+    const size_t T = (size_t)max_tokens, E = (size_t)cfg->num_experts, K = (size_t)c->kmax,
+                 H = (size_t)cfg->hidden_dim, M = (size_t)cfg->moe_intermediate,
+                 S = (size_t)(cfg->shared_intermediate > 0 ? cfg->shared_intermediate : 0);
+    const size_t ntile = (T * K) / GEMM_TILE_M + E + T / GEMM_TILE_M + 2;
+    struct { void **p; size_t bytes; } parts[] = {
+        {(void **)&c->logits, T * (E + 1) * 4}, {(void **)&c->idx, T * K * 4},
+        {(void **)&c->w, T * K * 4},           {(void **)&c->sgl, T * 4},
+        {(void **)&c->offsets, (E + 1) * 4},    {(void **)&c->pairs, T * K * 4},
+        {(void **)&c->pos, T * K * 4},          {(void **)&c->list, (2 * E + 2) * 4},
+        {(void **)&c->counter, 256},            {(void **)&c->tiles, (1 + 3 * ntile) * 4},
+        {(void **)&c->x16, T * H * 2},          {(void **)&c->act, T * K * M * 2},
+        {(void **)&c->act_sh, T * (S ? S : 1) * 2}, {(void **)&c->y, T * K * H * 4},
+        {(void **)&c->ysh, T * H * 4},          {(void **)&c->xnorm, T * H * 4},
+    };
+    size_t total = 0;
+    for (auto &p : parts) total += (p.bytes + 255) / 256 * 256;
+    if (hipMalloc(&c->arena, total) != hipSuccess) {
+        orome_fail(OROME_ENOMEM, "orome_hip_create: scratch arena of %zu bytes", total);
+        (void)hipStreamDestroy(c->stream);
+        free(c);
+        return NULL;
+    }
+    c->arena_bytes = total;
+    size_t off = 0;
+    for (auto &p : parts) {
+        *p.p = (uint8_t *)c->arena + off;
+        off += (p.bytes + 255) / 256 * 256;
+    }
+    /* the routing kernel's completion counter must start at zero; the kernel
+     * returns it to zero itself, so this is the only clear ever needed */
+    if (hipMemset(c->arena, 0, total) != hipSuccess || hipDeviceSynchronize() != hipSuccess) {
+        orome_fail(OROME_EHIP, "orome_hip_create: scratch clear failed");
+        (void)hipFree(c->arena);
+        (void)hipStreamDestroy(c->stream);
+        free(c);
+        return NULL;
+    }
+    return c;
+}
+
+extern "C" void orome_hip_destroy(orome_hip_ctx *c) {
+    if (!c) return;
+    (void)hipSetDevice(c->device);
+    (void)hipStreamSynchronize(c->stream);
+    (void)hipFree(c->arena);
+    (void)hipStreamDestroy(c->stream);
+    free(c);
+}
+
+extern "C" int orome_hip_sync(orome_hip_ctx *c) {
+    if (!c) return orome_fail(OROME_EINVAL, "orome_hip_sync: NULL ctx");
+    HIP_OK(hipStreamSynchronize(c->stream), OROME_EHIP);
+    return OROME_OK;
+}
+
+extern "C" void *orome_hip_get_stream(orome_hip_ctx *c) { return c ? (void *)c->stream : NULL; }
+
+extern "C" int orome_hip_set_path(orome_hip_ctx *c, int path) {
+    if (!c || path < OROME_PATH_AUTO || path > OROME_PATH_MFMA)
+        return orome_fail(OROME_EINVAL, "orome_hip_set_path: bad argument");
+    c->path = path;
+    return OROME_OK;
+}
+
+extern "C" void *orome_hip_malloc(orome_hip_ctx *c, size_t bytes) {
+    if (!c) { orome_fail(OROME_EINVAL, "orome_hip_malloc: NULL ctx"); return NULL; }
+    if (set_dev(c)) return NULL;
+    void *p = NULL;
+    /* 256 bytes of tail padding: the 2-byte-aligned block loads of the Q6_K /
+     * Q8_0 kernels may touch up to 4 bytes past a tensor's last block */
+    if (hipMalloc(&p, bytes + 256) != hipSuccess) {
+        orome_fail(OROME_ENOMEM, "hipMalloc(%zu) failed", bytes);
+        return NULL;
+    }
+    return p;
+}
+
+extern "C" int orome_hip_free(orome_hip_ctx *c, void *p) {
+    if (!c) return orome_fail(OROME_EINVAL, "orome_hip_free: NULL ctx");
+    if (set_dev(c)) return OROME_EHIP;
+    HIP_OK(hipFree(p), OROME_EHIP);
+    return OROME_OK;
+}
+
+extern "C" int orome_hip_htod(orome_hip_ctx *c, void *dst, const void *src, size_t bytes) {
+    if (!c || (!dst && bytes) || (!src && bytes)) return orome_fail(OROME_EINVAL, "orome_hip_htod: bad argument");
+    if (set_dev(c)) return OROME_EHIP;
+    HIP_OK(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, c->stream), OROME_EHIP);
+    HIP_OK(hipStreamSynchronize(c->stream), OROME_EHIP);
+    return OROME_OK;
+}
+
+extern "C" int orome_hip_dtoh(orome_hip_ctx *c, void *dst, const void *src, size_t bytes) {
+    if (!c || (!dst && bytes) || (!src && bytes)) return orome_fail(OROME_EINVAL, "orome_hip_dtoh: bad argument");
+    if (set_dev(c)) return OROME_EHIP;
+    HIP_OK(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, c->stream), OROME_EHIP);
+    HIP_OK(hipStreamSynchronize(c->stream), OROME_EHIP);
+    return OROME_OK;
+}
+
+/* --------------------------------------------------------------- forward */
+
+static const uint8_t *dev_addr(const void *buffer, size_t offset) {
+    return buffer ? (const uint8_t *)buffer + offset : NULL;
+}
+
+static int kfmt(QuantFormat f) {
+    switch (f) {
+        case QFMT_GGUF_Q4_K: return 0;
+        case QFMT_GGUF_Q6_K: return 2;
+        case QFMT_GGUF_Q8_0: return 3;
+        default: return -1;
+    }
+}
+
+static int launch_rc(int rc, const char *what) {
+    if (rc == 0) return OROME_OK;
+    if (rc == -2) return orome_fail(OROME_EUNSUPPORTED, "%s: shape or format not supported", what);
+    if (rc == -1) return orome_fail(OROME_EINVAL, "%s: invalid argument", what);
+    return orome_fail(OROME_EHIP, "%s: launch failed: %s", what, hipGetErrorString(hipGetLastError()));
+}
+
+#define LAUNCH(call, what)                  \
+    do {                                    \
+        int rc_ = launch_rc((call), (what)); \
+        if (rc_) return rc_;                \
+    } while (0)
+
+extern "C" int orome_moe_forward(orome_hip_ctx *c, const ModelConfig *cfg, const ExpertLayerRef *elr,
+                                 const LayerTensorCache *lt, const float *x, const float *h_in,
+                                 float *h_out, int T, int K) {
+    if (!c || !cfg || !elr || !lt || !x || !h_out)
+        return orome_fail(OROME_EINVAL, "orome_moe_forward: NULL argument");
+    const int H = cfg->hidden_dim, E = cfg->num_experts, M = cfg->moe_intermediate;
+    if (H != c->cfg.hidden_dim || E != c->cfg.num_experts || M != c->cfg.moe_intermediate ||
+        cfg->shared_intermediate > c->cfg.shared_intermediate)
+        return orome_fail(OROME_EINVAL, "orome_moe_forward: config differs from the context's");
+    if (T < 1 || T > c->tmax) return orome_fail(OROME_EINVAL, "orome_moe_forward: T=%d outside 1..%d", T, c->tmax);
+    if (K < 1 || K > OROME_MAX_ACTIVE || K > E)
+        return orome_fail(OROME_EINVAL, "orome_moe_forward: K=%d outside 1..min(%d, E)", K, OROME_MAX_ACTIVE);
+    if (H % 256 || M % 256) return orome_fail(OROME_EUNSUPPORTED, "orome_moe_forward: H and M must be multiples of 256");
+    if (!elr->buffer || elr->gate.format != QFMT_GGUF_Q4_K || elr->up.format != QFMT_GGUF_Q4_K)
+        return orome_fail(OROME_EUNSUPPORTED, "orome_moe_forward: routed gate/up must be Q4_K");
+    if (kfmt(elr->down.format) != 0 && kfmt(elr->down.format) != 2)
+        return orome_fail(OROME_EUNSUPPORTED, "orome_moe_forward: routed down must be Q4_K or Q6_K");
+    if (!lt->routing_gate.buffer || lt->routing_gate.format != QFMT_F32)
+        return orome_fail(OROME_EUNSUPPORTED, "orome_moe_forward: router must be F32");
+    const int S = lt->shared_gate.buffer ? (int)lt->shared_gate.out_dim : 0;
+    SharedSide sh = {NULL, NULL, NULL, 0, 0, 0};
+    if (S) {
+        if (S > c->cfg.shared_intermediate)
+            return orome_fail(OROME_EINVAL, "orome_moe_forward: shared expert larger than the context's");
+        if (!lt->shared_up.buffer || !lt->shared_down.buffer ||
+            lt->shared_gate.format != lt->shared_up.format || kfmt(lt->shared_gate.format) == 2 ||
+            kfmt(lt->shared_gate.format) < 0 || kfmt(lt->shared_down.format) < 0)
+            return orome_fail(OROME_EUNSUPPORTED, "orome_moe_forward: shared expert formats");
+        sh.gate = dev_addr(lt->shared_gate.buffer, lt->shared_gate.offset);
+        sh.up = dev_addr(lt->shared_up.buffer, lt->shared_up.offset);
+        sh.down = dev_addr(lt->shared_down.buffer, lt->shared_down.offset);
+        sh.gate_fmt = kfmt(lt->shared_gate.format);
+        sh.down_fmt = kfmt(lt->shared_down.format);
+        sh.S = S;
+    }
+    ExpertSide ex;
+    ex.gate = dev_addr(elr->buffer, elr->gate.offset);
+    ex.up = dev_addr(elr->buffer, elr->up.offset);
+    ex.down = dev_addr(elr->buffer, elr->down.offset);
+    ex.gate_stride = elr->gate.expert_stride;
+    ex.up_stride = elr->up.expert_stride;
+    ex.down_stride = elr->down.expert_stride;
+    ex.gate_fmt = 0;
+    ex.down_fmt = kfmt(elr->down.format);
+    if (set_dev(c)) return OROME_EHIP;
+
+    RouteArgs a;
+    a.W = (const float *)dev_addr(lt->routing_gate.buffer, lt->routing_gate.offset);
+    a.wsg = lt->shared_expert_gate.buffer && lt->shared_expert_gate.format == QFMT_F32
+                ? (const float *)dev_addr(lt->shared_expert_gate.buffer, lt->shared_expert_gate.offset)
+                : NULL;
+    a.bias = lt->routing_bias.buffer ? (const float *)dev_addr(lt->routing_bias.buffer, lt->routing_bias.offset) : NULL;
+    a.x = x;
+    a.T = T; a.E = E; a.H = H; a.K = K;
+    a.logits = c->logits; a.idx = c->idx; a.w = c->w; a.sgl = c->sgl;
+    a.offsets = c->offsets; a.pairs = c->pairs; a.pos = c->pos; a.list = c->list;
+    a.counter = c->counter;
+
+    int path = c->path;
+    if (path == OROME_PATH_AUTO) path = T <= 8 ? OROME_PATH_GEMV : OROME_PATH_MFMA;
+    hipStream_t s = c->stream;
+    if (path == OROME_PATH_GEMV) {
+        if (T > 8) return orome_fail(OROME_EUNSUPPORTED, "GEMV path handles T <= 8 (T=%d)", T);
+        LAUNCH(launch_route_small(a, s), "route");
+        LAUNCH(launch_gemv_gate_up(ex, sh, x, T, H, M, K, E, c->list, c->pairs, c->act, c->act_sh, s),
+               "gemv gate/up");
+        LAUNCH(launch_gemv_down_combine(ex, sh, c->act, c->act_sh, T, H, M, K, E, c->list, c->pairs,
+                                        c->w, c->sgl, h_in, h_out, s),
+               "gemv down+combine");
+    } else {
+        LAUNCH(launch_route_logits(a, s), "router logits");
+        LAUNCH(launch_topk(a, s), "top-k");
+        LAUNCH(launch_dispatch(a, c->tiles, GEMM_TILE_M, S ? 1 : 0, s), "dispatch");
+        LAUNCH(launch_to_f16(x, T, H, c->x16, s), "fp16 staging");
+        const int ntiles = (T * K) / GEMM_TILE_M + E + (S ? (T + GEMM_TILE_M - 1) / GEMM_TILE_M : 0);
+        LAUNCH(launch_gemm_gate_up(ex, sh, c->x16, T, H, M, K, E, c->tiles, ntiles, c->pairs, c->act,
+                                   c->act_sh, s),
+               "grouped gate/up");
+        LAUNCH(launch_gemm_down(ex, sh, c->act, c->act_sh, T, H, M, K, E, c->tiles, ntiles, c->y,
+                                c->ysh, s),
+               "grouped down");
+        LAUNCH(launch_combine(c->y, c->ysh, c->pos, c->w, c->sgl, S ? 1 : 0, h_in, h_out, T, H, K, s),
+               "combine");
+    }
+    c->last_T = T;
+    c->last_K = K;
+    return OROME_OK;
+}
+
+extern "C" int orome_moe_layer_forward(orome_hip_ctx *c, const ModelConfig *cfg,
+                                       const ExpertLayerRef *elr, const LayerTensorCache *lt,
+                                       float *h, int T, int K) {
+    if (!c || !cfg || !lt || !h) return orome_fail(OROME_EINVAL, "orome_moe_layer_forward: NULL argument");
+    if (T < 1 || T > c->tmax) return orome_fail(OROME_EINVAL, "orome_moe_layer_forward: T=%d", T);
+    if (set_dev(c)) return OROME_EHIP;
+    const float *nw = lt->post_norm.buffer && lt->post_norm.format == QFMT_F32
+                          ? (const float *)dev_addr(lt->post_norm.buffer, lt->post_norm.offset)
+                          : NULL;
+    LAUNCH(launch_rmsnorm(h, nw, T, cfg->hidden_dim, cfg->rms_norm_eps, c->xnorm, c->stream), "rmsnorm");
+    return orome_moe_forward(c, cfg, elr, lt, c->xnorm, h, h, T, K);
+}
+
+extern "C" int orome_moe_stack_forward(orome_hip_ctx *c, const ModelConfig *cfg,
+                                       const ExpertLayerRef *elrs, const LayerTensorCache *lts,
+                                       int n_layers, float *h, int T, int K) {
+    if (!elrs || !lts || n_layers < 0) return orome_fail(OROME_EINVAL, "orome_moe_stack_forward: bad arguments");
+    for (int l = 0; l < n_layers; l++) {
+        int rc = orome_moe_layer_forward(c, cfg, &elrs[l], &lts[l], h, T, K);
+        if (rc) return rc;
+    }
+    return OROME_OK;
+}
+
+extern "C" int orome_moe_debug_outputs(orome_hip_ctx *c, float *logits, int32_t *idx, float *w,
+                                       uint32_t *offsets, uint32_t *pairs) {
+    if (!c) return orome_fail(OROME_EINVAL, "orome_moe_debug_outputs: NULL ctx");
+    if (!c->last_T) return orome_fail(OROME_EINVAL, "orome_moe_debug_outputs: no forward yet");
+    const size_t T = (size_t)c->last_T, K = (size_t)c->last_K, E = (size_t)c->cfg.num_experts;
+    int rc = 0;
+    if (!rc && logits) rc = orome_hip_dtoh(c, logits, c->logits, T * (E + 1) * 4);
+    if (!rc && idx) rc = orome_hip_dtoh(c, idx, c->idx, T * K * 4);
+    if (!rc && w) rc = orome_hip_dtoh(c, w, c->w, T * K * 4);
+    if (!rc && offsets) rc = orome_hip_dtoh(c, offsets, c->offsets, (E + 1) * 4);
+    if (!rc && pairs) rc = orome_hip_dtoh(c, pairs, c->pairs, T * K * 4);
+    if (!rc) rc = orome_hip_sync(c);
+    return rc;
+}
+
+extern "C" int orome_moe_topk(orome_hip_ctx *c, const float *logits, const float *bias, int T, int E,
+                              int K, int32_t *idx, float *w) {
+    if (!c || !logits || !idx || !w) return orome_fail(OROME_EINVAL, "orome_moe_topk: NULL argument");
+    if (T < 1 || T > c->tmax || E < 1 || E > 1024 || K < 1 || K > OROME_MAX_ACTIVE || K > E)
+        return orome_fail(OROME_EINVAL, "orome_moe_topk: bad shape T=%d E=%d K=%d", T, E, K);
+    if (set_dev(c)) return OROME_EHIP;
+    RouteArgs a;
+    memset(&a, 0, sizeof a);
+    a.bias = bias; a.T = T; a.E = E; a.K = K;
+    a.logits = (float *)logits; a.idx = idx; a.w = w; a.sgl = c->sgl;
+    LAUNCH(launch_topk(a, c->stream), "top-k");
+    return OROME_OK;
+}
+
+extern "C" int orome_dequant_rows(orome_hip_ctx *c, QuantFormat fmt, const void *src, uint32_t rows,
+                                  uint32_t in_dim, float *out) {
+    if (!c || !src || !out) return orome_fail(OROME_EINVAL, "orome_dequant_rows: NULL argument");
+    if (set_dev(c)) return OROME_EHIP;
+    LAUNCH(launch_dequant(kfmt(fmt), (const uint8_t *)src, rows, in_dim, out, NULL, c->stream), "dequant");
+    return OROME_OK;
+}
+
+extern "C" int orome_dequant_rows_f16(orome_hip_ctx *c, QuantFormat fmt, const void *src,
+                                      uint32_t rows, uint32_t in_dim, uint16_t *out) {
+    if (!c || !src || !out) return orome_fail(OROME_EINVAL, "orome_dequant_rows_f16: NULL argument");
+    if (set_dev(c)) return OROME_EHIP;
+    LAUNCH(launch_dequant(kfmt(fmt), (const uint8_t *)src, rows, in_dim, NULL, (_Float16 *)out, c->stream),
+           "dequant f16");
+    return OROME_OK;
+}

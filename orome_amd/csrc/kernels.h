@@ -1,0 +1,78 @@
+/* kernels.h -- launch interface between the C-ABI host code and the kernels. */
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+/* Compact list of the experts a call touches, written by the routing kernels:
+ *   list[0]            n_active
+ *   list[1 + u]        expert id of active slot u (ascending), u < n_active
+ *   list[1 + E + u]    first sorted position of slot u; entry n_active = T*K */
+#define OROME_MAXK 16
+
+#define ACT_N(list) ((list)[0])
+#define ACT_E(list, u) ((list)[1 + (u)])
+#define ACT_OFF(list, E, u) ((list)[1 + (E) + (u)])
+
+struct RouteArgs {
+    const float *W;      /* [E][H] */
+    const float *wsg;    /* [H] or NULL */
+    const float *bias;   /* [E] or NULL */
+    const float *x;      /* [T][H] */
+    int T, E, H, K;
+    float *logits;       /* [T][E+1] */
+    int32_t *idx;        /* [T][K] */
+    float *w;            /* [T][K] */
+    float *sgl;          /* [T] shared-gate logit */
+    uint32_t *offsets;   /* [E+1] */
+    uint32_t *pairs;     /* [T*K] sorted pair ids */
+    uint32_t *pos;       /* [T*K] sorted position of pair p */
+    uint32_t *list;      /* active list, 2E+2 entries */
+    uint32_t *counter;   /* one zeroed word, returned to zero by the kernel */
+};
+
+struct ExpertSide {
+    const uint8_t *gate, *up, *down;  /* device addresses of expert 0 */
+    size_t gate_stride, up_stride, down_stride;
+    int gate_fmt, down_fmt;           /* gate and up share a format */
+};
+
+struct SharedSide {
+    const uint8_t *gate, *up, *down;  /* NULL gate: no shared expert */
+    int gate_fmt, down_fmt;
+    int S;
+};
+
+int launch_route_small(const RouteArgs &a, hipStream_t s);
+int launch_route_logits(const RouteArgs &a, hipStream_t s);
+int launch_topk(const RouteArgs &a, hipStream_t s);
+int launch_dispatch(const RouteArgs &a, uint32_t *tiles, int tile_m, int has_shared, hipStream_t s);
+
+int launch_gemv_gate_up(const ExpertSide &ex, const SharedSide &sh, const float *x, int T, int H,
+                        int M, int K, int E, const uint32_t *list, const uint32_t *pairs,
+                        _Float16 *act, _Float16 *act_sh, hipStream_t s);
+int launch_gemv_down_combine(const ExpertSide &ex, const SharedSide &sh, const _Float16 *act,
+                             const _Float16 *act_sh, int T, int H, int M, int K, int E,
+                             const uint32_t *list, const uint32_t *pairs, const float *w,
+                             const float *sgl, const float *h_in, float *h_out, hipStream_t s);
+
+int launch_rmsnorm(const float *h, const float *w, int T, int H, float eps, float *x, hipStream_t s);
+int launch_dequant(int fmt, const uint8_t *src, uint32_t rows, uint32_t n, float *out32,
+                   _Float16 *out16, hipStream_t s);
+
+/* prefill (MFMA) path */
+int launch_to_f16(const float *x, int T, int H, _Float16 *x16, hipStream_t s);
+int launch_gemm_gate_up(const ExpertSide &ex, const SharedSide &sh, const _Float16 *x16, int T,
+                        int H, int M, int K, int E, const uint32_t *tiles, int n_tiles_max,
+                        const uint32_t *pairs, _Float16 *act, _Float16 *act_sh, hipStream_t s);
+int launch_gemm_down(const ExpertSide &ex, const SharedSide &sh, const _Float16 *act,
+                     const _Float16 *act_sh, int T, int H, int M, int K, int E,
+                     const uint32_t *tiles, int n_tiles_max, float *y, float *ysh,
+                     hipStream_t s);
+int launch_combine(const float *y, const float *ysh, const uint32_t *pos, const float *w,
+                   const float *sgl, int has_shared, const float *h_in, float *h_out, int T,
+                   int H, int K, hipStream_t s);
+
+/* tile list for the grouped GEMM: tiles[0] = count, then (expert, first, rows)
+ * triples; expert == E denotes the shared expert over all T tokens */
+#define GEMM_TILE_M 32

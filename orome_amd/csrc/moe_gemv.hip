@@ -1,0 +1,443 @@
+/*
+ * moe_gemv.hip -- decode-path (T <= 8) expert products: fused dequant GEMV.
+ *
+ * Bandwidth-bound: every weight byte is read once per call, the expert set
+ * is deduplicated across the batch (one pass per active expert, over the
+ * tokens routed to it), and no matrix cores are used.
+ *
+ * Work unit ("chunk") = 32 weights of one row, held by one lane:
+ *   Q4_K  a 16-byte run of quant bytes (16 low + 16 high nibbles) plus the
+ *         super-block header (d, dmin, scales; eight lanes share it);
+ *   Q6_K  8 positions l of one 128-weight half: 4 x 8 weights at l, l+32,
+ *         l+64, l+96 (ql/qh bytes, four int8 scales);
+ *   Q8_0  one 34-byte block.
+ * Quants become exact fp16 values (v_perm into the 0x64xx exponent, minus
+ * the bias), are multiplied with fp16 activations by v_dot2_f32_f16 (exact
+ * products, fp32 sums), and the per-sub-block scale/min is applied in fp32:
+ *   sum_j (a*q_j - b) x_j = a * sum_j q_j x_j - b * sum_j x_j.
+ * Activations are rounded to fp16 exactly as the reference stages them
+ * (half(x): inference/src/shaders.metal:2252-2255, 2612-2613).
+ *
+ * Restates batch_expert_gate_up_swiglu_q4k_dyn (shaders.metal:2232-2310),
+ * shared_gate_up_swiglu_q4k/_q8_0 (2316-2445), batch_expert_down_q4k_dyn
+ * (2590-2668), dequant_matvec_q6k/_q8_0 (1888-1988, 1627-1701) and
+ * moe_combine_copy_sq_k8 (1079-1135).
+ */
+#include "dev_common.h"
+#include "kernels.h"
+
+enum { FQ4K = 0, FQ5K = 1, FQ6K = 2, FQ8 = 3 };
+
+DEV size_t row_bytes(int fmt, int n) {
+    return fmt == FQ4K ? (size_t)(n / 256) * 144 : fmt == FQ6K ? (size_t)(n / 256) * 210 : (size_t)(n / 32) * 34;
+}
+
+/* 16 consecutive fp32 -> 8 fp16 pairs (RNE) and the sum of the rounded values */
+DEV float load_x16_f32(const float *p, h2 *o) {
+    float s = 0.0f;
+#pragma unroll
+    for (int v = 0; v < 4; v++) {
+        f4 a = *(const f4 *)(p + 4 * v);
+        o[2 * v] = h2{(_Float16)a.x, (_Float16)a.y};
+        o[2 * v + 1] = h2{(_Float16)a.z, (_Float16)a.w};
+    }
+    const h2 one = {(_Float16)1.0f, (_Float16)1.0f};
+#pragma unroll
+    for (int v = 0; v < 8; v++) s = dot2(o[v], one, s);
+    return s;
+}
+/* 8 consecutive fp16 (16 bytes) -> 4 pairs */
+DEV void load_h8(const _Float16 *p, h2 *o) {
+    u4 v = ld_u4((const uint8_t *)p);
+    o[0] = as_h2(v.x); o[1] = as_h2(v.y); o[2] = as_h2(v.z); o[3] = as_h2(v.w);
+}
+DEV float hsum(const h2 *o, int n) {
+    const h2 one = {(_Float16)1.0f, (_Float16)1.0f};
+    float s = 0.0f;
+    for (int v = 0; v < n; v++) s = dot2(o[v], one, s);
+    return s;
+}
+
+/* Q4_K chunk: raw bytes */
+struct Q4Raw {
+    u4 q, hdr;
+};
+DEV Q4Raw q4_load(const uint8_t *row, int c) {
+    const uint8_t *sb = row + (c >> 3) * 144;
+    return Q4Raw{ld_u4(sb + 16 + (c & 7) * 16), ld_u4(sb)};
+}
+DEV void q4_pos(int c, int &klo) { klo = (c >> 3) * 256 + ((c & 7) >> 1) * 64 + (c & 1) * 16; }
+DEV float q4_dot(const Q4Raw &r, int c, const h2 *xl, const h2 *xh, float Xl, float Xh) {
+    Q4Affine af = q4k_affine(r.hdr, (c & 7) >> 1);
+    float sl = 0.0f, sh = 0.0f;
+    uint32_t w[4] = {r.q.x, r.q.y, r.q.z, r.q.w};
+#pragma unroll
+    for (int d = 0; d < 4; d++) {
+        h2 l01, l23, h01, h23;
+        q4_nibbles_h2(w[d], l01, l23, h01, h23);
+        sl = dot2(l01, xl[2 * d], sl);
+        sl = dot2(l23, xl[2 * d + 1], sl);
+        sh = dot2(h01, xh[2 * d], sh);
+        sh = dot2(h23, xh[2 * d + 1], sh);
+    }
+    return (af.a_lo * sl + af.a_hi * sh) - (af.b_lo * Xl + af.b_hi * Xh);
+}
+
+/* Q8_0 chunk = block c */
+struct Q8Raw {
+    u4 q0, q1;
+    uint32_t d;
+};
+DEV Q8Raw q8_load(const uint8_t *row, int c) {
+    const uint8_t *b = row + c * 34;
+    return Q8Raw{ld_u32x4_a2(b + 2), ld_u32x4_a2(b + 18), ld_u32_a2(b)};
+}
+DEV float q8_dot(const Q8Raw &r, const h2 *x /*16 pairs*/) {
+    uint32_t w[8] = {r.q0.x, r.q0.y, r.q0.z, r.q0.w, r.q1.x, r.q1.y, r.q1.z, r.q1.w};
+    float s = 0.0f;
+#pragma unroll
+    for (int d = 0; d < 8; d++) {
+        h2 p01, p23;
+        q8_h2(w[d], p01, p23);
+        s = dot2(p01, x[2 * d], s);
+        s = dot2(p23, x[2 * d + 1], s);
+    }
+    return f16_bits_to_f32(r.d) * s;
+}
+
+/* Q6_K chunk c: sb = c>>3, half h = (c>>2)&1, positions l0 = 8*(c&3) .. +7 */
+struct Q6Raw {
+    u2 qa, qb, qh, sc;
+    uint32_t d;
+};
+DEV Q6Raw q6_load(const uint8_t *row, int c) {
+    const uint8_t *sb = row + (c >> 3) * 210;
+    const int h = (c >> 2) & 1, l0 = 8 * (c & 3);
+    return Q6Raw{ld_u32x2_a2(sb + h * 64 + l0), ld_u32x2_a2(sb + h * 64 + 32 + l0),
+                 ld_u32x2_a2(sb + 128 + h * 32 + l0), ld_u32x2_a2(sb + 192 + h * 8),
+                 ld_u32_a2(sb + 208)};
+}
+DEV void q6_pos(int c, int &k0) { k0 = (c >> 3) * 256 + ((c >> 2) & 1) * 128 + 8 * (c & 3); }
+DEV float sc8(u2 sc, int i) {
+    uint32_t w = i < 4 ? sc.x : sc.y;
+    return (float)(int8_t)((w >> (8 * (i & 3))) & 0xFF);
+}
+/* x: 4 groups (offsets 0, 32, 64, 96) of 4 pairs */
+DEV float q6_dot(const Q6Raw &r, int c, const h2 *x) {
+    float s[4] = {0, 0, 0, 0};
+    uint32_t qa[2] = {r.qa.x, r.qa.y}, qb[2] = {r.qb.x, r.qb.y}, qh[2] = {r.qh.x, r.qh.y};
+#pragma unroll
+    for (int m = 0; m < 2; m++) {
+        h2 p01, p23;
+        q6_h2(qa[m], qh[m], 0, 0, p01, p23);
+        s[0] = dot2(p01, x[0 * 4 + 2 * m], s[0]);
+        s[0] = dot2(p23, x[0 * 4 + 2 * m + 1], s[0]);
+        q6_h2(qb[m], qh[m], 0, 2, p01, p23);
+        s[1] = dot2(p01, x[1 * 4 + 2 * m], s[1]);
+        s[1] = dot2(p23, x[1 * 4 + 2 * m + 1], s[1]);
+        q6_h2(qa[m], qh[m], 4, 4, p01, p23);
+        s[2] = dot2(p01, x[2 * 4 + 2 * m], s[2]);
+        s[2] = dot2(p23, x[2 * 4 + 2 * m + 1], s[2]);
+        q6_h2(qb[m], qh[m], 4, 6, p01, p23);
+        s[3] = dot2(p01, x[3 * 4 + 2 * m], s[3]);
+        s[3] = dot2(p23, x[3 * 4 + 2 * m + 1], s[3]);
+    }
+    const int is = (c & 3) >> 1;
+    float d = f16_bits_to_f32(r.d);
+    return d * (sc8(r.sc, is) * s[0] + sc8(r.sc, is + 2) * s[1] + sc8(r.sc, is + 4) * s[2] +
+                sc8(r.sc, is + 6) * s[3]);
+}
+
+/* =================================================================== */
+/* gate/up + SiLU-GLU.  Block = 4 waves x RPW rows (gate and up of each row).
+ * Grid = [routed blocks: Umax slots x M/(4*RPW)] + [shared: S/(4*RPW)]. */
+struct GUArgs {
+    const uint8_t *gate, *up;
+    size_t gate_stride, up_stride;
+    const uint8_t *sh_gate, *sh_up;
+    int sh_fmt, S;
+    const float *x;
+    int T, H, M, K, E;
+    const uint32_t *list, *pairs;
+    _Float16 *act, *act_sh;
+    int routed_blocks;
+};
+
+template <int NT, int RPW, int SFMT>
+DEV void gu_body(const GUArgs &a, const uint8_t *gbase, const uint8_t *ubase, int rows_total,
+                 int r0, int n, const int *tok, _Float16 *out, int out_ld, int lane) {
+    (void)rows_total;
+    const int H = a.H, NC = H / 32;
+    float ag[RPW][NT], au[RPW][NT];
+#pragma unroll
+    for (int i = 0; i < RPW; i++)
+#pragma unroll
+        for (int j = 0; j < NT; j++) ag[i][j] = au[i][j] = 0.0f;
+    const size_t rb = SFMT == FQ8 ? row_bytes(FQ8, H) : row_bytes(FQ4K, H);
+    for (int c = lane; c < NC; c += 64) {
+        int klo, khi;
+        if (SFMT == FQ8) { klo = c * 32; khi = klo + 16; }
+        else { q4_pos(c, klo); khi = klo + 32; }
+        if (SFMT == FQ8) {
+            Q8Raw g[RPW], u[RPW];
+#pragma unroll
+            for (int i = 0; i < RPW; i++) {
+                g[i] = q8_load(gbase + (size_t)(r0 + i) * rb, c);
+                u[i] = q8_load(ubase + (size_t)(r0 + i) * rb, c);
+            }
+#pragma unroll
+            for (int j = 0; j < NT; j++) {
+                if (j >= n) break;
+                h2 x[16];
+                load_x16_f32(a.x + (size_t)tok[j] * H + klo, x);
+                load_x16_f32(a.x + (size_t)tok[j] * H + khi, x + 8);
+#pragma unroll
+                for (int i = 0; i < RPW; i++) {
+                    ag[i][j] += q8_dot(g[i], x);
+                    au[i][j] += q8_dot(u[i], x);
+                }
+            }
+        } else {
+            Q4Raw g[RPW], u[RPW];
+#pragma unroll
+            for (int i = 0; i < RPW; i++) {
+                g[i] = q4_load(gbase + (size_t)(r0 + i) * rb, c);
+                u[i] = q4_load(ubase + (size_t)(r0 + i) * rb, c);
+            }
+#pragma unroll
+            for (int j = 0; j < NT; j++) {
+                if (j >= n) break;
+                h2 xl[8], xh[8];
+                float Xl = load_x16_f32(a.x + (size_t)tok[j] * H + klo, xl);
+                float Xh = load_x16_f32(a.x + (size_t)tok[j] * H + khi, xh);
+#pragma unroll
+                for (int i = 0; i < RPW; i++) {
+                    ag[i][j] += q4_dot(g[i], c, xl, xh, Xl, Xh);
+                    au[i][j] += q4_dot(u[i], c, xl, xh, Xl, Xh);
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < RPW; i++)
+#pragma unroll
+        for (int j = 0; j < NT; j++) {
+            if (j >= n) break;
+            float g = wave_sum_canon(ag[i][j]);
+            float u = wave_sum_canon(au[i][j]);
+            if (lane == 0) out[(size_t)j * out_ld + r0 + i] = (_Float16)(silu_f(g) * u);
+        }
+}
+
+template <int NT, int RPW>
+__global__ __launch_bounds__(256) void k_gemv_gate_up(GUArgs a) {
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int rows_blk = 4 * RPW;
+    int b = blockIdx.x;
+    int tok[NT];
+    if (b < a.routed_blocks) {
+        const int bpe = a.M / rows_blk;
+        const int u = b / bpe, tile = b % bpe;
+        const uint32_t n_act = ACT_N(a.list);
+        if ((uint32_t)u >= n_act) return;
+        const int e = (int)ACT_E(a.list, u);
+        const int s0 = (int)ACT_OFF(a.list, a.E, u), n = (int)ACT_OFF(a.list, a.E, u + 1) - s0;
+#pragma unroll
+        for (int j = 0; j < NT; j++) tok[j] = j < n ? (int)(a.pairs[s0 + j] / (uint32_t)a.K) : 0;
+        gu_body<NT, RPW, FQ4K>(a, a.gate + (size_t)e * a.gate_stride, a.up + (size_t)e * a.up_stride,
+                               a.M, tile * rows_blk + wv * RPW, n, tok, a.act + (size_t)s0 * a.M, a.M,
+                               lane);
+    } else {
+        const int tile = b - a.routed_blocks;
+#pragma unroll
+        for (int j = 0; j < NT; j++) tok[j] = j;
+        const int r0 = tile * rows_blk + wv * RPW;
+        if (a.sh_fmt == FQ8)
+            gu_body<NT, RPW, FQ8>(a, a.sh_gate, a.sh_up, a.S, r0, a.T, tok, a.act_sh, a.S, lane);
+        else
+            gu_body<NT, RPW, FQ4K>(a, a.sh_gate, a.sh_up, a.S, r0, a.T, tok, a.act_sh, a.S, lane);
+    }
+}
+
+/* =================================================================== */
+/* down + combine.  Block = 8 output rows x all active slots; waves split the
+ * rows (2 groups of 4) and the slots (even/odd).  A row pass is 16 lanes x
+ * 32 weights = 512 weights; in_dim must be a multiple of 512. */
+struct DownArgs {
+    const uint8_t *down;
+    size_t down_stride;
+    int fmt;
+    const uint8_t *sh_down;
+    int sh_fmt, S;
+    const _Float16 *act, *act_sh;
+    int T, H, M, K, E;
+    const uint32_t *list, *pairs;
+    const float *w, *sgl, *h_in;
+    float *h_out;
+};
+
+template <int NT, int FMT>
+DEV void down_slot(const uint8_t *row, int in_dim, int cl, int n, const _Float16 *const *xrow,
+                   float *acc) {
+    for (int c = cl; c < in_dim / 32; c += 16) {
+        if (FMT == FQ4K) {
+            Q4Raw r = q4_load(row, c);
+            int klo;
+            q4_pos(c, klo);
+#pragma unroll
+            for (int j = 0; j < NT; j++) {
+                if (j >= n) break;
+                h2 xl[8], xh[8];
+                load_h8(xrow[j] + klo, xl);
+                load_h8(xrow[j] + klo + 8, xl + 4);
+                load_h8(xrow[j] + klo + 32, xh);
+                load_h8(xrow[j] + klo + 40, xh + 4);
+                acc[j] += q4_dot(r, c, xl, xh, hsum(xl, 8), hsum(xh, 8));
+            }
+        } else if (FMT == FQ6K) {
+            Q6Raw r = q6_load(row, c);
+            int k0;
+            q6_pos(c, k0);
+#pragma unroll
+            for (int j = 0; j < NT; j++) {
+                if (j >= n) break;
+                h2 x[16];
+#pragma unroll
+                for (int gq = 0; gq < 4; gq++) load_h8(xrow[j] + k0 + 32 * gq, x + 4 * gq);
+                acc[j] += q6_dot(r, c, x);
+            }
+        } else {
+            Q8Raw r = q8_load(row, c);
+#pragma unroll
+            for (int j = 0; j < NT; j++) {
+                if (j >= n) break;
+                h2 x[16];
+#pragma unroll
+                for (int gq = 0; gq < 4; gq++) load_h8(xrow[j] + c * 32 + 8 * gq, x + 4 * gq);
+                acc[j] += q8_dot(r, x);
+            }
+        }
+    }
+}
+
+template <int NT>
+__global__ __launch_bounds__(256) void k_gemv_down(DownArgs a) {
+    extern __shared__ float lds[];
+    const int T = a.T, K = a.K;
+    float *ys = lds;                 /* [T*K][8] */
+    float *ysh = lds + T * K * 8;    /* [T][8] */
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int rg = wv & 1, par = wv >> 1;
+    const int rl = rg * 4 + (lane >> 4), cl = lane & 15;
+    const int r = blockIdx.x * 8 + rl;
+    const int n_act = (int)ACT_N(a.list);
+    const int has_sh = a.sh_down != nullptr;
+    for (int u = par; u < n_act + has_sh; u += 2) {
+        const bool sh = u == n_act;
+        const _Float16 *xrow[NT];
+        float acc[NT];
+        int n, s0 = 0;
+        const uint8_t *row;
+        int fmt, in_dim;
+        if (!sh) {
+            const int e = (int)ACT_E(a.list, u);
+            s0 = (int)ACT_OFF(a.list, a.E, u);
+            n = (int)ACT_OFF(a.list, a.E, u + 1) - s0;
+            fmt = a.fmt;
+            in_dim = a.M;
+            row = a.down + (size_t)e * a.down_stride + (size_t)r * row_bytes(fmt, in_dim);
+#pragma unroll
+            for (int j = 0; j < NT; j++) xrow[j] = a.act + (size_t)(s0 + (j < n ? j : 0)) * a.M;
+        } else {
+            n = T;
+            fmt = a.sh_fmt;
+            in_dim = a.S;
+            row = a.sh_down + (size_t)r * row_bytes(fmt, in_dim);
+#pragma unroll
+            for (int j = 0; j < NT; j++) xrow[j] = a.act_sh + (size_t)(j < n ? j : 0) * a.S;
+        }
+#pragma unroll
+        for (int j = 0; j < NT; j++) acc[j] = 0.0f;
+        if (fmt == FQ4K) down_slot<NT, FQ4K>(row, in_dim, cl, n, xrow, acc);
+        else if (fmt == FQ6K) down_slot<NT, FQ6K>(row, in_dim, cl, n, xrow, acc);
+        else down_slot<NT, FQ8>(row, in_dim, cl, n, xrow, acc);
+#pragma unroll
+        for (int j = 0; j < NT; j++) {
+            if (j >= n) break;
+            float v = group_sum<16>(acc[j]);
+            if (cl == 0) {
+                if (sh) ysh[j * 8 + rl] = v;
+                else ys[a.pairs[s0 + j] * 8 + rl] = v;
+            }
+        }
+    }
+    __syncthreads();
+    const int tid = threadIdx.x;
+    if (tid < T * 8) {
+        const int t = tid >> 3, q = tid & 7, ro = blockIdx.x * 8 + q;
+        float moe = 0.0f;
+        for (int k = 0; k < K; k++) moe += a.w[t * K + k] * ys[(t * K + k) * 8 + q];
+        float v = (a.h_in ? a.h_in[(size_t)t * a.H + ro] : 0.0f) + moe;
+        if (has_sh) v = v + sigmoid_f(a.sgl[t]) * ysh[t * 8 + q];
+        a.h_out[(size_t)t * a.H + ro] = v;
+    }
+}
+
+/* ------------------------------------------------------------ launch */
+template <int NT>
+static void gu_launch(const GUArgs &a, int rows_blk, int blocks, hipStream_t s) {
+    constexpr int RPW = NT == 1 ? 4 : (NT == 2 ? 2 : 1);
+    (void)rows_blk;
+    hipLaunchKernelGGL((k_gemv_gate_up<NT, RPW>), dim3(blocks), dim3(256), 0, s, a);
+}
+
+static int nt_for(int T) { return T <= 1 ? 1 : T <= 2 ? 2 : T <= 4 ? 4 : T <= 8 ? 8 : 0; }
+
+int launch_gemv_gate_up(const ExpertSide &ex, const SharedSide &sh, const float *x, int T, int H,
+                        int M, int K, int E, const uint32_t *list, const uint32_t *pairs,
+                        _Float16 *act, _Float16 *act_sh, hipStream_t s) {
+    const int NT = nt_for(T);
+    if (!NT || H % 256 || ex.gate_fmt != FQ4K) return -2;
+    const int RPW = NT == 1 ? 4 : (NT == 2 ? 2 : 1), rows_blk = 4 * RPW;
+    if (M % rows_blk || (sh.gate && sh.S % rows_blk)) return -2;
+    if (sh.gate && sh.gate_fmt != FQ4K && sh.gate_fmt != FQ8) return -2;
+    GUArgs a;
+    a.gate = ex.gate; a.up = ex.up; a.gate_stride = ex.gate_stride; a.up_stride = ex.up_stride;
+    a.sh_gate = sh.gate; a.sh_up = sh.up; a.sh_fmt = sh.gate_fmt; a.S = sh.gate ? sh.S : 0;
+    a.x = x; a.T = T; a.H = H; a.M = M; a.K = K; a.E = E; a.list = list; a.pairs = pairs;
+    a.act = act; a.act_sh = act_sh;
+    const int umax = T * K < E ? T * K : E;
+    a.routed_blocks = umax * (M / rows_blk);
+    const int blocks = a.routed_blocks + (sh.gate ? sh.S / rows_blk : 0);
+    switch (NT) {
+        case 1: gu_launch<1>(a, rows_blk, blocks, s); break;
+        case 2: gu_launch<2>(a, rows_blk, blocks, s); break;
+        case 4: gu_launch<4>(a, rows_blk, blocks, s); break;
+        default: gu_launch<8>(a, rows_blk, blocks, s); break;
+    }
+    return hipGetLastError() == hipSuccess ? 0 : -3;
+}
+
+int launch_gemv_down_combine(const ExpertSide &ex, const SharedSide &sh, const _Float16 *act,
+                             const _Float16 *act_sh, int T, int H, int M, int K, int E,
+                             const uint32_t *list, const uint32_t *pairs, const float *w,
+                             const float *sgl, const float *h_in, float *h_out, hipStream_t s) {
+    const int NT = nt_for(T);
+    if (!NT || H % 8 || M % 512 || (sh.gate && sh.S % 512)) return -2;
+    if (ex.down_fmt != FQ4K && ex.down_fmt != FQ6K) return -2;
+    if (sh.gate && sh.down_fmt != FQ4K && sh.down_fmt != FQ6K && sh.down_fmt != FQ8) return -2;
+    DownArgs a;
+    a.down = ex.down; a.down_stride = ex.down_stride; a.fmt = ex.down_fmt;
+    a.sh_down = sh.gate ? sh.down : nullptr; a.sh_fmt = sh.down_fmt; a.S = sh.S;
+    a.act = act; a.act_sh = act_sh; a.T = T; a.H = H; a.M = M; a.K = K; a.E = E;
+    a.list = list; a.pairs = pairs; a.w = w; a.sgl = sgl; a.h_in = h_in; a.h_out = h_out;
+    const size_t lds = sizeof(float) * (size_t)(T * K * 8 + T * 8);
+    dim3 grid(H / 8);
+    switch (NT) {
+        case 1: hipLaunchKernelGGL(k_gemv_down<1>, grid, dim3(256), lds, s, a); break;
+        case 2: hipLaunchKernelGGL(k_gemv_down<2>, grid, dim3(256), lds, s, a); break;
+        case 4: hipLaunchKernelGGL(k_gemv_down<4>, grid, dim3(256), lds, s, a); break;
+        default: hipLaunchKernelGGL(k_gemv_down<8>, grid, dim3(256), lds, s, a); break;
+    }
+    return hipGetLastError() == hipSuccess ? 0 : -3;
+}

@@ -1,0 +1,126 @@
+/*
+ * moe_misc.hip -- scalar dequant kernels, fp16 staging and the prefill combine.
+ */
+#include "dev_common.h"
+#include "kernels.h"
+
+/* Row dequant to fp32 (and optionally fp16 RNE), one thread per 32-weight
+ * chunk.  Arithmetic restates format_decode_row_f32
+ * (inference/src/format.m:66-174): Q4_K (d*sc)*q - dmin*m, Q6_K (d*sc)*q,
+ * Q8_0 d*q; every product is exact in fp32, so fused or not the result is
+ * the same. */
+__global__ void k_dequant(int fmt, const uint8_t *src, uint32_t rows, uint32_t n, float *o32,
+                          _Float16 *o16) {
+    const uint32_t nch = n / 32;
+    const size_t gid = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (gid >= (size_t)rows * nch) return;
+    const uint32_t r = (uint32_t)(gid / nch), c = (uint32_t)(gid % nch);
+    float v[32];
+    int pos[32];
+    if (fmt == 0) { /* Q4_K: chunk = (super-block, group g, half of the 32 bytes) */
+        const uint8_t *sb = src + (size_t)r * (n / 256) * 144 + (c >> 3) * 144;
+        u4 hdr = ld_u4(sb);
+        const int g = (c & 7) >> 1, lh = (c & 1) * 16;
+        Q4Affine af = q4k_affine(hdr, g);
+        for (int i = 0; i < 16; i++) {
+            uint32_t byte = sb[16 + g * 32 + lh + i];
+            int k = (c >> 3) * 256 + g * 64 + lh + i;
+            v[i] = af.a_lo * (float)(byte & 0xF) - af.b_lo;
+            pos[i] = k;
+            v[16 + i] = af.a_hi * (float)(byte >> 4) - af.b_hi;
+            pos[16 + i] = k + 32;
+        }
+    } else if (fmt == 2) { /* Q6_K: chunk = (super-block, half, 8 positions) */
+        const uint8_t *sb = src + (size_t)r * (n / 256) * 210 + (c >> 3) * 210;
+        const int h = (c >> 2) & 1, l0 = 8 * (c & 3);
+        const uint8_t *ql = sb + h * 64, *qh = sb + 128 + h * 32;
+        const int8_t *sc = (const int8_t *)(sb + 192) + h * 8;
+        float d = f16_bits_to_f32((uint32_t)sb[208] | ((uint32_t)sb[209] << 8));
+        for (int i = 0; i < 8; i++) {
+            int l = l0 + i, is = l / 16, base = (c >> 3) * 256 + h * 128;
+            int q1 = (int)((ql[l] & 0xF) | ((qh[l] & 3) << 4)) - 32;
+            int q2 = (int)((ql[l + 32] & 0xF) | (((qh[l] >> 2) & 3) << 4)) - 32;
+            int q3 = (int)((ql[l] >> 4) | (((qh[l] >> 4) & 3) << 4)) - 32;
+            int q4 = (int)((ql[l + 32] >> 4) | (((qh[l] >> 6) & 3) << 4)) - 32;
+            v[i] = d * (float)sc[is] * (float)q1; pos[i] = base + l;
+            v[8 + i] = d * (float)sc[is + 2] * (float)q2; pos[8 + i] = base + l + 32;
+            v[16 + i] = d * (float)sc[is + 4] * (float)q3; pos[16 + i] = base + l + 64;
+            v[24 + i] = d * (float)sc[is + 6] * (float)q4; pos[24 + i] = base + l + 96;
+        }
+    } else { /* Q8_0: chunk = block */
+        const uint8_t *b = src + (size_t)r * (n / 32) * 34 + c * 34;
+        float d = f16_bits_to_f32((uint32_t)b[0] | ((uint32_t)b[1] << 8));
+        for (int i = 0; i < 32; i++) {
+            v[i] = d * (float)(int8_t)b[2 + i];
+            pos[i] = c * 32 + i;
+        }
+    }
+    for (int i = 0; i < 32; i++) {
+        if (o32) o32[(size_t)r * n + pos[i]] = v[i];
+        if (o16) o16[(size_t)r * n + pos[i]] = (_Float16)v[i];
+    }
+}
+
+int launch_dequant(int fmt, const uint8_t *src, uint32_t rows, uint32_t n, float *o32,
+                   _Float16 *o16, hipStream_t s) {
+    if (fmt != 0 && fmt != 2 && fmt != 3) return -2;
+    if ((fmt == 3 && n % 32) || (fmt != 3 && n % 256)) return -1;
+    size_t work = (size_t)rows * (n / 32);
+    if (!work) return 0;
+    hipLaunchKernelGGL(k_dequant, dim3((unsigned)((work + 255) / 256)), dim3(256), 0, s, fmt, src,
+                       rows, n, o32, o16);
+    return hipGetLastError() == hipSuccess ? 0 : -3;
+}
+
+/* x fp32 -> fp16 RNE (the reference's half(x) staging) */
+__global__ void k_to_f16(const float *x, size_t n, _Float16 *o) {
+    size_t i = ((size_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
+    if (i + 4 <= n) {
+        f4 v = *(const f4 *)(x + i);
+        h4 h = {(_Float16)v.x, (_Float16)v.y, (_Float16)v.z, (_Float16)v.w};
+        *(h4 *)(o + i) = h;
+    } else {
+        for (; i < n; i++) o[i] = (_Float16)x[i];
+    }
+}
+
+int launch_to_f16(const float *x, int T, int H, _Float16 *x16, hipStream_t s) {
+    size_t n = (size_t)T * H;
+    hipLaunchKernelGGL(k_to_f16, dim3((unsigned)((n / 4 + 255) / 256 + 1)), dim3(256), 0, s, x, n, x16);
+    return hipGetLastError() == hipSuccess ? 0 : -3;
+}
+
+/* Prefill combine (moe_combine_copy_sq_k8, shaders.metal:1079-1135):
+ *   h_out = (h_in + sum_k w_k y[pos(t,k)]) + sigmoid(s_t) * y_shared[t]
+ * y holds expert outputs in expert-sorted pair order. 4 columns per thread. */
+__global__ void k_combine(const float *y, const float *ysh, const uint32_t *pos, const float *w,
+                          const float *sgl, int has_sh, const float *h_in, float *h_out, int T,
+                          int H, int K) {
+    const int t = blockIdx.y;
+    const int c = (blockIdx.x * blockDim.x + threadIdx.x) * 4;
+    if (c >= H) return;
+    f4 moe = {0, 0, 0, 0};
+    for (int k = 0; k < K; k++) {
+        const float wk = w[t * K + k];
+        f4 v = *(const f4 *)(y + (size_t)pos[t * K + k] * H + c);
+        moe.x += wk * v.x; moe.y += wk * v.y; moe.z += wk * v.z; moe.w += wk * v.w;
+    }
+    f4 base = h_in ? *(const f4 *)(h_in + (size_t)t * H + c) : f4{0, 0, 0, 0};
+    f4 o = {base.x + moe.x, base.y + moe.y, base.z + moe.z, base.w + moe.w};
+    if (has_sh) {
+        const float g = sigmoid_f(sgl[t]);
+        f4 sv = *(const f4 *)(ysh + (size_t)t * H + c);
+        o.x = o.x + g * sv.x; o.y = o.y + g * sv.y; o.z = o.z + g * sv.z; o.w = o.w + g * sv.w;
+    }
+    *(f4 *)(h_out + (size_t)t * H + c) = o;
+}
+
+int launch_combine(const float *y, const float *ysh, const uint32_t *pos, const float *w,
+                   const float *sgl, int has_shared, const float *h_in, float *h_out, int T, int H,
+                   int K, hipStream_t s) {
+    if (H % 4) return -2;
+    dim3 grid((H / 4 + 255) / 256, T);
+    hipLaunchKernelGGL(k_combine, grid, dim3(256), 0, s, y, ysh, pos, w, sgl, has_shared, h_in,
+                       h_out, T, H, K);
+    return hipGetLastError() == hipSuccess ? 0 : -3;
+}
