@@ -264,6 +264,30 @@ int orome_dequant_rows(orome_hip_ctx *ctx, QuantFormat fmt, const void *src_dev,
 int orome_dequant_rows_f16(orome_hip_ctx *ctx, QuantFormat fmt, const void *src_dev,
                            uint32_t rows, uint32_t in_dim, uint16_t *out_dev);
 
+/* ------------------------------------------------- graphs and timing */
+
+/* Capture the work queued on the context stream into a HIP graph and replay
+ * it.  Counterpart of the reference's one command buffer per token, encoded
+ * once and committed (inference/src/engine.m:453-454, 1048-1050); a graph
+ * removes per-kernel launch cost from decode.  Forward calls made between
+ * begin and end are recorded, not executed.  No memset nodes are recorded:
+ * the forward path clears nothing with hipMemset. */
+int orome_hip_capture_begin(orome_hip_ctx *ctx);
+int orome_hip_capture_end(orome_hip_ctx *ctx, void **graph_exec);
+int orome_hip_graph_launch(orome_hip_ctx *ctx, void *graph_exec);
+int orome_hip_graph_destroy(void *graph_exec);
+
+/* Per-stage kernel timing with HIP events around each launch of eager
+ * (non-captured) forward calls; `capacity` samples are kept per stage
+ * (0 turns timing off).  Replaces the reference's CPU-side [profile]
+ * timers (inference/src/engine.m:687-693, 1063-1068), which measured
+ * encode time rather than GPU time.  Stages: 0 norm, 1 router, 2 top-k,
+ * 3 dispatch, 4 fp16 staging, 5 gate/up, 6 down, 7 combine. */
+#define OROME_N_STAGES 8
+int orome_hip_stage_timing(orome_hip_ctx *ctx, int capacity);
+/* total milliseconds and sample counts per stage since timing was enabled */
+int orome_hip_stage_times(orome_hip_ctx *ctx, float *total_ms, int *counts, int n);
+
 /* Library version string. */
 const char *orome_version(void);
 

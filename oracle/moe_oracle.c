@@ -276,8 +276,8 @@ ORC_API float orc_canon_dot(const float *a, const float *b, uint32_t n) {
             }
         p[L] = acc;
     }
-    for (int off = 32; off >= 1; off >>= 1)
-        for (int L = 0; L < off; L++) p[L] = p[L] + p[L + off];
+    for (int off = 1; off < 64; off <<= 1)
+        for (int L = 0; L < 64; L += 2 * off) p[L] = p[L] + p[L + off];
     return p[0];
 }
 

@@ -1,7 +1,7 @@
 """ctypes binding of liborome_moe.so (the C ABI declared in include/orome_moe.h
 and include/orome_synth.h).
 
-The library is built in-tree by ``python -m orome_amd.build``.  Importing
+The library is built in-tree by ``python orome_amd/build.py``.  Importing
 this module without the built library raises immediately: there is no
 fallback implementation of any kernel.
 """
@@ -16,6 +16,7 @@ QFMT_GGUF_Q4_K, QFMT_GGUF_Q5_K, QFMT_GGUF_Q6_K, QFMT_GGUF_Q8_0, QFMT_F16, QFMT_B
 FFN_MOE, FFN_DENSE = 0, 1
 OROME_PATH_AUTO, OROME_PATH_GEMV, OROME_PATH_MFMA = 0, 1, 2
 OROME_MAX_ACTIVE = 16
+STAGES = ["norm", "router", "topk", "dispatch", "stage_f16", "gate_up", "down", "combine"]
 ERRORS = {0: "OK", -1: "EINVAL", -2: "EUNSUPPORTED", -3: "EHIP", -4: "ENOMEM", -5: "ENOTFOUND",
           -6: "EFORMAT"}
 GGML_Q4_K, GGML_Q6_K, GGML_Q8_0, GGML_F32 = 12, 14, 8, 0
@@ -116,6 +117,12 @@ SIGNATURES = {
     "orome_dequant_rows": (I, [VP, I, VP, U32, U32, VP]),
     "orome_dequant_rows_f16": (I, [VP, I, VP, U32, U32, VP]),
     "orome_version": (C.c_char_p, []),
+    "orome_hip_capture_begin": (I, [VP]),
+    "orome_hip_capture_end": (I, [VP, P(VP)]),
+    "orome_hip_graph_launch": (I, [VP, VP]),
+    "orome_hip_graph_destroy": (I, [VP]),
+    "orome_hip_stage_timing": (I, [VP, I]),
+    "orome_hip_stage_times": (I, [VP, F32P, P(I), I]),
     "orome_synth_gguf_size": (SZ, [P(SynthSpec)]),
     "orome_synth_gguf_write": (I, [P(SynthSpec), VP, SZ]),
     "orome_synth_normal": (I, [C.c_uint64, C.c_uint64, C.c_float, VP, SZ]),
@@ -128,7 +135,7 @@ class OromeError(RuntimeError):
 
 def load(path=LIB_PATH):
     if not os.path.exists(path):
-        raise ImportError("liborome_moe.so is not built (%s); run `python -m orome_amd.build`" % path)
+        raise ImportError("liborome_moe.so is not built (%s); run `python orome_amd/build.py`" % path)
     lib = C.CDLL(path)
     for name, (res, args) in SIGNATURES.items():
         fn = getattr(lib, name)

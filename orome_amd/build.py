@@ -2,7 +2,8 @@
 
 C sources are compiled with gcc, HIP sources with hipcc for gfx950 only, and
 everything is linked by hipcc into orome_amd/liborome_moe.so (in-tree, so the
-library travels with the source tree).  Run `python -m orome_amd.build`.
+library travels with the source tree).  Run `python orome_amd/build.py` (a plain script: it must not import the
+package, whose import loads the library it builds).
 """
 import os
 import subprocess

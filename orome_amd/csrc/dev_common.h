@@ -32,20 +32,51 @@ DEV float f16_bits_to_f32(uint32_t bits16) {
     return (float)__builtin_bit_cast(_Float16, (uint16_t)(bits16 & 0xFFFFu));
 }
 
-/* Canonical wave64 sum: xor butterfly 32,16,8,4,2,1 (every lane ends with
- * the total).  The order is part of the router/norm bit-exact contract. */
-DEV float wave_sum_canon(float v) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v = v + __shfl_xor(v, off, 64);
+/* DPP lane exchange (compile-time control word). */
+template <int CTRL>
+DEV float dppf(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
+}
+template <int CTRL>
+DEV uint32_t dppu(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, CTRL, 0xF, 0xF, true);
+}
+#define DPP_XOR1 0xB1        /* quad_perm [1,0,3,2] */
+#define DPP_XOR2 0x4E        /* quad_perm [2,3,0,1] */
+#define DPP_HALF_MIRROR 0x141 /* lane i <-> 7-i within each 8 */
+#define DPP_MIRROR 0x140     /* lane i <-> 15-i within each 16 */
+
+/* Sum over each row of 16 lanes; every lane gets its row's total.  Lane 0 of
+ * the row holds ((p0+p1)+(p2+p3)) + ((p4+p5)+(p6+p7)) + ... exactly as an xor
+ * butterfly 1,2,4,8 would leave it (adds are commutative, so the mirrored
+ * partner yields the same bits). */
+DEV float row_sum16(float v) {
+    v = v + dppf<DPP_XOR1>(v);
+    v = v + dppf<DPP_XOR2>(v);
+    v = v + dppf<DPP_HALF_MIRROR>(v);
+    v = v + dppf<DPP_MIRROR>(v);
     return v;
 }
 
-/* Sum over aligned groups of `width` lanes (width a power of two <= 64). */
+/* Canonical wave64 sum: the xor butterfly 1,2,4,8,16,32 as seen by lane 0,
+ * i.e. rows r0..r3 of 16 lanes reduced as above, then (r0+r1)+(r2+r3).
+ * Every lane returns the same value.  This order is part of the router/norm
+ * bit-exact contract with the C oracle. */
+DEV float wave_sum_canon(float v) {
+    v = row_sum16(v);
+    int b = __builtin_bit_cast(int, v);
+    float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 0));
+    float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 16));
+    float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 32));
+    float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 48));
+    return (r0 + r1) + (r2 + r3);
+}
+
+/* Sum over aligned groups of 16 lanes (a DPP row). */
 template <int WIDTH>
 DEV float group_sum(float v) {
-#pragma unroll
-    for (int off = WIDTH / 2; off >= 1; off >>= 1) v = v + __shfl_xor(v, off, 64);
-    return v;
+    static_assert(WIDTH == 16, "row sums only");
+    return row_sum16(v);
 }
 
 DEV float silu_f(float g) { return g / (1.0f + __expf(-g)); }

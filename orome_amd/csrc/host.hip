@@ -37,6 +37,8 @@ extern "C" const char *orome_version(void) { return "orome-mi355x 0.1 (gfx950)";
             return orome_fail(code, "%s failed: %s", #expr, hipGetErrorString(e_));         \
     } while (0)
 
+enum { ST_NORM, ST_ROUTE, ST_TOPK, ST_DISPATCH, ST_STAGE, ST_GATE_UP, ST_DOWN, ST_COMBINE, N_STAGES };
+
 struct orome_hip_ctx {
     int device;
     hipStream_t stream;
@@ -50,6 +52,10 @@ struct orome_hip_ctx {
     void *arena;
     size_t arena_bytes;
     int last_T, last_K;
+    /* per-stage kernel timing (eager launches only) */
+    int timing, tcap;
+    hipEvent_t *ev;          /* [N_STAGES][tcap][2] */
+    int tcount[N_STAGES];
 };
 
 static int set_dev(orome_hip_ctx *c) {
@@ -118,10 +124,19 @@ extern "C" orome_hip_ctx *orome_hip_create(const ModelConfig *cfg, int max_token
     return c;
 }
 
+static void free_timing(orome_hip_ctx *c) {
+    if (!c->ev) return;
+    for (int i = 0; i < N_STAGES * c->tcap * 2; i++) (void)hipEventDestroy(c->ev[i]);
+    free(c->ev);
+    c->ev = NULL;
+    c->timing = 0;
+}
+
 extern "C" void orome_hip_destroy(orome_hip_ctx *c) {
     if (!c) return;
     (void)hipSetDevice(c->device);
     (void)hipStreamSynchronize(c->stream);
+    free_timing(c);
     (void)hipFree(c->arena);
     (void)hipStreamDestroy(c->stream);
     free(c);
@@ -206,6 +221,21 @@ static int launch_rc(int rc, const char *what) {
         if (rc_) return rc_;                \
     } while (0)
 
+/* launch with optional per-stage event bracketing */
+#define TLAUNCH(c, st, call, what)                                                         \
+    do {                                                                                   \
+        hipEvent_t *ev_ = NULL;                                                            \
+        if ((c)->timing) {                                                                 \
+            ev_ = &(c)->ev[((st) * (c)->tcap + (c)->tcount[st] % (c)->tcap) * 2];          \
+            (void)hipEventRecord(ev_[0], (c)->stream);                                     \
+        }                                                                                  \
+        LAUNCH(call, what);                                                                \
+        if (ev_) {                                                                         \
+            (void)hipEventRecord(ev_[1], (c)->stream);                                     \
+            (c)->tcount[st]++;                                                             \
+        }                                                                                  \
+    } while (0)
+
 extern "C" int orome_moe_forward(orome_hip_ctx *c, const ModelConfig *cfg, const ExpertLayerRef *elr,
                                  const LayerTensorCache *lt, const float *x, const float *h_in,
                                  float *h_out, int T, int K) {
@@ -269,25 +299,27 @@ extern "C" int orome_moe_forward(orome_hip_ctx *c, const ModelConfig *cfg, const
     hipStream_t s = c->stream;
     if (path == OROME_PATH_GEMV) {
         if (T > 8) return orome_fail(OROME_EUNSUPPORTED, "GEMV path handles T <= 8 (T=%d)", T);
-        LAUNCH(launch_route_small(a, s), "route");
-        LAUNCH(launch_gemv_gate_up(ex, sh, x, T, H, M, K, E, c->list, c->pairs, c->act, c->act_sh, s),
-               "gemv gate/up");
-        LAUNCH(launch_gemv_down_combine(ex, sh, c->act, c->act_sh, T, H, M, K, E, c->list, c->pairs,
-                                        c->w, c->sgl, h_in, h_out, s),
-               "gemv down+combine");
+        TLAUNCH(c, ST_ROUTE, launch_route_small(a, s), "router logits");
+        TLAUNCH(c, ST_TOPK, launch_topk_dispatch_small(a, s), "top-k + dispatch");
+        TLAUNCH(c, ST_GATE_UP, launch_gemv_gate_up(ex, sh, x, T, H, M, K, E, c->list, c->pairs, c->act, c->act_sh, s),
+                "gemv gate/up");
+        TLAUNCH(c, ST_DOWN, launch_gemv_down(ex, sh, c->act, c->act_sh, T, H, M, K, E, c->list, c->y, c->ysh, s),
+                "gemv down");
+        TLAUNCH(c, ST_COMBINE, launch_combine(c->y, c->ysh, c->pos, c->w, c->sgl, S ? 1 : 0, h_in, h_out, T, H, K, s),
+                "combine");
     } else {
-        LAUNCH(launch_route_logits(a, s), "router logits");
-        LAUNCH(launch_topk(a, s), "top-k");
-        LAUNCH(launch_dispatch(a, c->tiles, GEMM_TILE_M, S ? 1 : 0, s), "dispatch");
-        LAUNCH(launch_to_f16(x, T, H, c->x16, s), "fp16 staging");
+        TLAUNCH(c, ST_ROUTE, launch_route_logits(a, s), "router logits");
+        TLAUNCH(c, ST_TOPK, launch_topk(a, s), "top-k");
+        TLAUNCH(c, ST_DISPATCH, launch_dispatch(a, c->tiles, GEMM_TILE_M, S ? 1 : 0, s), "dispatch");
+        TLAUNCH(c, ST_STAGE, launch_to_f16(x, T, H, c->x16, s), "fp16 staging");
         const int ntiles = (T * K) / GEMM_TILE_M + E + (S ? (T + GEMM_TILE_M - 1) / GEMM_TILE_M : 0);
-        LAUNCH(launch_gemm_gate_up(ex, sh, c->x16, T, H, M, K, E, c->tiles, ntiles, c->pairs, c->act,
+        TLAUNCH(c, ST_GATE_UP, launch_gemm_gate_up(ex, sh, c->x16, T, H, M, K, E, c->tiles, ntiles, c->pairs, c->act,
                                    c->act_sh, s),
                "grouped gate/up");
-        LAUNCH(launch_gemm_down(ex, sh, c->act, c->act_sh, T, H, M, K, E, c->tiles, ntiles, c->y,
+        TLAUNCH(c, ST_DOWN, launch_gemm_down(ex, sh, c->act, c->act_sh, T, H, M, K, E, c->tiles, ntiles, c->y,
                                 c->ysh, s),
                "grouped down");
-        LAUNCH(launch_combine(c->y, c->ysh, c->pos, c->w, c->sgl, S ? 1 : 0, h_in, h_out, T, H, K, s),
+        TLAUNCH(c, ST_COMBINE, launch_combine(c->y, c->ysh, c->pos, c->w, c->sgl, S ? 1 : 0, h_in, h_out, T, H, K, s),
                "combine");
     }
     c->last_T = T;
@@ -304,7 +336,7 @@ extern "C" int orome_moe_layer_forward(orome_hip_ctx *c, const ModelConfig *cfg,
     const float *nw = lt->post_norm.buffer && lt->post_norm.format == QFMT_F32
                           ? (const float *)dev_addr(lt->post_norm.buffer, lt->post_norm.offset)
                           : NULL;
-    LAUNCH(launch_rmsnorm(h, nw, T, cfg->hidden_dim, cfg->rms_norm_eps, c->xnorm, c->stream), "rmsnorm");
+    TLAUNCH(c, ST_NORM, launch_rmsnorm(h, nw, T, cfg->hidden_dim, cfg->rms_norm_eps, c->xnorm, c->stream), "rmsnorm");
     return orome_moe_forward(c, cfg, elr, lt, c->xnorm, h, h, T, K);
 }
 
@@ -362,5 +394,72 @@ extern "C" int orome_dequant_rows_f16(orome_hip_ctx *c, QuantFormat fmt, const v
     if (set_dev(c)) return OROME_EHIP;
     LAUNCH(launch_dequant(kfmt(fmt), (const uint8_t *)src, rows, in_dim, NULL, (_Float16 *)out, c->stream),
            "dequant f16");
+    return OROME_OK;
+}
+
+/* ------------------------------------------------------- graphs, timing */
+
+extern "C" int orome_hip_capture_begin(orome_hip_ctx *c) {
+    if (!c) return orome_fail(OROME_EINVAL, "orome_hip_capture_begin: NULL ctx");
+    if (c->timing) return orome_fail(OROME_EINVAL, "stage timing must be off while capturing");
+    if (set_dev(c)) return OROME_EHIP;
+    HIP_OK(hipStreamBeginCapture(c->stream, hipStreamCaptureModeRelaxed), OROME_EHIP);
+    return OROME_OK;
+}
+
+extern "C" int orome_hip_capture_end(orome_hip_ctx *c, void **exec) {
+    if (!c || !exec) return orome_fail(OROME_EINVAL, "orome_hip_capture_end: NULL argument");
+    hipGraph_t g = NULL;
+    HIP_OK(hipStreamEndCapture(c->stream, &g), OROME_EHIP);
+    hipGraphExec_t ge = NULL;
+    hipError_t e = hipGraphInstantiate(&ge, g, NULL, NULL, 0);
+    (void)hipGraphDestroy(g);
+    if (e != hipSuccess) return orome_fail(OROME_EHIP, "hipGraphInstantiate: %s", hipGetErrorString(e));
+    *exec = (void *)ge;
+    return OROME_OK;
+}
+
+extern "C" int orome_hip_graph_launch(orome_hip_ctx *c, void *exec) {
+    if (!c || !exec) return orome_fail(OROME_EINVAL, "orome_hip_graph_launch: NULL argument");
+    HIP_OK(hipGraphLaunch((hipGraphExec_t)exec, c->stream), OROME_EHIP);
+    return OROME_OK;
+}
+
+extern "C" int orome_hip_graph_destroy(void *exec) {
+    if (exec) HIP_OK(hipGraphExecDestroy((hipGraphExec_t)exec), OROME_EHIP);
+    return OROME_OK;
+}
+
+extern "C" int orome_hip_stage_timing(orome_hip_ctx *c, int capacity) {
+    if (!c || capacity < 0) return orome_fail(OROME_EINVAL, "orome_hip_stage_timing: bad argument");
+    if (set_dev(c)) return OROME_EHIP;
+    (void)hipStreamSynchronize(c->stream);
+    free_timing(c);
+    memset(c->tcount, 0, sizeof c->tcount);
+    if (!capacity) return OROME_OK;
+    c->ev = (hipEvent_t *)calloc((size_t)N_STAGES * capacity * 2, sizeof(hipEvent_t));
+    for (int i = 0; i < N_STAGES * capacity * 2; i++)
+        HIP_OK(hipEventCreate(&c->ev[i]), OROME_EHIP);
+    c->tcap = capacity;
+    c->timing = 1;
+    return OROME_OK;
+}
+
+extern "C" int orome_hip_stage_times(orome_hip_ctx *c, float *total_ms, int *counts, int n) {
+    if (!c || !total_ms || !counts || n < 1) return orome_fail(OROME_EINVAL, "orome_hip_stage_times: bad argument");
+    HIP_OK(hipStreamSynchronize(c->stream), OROME_EHIP);
+    for (int st = 0; st < n; st++) {
+        total_ms[st] = 0.0f;
+        counts[st] = 0;
+        if (st >= N_STAGES || !c->timing) continue;
+        int k = c->tcount[st] < c->tcap ? c->tcount[st] : c->tcap;
+        for (int i = 0; i < k; i++) {
+            float ms = 0.0f;
+            HIP_OK(hipEventElapsedTime(&ms, c->ev[(st * c->tcap + i) * 2], c->ev[(st * c->tcap + i) * 2 + 1]),
+                   OROME_EHIP);
+            total_ms[st] += ms;
+        }
+        counts[st] = k;
+    }
     return OROME_OK;
 }

@@ -44,6 +44,7 @@ struct SharedSide {
 };
 
 int launch_route_small(const RouteArgs &a, hipStream_t s);
+int launch_topk_dispatch_small(const RouteArgs &a, hipStream_t s);
 int launch_route_logits(const RouteArgs &a, hipStream_t s);
 int launch_topk(const RouteArgs &a, hipStream_t s);
 int launch_dispatch(const RouteArgs &a, uint32_t *tiles, int tile_m, int has_shared, hipStream_t s);
@@ -51,10 +52,9 @@ int launch_dispatch(const RouteArgs &a, uint32_t *tiles, int tile_m, int has_sha
 int launch_gemv_gate_up(const ExpertSide &ex, const SharedSide &sh, const float *x, int T, int H,
                         int M, int K, int E, const uint32_t *list, const uint32_t *pairs,
                         _Float16 *act, _Float16 *act_sh, hipStream_t s);
-int launch_gemv_down_combine(const ExpertSide &ex, const SharedSide &sh, const _Float16 *act,
-                             const _Float16 *act_sh, int T, int H, int M, int K, int E,
-                             const uint32_t *list, const uint32_t *pairs, const float *w,
-                             const float *sgl, const float *h_in, float *h_out, hipStream_t s);
+int launch_gemv_down(const ExpertSide &ex, const SharedSide &sh, const _Float16 *act,
+                     const _Float16 *act_sh, int T, int H, int M, int K, int E, const uint32_t *list,
+                     float *y, float *ysh, hipStream_t s);
 
 int launch_rmsnorm(const float *h, const float *w, int T, int H, float eps, float *x, hipStream_t s);
 int launch_dequant(int fmt, const uint8_t *src, uint32_t rows, uint32_t n, float *out32,

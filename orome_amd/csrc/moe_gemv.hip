@@ -260,9 +260,11 @@ __global__ __launch_bounds__(256) void k_gemv_gate_up(GUArgs a) {
 }
 
 /* =================================================================== */
-/* down + combine.  Block = 8 output rows x all active slots; waves split the
- * rows (2 groups of 4) and the slots (even/odd).  A row pass is 16 lanes x
- * 32 weights = 512 weights; in_dim must be a multiple of 512. */
+/* down.  One block = one active slot (routed expert or the shared expert) x
+ * 8 output rows; each wave covers 4 rows with 16 lanes per row (a row pass
+ * is 16 x 32 = 512 weights; in_dim % 512 == 0).  Results go to
+ * y[sorted pair position][H] and ysh[t][H]; the combine kernel applies the
+ * routing weights (kernel boundaries order the two, no cross-block fences). */
 struct DownArgs {
     const uint8_t *down;
     size_t down_stride;
@@ -271,9 +273,8 @@ struct DownArgs {
     int sh_fmt, S;
     const _Float16 *act, *act_sh;
     int T, H, M, K, E;
-    const uint32_t *list, *pairs;
-    const float *w, *sgl, *h_in;
-    float *h_out;
+    const uint32_t *list;
+    float *y, *ysh;
 };
 
 template <int NT, int FMT>
@@ -321,65 +322,51 @@ DEV void down_slot(const uint8_t *row, int in_dim, int cl, int n, const _Float16
 }
 
 template <int NT>
-__global__ __launch_bounds__(256) void k_gemv_down(DownArgs a) {
-    extern __shared__ float lds[];
-    const int T = a.T, K = a.K;
-    float *ys = lds;                 /* [T*K][8] */
-    float *ysh = lds + T * K * 8;    /* [T][8] */
-    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-    const int rg = wv & 1, par = wv >> 1;
-    const int rl = rg * 4 + (lane >> 4), cl = lane & 15;
-    const int r = blockIdx.x * 8 + rl;
+__global__ __launch_bounds__(128) void k_gemv_down(DownArgs a) {
+    const int T = a.T, H = a.H;
+    const int ntile = H / 8;
+    const int u = blockIdx.x / ntile, tile = blockIdx.x % ntile;
     const int n_act = (int)ACT_N(a.list);
     const int has_sh = a.sh_down != nullptr;
-    for (int u = par; u < n_act + has_sh; u += 2) {
-        const bool sh = u == n_act;
-        const _Float16 *xrow[NT];
-        float acc[NT];
-        int n, s0 = 0;
-        const uint8_t *row;
-        int fmt, in_dim;
-        if (!sh) {
-            const int e = (int)ACT_E(a.list, u);
-            s0 = (int)ACT_OFF(a.list, a.E, u);
-            n = (int)ACT_OFF(a.list, a.E, u + 1) - s0;
-            fmt = a.fmt;
-            in_dim = a.M;
-            row = a.down + (size_t)e * a.down_stride + (size_t)r * row_bytes(fmt, in_dim);
+    if (u >= n_act + has_sh) return;
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int rl = wv * 4 + (lane >> 4), cl = lane & 15;
+    const int r = tile * 8 + rl;
+    const bool sh = u == n_act;
+    const _Float16 *xrow[NT];
+    float acc[NT];
+    int n, s0 = 0, fmt, in_dim;
+    const uint8_t *row;
+    if (!sh) {
+        const int e = (int)ACT_E(a.list, u);
+        s0 = (int)ACT_OFF(a.list, a.E, u);
+        n = (int)ACT_OFF(a.list, a.E, u + 1) - s0;
+        fmt = a.fmt;
+        in_dim = a.M;
+        row = a.down + (size_t)e * a.down_stride + (size_t)r * row_bytes(fmt, in_dim);
 #pragma unroll
-            for (int j = 0; j < NT; j++) xrow[j] = a.act + (size_t)(s0 + (j < n ? j : 0)) * a.M;
-        } else {
-            n = T;
-            fmt = a.sh_fmt;
-            in_dim = a.S;
-            row = a.sh_down + (size_t)r * row_bytes(fmt, in_dim);
+        for (int j = 0; j < NT; j++) xrow[j] = a.act + (size_t)(s0 + (j < n ? j : 0)) * a.M;
+    } else {
+        n = T;
+        fmt = a.sh_fmt;
+        in_dim = a.S;
+        row = a.sh_down + (size_t)r * row_bytes(fmt, in_dim);
 #pragma unroll
-            for (int j = 0; j < NT; j++) xrow[j] = a.act_sh + (size_t)(j < n ? j : 0) * a.S;
-        }
-#pragma unroll
-        for (int j = 0; j < NT; j++) acc[j] = 0.0f;
-        if (fmt == FQ4K) down_slot<NT, FQ4K>(row, in_dim, cl, n, xrow, acc);
-        else if (fmt == FQ6K) down_slot<NT, FQ6K>(row, in_dim, cl, n, xrow, acc);
-        else down_slot<NT, FQ8>(row, in_dim, cl, n, xrow, acc);
-#pragma unroll
-        for (int j = 0; j < NT; j++) {
-            if (j >= n) break;
-            float v = group_sum<16>(acc[j]);
-            if (cl == 0) {
-                if (sh) ysh[j * 8 + rl] = v;
-                else ys[a.pairs[s0 + j] * 8 + rl] = v;
-            }
-        }
+        for (int j = 0; j < NT; j++) xrow[j] = a.act_sh + (size_t)(j < n ? j : 0) * a.S;
     }
-    __syncthreads();
-    const int tid = threadIdx.x;
-    if (tid < T * 8) {
-        const int t = tid >> 3, q = tid & 7, ro = blockIdx.x * 8 + q;
-        float moe = 0.0f;
-        for (int k = 0; k < K; k++) moe += a.w[t * K + k] * ys[(t * K + k) * 8 + q];
-        float v = (a.h_in ? a.h_in[(size_t)t * a.H + ro] : 0.0f) + moe;
-        if (has_sh) v = v + sigmoid_f(a.sgl[t]) * ysh[t * 8 + q];
-        a.h_out[(size_t)t * a.H + ro] = v;
+#pragma unroll
+    for (int j = 0; j < NT; j++) acc[j] = 0.0f;
+    if (fmt == FQ4K) down_slot<NT, FQ4K>(row, in_dim, cl, n, xrow, acc);
+    else if (fmt == FQ6K) down_slot<NT, FQ6K>(row, in_dim, cl, n, xrow, acc);
+    else down_slot<NT, FQ8>(row, in_dim, cl, n, xrow, acc);
+#pragma unroll
+    for (int j = 0; j < NT; j++) {
+        if (j >= n) break;
+        float v = row_sum16(acc[j]);
+        if (cl == 0) {
+            if (sh) a.ysh[(size_t)j * H + r] = v;
+            else a.y[(size_t)(s0 + j) * H + r] = v;
+        }
     }
 }
 
@@ -418,10 +405,9 @@ int launch_gemv_gate_up(const ExpertSide &ex, const SharedSide &sh, const float 
     return hipGetLastError() == hipSuccess ? 0 : -3;
 }
 
-int launch_gemv_down_combine(const ExpertSide &ex, const SharedSide &sh, const _Float16 *act,
-                             const _Float16 *act_sh, int T, int H, int M, int K, int E,
-                             const uint32_t *list, const uint32_t *pairs, const float *w,
-                             const float *sgl, const float *h_in, float *h_out, hipStream_t s) {
+int launch_gemv_down(const ExpertSide &ex, const SharedSide &sh, const _Float16 *act,
+                     const _Float16 *act_sh, int T, int H, int M, int K, int E, const uint32_t *list,
+                     float *y, float *ysh, hipStream_t s) {
     const int NT = nt_for(T);
     if (!NT || H % 8 || M % 512 || (sh.gate && sh.S % 512)) return -2;
     if (ex.down_fmt != FQ4K && ex.down_fmt != FQ6K) return -2;
@@ -430,14 +416,14 @@ int launch_gemv_down_combine(const ExpertSide &ex, const SharedSide &sh, const _
     a.down = ex.down; a.down_stride = ex.down_stride; a.fmt = ex.down_fmt;
     a.sh_down = sh.gate ? sh.down : nullptr; a.sh_fmt = sh.down_fmt; a.S = sh.S;
     a.act = act; a.act_sh = act_sh; a.T = T; a.H = H; a.M = M; a.K = K; a.E = E;
-    a.list = list; a.pairs = pairs; a.w = w; a.sgl = sgl; a.h_in = h_in; a.h_out = h_out;
-    const size_t lds = sizeof(float) * (size_t)(T * K * 8 + T * 8);
-    dim3 grid(H / 8);
+    a.list = list; a.y = y; a.ysh = ysh;
+    const int umax = T * K < E ? T * K : E;
+    dim3 grid((umax + (sh.gate ? 1 : 0)) * (H / 8));
     switch (NT) {
-        case 1: hipLaunchKernelGGL(k_gemv_down<1>, grid, dim3(256), lds, s, a); break;
-        case 2: hipLaunchKernelGGL(k_gemv_down<2>, grid, dim3(256), lds, s, a); break;
-        case 4: hipLaunchKernelGGL(k_gemv_down<4>, grid, dim3(256), lds, s, a); break;
-        default: hipLaunchKernelGGL(k_gemv_down<8>, grid, dim3(256), lds, s, a); break;
+        case 1: hipLaunchKernelGGL(k_gemv_down<1>, grid, dim3(128), 0, s, a); break;
+        case 2: hipLaunchKernelGGL(k_gemv_down<2>, grid, dim3(128), 0, s, a); break;
+        case 4: hipLaunchKernelGGL(k_gemv_down<4>, grid, dim3(128), 0, s, a); break;
+        default: hipLaunchKernelGGL(k_gemv_down<8>, grid, dim3(128), 0, s, a); break;
     }
     return hipGetLastError() == hipSuccess ? 0 : -3;
 }

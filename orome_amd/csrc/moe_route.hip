@@ -4,8 +4,10 @@
  * Router logits restate matvec_f32_pair (inference/src/shaders.metal:1368-1392)
  * with a fixed reduction order shared bit-for-bit with the C oracle:
  *   lane L of a wave64 owns elements j = 256*i + 4*L + c, summed in (i, c)
- *   order with fused multiply-adds from zero, then an xor butterfly
- *   32,16,8,4,2,1.  Identical logits make the selected experts identical.
+ *   order with fused multiply-adds from zero, then a balanced tree over
+ *   contiguous lanes (xor butterfly 1,2,...,32 as seen by lane 0), done with
+ *   DPP within rows of 16 and readlanes across rows.  Identical logits make
+ *   the selected experts identical.
  * Selection restates softmax_topk_route (shaders.metal:1141-1234): K rounds
  * of argmax, ties to the lower expert index, softmax over the K winners.
  * It runs as a wave64 max over 64-bit keys (order-preserving float bits,
@@ -29,11 +31,22 @@ DEV float key_value(uint64_t k) {
 }
 DEV int key_expert(uint64_t k) { return (int)(0xFFFFFFFFu - (uint32_t)k); }
 
-DEV uint64_t shfl_xor_u64(uint64_t v, int off) {
-    uint32_t lo = (uint32_t)v, hi = (uint32_t)(v >> 32);
-    lo = __shfl_xor(lo, off, 64);
-    hi = __shfl_xor(hi, off, 64);
-    return ((uint64_t)hi << 32) | lo;
+template <int CTRL>
+DEV uint64_t dpp64(uint64_t v) {
+    return ((uint64_t)dppu<CTRL>((uint32_t)(v >> 32)) << 32) | dppu<CTRL>((uint32_t)v);
+}
+DEV uint64_t max64(uint64_t a, uint64_t b) { return a > b ? a : b; }
+DEV uint64_t readlane64(uint64_t v, int l) {
+    return ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(v >> 32), l) << 32) |
+           (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, l);
+}
+/* wave64 maximum of a 64-bit key (DPP within rows, then the four row maxima) */
+DEV uint64_t wave_max64(uint64_t m) {
+    m = max64(m, dpp64<DPP_XOR1>(m));
+    m = max64(m, dpp64<DPP_XOR2>(m));
+    m = max64(m, dpp64<DPP_HALF_MIRROR>(m));
+    m = max64(m, dpp64<DPP_MIRROR>(m));
+    return max64(max64(readlane64(m, 0), readlane64(m, 16)), max64(readlane64(m, 32), readlane64(m, 48)));
 }
 
 /* One token's top-K on one wave.  Lane 0 writes idx/w/sgl; e_out (LDS, may be
@@ -60,11 +73,7 @@ DEV void wave_topk(const float *l, const float *bias, int E, int K, int lane, in
             uint64_t m = key[0];
 #pragma unroll
             for (int j = 1; j < EPL; j++) m = key[j] > m ? key[j] : m;
-#pragma unroll
-            for (int off = 32; off >= 1; off >>= 1) {
-                uint64_t o = shfl_xor_u64(m, off);
-                m = o > m ? o : m;
-            }
+            m = wave_max64(m);
 #pragma unroll
             for (int j = 0; j < EPL; j++)
                 if (key[j] == m) key[j] = 0;
@@ -92,63 +101,67 @@ DEV void wave_topk(const float *l, const float *bias, int E, int K, int lane, in
     }
 }
 
-/* canonical dot of one wave over H (H % 256 == 0), for up to TMAX tokens */
+/* canonical dot of one wave over H (H % 256 == 0, H <= 4096), for up to
+ * TMAX tokens; all loads of a row are issued before the multiply-adds */
+#define CANON_NI 16
 template <int TMAX>
 DEV void canon_dots(const float *wrow, const float *x, int T, int H, int lane, float *acc) {
+    const int NI = H / 256;
+    f4 wv[CANON_NI];
 #pragma unroll
-    for (int t = 0; t < TMAX; t++) acc[t] = 0.0f;
-    for (int i = 0; i < H / 256; i++) {
-        f4 wv = *(const f4 *)(wrow + 256 * i + 4 * lane);
+    for (int i = 0; i < CANON_NI; i++)
+        if (i < NI) wv[i] = *(const f4 *)(wrow + 256 * i + 4 * lane);
 #pragma unroll
-        for (int t = 0; t < TMAX; t++) {
-            if (t < T) {
-                f4 xv = *(const f4 *)(x + (size_t)t * H + 256 * i + 4 * lane);
-                acc[t] = __builtin_fmaf(wv.x, xv.x, acc[t]);
-                acc[t] = __builtin_fmaf(wv.y, xv.y, acc[t]);
-                acc[t] = __builtin_fmaf(wv.z, xv.z, acc[t]);
-                acc[t] = __builtin_fmaf(wv.w, xv.w, acc[t]);
-            }
+    for (int t = 0; t < TMAX; t++) {
+        acc[t] = 0.0f;
+        if (t < T) {
+            f4 xv[CANON_NI];
+#pragma unroll
+            for (int i = 0; i < CANON_NI; i++)
+                if (i < NI) xv[i] = *(const f4 *)(x + (size_t)t * H + 256 * i + 4 * lane);
+            float a = 0.0f;
+#pragma unroll
+            for (int i = 0; i < CANON_NI; i++)
+                if (i < NI) {
+                    a = __builtin_fmaf(wv[i].x, xv[i].x, a);
+                    a = __builtin_fmaf(wv[i].y, xv[i].y, a);
+                    a = __builtin_fmaf(wv[i].z, xv[i].z, a);
+                    a = __builtin_fmaf(wv[i].w, xv[i].w, a);
+                }
+            acc[t] = wave_sum_canon(a);
         }
     }
-#pragma unroll
-    for (int t = 0; t < TMAX; t++)
-        if (t < T) acc[t] = wave_sum_canon(acc[t]);
 }
 
-/* Small-batch routing (T <= 16): every wave computes one router row for all
- * tokens; the last block to finish (agent-scope fence + counter) runs the
- * selection and the dispatch, so decode needs a single launch for routing. */
-template <int EPL>
+/* Small-batch router logits (T <= 16): every wave computes one router row
+ * (or the shared-gate row) for all tokens. */
 __global__ __launch_bounds__(256) void k_route_small(RouteArgs a) {
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int row = blockIdx.x * 4 + wv;
-    const int E = a.E, H = a.H, T = a.T, K = a.K;
-    if (row <= E) {
-        const float *wr = row < E ? a.W + (size_t)row * H : a.wsg;
-        float acc[16];
-        if (wr) {
-            canon_dots<16>(wr, a.x, T, H, lane, acc);
-        } else {
+    const int E = a.E, H = a.H, T = a.T;
+    if (row > E) return;
+    const float *wr = row < E ? a.W + (size_t)row * H : a.wsg;
+    float acc[16];
+    if (wr) {
+        canon_dots<16>(wr, a.x, T, H, lane, acc);
+    } else {
 #pragma unroll
-            for (int t = 0; t < 16; t++) acc[t] = 0.0f;
-        }
-        if (lane == 0) {
+        for (int t = 0; t < 16; t++) acc[t] = 0.0f;
+    }
+    if (lane == 0) {
 #pragma unroll
-            for (int t = 0; t < 16; t++)
-                if (t < T) a.logits[(size_t)t * (E + 1) + row] = acc[t];
-        }
+        for (int t = 0; t < 16; t++)
+            if (t < T) a.logits[(size_t)t * (E + 1) + row] = acc[t];
     }
-    __shared__ int s_last;
-    __threadfence();
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        uint32_t prev = atomicAdd(a.counter, 1u);
-        s_last = prev == gridDim.x - 1;
-    }
-    __syncthreads();
-    if (!s_last) return;
-    __threadfence();
+}
 
+/* Small-batch selection and dispatch (T*K <= 256), one block: a wave per
+ * token for the top-k, then the stable counting sort of the T*K pairs by
+ * ranking each pair against all others. */
+template <int EPL>
+__global__ __launch_bounds__(256) void k_topk_dispatch_small(RouteArgs a) {
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int E = a.E, T = a.T, K = a.K;
     __shared__ int s_e[256];
     __shared__ int s_head[256];
     for (int t = wv; t < T; t += 4)
@@ -187,7 +200,6 @@ __global__ __launch_bounds__(256) void k_route_small(RouteArgs a) {
         for (int q = 0; q < NP; q++) c += s_e[q] < ee;
         a.offsets[ee] = (uint32_t)c;
     }
-    if (threadIdx.x == 0) atomicExch(a.counter, 0u);
 }
 
 /* Large-batch router logits: a block computes 16 rows x 8 tokens; each wave
@@ -354,7 +366,8 @@ __global__ __launch_bounds__(64) void k_rmsnorm(const float *h, const float *w, 
         acc = __builtin_fmaf(v.w, v.w, acc);
     }
     float ss = wave_sum_canon(acc);
-    float scale = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)H), eps)));
+    /* sqrtf and / lower to correctly rounded sequences (__fsqrt_rn does not) */
+    float scale = 1.0f / sqrtf(ss / (float)H + eps);
     for (int j = lane; j < H; j += 64) {
         float wj = w ? __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, w[j]) & 0xFFFF0000u) : 1.0f;
         x[(size_t)t * H + j] = __fmul_rn(__fmul_rn(ht[j], scale), wj);
@@ -382,9 +395,14 @@ static int epl_for(int E) {
     }
 
 int launch_route_small(const RouteArgs &a, hipStream_t s) {
-    if (a.T < 1 || a.T > 16 || a.T * a.K > 256 || a.H % 256) return -2;
-    dim3 grid((a.E + 1 + 3) / 4);
-    EPL_SWITCH(a.E, k_route_small, grid, dim3(256), 0, s, a);
+    if (a.T < 1 || a.T > 16 || a.T * a.K > 256 || a.H % 256 || a.H > 4096) return -2;
+    hipLaunchKernelGGL(k_route_small, dim3((a.E + 1 + 3) / 4), dim3(256), 0, s, a);
+    return hipGetLastError() == hipSuccess ? 0 : -3;
+}
+
+int launch_topk_dispatch_small(const RouteArgs &a, hipStream_t s) {
+    if (a.T < 1 || a.T * a.K > 256) return -2;
+    EPL_SWITCH(a.E, k_topk_dispatch_small, dim3(1), dim3(256), 0, s, a);
     return hipGetLastError() == hipSuccess ? 0 : -3;
 }
 

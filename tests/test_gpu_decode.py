@@ -200,3 +200,37 @@ def test_layer_forward_and_stack():
     p.ctx.sync()
     assert np.array_equal(dh2.download(np.float32, (T, p.H)), h)
     p.gm.close()
+
+
+def test_graph_replay_matches_eager(base):
+    """Capture three forwards in a HIP graph, replay it several times with eager
+    work and synchronisations in between, and check every replay."""
+    banner("graph replay vs eager")
+    import ctypes as C
+    ctx = base.ctx
+    ins = [base.inputs(T, seed=900 + T) for T in (1, 4, 8)]
+    bufs = [(DeviceBuffer.from_array(ctx, x), DeviceBuffer.from_array(ctx, h), DeviceBuffer(ctx, h.nbytes))
+            for x, h in ins]
+    ctx.set_path(_lib.OROME_PATH_AUTO)
+    eager = []
+    for (x, h), (dx, dh, do) in zip(ins, bufs):
+        base.gm.forward(0, dx, dh, do, x.shape[0])
+        ctx.sync()
+        eager.append(do.download(np.float32, h.shape))
+    check(lib.orome_hip_capture_begin(ctx.handle))
+    for (x, h), (dx, dh, do) in zip(ins, bufs):
+        base.gm.forward(0, dx, dh, do, x.shape[0])
+    ex = C.c_void_p()
+    check(lib.orome_hip_capture_end(ctx.handle, C.byref(ex)))
+    for rep in range(3):
+        for (_, h), (_, _, do) in zip(ins, bufs):
+            do.upload(np.zeros_like(h))
+        check(lib.orome_hip_graph_launch(ctx.handle, ex))
+        ctx.sync()
+        for e, (x, h), (_, _, do) in zip(eager, ins, bufs):
+            assert np.array_equal(do.download(np.float32, h.shape), e), "replay %d" % rep
+        # eager work between replays
+        x, h = ins[1]
+        base.gm.forward(0, bufs[1][0], bufs[1][1], bufs[1][2], x.shape[0])
+        ctx.sync()
+    check(lib.orome_hip_graph_destroy(ex))
