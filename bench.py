@@ -1,16 +1,17 @@
-"""MoE-layer throughput benchmark (one MI355X).
+"""MoE-layer throughput benchmark on one MI355X.
 
-A step is one MoE feed-forward block (router, top-k, dispatch, routed experts,
-shared expert, combine) over one batch of T tokens, all on the GPU through
-the C ABI.  The timed steps replay a HIP graph; inputs are resident in HBM
-before timing starts.  Weights rotate over several independently seeded
-layers and inputs over a bank of seeded vectors, so routed experts are
-mostly cold in the 256 MB last-level cache (a single layer is 457 MB of
-expert weights, and each step touches a different 8-expert subset).
+A step is one pass of the hot path over one batch: one MoE feed-forward block
+(router, top-k, dispatch, routed experts, shared expert, combine) over T
+tokens, or for config 4 the whole 40-layer stack (RMSNorm + MoE + residual per
+layer).  Inputs and all weights are resident in HBM before timing; the timed
+steps replay a HIP graph.  Layer-mode configs rotate over several
+independently seeded layers and a bank of seeded inputs, so the routed
+experts of a step are mostly cold in the 256 MB last-level cache.
 
-Prints one JSON line (driver contract).  Extra fields: roofline (dominant
-kernel, from per-launch HIP event timing of the same workload), cpu_baseline
-(the C oracle on this host, bounded sample) and per-stage kernel times.
+Default (no flags): config 0, B=1 decode, the headline of BASELINE.json.
+Prints one JSON line; extra fields hold the roofline of the dominant kernel
+(per-launch HIP event timing inside a replay of the same graph), the C
+oracle on this host as CPU baseline, and per-stage kernel times.
 """
 import argparse
 import ctypes as C
@@ -27,11 +28,20 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
 MFMA_F16_PEAK_TFLOPS = 2500.0
+Q4K, Q6K = 12, 14
 
-# T, synthetic spec overrides
+# name, tokens/step, mode, rotating layers (layer mode) or stack depth, spec
 CONFIGS = {
-    0: dict(T=1, name="moe_decode_b1", spec=dict(), layers=8),
-    1: dict(T=8, name="moe_decode_b8", spec=dict(), layers=8),
+    "0": dict(T=1, name="moe_decode_b1", mode="layer", layers=8, spec={}, xbank=64, steps=2000),
+    "1": dict(T=8, name="moe_decode_b8", mode="layer", layers=8, spec={}, xbank=64, steps=2000),
+    "2": dict(T=512, name="moe_prefill_512_balanced", mode="layer", layers=4, spec={}, xbank=4,
+              steps=200),
+    "3": dict(T=512, name="moe_prefill_512_zipf_q6k", mode="layer", layers=4,
+              spec=dict(down=Q6K, zipf=True), xbank=4, steps=200),
+    "4d": dict(T=1, name="moe_stack40_decode_b1", mode="stack", layers=40,
+               spec=dict(q6k_every=4, centered=True), xbank=16, steps=100),
+    "4p": dict(T=2048, name="moe_stack40_prefill_2048", mode="stack", layers=40,
+               spec=dict(q6k_every=4, centered=True), xbank=2, steps=4),
 }
 
 
@@ -39,14 +49,16 @@ def q4k_bytes(rows, cols):
     return rows * (cols // 256) * 144
 
 
+def q6k_bytes(rows, cols):
+    return rows * (cols // 256) * 210
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=2000)
-    ap.add_argument("--warmup", type=int, default=200)
-    ap.add_argument("--config", type=int, default=0, choices=sorted(CONFIGS))
-    ap.add_argument("--xbank", type=int, default=64)
-    ap.add_argument("--graph-steps", type=int, default=200)
+    ap.add_argument("--steps", type=int, default=None)
+    ap.add_argument("--warmup", type=int, default=None)
+    ap.add_argument("--config", default="0", choices=sorted(CONFIGS))
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     args = ap.parse_args()
@@ -61,47 +73,64 @@ def main():
     from orome_amd.moe import DeviceBuffer
 
     cf = CONFIGS[args.config]
-    T, L = cf["T"], cf["layers"]
+    T, L, NX = cf["T"], cf["layers"], cf["xbank"]
+    steps = args.steps or cf["steps"]
+    warmup = args.warmup if args.warmup is not None else max(1, steps // 10)
     H, E, K, M, S = 2048, 256, 8, 512, 512
     spec = orome_amd.make_spec(layers=L, H=H, E=E, K=K, M=M, S=S, seed=1234, **cf["spec"])
-    print("[bench] config %d (%s): building %d synthetic layers" % (args.config, cf["name"], L),
+    print("[bench] config %s (%s): %d synthetic layers, T=%d" % (args.config, cf["name"], L, T),
           file=sys.stderr, flush=True)
     img = orome_amd.synth_gguf(spec)
     gm = orome_amd.MoEModel(image=img, max_tokens=max(T, 16))
     ctx = gm.ctx
-    NX = args.xbank
-    xs = [DeviceBuffer.from_array(ctx, orome_amd.synth_normal(77, i, T * H).reshape(T, H)) for i in range(NX)]
-    hs = [DeviceBuffer.from_array(ctx, orome_amd.synth_normal(78, i, T * H).reshape(T, H)) for i in range(NX)]
+    stack = cf["mode"] == "stack"
+    xs_h = [orome_amd.synth_normal(77, i, T * H).reshape(T, H) for i in range(NX)]
+    hs_h = [orome_amd.synth_normal(78, i, T * H).reshape(T, H) for i in range(NX)]
+    xs = [DeviceBuffer.from_array(ctx, v) for v in xs_h]
+    hs = [DeviceBuffer.from_array(ctx, v) for v in hs_h]
     outs = [DeviceBuffer(ctx, T * H * 4) for _ in range(2)]
 
     def step(i):
-        gm.forward(i % L, xs[i % NX], hs[i % NX], outs[i % 2], T)
+        if stack:  # h = x_i, then 40 x (h += MoE_l(RMSNorm(h))) in place
+            gm.stack_forward(xs[i % NX], T)
+        else:
+            gm.forward(i % L, xs[i % NX], hs[i % NX], outs[i % 2], T)
 
-    # unique experts per (layer, input) combination, for the algorithmic bytes
-    combos = sorted({(i % L, i % NX) for i in range(args.graph_steps)})
-    uniq = {}
-    for (l, xi) in combos:
-        gm.forward(l, xs[xi], hs[xi], outs[0], T)
-        off = gm.debug_outputs(T)["offsets"]
-        uniq[(l, xi)] = int(np.count_nonzero(np.diff(off.astype(np.int64))))
-    u_mean = float(np.mean([uniq[(i % L, i % NX)] for i in range(args.graph_steps)]))
+    if stack:
+        # the stack works in place: keep pristine copies to restore between runs
+        def restore():
+            for b, v in zip(xs, xs_h):
+                b.upload(v)
+    else:
+        def restore():
+            pass
 
-    # graphs: G steps per replay, plus a remainder graph so exactly K steps are timed
-    G = min(args.graph_steps, args.steps)
+    # touched experts per step (weights are counted once per touched expert)
+    G = min(steps, 200 if not stack else max(1, min(steps, 10)))
+    touched = []
+    for i in range(min(G, 64)):
+        if stack:
+            gm.layer_forward(L - 1, xs[i % NX], T)
+        else:
+            gm.forward(i % L, xs[i % NX], hs[i % NX], outs[0], T)
+        off = gm.debug_outputs(T)["offsets"].astype(np.int64)
+        touched.append(int(np.count_nonzero(np.diff(off))))
+    restore()
+    u_mean = float(np.mean(touched))
 
-    def capture(n, start=0):
+    def capture(n):
         check(lib.orome_hip_capture_begin(ctx.handle), "capture")
         for i in range(n):
-            step(start + i)
+            step(i)
         ex = C.c_void_p()
         check(lib.orome_hip_capture_end(ctx.handle, C.byref(ex)), "capture_end")
         return ex
 
     g_main = capture(G)
-    rem = args.steps % G
+    rem = steps % G
     g_rem = capture(rem) if rem else None
-    reps = args.steps // G
-    for _ in range(max(1, math.ceil(args.warmup / G))):
+    reps = steps // G
+    for _ in range(max(1, math.ceil(warmup / G))):
         check(lib.orome_hip_graph_launch(ctx.handle, g_main))
     ctx.sync()
     t0 = time.perf_counter()
@@ -110,83 +139,110 @@ def main():
     if g_rem:
         check(lib.orome_hip_graph_launch(ctx.handle, g_rem))
     ctx.sync()
-    t1 = time.perf_counter()
-    elapsed = t1 - t0
-    K_steps = args.steps
+    elapsed = time.perf_counter() - t0
 
-    # per-kernel durations: the same steps, eager, with HIP events around each
-    # launch on the context stream
-    n_prof = min(args.steps, 1000)
-    check(lib.orome_hip_stage_timing(ctx.handle, n_prof))
+    # per-kernel durations: the same steps launched eagerly with HIP event
+    # pairs around every launch, queued behind a GPU delay so the kernels run
+    # back to back (no host launch gaps inside the brackets)
+    n_prof = min(steps, 400 if not stack else 8)
+    check(lib.orome_hip_stage_timing(ctx.handle, n_prof * (L if stack else 1)))
+    check(lib.orome_hip_stream_delay(ctx.handle, 400000))
     for i in range(n_prof):
         step(i)
     tot = (C.c_float * 8)()
     cnt = (C.c_int * 8)()
     check(lib.orome_hip_stage_times(ctx.handle, tot, cnt, 8))
     check(lib.orome_hip_stage_timing(ctx.handle, 0))
-    stage_us = {_lib.STAGES[i]: (tot[i] / cnt[i] * 1000.0 if cnt[i] else None) for i in range(8)}
+    stage_us = {_lib.STAGES[i]: (round(tot[i] / cnt[i] * 1000.0, 3) if cnt[i] else None)
+                for i in range(8)}
+    restore()
 
-    # algorithmic bytes (weights counted once per unique expert, activations once)
-    w_exp = 3 * q4k_bytes(M, H)          # gate + up + down of one expert (Q4_K)
-    w_sh = 3 * q4k_bytes(S, H)
-    gu_bytes = (u_mean + 1) * 2 * q4k_bytes(M, H) + T * H * 4 + (T * K + T) * M * 2
-    layer_bytes = (u_mean * w_exp + w_sh + E * H * 4 + H * 4 + T * H * 4 + 2 * T * H * 4)
+    # algorithmic work per gate/up launch and per MoE layer
+    nl = L if stack else 1
+    n_q6 = sum(1 for l in range(L) if cf["spec"].get("q6k_every") and l % 4 == 3) if stack else 0
+    down_e = q6k_bytes(H, M) if cf["spec"].get("down") == Q6K else q4k_bytes(H, M)
+    rows = T * K + T  # routed pairs plus shared-expert rows
+    gu_bytes = (u_mean + 1) * 2 * q4k_bytes(M, H) + T * H * (4 if T <= 8 else 2) + rows * M * 2
+    gu_flops = 2.0 * 2 * rows * M * H
+    layer_bytes = (u_mean * (2 * q4k_bytes(M, H) + down_e) + 3 * q4k_bytes(S, H) + E * H * 4 + H * 4
+                   + T * H * 4 * 3)
+    if stack:
+        layer_bytes += (q6k_bytes(H, M) - q4k_bytes(H, M)) * u_mean * n_q6 / L
+    step_bytes = layer_bytes * nl
+    step_flops = 2.0 * (rows * M * H * 3 + T * (E + 1) * H) * nl
     gu_us = stage_us["gate_up"]
-    achieved = gu_bytes / (gu_us * 1e-6) / 1e9
+    gu_gbs = gu_bytes / (gu_us * 1e-6) / 1e9
+    gu_tflops = gu_flops / (gu_us * 1e-6) / 1e12
+    mfma_bound = T >= 2048
+    if mfma_bound:
+        roof = {"bound": "mfma", "kernel": "gemm_gate_up", "achieved": round(gu_tflops, 2),
+                "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(gu_tflops / MFMA_F16_PEAK_TFLOPS, 4)}
+    else:
+        roof = {"bound": "hbm", "kernel": "gemv_gate_up" if T <= 8 else "gemm_gate_up",
+                "achieved": round(gu_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(gu_gbs / HBM_PEAK_GBS, 4)}
     traffic = None
     tf = os.path.join(ROOT, "profiles", "traffic_%s.json" % cf["name"])
     if os.path.exists(tf):
         traffic = json.load(open(tf)).get("gate_up_hbm_bytes_per_launch")
+    roof.update({"traffic": traffic, "algorithmic_bytes_per_launch": int(gu_bytes),
+                 "algorithmic_flops_per_launch": gu_flops, "avg_launch_us": gu_us,
+                 "gbs": round(gu_gbs, 1), "tflops": round(gu_tflops, 2)})
 
     cpu = None
     if not args.no_cpu:
         sys.path.insert(0, os.path.join(ROOT, "oracle"))
         import oracle as O
         om = O.OracleModel(img)
-        xh = [orome_amd.synth_normal(77, i, T * H).reshape(T, H) for i in range(NX)]
-        hh = [orome_amd.synth_normal(78, i, T * H).reshape(T, H) for i in range(NX)]
+        tsub = min(T, 64)
         n = 0
         c0 = time.perf_counter()
         while time.perf_counter() - c0 < args.cpu_seconds:
-            om.forward(n % L, xh[n % NX], hh[n % NX], omp=False)
+            xi = xs_h[n % NX][:tsub]
+            if stack:
+                om.layer_forward(n % L, xi.copy(), omp=False)
+            else:
+                om.forward(n % L, xi, hs_h[n % NX][:tsub], omp=False)
             n += 1
         ct = time.perf_counter() - c0
-        cpu = {"value": round(n * T / ct, 3), "unit": "tokens/s", "cores": 1, "kind": "port",
-               "sample": "%d steps (%d tokens) of the same workload, scalar C oracle, 1 thread, "
-                         "%.1f s" % (n, n * T, ct)}
+        rate = n * tsub / ct / nl  # tokens/s for a full step (nl layers)
+        cpu = {"value": round(rate, 4), "unit": "tokens/s", "cores": 1, "kind": "port",
+               "sample": "%d single-layer passes of %d token(s) (%s), scalar C oracle, 1 thread, %.1f s%s"
+                         % (n, tsub, "first %d of each batch" % tsub if tsub < T else "full batch",
+                            ct, "; scaled to the %d-layer step" % nl if nl > 1 else "")}
 
-    value = T * K_steps / elapsed
+    value = T * steps / elapsed
     out = {
-        "metric": "MoE-layer tokens/s (B=%d decode, one MoE FFN block per step)" % T,
+        "metric": "MoE-layer tokens/s" if not stack else "MoE 40-layer stack tokens/s",
         "value": round(value, 1),
         "unit": "tokens/s",
         "n_gpus": 1,
-        "steps": K_steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(elapsed / K_steps * 1000, 5),
+        "steps": steps,
+        "warmup": warmup,
+        "ms_per_step": round(elapsed / steps * 1000, 5),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "q4_k weights, fp16 activations, fp32 accumulate",
-        "data": "synthetic (seeded GGUF Q4_K per BASELINE config %d, %d rotating layers, %d inputs)"
+        "dtype": "q4_k/q6_k weights, fp16 activations, fp32 accumulate",
+        "data": "synthetic seeded GGUF per BASELINE config %s (%d layers, %d input batches)"
                 % (args.config, L, NX),
         "config": {"workload": cf["name"], "baseline_config": args.config, "tokens_per_step": T,
-                   "hidden": H, "experts": E, "top_k": K, "expert_intermediate": M,
-                   "shared_intermediate": S, "parallelism": "single GPU"},
-        "roofline": {"bound": "hbm", "kernel": "gemv_gate_up", "achieved": round(achieved, 1),
-                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": traffic, "algorithmic_bytes_per_launch": int(gu_bytes),
-                     "avg_launch_us": round(gu_us, 3)},
-        "layer": {"algorithmic_bytes_per_step": int(layer_bytes), "unique_experts_per_step": u_mean,
-                  "gbs": round(layer_bytes * K_steps / elapsed / 1e9, 1),
-                  "frac_of_hbm_peak": round(layer_bytes * K_steps / elapsed / 1e9 / HBM_PEAK_GBS, 4)},
-        "stage_us": {k: (round(v, 3) if v is not None else None) for k, v in stage_us.items()},
+                   "layers_per_step": nl, "hidden": H, "experts": E, "top_k": K,
+                   "expert_intermediate": M, "shared_intermediate": S, "parallelism": "single GPU"},
+        "roofline": roof,
+        "step": {"algorithmic_bytes": int(step_bytes), "touched_experts_per_layer": u_mean,
+                 "gbs": round(step_bytes * steps / elapsed / 1e9, 1),
+                 "hbm_frac": round(step_bytes * steps / elapsed / 1e9 / HBM_PEAK_GBS, 4),
+                 "tflops": round(step_flops * steps / elapsed / 1e12, 2),
+                 "mfma_frac": round(step_flops * steps / elapsed / 1e12 / MFMA_F16_PEAK_TFLOPS, 4),
+                 "us_per_layer": round(elapsed / steps / nl * 1e6, 3)},
+        "stage_us": stage_us,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)
-    lib.orome_hip_graph_destroy(g_main)
-    if g_rem:
-        lib.orome_hip_graph_destroy(g_rem)
+    for g in (g_main, g_rem):
+        if g:
+            lib.orome_hip_graph_destroy(g)
 
 
 if __name__ == "__main__":

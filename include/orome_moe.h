@@ -285,6 +285,11 @@ int orome_hip_graph_destroy(void *graph_exec);
  * 3 dispatch, 4 fp16 staging, 5 gate/up, 6 down, 7 combine. */
 #define OROME_N_STAGES 8
 int orome_hip_stage_timing(orome_hip_ctx *ctx, int capacity);
+/* Queue a bounded GPU busy-wait of `usec` microseconds (<= 10 s) on the
+ * context stream, so that work queued behind it runs back to back and event
+ * pairs bracket kernels rather than host launch gaps.  No counterpart in the
+ * reference. */
+int orome_hip_stream_delay(orome_hip_ctx *ctx, uint32_t usec);
 /* total milliseconds and sample counts per stage since timing was enabled */
 int orome_hip_stage_times(orome_hip_ctx *ctx, float *total_ms, int *counts, int n);
 

@@ -122,6 +122,7 @@ SIGNATURES = {
     "orome_hip_graph_launch": (I, [VP, VP]),
     "orome_hip_graph_destroy": (I, [VP]),
     "orome_hip_stage_timing": (I, [VP, I]),
+    "orome_hip_stream_delay": (I, [VP, U32]),
     "orome_hip_stage_times": (I, [VP, F32P, P(I), I]),
     "orome_synth_gguf_size": (SZ, [P(SynthSpec)]),
     "orome_synth_gguf_write": (I, [P(SynthSpec), VP, SZ]),

@@ -463,3 +463,10 @@ extern "C" int orome_hip_stage_times(orome_hip_ctx *c, float *total_ms, int *cou
     }
     return OROME_OK;
 }
+
+extern "C" int orome_hip_stream_delay(orome_hip_ctx *c, uint32_t usec) {
+    if (!c || usec > 10000000u) return orome_fail(OROME_EINVAL, "orome_hip_stream_delay: bad argument");
+    if (set_dev(c)) return OROME_EHIP;
+    LAUNCH(launch_delay(usec, c->stream), "delay");
+    return OROME_OK;
+}

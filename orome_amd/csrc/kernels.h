@@ -56,6 +56,7 @@ int launch_gemv_down(const ExpertSide &ex, const SharedSide &sh, const _Float16 
                      const _Float16 *act_sh, int T, int H, int M, int K, int E, const uint32_t *list,
                      float *y, float *ysh, hipStream_t s);
 
+int launch_delay(uint32_t usec, hipStream_t s);
 int launch_rmsnorm(const float *h, const float *w, int T, int H, float eps, float *x, hipStream_t s);
 int launch_dequant(int fmt, const uint8_t *src, uint32_t rows, uint32_t n, float *out32,
                    _Float16 *out16, hipStream_t s);

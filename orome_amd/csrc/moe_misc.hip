@@ -99,12 +99,22 @@ __global__ void k_combine(const float *y, const float *ysh, const uint32_t *pos,
     const int t = blockIdx.y;
     const int c = (blockIdx.x * blockDim.x + threadIdx.x) * 4;
     if (c >= H) return;
+    /* all pair positions first, then all expert rows in flight together */
+    uint32_t pk[OROME_MAXK];
+    f4 v[OROME_MAXK];
+#pragma unroll
+    for (int k = 0; k < OROME_MAXK; k++)
+        if (k < K) pk[k] = pos[t * K + k];
+#pragma unroll
+    for (int k = 0; k < OROME_MAXK; k++)
+        if (k < K) v[k] = *(const f4 *)(y + (size_t)pk[k] * H + c);
     f4 moe = {0, 0, 0, 0};
-    for (int k = 0; k < K; k++) {
-        const float wk = w[t * K + k];
-        f4 v = *(const f4 *)(y + (size_t)pos[t * K + k] * H + c);
-        moe.x += wk * v.x; moe.y += wk * v.y; moe.z += wk * v.z; moe.w += wk * v.w;
-    }
+#pragma unroll
+    for (int k = 0; k < OROME_MAXK; k++)
+        if (k < K) {
+            const float wk = w[t * K + k];
+            moe.x += wk * v[k].x; moe.y += wk * v[k].y; moe.z += wk * v[k].z; moe.w += wk * v[k].w;
+        }
     f4 base = h_in ? *(const f4 *)(h_in + (size_t)t * H + c) : f4{0, 0, 0, 0};
     f4 o = {base.x + moe.x, base.y + moe.y, base.z + moe.z, base.w + moe.w};
     if (has_sh) {
@@ -122,5 +132,22 @@ int launch_combine(const float *y, const float *ysh, const uint32_t *pos, const 
     dim3 grid((H / 4 + 255) / 256, T);
     hipLaunchKernelGGL(k_combine, grid, dim3(256), 0, s, y, ysh, pos, w, sgl, has_shared, h_in,
                        h_out, T, H, K);
+    return hipGetLastError() == hipSuccess ? 0 : -3;
+}
+
+/* Bounded busy-wait on the GPU (one lane): holds the stream for `ticks` of the
+ * 100 MHz real-time counter so the host can queue work behind it.  The loop
+ * always ends (tick deadline or iteration cap). */
+__global__ void k_delay(uint64_t ticks) {
+    if (threadIdx.x != 0) return;
+    const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+    for (uint32_t it = 0; it < (1u << 26); it++) {
+        if (__builtin_amdgcn_s_memrealtime() - t0 >= ticks) break;
+        __builtin_amdgcn_s_sleep(127);
+    }
+}
+
+int launch_delay(uint32_t usec, hipStream_t s) {
+    hipLaunchKernelGGL(k_delay, dim3(1), dim3(64), 0, s, (uint64_t)usec * 100u);
     return hipGetLastError() == hipSuccess ? 0 : -3;
 }
