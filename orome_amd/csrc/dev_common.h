@@ -72,6 +72,16 @@ DEV float wave_sum_canon(float v) {
     return (r0 + r1) + (r2 + r3);
 }
 
+/* Wave64 sum in no particular order (every lane gets the total). */
+DEV float wave_sum_fast(float v) {
+    v = row_sum16(v);
+    int b = __builtin_bit_cast(int, v);
+    return (__builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 0)) +
+            __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 16))) +
+           (__builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 32)) +
+            __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 48)));
+}
+
 /* Sum over aligned groups of 16 lanes (a DPP row). */
 template <int WIDTH>
 DEV float group_sum(float v) {
@@ -188,6 +198,14 @@ DEV u4 ld_u4(const uint8_t *p) {
     typedef const __attribute__((address_space(1))) u4 *gp4;
     return *(gp4)(uintptr_t)p;
 }
+
+/* Cross-block hand-off inside one kernel without cache maintenance: data is
+ * stored and loaded with device-coherent (sc1) accesses, the writer drains
+ * its memory counter before signalling on an atomic counter, and the block
+ * that observes the last arrival reads the data back coherently. */
+DEV void st_coh(float *p, float v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+DEV float ld_coh(const float *p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+DEV void drain_mem() { __builtin_amdgcn_s_waitcnt(0); }
 
 /* ------------------------------------------------------------ dots */
 DEV float dot2(h2 a, h2 b, float c) { return __builtin_amdgcn_fdot2(a, b, c, false); }

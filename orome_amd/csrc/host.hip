@@ -300,8 +300,11 @@ extern "C" int orome_moe_forward(orome_hip_ctx *c, const ModelConfig *cfg, const
     if (path == OROME_PATH_GEMV) {
         if (T > 8) return orome_fail(OROME_EUNSUPPORTED, "GEMV path handles T <= 8 (T=%d)", T);
         TLAUNCH(c, ST_ROUTE, launch_route_small(a, s), "router logits");
-        TLAUNCH(c, ST_TOPK, launch_topk_dispatch_small(a, s), "top-k + dispatch");
-        TLAUNCH(c, ST_GATE_UP, launch_gemv_gate_up(ex, sh, x, T, H, M, K, E, c->list, c->pairs, c->act, c->act_sh, s),
+        /* one or two tokens: every gate/up block selects the experts itself
+         * (saves a launch); larger batches route once in a separate kernel */
+        const int fold = T <= 2;
+        if (!fold) TLAUNCH(c, ST_TOPK, launch_topk_dispatch_small(a, s), "top-k + dispatch");
+        TLAUNCH(c, ST_GATE_UP, launch_gemv_gate_up(ex, sh, a, fold, x, T, H, M, K, E, c->act, c->act_sh, s),
                 "gemv gate/up");
         TLAUNCH(c, ST_DOWN, launch_gemv_down(ex, sh, c->act, c->act_sh, T, H, M, K, E, c->list, c->y, c->ysh, s),
                 "gemv down");

@@ -44,14 +44,18 @@ struct SharedSide {
 };
 
 int launch_route_small(const RouteArgs &a, hipStream_t s);
-int launch_topk_dispatch_small(const RouteArgs &a, hipStream_t s);
 int launch_route_logits(const RouteArgs &a, hipStream_t s);
 int launch_topk(const RouteArgs &a, hipStream_t s);
 int launch_dispatch(const RouteArgs &a, uint32_t *tiles, int tile_m, int has_shared, hipStream_t s);
 
-int launch_gemv_gate_up(const ExpertSide &ex, const SharedSide &sh, const float *x, int T, int H,
-                        int M, int K, int E, const uint32_t *list, const uint32_t *pairs,
-                        _Float16 *act, _Float16 *act_sh, hipStream_t s);
+/* decode gate/up; with route_in_block the top-k + dispatch of the call is
+ * folded in (every block selects; block 0 publishes the routing outputs in
+ * `ra`), otherwise it reads the routing written by launch_topk_dispatch_small */
+int launch_gemv_gate_up(const ExpertSide &ex, const SharedSide &sh, const RouteArgs &ra, int route_in_block,
+                        const float *x, int T, int H, int M, int K, int E, _Float16 *act, _Float16 *act_sh,
+                        hipStream_t s);
+int launch_topk_dispatch_small(const RouteArgs &a, hipStream_t s);
+
 int launch_gemv_down(const ExpertSide &ex, const SharedSide &sh, const _Float16 *act,
                      const _Float16 *act_sh, int T, int H, int M, int K, int E, const uint32_t *list,
                      float *y, float *ysh, hipStream_t s);

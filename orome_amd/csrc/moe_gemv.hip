@@ -25,6 +25,7 @@
  */
 #include "dev_common.h"
 #include "kernels.h"
+#include "route_dev.h"
 
 enum { FQ4K = 0, FQ5K = 1, FQ6K = 2, FQ8 = 3 };
 
@@ -46,9 +47,12 @@ DEV float load_x16_f32(const float *p, h2 *o) {
     for (int v = 0; v < 8; v++) s = dot2(o[v], one, s);
     return s;
 }
-/* 8 consecutive fp16 (16 bytes) -> 4 pairs */
+/* 8 consecutive fp16 (16 bytes) -> 4 pairs; LX: p points into LDS */
+template <bool LX = false>
 DEV void load_h8(const _Float16 *p, h2 *o) {
-    u4 v = ld_u4((const uint8_t *)p);
+    u4 v;
+    if constexpr (LX) v = *(const __attribute__((address_space(3))) u4 *)p;
+    else v = ld_u4((const uint8_t *)p);
     o[0] = as_h2(v.x); o[1] = as_h2(v.y); o[2] = as_h2(v.z); o[3] = as_h2(v.w);
 }
 DEV float hsum(const h2 *o, int n) {
@@ -163,99 +167,122 @@ struct GUArgs {
     int routed_blocks;
 };
 
-template <int NT, int RPW, int SFMT>
-DEV void gu_body(const GUArgs &a, const uint8_t *gbase, const uint8_t *ubase, int rows_total,
-                 int r0, int n, const int *tok, _Float16 *out, int out_ld, int lane) {
-    (void)rows_total;
+/* One wave: RPW gate rows and RPW up rows for the n tokens of a slot.  Raw
+ * weight chunks of all rows are loaded first; the token loop is a runtime
+ * loop (register use does not grow with the batch), and each (row, token)
+ * sum is reduced across the wave at once.  Lane 0 keeps running totals in
+ * `red` when a row needs more than one pass of 64 chunks (H > 2048). */
+template <int RPW, int SFMT>
+DEV void gu_body(const GUArgs &a, const uint8_t *gbase, const uint8_t *ubase, int r0, int n,
+                 const int *tok, _Float16 *out, int out_ld, int lane, float *red) {
     const int H = a.H, NC = H / 32;
-    float ag[RPW][NT], au[RPW][NT];
-#pragma unroll
-    for (int i = 0; i < RPW; i++)
-#pragma unroll
-        for (int j = 0; j < NT; j++) ag[i][j] = au[i][j] = 0.0f;
     const size_t rb = SFMT == FQ8 ? row_bytes(FQ8, H) : row_bytes(FQ4K, H);
-    for (int c = lane; c < NC; c += 64) {
+    for (int c0 = 0; c0 < NC; c0 += 64) {
+        const int c = c0 + lane;
+        const bool live = c < NC;
+        const int cc = live ? c : c0;
         int klo, khi;
-        if (SFMT == FQ8) { klo = c * 32; khi = klo + 16; }
-        else { q4_pos(c, klo); khi = klo + 32; }
+        if (SFMT == FQ8) { klo = cc * 32; khi = klo + 16; }
+        else { q4_pos(cc, klo); khi = klo + 32; }
         if (SFMT == FQ8) {
             Q8Raw g[RPW], u[RPW];
 #pragma unroll
             for (int i = 0; i < RPW; i++) {
-                g[i] = q8_load(gbase + (size_t)(r0 + i) * rb, c);
-                u[i] = q8_load(ubase + (size_t)(r0 + i) * rb, c);
+                g[i] = q8_load(gbase + (size_t)(r0 + i) * rb, cc);
+                u[i] = q8_load(ubase + (size_t)(r0 + i) * rb, cc);
             }
-#pragma unroll
-            for (int j = 0; j < NT; j++) {
-                if (j >= n) break;
+            for (int j = 0; j < n; j++) {
                 h2 x[16];
                 load_x16_f32(a.x + (size_t)tok[j] * H + klo, x);
                 load_x16_f32(a.x + (size_t)tok[j] * H + khi, x + 8);
 #pragma unroll
                 for (int i = 0; i < RPW; i++) {
-                    ag[i][j] += q8_dot(g[i], x);
-                    au[i][j] += q8_dot(u[i], x);
+                    float pg = live ? q8_dot(g[i], x) : 0.0f, pu = live ? q8_dot(u[i], x) : 0.0f;
+                    pg = wave_sum_fast(pg);
+                    pu = wave_sum_fast(pu);
+                    if (lane == 0) {
+                        red[(i * 2) * 16 + j] += pg;
+                        red[(i * 2 + 1) * 16 + j] += pu;
+                    }
                 }
             }
         } else {
             Q4Raw g[RPW], u[RPW];
 #pragma unroll
             for (int i = 0; i < RPW; i++) {
-                g[i] = q4_load(gbase + (size_t)(r0 + i) * rb, c);
-                u[i] = q4_load(ubase + (size_t)(r0 + i) * rb, c);
+                g[i] = q4_load(gbase + (size_t)(r0 + i) * rb, cc);
+                u[i] = q4_load(ubase + (size_t)(r0 + i) * rb, cc);
             }
-#pragma unroll
-            for (int j = 0; j < NT; j++) {
-                if (j >= n) break;
+            for (int j = 0; j < n; j++) {
                 h2 xl[8], xh[8];
                 float Xl = load_x16_f32(a.x + (size_t)tok[j] * H + klo, xl);
                 float Xh = load_x16_f32(a.x + (size_t)tok[j] * H + khi, xh);
 #pragma unroll
                 for (int i = 0; i < RPW; i++) {
-                    ag[i][j] += q4_dot(g[i], c, xl, xh, Xl, Xh);
-                    au[i][j] += q4_dot(u[i], c, xl, xh, Xl, Xh);
+                    float pg = live ? q4_dot(g[i], cc, xl, xh, Xl, Xh) : 0.0f;
+                    float pu = live ? q4_dot(u[i], cc, xl, xh, Xl, Xh) : 0.0f;
+                    pg = wave_sum_fast(pg);
+                    pu = wave_sum_fast(pu);
+                    if (lane == 0) {
+                        red[(i * 2) * 16 + j] += pg;
+                        red[(i * 2 + 1) * 16 + j] += pu;
+                    }
                 }
             }
         }
     }
+    if (lane == 0)
+        for (int j = 0; j < n; j++)
 #pragma unroll
-    for (int i = 0; i < RPW; i++)
-#pragma unroll
-        for (int j = 0; j < NT; j++) {
-            if (j >= n) break;
-            float g = wave_sum_canon(ag[i][j]);
-            float u = wave_sum_canon(au[i][j]);
-            if (lane == 0) out[(size_t)j * out_ld + r0 + i] = (_Float16)(silu_f(g) * u);
-        }
+            for (int i = 0; i < RPW; i++)
+                out[(size_t)j * out_ld + r0 + i] =
+                    (_Float16)(silu_f(red[(i * 2) * 16 + j]) * red[(i * 2 + 1) * 16 + j]);
 }
 
-template <int NT, int RPW>
-__global__ __launch_bounds__(256) void k_gemv_gate_up(GUArgs a) {
+#define GU_RPW 4
+/* Decode gate/up with the routing folded in: routed blocks select the
+ * experts themselves from the router logits (block 0 publishes the routing
+ * for the down kernel); shared-expert blocks start at once. */
+template <int EPL, bool ROUTE>
+__global__ __launch_bounds__(256) void k_gemv_gate_up(GUArgs a, RouteArgs ra) {
+    __shared__ float red_all[4][GU_RPW * 2 * 16];
+    __shared__ int tok[16];
+    __shared__ RouteLds r;
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-    const int rows_blk = 4 * RPW;
+    const int rows_blk = 4 * GU_RPW;
+    float *red = red_all[wv];
+    for (int i = lane; i < GU_RPW * 2 * 16; i += 64) red[i] = 0.0f;
     int b = blockIdx.x;
-    int tok[NT];
     if (b < a.routed_blocks) {
         const int bpe = a.M / rows_blk;
         const int u = b / bpe, tile = b % bpe;
-        const uint32_t n_act = ACT_N(a.list);
-        if ((uint32_t)u >= n_act) return;
-        const int e = (int)ACT_E(a.list, u);
-        const int s0 = (int)ACT_OFF(a.list, a.E, u), n = (int)ACT_OFF(a.list, a.E, u + 1) - s0;
-#pragma unroll
-        for (int j = 0; j < NT; j++) tok[j] = j < n ? (int)(a.pairs[s0 + j] / (uint32_t)a.K) : 0;
-        gu_body<NT, RPW, FQ4K>(a, a.gate + (size_t)e * a.gate_stride, a.up + (size_t)e * a.up_stride,
-                               a.M, tile * rows_blk + wv * RPW, n, tok, a.act + (size_t)s0 * a.M, a.M,
-                               lane);
+        int e, s0, n;
+        if constexpr (ROUTE) {
+            route_block_lds<EPL>(ra, r, b == 0);
+            if (u >= r.nact) return;
+            e = r.act_e[u];
+            s0 = r.act_off[u];
+            n = r.act_off[u + 1] - s0;
+            if (threadIdx.x < n) tok[threadIdx.x] = r.pairs[s0 + threadIdx.x] / a.K;
+        } else {
+            if ((uint32_t)u >= ACT_N(a.list)) return;
+            e = (int)ACT_E(a.list, u);
+            s0 = (int)ACT_OFF(a.list, a.E, u);
+            n = (int)ACT_OFF(a.list, a.E, u + 1) - s0;
+            if (threadIdx.x < n) tok[threadIdx.x] = (int)(a.pairs[s0 + threadIdx.x] / (uint32_t)a.K);
+        }
+        __syncthreads();
+        gu_body<GU_RPW, FQ4K>(a, a.gate + (size_t)e * a.gate_stride, a.up + (size_t)e * a.up_stride,
+                              tile * rows_blk + wv * GU_RPW, n, tok, a.act + (size_t)s0 * a.M, a.M, lane, red);
     } else {
         const int tile = b - a.routed_blocks;
-#pragma unroll
-        for (int j = 0; j < NT; j++) tok[j] = j;
-        const int r0 = tile * rows_blk + wv * RPW;
+        if (threadIdx.x < a.T) tok[threadIdx.x] = threadIdx.x;
+        __syncthreads();
+        const int r0 = tile * rows_blk + wv * GU_RPW;
         if (a.sh_fmt == FQ8)
-            gu_body<NT, RPW, FQ8>(a, a.sh_gate, a.sh_up, a.S, r0, a.T, tok, a.act_sh, a.S, lane);
+            gu_body<GU_RPW, FQ8>(a, a.sh_gate, a.sh_up, r0, a.T, tok, a.act_sh, a.S, lane, red);
         else
-            gu_body<NT, RPW, FQ4K>(a, a.sh_gate, a.sh_up, a.S, r0, a.T, tok, a.act_sh, a.S, lane);
+            gu_body<GU_RPW, FQ4K>(a, a.sh_gate, a.sh_up, r0, a.T, tok, a.act_sh, a.S, lane, red);
     }
 }
 
@@ -371,39 +398,43 @@ __global__ __launch_bounds__(128) void k_gemv_down(DownArgs a) {
 }
 
 /* ------------------------------------------------------------ launch */
-template <int NT>
-static void gu_launch(const GUArgs &a, int rows_blk, int blocks, hipStream_t s) {
-    constexpr int RPW = NT == 1 ? 4 : (NT == 2 ? 2 : 1);
-    (void)rows_blk;
-    hipLaunchKernelGGL((k_gemv_gate_up<NT, RPW>), dim3(blocks), dim3(256), 0, s, a);
-}
 
-static int nt_for(int T) { return T <= 1 ? 1 : T <= 2 ? 2 : T <= 4 ? 4 : T <= 8 ? 8 : 0; }
+static int epl_of(int E) { return E <= 64 ? 1 : E <= 128 ? 2 : E <= 256 ? 4 : E <= 512 ? 8 : E <= 1024 ? 16 : 0; }
 
-int launch_gemv_gate_up(const ExpertSide &ex, const SharedSide &sh, const float *x, int T, int H,
-                        int M, int K, int E, const uint32_t *list, const uint32_t *pairs,
-                        _Float16 *act, _Float16 *act_sh, hipStream_t s) {
-    const int NT = nt_for(T);
-    if (!NT || H % 256 || ex.gate_fmt != FQ4K) return -2;
-    const int RPW = NT == 1 ? 4 : (NT == 2 ? 2 : 1), rows_blk = 4 * RPW;
+int launch_gemv_gate_up(const ExpertSide &ex, const SharedSide &sh, const RouteArgs &ra, int route_in_block,
+                        const float *x, int T, int H, int M, int K, int E, _Float16 *act, _Float16 *act_sh,
+                        hipStream_t s) {
+    const int rows_blk = 4 * GU_RPW;
+    if (T < 1 || T > 16 || T * K > 256 || H % 256 || ex.gate_fmt != FQ4K || !epl_of(E)) return -2;
     if (M % rows_blk || (sh.gate && sh.S % rows_blk)) return -2;
     if (sh.gate && sh.gate_fmt != FQ4K && sh.gate_fmt != FQ8) return -2;
     GUArgs a;
     a.gate = ex.gate; a.up = ex.up; a.gate_stride = ex.gate_stride; a.up_stride = ex.up_stride;
     a.sh_gate = sh.gate; a.sh_up = sh.up; a.sh_fmt = sh.gate_fmt; a.S = sh.gate ? sh.S : 0;
-    a.x = x; a.T = T; a.H = H; a.M = M; a.K = K; a.E = E; a.list = list; a.pairs = pairs;
+    a.x = x; a.T = T; a.H = H; a.M = M; a.K = K; a.E = E; a.list = ra.list; a.pairs = ra.pairs;
     a.act = act; a.act_sh = act_sh;
     const int umax = T * K < E ? T * K : E;
     a.routed_blocks = umax * (M / rows_blk);
     const int blocks = a.routed_blocks + (sh.gate ? sh.S / rows_blk : 0);
-    switch (NT) {
-        case 1: gu_launch<1>(a, rows_blk, blocks, s); break;
-        case 2: gu_launch<2>(a, rows_blk, blocks, s); break;
-        case 4: gu_launch<4>(a, rows_blk, blocks, s); break;
-        default: gu_launch<8>(a, rows_blk, blocks, s); break;
+#define GU_LAUNCH(EPLV)                                                                          \
+    do {                                                                                          \
+        if (route_in_block)                                                                       \
+            hipLaunchKernelGGL((k_gemv_gate_up<EPLV, true>), dim3(blocks), dim3(256), 0, s, a, ra);  \
+        else                                                                                      \
+            hipLaunchKernelGGL((k_gemv_gate_up<EPLV, false>), dim3(blocks), dim3(256), 0, s, a, ra); \
+    } while (0)
+    switch (epl_of(E)) {
+        case 1: GU_LAUNCH(1); break;
+        case 2: GU_LAUNCH(2); break;
+        case 4: GU_LAUNCH(4); break;
+        case 8: GU_LAUNCH(8); break;
+        default: GU_LAUNCH(16); break;
     }
     return hipGetLastError() == hipSuccess ? 0 : -3;
 }
+
+
+static int nt_for(int T) { return T <= 1 ? 1 : T <= 2 ? 2 : T <= 4 ? 4 : T <= 8 ? 8 : 0; }
 
 int launch_gemv_down(const ExpertSide &ex, const SharedSide &sh, const _Float16 *act,
                      const _Float16 *act_sh, int T, int H, int M, int K, int E, const uint32_t *list,

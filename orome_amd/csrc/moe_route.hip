@@ -17,89 +17,7 @@
 #include "dev_common.h"
 #include "kernels.h"
 
-/* -------------------------------------------------------- key helpers */
-DEV uint64_t route_key(float v, int e) {
-    if (v == 0.0f) v = 0.0f; /* -0 and +0 tie by index, as in IEEE compare */
-    uint32_t b = __builtin_bit_cast(uint32_t, v);
-    uint32_t ord = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
-    return ((uint64_t)ord << 32) | (uint64_t)(0xFFFFFFFFu - (uint32_t)e);
-}
-DEV float key_value(uint64_t k) {
-    uint32_t ord = (uint32_t)(k >> 32);
-    uint32_t b = (ord & 0x80000000u) ? (ord & 0x7FFFFFFFu) : ~ord;
-    return __builtin_bit_cast(float, b);
-}
-DEV int key_expert(uint64_t k) { return (int)(0xFFFFFFFFu - (uint32_t)k); }
-
-template <int CTRL>
-DEV uint64_t dpp64(uint64_t v) {
-    return ((uint64_t)dppu<CTRL>((uint32_t)(v >> 32)) << 32) | dppu<CTRL>((uint32_t)v);
-}
-DEV uint64_t max64(uint64_t a, uint64_t b) { return a > b ? a : b; }
-DEV uint64_t readlane64(uint64_t v, int l) {
-    return ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(v >> 32), l) << 32) |
-           (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, l);
-}
-/* wave64 maximum of a 64-bit key (DPP within rows, then the four row maxima) */
-DEV uint64_t wave_max64(uint64_t m) {
-    m = max64(m, dpp64<DPP_XOR1>(m));
-    m = max64(m, dpp64<DPP_XOR2>(m));
-    m = max64(m, dpp64<DPP_HALF_MIRROR>(m));
-    m = max64(m, dpp64<DPP_MIRROR>(m));
-    return max64(max64(readlane64(m, 0), readlane64(m, 16)), max64(readlane64(m, 32), readlane64(m, 48)));
-}
-
-/* One token's top-K on one wave.  Lane 0 writes idx/w/sgl; e_out (LDS, may be
- * NULL) receives the K expert ids. */
-template <int EPL>
-DEV void wave_topk(const float *l, const float *bias, int E, int K, int lane, int32_t *idx_out,
-                   float *w_out, float *sgl_out, int *e_out) {
-    uint64_t key[EPL];
-#pragma unroll
-    for (int j = 0; j < EPL; j++) {
-        int e = lane + 64 * j;
-        key[j] = 0;
-        if (e < E) {
-            float v = l[e];
-            if (bias) v = v + bias[e];
-            key[j] = route_key(v, e);
-        }
-    }
-    float vals[OROME_MAXK];
-    int ids[OROME_MAXK];
-#pragma unroll
-    for (int k = 0; k < OROME_MAXK; k++) {
-        if (k < K) {
-            uint64_t m = key[0];
-#pragma unroll
-            for (int j = 1; j < EPL; j++) m = key[j] > m ? key[j] : m;
-            m = wave_max64(m);
-#pragma unroll
-            for (int j = 0; j < EPL; j++)
-                if (key[j] == m) key[j] = 0;
-            vals[k] = key_value(m);
-            ids[k] = key_expert(m);
-        }
-    }
-    if (lane == 0) {
-        float mx = vals[0], sum = 0.0f, tw[OROME_MAXK];
-#pragma unroll
-        for (int k = 0; k < OROME_MAXK; k++)
-            if (k < K) {
-                tw[k] = expf(vals[k] - mx);
-                sum += tw[k];
-            }
-        float inv = sum > 0.0f ? 1.0f / sum : 0.0f;
-#pragma unroll
-        for (int k = 0; k < OROME_MAXK; k++)
-            if (k < K) {
-                idx_out[k] = ids[k];
-                w_out[k] = tw[k] * inv;
-                if (e_out) e_out[k] = ids[k];
-            }
-        *sgl_out = l[E];
-    }
-}
+#include "route_dev.h"
 
 /* canonical dot of one wave over H (H % 256 == 0, H <= 4096), for up to
  * TMAX tokens; all loads of a row are issued before the multiply-adds */
@@ -155,51 +73,9 @@ __global__ __launch_bounds__(256) void k_route_small(RouteArgs a) {
     }
 }
 
-/* Small-batch selection and dispatch (T*K <= 256), one block: a wave per
- * token for the top-k, then the stable counting sort of the T*K pairs by
- * ranking each pair against all others. */
 template <int EPL>
 __global__ __launch_bounds__(256) void k_topk_dispatch_small(RouteArgs a) {
-    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-    const int E = a.E, T = a.T, K = a.K;
-    __shared__ int s_e[256];
-    __shared__ int s_head[256];
-    for (int t = wv; t < T; t += 4)
-        wave_topk<EPL>(a.logits + (size_t)t * (E + 1), a.bias, E, K, lane, a.idx + t * K, a.w + t * K,
-                       a.sgl + t, s_e + t * K);
-    __syncthreads();
-    const int NP = T * K, p = threadIdx.x;
-    int e = 0, less = 0, before = 0;
-    if (p < NP) {
-        e = s_e[p];
-        for (int q = 0; q < NP; q++) {
-            int eq = s_e[q];
-            less += eq < e;
-            before += (q < p) & (eq == e);
-        }
-        uint32_t pos = (uint32_t)(less + before);
-        a.pairs[pos] = (uint32_t)p;
-        a.pos[p] = pos;
-        s_head[p] = before == 0;
-    }
-    __syncthreads();
-    if (p < NP && s_head[p]) {
-        int rank = 0;
-        for (int q = 0; q < NP; q++) rank += s_head[q] & (s_e[q] < e);
-        ACT_E(a.list, rank) = (uint32_t)e;
-        ACT_OFF(a.list, E, rank) = (uint32_t)less;
-    }
-    if (threadIdx.x == 0) {
-        int n = 0;
-        for (int q = 0; q < NP; q++) n += s_head[q];
-        ACT_N(a.list) = (uint32_t)n;
-        ACT_OFF(a.list, E, n) = (uint32_t)NP;
-    }
-    for (int ee = threadIdx.x; ee <= E; ee += 256) {
-        int c = 0;
-        for (int q = 0; q < NP; q++) c += s_e[q] < ee;
-        a.offsets[ee] = (uint32_t)c;
-    }
+    topk_dispatch_block<EPL, false>(a);
 }
 
 /* Large-batch router logits: a block computes 16 rows x 8 tokens; each wave
@@ -257,97 +133,123 @@ __global__ __launch_bounds__(256) void k_topk(RouteArgs a) {
                    a.w + t * a.K, a.sgl + t, nullptr);
 }
 
+/* Block-wide exclusive scan of three counters per expert (one thread per
+ * expert, E <= DSP_THREADS), Hillis-Steele over LDS. */
+#define DSP_THREADS 1024
+DEV void block_scan3(uint32_t *a, uint32_t *b, uint32_t *c, int n) {
+    const int tid = threadIdx.x;
+    for (int off = 1; off < n; off <<= 1) {
+        uint32_t va = 0, vb = 0, vc = 0;
+        if (tid < n && tid >= off) { va = a[tid - off]; vb = b[tid - off]; vc = c[tid - off]; }
+        __syncthreads();
+        if (tid < n && tid >= off) { a[tid] += va; b[tid] += vb; c[tid] += vc; }
+        __syncthreads();
+    }
+}
+
 /* Dispatch for any T (one block of 1024 threads):
- *  1. LDS histogram of the T*K expert ids; exclusive scan -> offsets.
+ *  1. LDS histogram of the T*K expert ids; block scans give the offsets, the
+ *     active-expert ranks and the GEMM tile offsets.
  *  2. Stable scatter in chunks of 1024 tokens: each expert keeps a 1024-bit
  *     membership mask of the chunk's tokens, so a pair's rank inside its
  *     expert is the popcount of the mask below its token, plus the count
  *     carried from earlier chunks.
  *  3. Active-expert list and GEMM tile list (expert, first row, rows), tiles
- *     of GEMM_TILE_M rows; the shared expert (id E) covers tokens 0..T-1. */
-#define DSP_THREADS 1024
+ *     of tile_m rows; the shared expert (id E) covers tokens 0..T-1. */
 __global__ __launch_bounds__(DSP_THREADS) void k_dispatch(RouteArgs a, uint32_t *tiles, int tile_m,
                                                           int has_shared) {
     extern __shared__ uint32_t lds[];
     const int E = a.E, K = a.K, T = a.T, tid = threadIdx.x;
-    uint32_t *hist = lds;                  /* E */
-    uint32_t *offs = hist + E;             /* E+1 */
-    uint32_t *cursor = offs + E + 1;       /* E */
-    uint32_t *mask = cursor + E;           /* E * 32 */
+    uint32_t *hist = lds;                   /* E */
+    uint32_t *offs = hist + E;              /* E (inclusive scan of hist) */
+    uint32_t *arank = offs + E;             /* E (inclusive scan of active) */
+    uint32_t *toff = arank + E;             /* E (inclusive scan of tile counts) */
+    uint32_t *cursor = toff + E;            /* E */
+    uint32_t *mask = cursor + E;            /* E * 32 */
     uint32_t *wpre = mask + (size_t)E * 32; /* E * 32 */
     for (int e = tid; e < E; e += DSP_THREADS) { hist[e] = 0; cursor[e] = 0; }
     __syncthreads();
     for (int p = tid; p < T * K; p += DSP_THREADS) atomicAdd(&hist[a.idx[p]], 1u);
     __syncthreads();
-    if (tid == 0) {
-        uint32_t s = 0;
-        for (int e = 0; e < E; e++) {
-            offs[e] = s;
-            s += hist[e];
-        }
-        offs[E] = s;
+    if (tid < E) {
+        offs[tid] = hist[tid];
+        arank[tid] = hist[tid] != 0;
+        toff[tid] = (hist[tid] + tile_m - 1) / tile_m;
     }
     __syncthreads();
-    for (int e = tid; e <= E; e += DSP_THREADS) a.offsets[e] = offs[e];
+    block_scan3(offs, arank, toff, E);
+    /* inclusive -> exclusive views: ex(x)[e] = x[e] - own */
+    if (tid < E) {
+        const uint32_t c = hist[tid];
+        const uint32_t o = offs[tid] - c;
+        a.offsets[tid] = o;
+        if (c) {
+            const uint32_t r = arank[tid] - 1;
+            ACT_E(a.list, r) = (uint32_t)tid;
+            ACT_OFF(a.list, E, r) = o;
+            const uint32_t nt = (c + tile_m - 1) / tile_m, t0 = toff[tid] - nt;
+            for (uint32_t j = 0; j < nt; j++) {
+                tiles[1 + 3 * (t0 + j)] = (uint32_t)tid;
+                tiles[2 + 3 * (t0 + j)] = o + j * tile_m;
+                tiles[3 + 3 * (t0 + j)] = min((uint32_t)tile_m, c - j * tile_m);
+            }
+        }
+    }
+    if (tid == 0) {
+        const uint32_t n_act = arank[E - 1], nt = toff[E - 1];
+        a.offsets[E] = offs[E - 1];
+        ACT_N(a.list) = n_act;
+        ACT_OFF(a.list, E, n_act) = offs[E - 1];
+        const uint32_t nsh = has_shared ? (uint32_t)((T + tile_m - 1) / tile_m) : 0;
+        tiles[0] = nt + nsh;
+    }
+    if (has_shared) {
+        const uint32_t nt = toff[E - 1];
+        for (int j = tid; j * tile_m < T; j += DSP_THREADS) {
+            tiles[1 + 3 * (nt + j)] = (uint32_t)E;
+            tiles[2 + 3 * (nt + j)] = (uint32_t)(j * tile_m);
+            tiles[3 + 3 * (nt + j)] = (uint32_t)min(tile_m, T - j * tile_m);
+        }
+    }
     for (int base = 0; base < T; base += 1024) {
         for (int i = tid; i < E * 32; i += DSP_THREADS) mask[i] = 0;
         __syncthreads();
         const int t = base + tid;
         const bool live = t < T;
+        int ek[OROME_MAXK];
+#pragma unroll
+        for (int k = 0; k < OROME_MAXK; k++)
+            if (k < K) ek[k] = live ? a.idx[t * K + k] : 0;
         if (live)
-            for (int k = 0; k < K; k++) {
-                int e = a.idx[t * K + k];
-                atomicOr(&mask[e * 32 + (tid >> 5)], 1u << (tid & 31));
-            }
+#pragma unroll
+            for (int k = 0; k < OROME_MAXK; k++)
+                if (k < K) atomicOr(&mask[ek[k] * 32 + (tid >> 5)], 1u << (tid & 31));
         __syncthreads();
-        for (int e = tid; e < E; e += DSP_THREADS) {
+        for (int i = tid; i < E * 32; i += DSP_THREADS) {
+            /* prefix popcount over the 32 words of one expert: word w of
+             * expert e sums words 0..w-1 (32 lanes of a wave share e) */
+            const int e = i >> 5, w = i & 31;
             uint32_t s = 0;
-            for (int w = 0; w < 32; w++) {
-                wpre[e * 32 + w] = s;
-                s += __popc(mask[e * 32 + w]);
-            }
+            for (int v = 0; v < w; v++) s += __popc(mask[e * 32 + v]);
+            wpre[i] = s;
         }
         __syncthreads();
         if (live)
-            for (int k = 0; k < K; k++) {
-                int e = a.idx[t * K + k];
-                uint32_t wd = mask[e * 32 + (tid >> 5)];
-                uint32_t rank = cursor[e] + wpre[e * 32 + (tid >> 5)] + __popc(wd & ((1u << (tid & 31)) - 1u));
-                uint32_t pos = offs[e] + rank;
-                uint32_t p = (uint32_t)(t * K + k);
-                a.pairs[pos] = p;
-                a.pos[p] = pos;
-            }
+#pragma unroll
+            for (int k = 0; k < OROME_MAXK; k++)
+                if (k < K) {
+                    const int e = ek[k];
+                    const uint32_t wd = mask[e * 32 + (tid >> 5)];
+                    const uint32_t rank = cursor[e] + wpre[e * 32 + (tid >> 5)] + __popc(wd & ((1u << (tid & 31)) - 1u));
+                    const uint32_t pos = offs[e] - hist[e] + rank;
+                    const uint32_t p = (uint32_t)(t * K + k);
+                    a.pairs[pos] = p;
+                    a.pos[p] = pos;
+                }
         __syncthreads();
         for (int e = tid; e < E; e += DSP_THREADS)
             cursor[e] += wpre[e * 32 + 31] + __popc(mask[e * 32 + 31]);
         __syncthreads();
-    }
-    if (tid == 0) {
-        uint32_t n = 0, nt = 0;
-        for (int e = 0; e < E; e++) {
-            uint32_t c = hist[e];
-            if (!c) continue;
-            ACT_E(a.list, n) = (uint32_t)e;
-            ACT_OFF(a.list, E, n) = offs[e];
-            n++;
-            for (uint32_t r = 0; r < c; r += (uint32_t)tile_m) {
-                tiles[1 + 3 * nt] = (uint32_t)e;
-                tiles[2 + 3 * nt] = offs[e] + r;
-                tiles[3 + 3 * nt] = min((uint32_t)tile_m, c - r);
-                nt++;
-            }
-        }
-        ACT_N(a.list) = n;
-        ACT_OFF(a.list, E, n) = offs[E];
-        if (has_shared)
-            for (int r = 0; r < T; r += tile_m) {
-                tiles[1 + 3 * nt] = (uint32_t)E;
-                tiles[2 + 3 * nt] = (uint32_t)r;
-                tiles[3 + 3 * nt] = (uint32_t)min(tile_m, T - r);
-                nt++;
-            }
-        tiles[0] = nt;
     }
 }
 
@@ -357,21 +259,35 @@ __global__ __launch_bounds__(64) void k_rmsnorm(const float *h, const float *w, 
                                                 float *x) {
     const int lane = threadIdx.x, t = blockIdx.x;
     const float *ht = h + (size_t)t * H;
+    const int NI = H / 256;
+    f4 v[CANON_NI];
+#pragma unroll
+    for (int i = 0; i < CANON_NI; i++)
+        if (i < NI) v[i] = *(const f4 *)(ht + 256 * i + 4 * lane);
     float acc = 0.0f;
-    for (int i = 0; i < H / 256; i++) {
-        f4 v = *(const f4 *)(ht + 256 * i + 4 * lane);
-        acc = __builtin_fmaf(v.x, v.x, acc);
-        acc = __builtin_fmaf(v.y, v.y, acc);
-        acc = __builtin_fmaf(v.z, v.z, acc);
-        acc = __builtin_fmaf(v.w, v.w, acc);
-    }
+#pragma unroll
+    for (int i = 0; i < CANON_NI; i++)
+        if (i < NI) {
+            acc = __builtin_fmaf(v[i].x, v[i].x, acc);
+            acc = __builtin_fmaf(v[i].y, v[i].y, acc);
+            acc = __builtin_fmaf(v[i].z, v[i].z, acc);
+            acc = __builtin_fmaf(v[i].w, v[i].w, acc);
+        }
     float ss = wave_sum_canon(acc);
     /* sqrtf and / lower to correctly rounded sequences (__fsqrt_rn does not) */
     float scale = 1.0f / sqrtf(ss / (float)H + eps);
-    for (int j = lane; j < H; j += 64) {
-        float wj = w ? __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, w[j]) & 0xFFFF0000u) : 1.0f;
-        x[(size_t)t * H + j] = __fmul_rn(__fmul_rn(ht[j], scale), wj);
-    }
+#pragma unroll
+    for (int i = 0; i < CANON_NI; i++)
+        if (i < NI) {
+            const int j = 256 * i + 4 * lane;
+            f4 wv = w ? *(const f4 *)(w + j) : f4{1, 1, 1, 1};
+            f4 o;
+            o.x = (v[i].x * scale) * __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, wv.x) & 0xFFFF0000u);
+            o.y = (v[i].y * scale) * __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, wv.y) & 0xFFFF0000u);
+            o.z = (v[i].z * scale) * __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, wv.z) & 0xFFFF0000u);
+            o.w = (v[i].w * scale) * __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, wv.w) & 0xFFFF0000u);
+            *(f4 *)(x + (size_t)t * H + j) = o;
+        }
 }
 
 /* ------------------------------------------------------------ launch */
@@ -420,14 +336,14 @@ int launch_topk(const RouteArgs &a, hipStream_t s) {
 }
 
 int launch_dispatch(const RouteArgs &a, uint32_t *tiles, int tile_m, int has_shared, hipStream_t s) {
-    size_t lds = sizeof(uint32_t) * ((size_t)a.E * 3 + 1 + (size_t)a.E * 64);
-    if (lds > 160 * 1024) return -2;
+    size_t lds = sizeof(uint32_t) * ((size_t)a.E * 5 + (size_t)a.E * 64);
+    if (lds > 160 * 1024 || a.E > DSP_THREADS) return -2;
     hipLaunchKernelGGL(k_dispatch, dim3(1), dim3(DSP_THREADS), lds, s, a, tiles, tile_m, has_shared);
     return hipGetLastError() == hipSuccess ? 0 : -3;
 }
 
 int launch_rmsnorm(const float *h, const float *w, int T, int H, float eps, float *x, hipStream_t s) {
-    if (H % 256) return -2;
+    if (H % 256 || H > 256 * CANON_NI) return -2;
     hipLaunchKernelGGL(k_rmsnorm, dim3(T), dim3(64), 0, s, h, w, H, eps, x);
     return hipGetLastError() == hipSuccess ? 0 : -3;
 }
