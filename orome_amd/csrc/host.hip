@@ -87,7 +87,7 @@ extern "C" orome_hip_ctx *orome_hip_create(const ModelConfig *cfg, int max_token
     const size_t T = (size_t)max_tokens, E = (size_t)cfg->num_experts, K = (size_t)c->kmax,
                  H = (size_t)cfg->hidden_dim, M = (size_t)cfg->moe_intermediate,
                  S = (size_t)(cfg->shared_intermediate > 0 ? cfg->shared_intermediate : 0);
-    const size_t ntile = (T * K) / GEMM_TILE_M + E + T / GEMM_TILE_M + 2;
+    const size_t ntile = (T * K) / GEMM_TILE_TOKENS + E + T / GEMM_TILE_TOKENS + 2;
     struct { void **p; size_t bytes; } parts[] = {
         {(void **)&c->logits, T * (E + 1) * 4}, {(void **)&c->idx, T * K * 4},
         {(void **)&c->w, T * K * 4},           {(void **)&c->sgl, T * 4},
@@ -313,9 +313,10 @@ extern "C" int orome_moe_forward(orome_hip_ctx *c, const ModelConfig *cfg, const
     } else {
         TLAUNCH(c, ST_ROUTE, launch_route_logits(a, s), "router logits");
         TLAUNCH(c, ST_TOPK, launch_topk(a, s), "top-k");
-        TLAUNCH(c, ST_DISPATCH, launch_dispatch(a, c->tiles, GEMM_TILE_M, S ? 1 : 0, s), "dispatch");
+        const int tile_m = GEMM_TILE_TOKENS;
+        TLAUNCH(c, ST_DISPATCH, launch_dispatch(a, c->tiles, tile_m, S ? 1 : 0, s), "dispatch");
         TLAUNCH(c, ST_STAGE, launch_to_f16(x, T, H, c->x16, s), "fp16 staging");
-        const int ntiles = (T * K) / GEMM_TILE_M + E + (S ? (T + GEMM_TILE_M - 1) / GEMM_TILE_M : 0);
+        const int ntiles = (T * K) / tile_m + E + (S ? (T + tile_m - 1) / tile_m : 0);
         TLAUNCH(c, ST_GATE_UP, launch_gemm_gate_up(ex, sh, c->x16, T, H, M, K, E, c->tiles, ntiles, c->pairs, c->act,
                                    c->act_sh, s),
                "grouped gate/up");

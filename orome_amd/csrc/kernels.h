@@ -80,4 +80,6 @@ int launch_combine(const float *y, const float *ysh, const uint32_t *pos, const 
 
 /* tile list for the grouped GEMM: tiles[0] = count, then (expert, first, rows)
  * triples; expert == E denotes the shared expert over all T tokens */
-#define GEMM_TILE_M 32
+#ifndef GEMM_TILE_TOKENS
+#define GEMM_TILE_TOKENS 96
+#endif

@@ -1,22 +1,32 @@
 /*
  * moe_gemm.hip -- prefill-path grouped expert GEMMs on the matrix cores.
  *
- * Work list: the dispatch kernel emits tiles (expert, first row, rows <= 32)
+ * Work list: the dispatch kernel emits tiles (expert, first row, rows <= GEMM_TILE_TOKENS)
  * over the expert-sorted pair list; the shared expert is expert E over the
- * token order.  One block computes one tile x 64 output rows:
+ * token order.  One block computes one tile x NB output rows:
  *   gate/up  D[row][token] = W_{gate,up}[e][row] . x16[token]      (K = H)
  *   down     y[pos][row]   = W_down[e][row]    . act[pos]         (K = M)
  * with v_mfma_f32_16x16x32_f16 (A = 16 weight rows x 32 k, B = 32 k x 16
- * tokens, fp32 accumulate).  Each wave owns 16 weight rows (both gate and up
- * rows for the first GEMM) for all 32 tokens of the tile.
+ * tokens, fp32 accumulate).  Each of the 4 waves owns 2 x 16 weight rows (of
+ * gate and of up for the first GEMM) for all TB = ceil(rows/16) token blocks
+ * of the tile, so one dequantised A fragment feeds TB matrix instructions and
+ * one B fragment read from LDS feeds 2 (down) or 4 (gate/up).
  *
- * Weights are dequantised straight into the A fragments: the exact fp32
- * value of format_decode_row_f32 (inference/src/format.m:81-174, products
- * exact), rounded once to fp16 (RNE).  A lane's 8 k-values per MFMA are two
- * runs of 4 consecutive k (k_a.., k_b..) chosen so that they come from one
- * quant dword; the B fragment reads the same k positions of the token rows
- * staged in LDS, so the contraction is the plain dot product.
- * Activations are fp16 as the reference stages them (half(x), half(act)).
+ * Weights are dequantised straight into A fragments with packed fp16
+ * arithmetic on exactly factored terms (q arrives as the exact fp16 1024+q by
+ * OR-ing the quant bits under the 0x64 exponent byte):
+ *   Q4_K  t = fma(1024+q, sc, -1024 sc) = q sc   (exact, <= 945)
+ *         w = fma(t, d, -fp16(dmin m))          one rounding, plus the
+ *         rounding of dmin*m (~7% of |w|): within one fp16 ulp of exact
+ *   Q6_K  w = (q sc) d   exact product when |q sc| <= 2048, else two roundings
+ *   Q8_0  w = q d        one rounding
+ * The B operand (activations, fp16 as the reference stages half(x) and
+ * half(act)) sits in LDS in fragment order: the 8 k values lane (i, kg) needs
+ * at step s of a 128-wide k stage are 16 contiguous bytes at (4 s + kg) * 8,
+ * so a B fragment is one ds_read_b128; the staging store applies the
+ * per-format k permutation.  Stages are double-buffered: the next stage's
+ * activations and weight bytes are fetched to registers before the current
+ * stage's matrix work.
  */
 #include "dev_common.h"
 #include "kernels.h"
@@ -25,149 +35,291 @@ enum { FQ4K = 0, FQ6K = 2, FQ8 = 3 };
 
 typedef float f4v __attribute__((ext_vector_type(4)));
 
-#define TM GEMM_TILE_M   /* tokens per tile (32) */
-#define NB 64            /* weight rows per block */
-#define KC 256           /* k per super-block step */
-#define XS_LD (KC + 8)   /* padded LDS row (halves) */
+#define MDEV __device__ __forceinline__ /* member functions */
+#define WAVES 8                         /* waves per block */
+#define KC 128                          /* k per stage (one A fragment set) */
+#define KCH 256                         /* k per LDS activation chunk */
+#define BLD (KCH + 8)                   /* chunk row pitch (halves) */
+#define TILE GEMM_TILE_TOKENS           /* tokens per tile */
+#define TBMAX (TILE / 16)
 
 DEV size_t gemm_row_bytes(int fmt, int n) {
     return fmt == FQ4K ? (size_t)(n / 256) * 144 : fmt == FQ6K ? (size_t)(n / 256) * 210 : (size_t)(n / 32) * 34;
 }
+DEV uint32_t u4_at(u4 v, int i) { return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w; }
+DEV h2 splat(_Float16 v) { return h2{v, v}; }
+DEV h2 hfma(h2 a, h2 b, h2 c) { return __builtin_elementwise_fma(a, b, c); }
+DEV h2 or_bias(uint32_t v) { return as_h2(v | 0x64006400u); }
+DEV h8 cat4(h2 a, h2 b, h2 c, h2 d) { return h8{a.x, a.y, b.x, b.y, c.x, c.y, d.x, d.y}; }
 
-/* Raw bytes of one 256-weight span of one row, as held by lane kg (0..3). */
-struct SpanRaw {
-    u4 a, b, c;      /* Q4_K: hdr, piece kg, piece kg+4 | Q6_K: ql 32B (a,b), qh 16B half (c) */
-    u4 d;            /* Q6_K: other 16B of qh; scales in e */
-    u4 e;            /* Q6_K: 16 scale bytes | Q8_0: d of the 8 blocks (packed) */
-    uint32_t f;      /* Q6_K: d */
+/* ------------------------------------------------- k order in LDS */
+/* Position (halves) inside a stage row of the 4 k values [4c, 4c+4), i.e. of
+ * fragment (s, kg) elements j0..j0+3.  Mirrors the lane -> k mapping of each
+ * Span below; Q4_K groups are additionally stored in (0,2,1,3) order. */
+template <int FMT>
+DEV int frag_pos(int c) {
+    if (FMT == FQ4K) { /* lane kg, step s: k = 64(kg>>1) + 16(kg&1) + 4s (+32 high nibbles) */
+        const int g = c >> 4, r = c & 15, hi = r >> 3, rr = r & 7;
+        return (((rr & 3) * 4 + 2 * g + (rr >> 2)) * 8) + 4 * hi;
+    } else if (FMT == FQ6K) { /* k = 32(kg&1) + 16(kg>>1) + 4s (+64 high nibbles) */
+        const int hi = c >> 4, r = c & 15, odd = r >> 3, q = r & 7;
+        return (((q & 3) * 4 + 2 * (q >> 2) + odd) * 8) + 4 * hi;
+    } else { /* k = 32s + 8kg .. +7 */
+        return ((c >> 3) * 4 + ((c & 7) >> 1)) * 8 + 4 * (c & 1);
+    }
+}
+
+/* ------------------------------------------------------------ spans */
+/* One weight row's share of a 128-wide k stage j for lane group kg (0..3):
+ * raw bytes (load), per-stage constants (prepare), A fragment at step s. */
+template <int FMT>
+struct Span;
+
+template <>
+struct Span<FQ4K> {
+    u4 hdr, q;
+    MDEV void init(int) {}
+    MDEV void load(const uint8_t *row, int j, int kg) {
+        const uint8_t *p = row + (size_t)(j >> 1) * 144;
+        hdr = ld_u4(p);
+        q = ld_u4(p + 16 + 16 * (kg + 4 * (j & 1)));
+    }
+    h2 d, scl, ncl, sch, nch, mbl, mbh;
+    MDEV void prepare(int j, int kg) {
+        /* the first half-block never reads hdr.w: consume it here so its
+         * register is not recycled (a write-after-write wait on the load
+         * still in flight) before this unit */
+        asm volatile("" ::"v"(hdr.w));
+        uint32_t sl, sh, ml, mh;
+        q4k_scale_min(hdr, (kg + 4 * (j & 1)) >> 1, sl, sh, ml, mh);
+        const float dmin = f16_bits_to_f32(hdr.x >> 16);
+        d = splat(__builtin_bit_cast(_Float16, (uint16_t)(hdr.x & 0xFFFFu)));
+        scl = splat((_Float16)(float)sl);
+        ncl = splat((_Float16)(-1024.0f * (float)sl));
+        sch = splat((_Float16)((float)sh * 0.0625f));
+        nch = splat((_Float16)(-64.0f * (float)sh));
+        mbl = splat((_Float16)(-(dmin * (float)ml)));
+        mbh = splat((_Float16)(-(dmin * (float)mh)));
+    }
+    /* k order of the result: l, l+2, l+1, l+3, l+32, l+34, l+33, l+35 */
+    MDEV h8 frag(int s) const {
+        const uint32_t w = u4_at(q, s), w8 = w >> 8;
+        const h2 t0 = hfma(or_bias(w & 0x000F000Fu), scl, ncl);
+        const h2 t1 = hfma(or_bias(w8 & 0x000F000Fu), scl, ncl);
+        const h2 t2 = hfma(or_bias(w & 0x00F000F0u), sch, nch);
+        const h2 t3 = hfma(or_bias(w8 & 0x00F000F0u), sch, nch);
+        return cat4(hfma(t0, d, mbl), hfma(t1, d, mbl), hfma(t2, d, mbh), hfma(t3, d, mbh));
+    }
 };
 
-template <int FMT>
-DEV SpanRaw span_load(const uint8_t *row, int sb, int kg) {
-    SpanRaw r;
-    if (FMT == FQ4K) {
-        const uint8_t *p = row + (size_t)sb * 144;
-        r.a = ld_u4(p);
-        r.b = ld_u4(p + 16 + 16 * kg);
-        r.c = ld_u4(p + 16 + 16 * (kg + 4));
-    } else if (FMT == FQ6K) {
-        const uint8_t *p = row + (size_t)sb * 210;
-        const int h = kg >> 1;
-        r.a = ld_u32x4_a2(p + 32 * kg);
-        r.b = ld_u32x4_a2(p + 32 * kg + 16);
-        r.c = ld_u32x4_a2(p + 128 + 32 * h);
-        r.d = ld_u32x4_a2(p + 128 + 32 * h + 16);
-        r.e = ld_u32x4_a2(p + 192);
-        r.f = ld_u32_a2(p + 208);
-    } else {
-        /* Q8_0: 8 blocks of 34 B; lane kg takes quant bytes 8kg..8kg+7 of each */
-        const uint8_t *p = row + (size_t)sb * 8 * 34;
-        uint32_t q[16];
-        uint32_t dd[8];
-#pragma unroll
-        for (int s = 0; s < 8; s++) {
-            u2 v = ld_u32x2_a2(p + s * 34 + 2 + 8 * kg);
-            q[2 * s] = v.x;
-            q[2 * s + 1] = v.y;
-            dd[s] = ld_u32_a2(p + s * 34) & 0xFFFFu;
-        }
-        r.a = u4{q[0], q[1], q[2], q[3]};
-        r.b = u4{q[4], q[5], q[6], q[7]};
-        r.c = u4{q[8], q[9], q[10], q[11]};
-        r.d = u4{q[12], q[13], q[14], q[15]};
-        r.e = u4{dd[0] | (dd[1] << 16), dd[2] | (dd[3] << 16), dd[4] | (dd[5] << 16), dd[6] | (dd[7] << 16)};
+template <>
+struct Span<FQ6K> {
+    u4 ql, qh;
+    u2 sc8;
+    uint32_t dw;
+    int odd2;
+    MDEV void init(int kg) { odd2 = 2 * (kg & 1); }
+    MDEV void load(const uint8_t *row, int j, int kg) {
+        const uint8_t *p = row + (size_t)(j >> 1) * 210;
+        const int h = j & 1, lq = 16 * (kg >> 1);
+        ql = ld_u32x4_a2(p + h * 64 + 32 * (kg & 1) + lq);
+        qh = ld_u32x4_a2(p + 128 + h * 32 + lq);
+        sc8 = ld_u32x2_a2(p + 192 + h * 8);
+        dw = ld_u32_a2(p + 208);
     }
-    return r;
-}
+    h2 d, scl, sch;
+    MDEV void prepare(int, int kg) {
+        const int b = (kg >> 1) + 2 * (kg & 1); /* scale is + 2 odd, is = l / 16 = kg >> 1 */
+        d = splat(__builtin_bit_cast(_Float16, (uint16_t)(dw & 0xFFFFu)));
+        scl = splat((_Float16)(float)(int8_t)((sc8.x >> (8 * b)) & 0xFF));
+        sch = splat((_Float16)(float)(int8_t)((sc8.y >> (8 * b)) & 0xFF));
+    }
+    MDEV h8 frag(int s) const {
+        const uint32_t a = u4_at(ql, s), b = u4_at(qh, s);
+        h2 p01, p23, r01, r23;
+        q6_h2(a, b, 0, odd2, p01, p23);
+        q6_h2(a, b, 4, 4 + odd2, r01, r23);
+        return cat4((p01 * scl) * d, (p23 * scl) * d, (r01 * sch) * d, (r23 * sch) * d);
+    }
+};
 
-DEV uint32_t u4_at(u4 v, int i) { return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w; }
-
-DEV h2 pk_f16(float a, float b) { return h2{(_Float16)a, (_Float16)b}; }
-
-/* Step s (0..7) of a span: the lane's 8 weights as fp16 and the two k runs
- * (offsets inside the 256-wide span). */
-template <int FMT>
-DEV h8 span_step(const SpanRaw &r, int s, int kg, int &ka, int &kb) {
-    float w[8];
-    if (FMT == FQ4K) {
-        const int p = kg + 4 * (s >> 2);
-        const int g = p >> 1, l0 = (p & 1) * 16 + 4 * (s & 3);
-        ka = g * 64 + l0;
-        kb = ka + 32;
-        Q4Affine af = q4k_affine(r.a, g);
-        uint32_t q = u4_at((s >> 2) ? r.c : r.b, s & 3);
+template <>
+struct Span<FQ8> {
+    u2 qv[4];
+    uint32_t dd[4];
+    MDEV void init(int) {}
+    MDEV void load(const uint8_t *row, int j, int kg) {
+        const uint8_t *p = row + (size_t)(4 * j) * 34;
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            uint32_t byte = (q >> (8 * i)) & 0xFFu;
-            w[i] = af.a_lo * (float)(byte & 0xFu) - af.b_lo;
-            w[4 + i] = af.a_hi * (float)(byte >> 4) - af.b_hi;
-        }
-    } else if (FMT == FQ6K) {
-        const int h = kg >> 1, odd = kg & 1, l = 4 * s;
-        ka = h * 128 + (odd ? 32 : 0) + l;
-        kb = ka + 64;
-        uint32_t ql = u4_at(s < 4 ? r.a : r.b, s & 3);
-        uint32_t qh = u4_at(l < 16 ? r.c : r.d, (l >> 2) & 3);
-        const int sh_lo = odd ? 2 : 0, sh_hi = odd ? 6 : 4;
-        const int is = l >> 4;
-        const int grp_lo = odd ? 1 : 0, grp_hi = odd ? 3 : 2;
-        const int sci_lo = h * 8 + is + 2 * grp_lo, sci_hi = h * 8 + is + 2 * grp_hi;
-        float d = f16_bits_to_f32(r.f);
-        float sc_lo = (float)(int8_t)((u4_at(r.e, sci_lo >> 2) >> (8 * (sci_lo & 3))) & 0xFF);
-        float sc_hi = (float)(int8_t)((u4_at(r.e, sci_hi >> 2) >> (8 * (sci_hi & 3))) & 0xFF);
-        float a_lo = d * sc_lo, a_hi = d * sc_hi;
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            uint32_t b = (ql >> (8 * i)) & 0xFFu, hb = (qh >> (8 * i)) & 0xFFu;
-            int q1 = (int)((b & 0xFu) | (((hb >> sh_lo) & 3u) << 4)) - 32;
-            int q2 = (int)((b >> 4) | (((hb >> sh_hi) & 3u) << 4)) - 32;
-            w[i] = a_lo * (float)q1;
-            w[4 + i] = a_hi * (float)q2;
-        }
-    } else {
-        ka = s * 32 + 8 * kg;
-        kb = ka + 4;
-        uint32_t q0 = u4_at(s < 2 ? r.a : s < 4 ? r.b : s < 6 ? r.c : r.d, (2 * s) & 3);
-        uint32_t q1 = u4_at(s < 2 ? r.a : s < 4 ? r.b : s < 6 ? r.c : r.d, (2 * s + 1) & 3);
-        float d = f16_bits_to_f32(u4_at(r.e, s >> 1) >> (16 * (s & 1)));
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            w[i] = d * (float)(int8_t)((q0 >> (8 * i)) & 0xFF);
-            w[4 + i] = d * (float)(int8_t)((q1 >> (8 * i)) & 0xFF);
+        for (int s = 0; s < 4; s++) {
+            qv[s] = ld_u32x2_a2(p + s * 34 + 2 + 8 * kg);
+            dd[s] = ld_u32_a2(p + s * 34);
         }
     }
-    h8 o;
-#pragma unroll
-    for (int i = 0; i < 8; i++) o[i] = (_Float16)w[i];
-    return o;
-}
-
-DEV h8 lds_b_frag(const _Float16 *xs, int tok, int ka, int kb) {
-    const _Float16 *p = xs + tok * XS_LD;
-    h4 a = *(const h4 *)(p + ka);
-    h4 b = *(const h4 *)(p + kb);
-    return h8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
-}
+    MDEV void prepare(int, int) {}
+    MDEV h8 frag(int s) const {
+        const h2 d = splat(__builtin_bit_cast(_Float16, (uint16_t)(dd[s] & 0xFFFFu)));
+        h2 p01, p23, p45, p67;
+        q8_h2(qv[s].x, p01, p23);
+        q8_h2(qv[s].y, p45, p67);
+        return cat4(p01 * d, p23 * d, p45 * d, p67 * d);
+    }
+};
 
 DEV f4v mfma(h8 a, h8 b, f4v c) { return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0); }
 
-/* stage rows (TM tokens) x KC halves of the B operand into LDS */
-DEV void stage_tile(_Float16 *xs, const _Float16 *src, const int *rowoff, int ld, int k0) {
-    /* 256 threads, TM*KC/8 = 1024 16-byte vectors */
-    for (int v = threadIdx.x; v < TM * KC / 8; v += 256) {
-        const int t = v / (KC / 8), c = (v % (KC / 8)) * 8;
-        u4 val = u4{0, 0, 0, 0};
-        if (rowoff[t] >= 0) val = ld_u4((const uint8_t *)(src + (size_t)rowoff[t] * ld + k0 + c));
-        *(u4 *)(xs + t * XS_LD + c) = val;
+/* ------------------------------------------------------- B chunks */
+/* A chunk is KCH (256) k of the tile's token rows in LDS, row pitch BLD
+ * halves (132 dwords: 16 rows x 16 bytes per lane group hit distinct banks),
+ * each 128-k half in the fragment order of FMT.  A thread's vector n covers
+ * token 16n + tid/32, k 8 (tid%32) .. +7.  Every thread loads and stores all
+ * TBMAX vectors (rows past the tile read a valid row and are zeroed by a
+ * select): the loads stay straight-line code, so the compiler's wait counts
+ * for the weight prefetch ring stay exact. */
+struct Chunk {
+    u4 v[TBMAX];
+    MDEV void fetch(const _Float16 *src, const int *rowoff, int ld, int k0) {
+        const int cc = (threadIdx.x & 31) * 8;
+#pragma unroll
+        for (int n = 0; n < TBMAX; n++)
+            v[n] = ld_u4((const uint8_t *)(src + (size_t)rowoff[16 * n + (threadIdx.x >> 5)] * ld + k0 + cc));
+    }
+    /* the zero select for rows past the tile happens here, not at the load,
+     * so nothing waits on the fetch before the chunk is due */
+    template <int FMT>
+    MDEV void store(_Float16 *xs, int rows) const {
+        const int col = threadIdx.x & 31, half = col >> 4, c0 = (col & 15) * 2;
+        const int p0 = half * KC + frag_pos<FMT>(c0), p1 = half * KC + frag_pos<FMT>(c0 + 1);
+#pragma unroll
+        for (int n = 0; n < TBMAX; n++) {
+            const int t = 16 * n + (threadIdx.x >> 5);
+            _Float16 *row = xs + t * BLD;
+            const u4 x = t < rows ? v[n] : u4{0, 0, 0, 0};
+            u2 g0 = {x.x, x.y}, g1 = {x.z, x.w};
+            if (FMT == FQ4K) { /* (x0,x1),(x2,x3) -> (x0,x2),(x1,x3) */
+                g0 = u2{__builtin_amdgcn_perm(g0.y, g0.x, 0x05040100u), __builtin_amdgcn_perm(g0.y, g0.x, 0x07060302u)};
+                g1 = u2{__builtin_amdgcn_perm(g1.y, g1.x, 0x05040100u), __builtin_amdgcn_perm(g1.y, g1.x, 0x07060302u)};
+            }
+            *(u2 *)(row + p0) = g0;
+            *(u2 *)(row + p1) = g1;
+        }
+    }
+};
+
+/* ------------------------------------------------------------- tile */
+/* One block: WAVES waves, wave w owns RPW row blocks of 16 rows (rows
+ * blockIdx.y*NB + (w*RPW + rb)*16 ..) of NMAT matrices (gate+up, or down).
+ * A wave walks units u = (rb, stage j) in order, stage j = 128 k; weight
+ * bytes for unit u+DEPTH are in flight while unit u computes.  Activation
+ * chunks (256 k) sit in two LDS buffers: with <= 2 chunks both stay resident
+ * (one barrier in all); with more, chunk c+2 is written into c's buffer
+ * after the barrier that ends chunk c (RPW must be 1 then). */
+template <int FMT, int NMAT, int RPW, int DEPTH, int NST, typename Epi>
+DEV void tile_run(const uint8_t *w0, const uint8_t *w1, int in_dim, const _Float16 *src, int ld,
+                  const int *rowoff, int rows, _Float16 *xs, const Epi &epi) {
+    const int tb = (rows + 15) >> 4;
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int kg = lane >> 4, i = lane & 15;
+    const size_t rbytes = gemm_row_bytes(FMT, in_dim);
+    /* NST > 0: stage count fixed at compile time, so the unit loop unrolls
+     * completely and the prefetch ring never crosses a loop back-edge (where
+     * the register copies would wait for every load in flight) */
+    const int nst = NST ? NST : in_dim / KC, nch = nst / 2, U = RPW * nst;
+    const int rbase = blockIdx.y * (WAVES * 16 * RPW) + wv * 16 * RPW;
+    const uint8_t *rw0 = w0 + (size_t)(rbase + i) * rbytes;
+    const uint8_t *rw1 = NMAT > 1 ? w1 + (size_t)(rbase + i) * rbytes : nullptr;
+
+    /* U is a multiple of DEPTH (checked by the launchers); the last DEPTH
+     * units reload unit U-1 instead of branching */
+    Span<FMT> ring[DEPTH][NMAT];
+#pragma unroll
+    for (int d = 0; d < DEPTH; d++) {
+        const int rb = d / nst, j = d - rb * nst;
+#pragma unroll
+        for (int m = 0; m < NMAT; m++) {
+            ring[d][m].init(kg);
+            ring[d][m].load((m ? rw1 : rw0) + (size_t)rb * 16 * rbytes, j, kg);
+        }
+    }
+
+    Chunk ch;
+    ch.fetch(src, rowoff, ld, 0);
+    ch.store<FMT>(xs, rows);
+    if (nch > 1) {
+        ch.fetch(src, rowoff, ld, KCH);
+        ch.store<FMT>(xs + TILE * BLD, rows);
+    }
+    if (nch > 2) ch.fetch(src, rowoff, ld, 2 * KCH);
+    __syncthreads();
+
+    f4v c[NMAT][TBMAX];
+#pragma unroll
+    for (int m = 0; m < NMAT; m++)
+#pragma unroll
+        for (int t = 0; t < TBMAX; t++) c[m][t] = f4v{0, 0, 0, 0};
+
+#pragma unroll
+    for (int u0 = 0; u0 < U; u0 += DEPTH) {
+#pragma unroll
+        for (int d = 0; d < DEPTH; d++) {
+            const int u = u0 + d;
+            const int rb = u / nst, j = u - rb * nst;
+            /* keep units apart (register pressure): no scheduling across
+             * them, and no reuse of B fragments loaded by an earlier unit
+             * (row blocks of one wave read the same LDS addresses) */
+            __builtin_amdgcn_sched_barrier(0);
+            asm volatile("" ::: "memory");
+            Span<FMT> cur[NMAT];
+#pragma unroll
+            for (int m = 0; m < NMAT; m++) {
+                cur[m] = ring[d][m];
+                cur[m].prepare(j, kg);
+            }
+            {
+                const int u2 = min(u + DEPTH, U - 1), rb2 = u2 / nst, j2 = u2 - rb2 * nst;
+#pragma unroll
+                for (int m = 0; m < NMAT; m++) ring[d][m].load((m ? rw1 : rw0) + (size_t)rb2 * 16 * rbytes, j2, kg);
+            }
+            const _Float16 *bp = xs + ((j >> 1) & 1) * (TILE * BLD) + (j & 1) * KC + i * BLD + kg * 8;
+#pragma unroll
+            for (int s = 0; s < 4; s++) {
+                h8 a[NMAT];
+#pragma unroll
+                for (int m = 0; m < NMAT; m++) a[m] = cur[m].frag(s);
+                /* B reads for every token block (rows past the tile hold
+                 * zeros): straight-line LDS traffic the scheduler can hoist */
+                h8 b[TBMAX];
+#pragma unroll
+                for (int t = 0; t < TBMAX; t++) b[t] = *(const h8 *)(bp + t * 16 * BLD + s * 32);
+#pragma unroll
+                for (int t = 0; t < TBMAX; t++)
+                    if (t < tb) {
+#pragma unroll
+                        for (int m = 0; m < NMAT; m++) c[m][t] = mfma(a[m], b[t], c[m][t]);
+                    }
+            }
+            if (j == nst - 1) {
+                epi(c, rbase + rb * 16 + 4 * kg, tb);
+#pragma unroll
+                for (int m = 0; m < NMAT; m++)
+#pragma unroll
+                    for (int t = 0; t < TBMAX; t++) c[m][t] = f4v{0, 0, 0, 0};
+            }
+            if (nch > 2 && (j & 1) && (j >> 1) + 2 < nch) {
+                __syncthreads();
+                ch.store<FMT>(xs + ((j >> 1) & 1) * (TILE * BLD), rows);
+                if ((j >> 1) + 3 < nch) ch.fetch(src, rowoff, ld, ((j >> 1) + 3) * KCH);
+            } else if (nch > 2 && (j & 1) && (j >> 1) + 1 < nch) {
+                __syncthreads(); /* chunk c+1 was stored before the previous barrier */
+            }
+        }
     }
 }
 
 struct GemmArgs {
     const uint8_t *wa, *wb;   /* gate/up (wb NULL for down) of expert 0 */
     size_t stride_a, stride_b;
-    int fmt;
     const uint8_t *sh_a, *sh_b;
-    int sh_fmt;
     const _Float16 *src;      /* x16 [T][H] (gate/up) or act [pairs][M] (down) */
     const _Float16 *src_sh;   /* down: act_sh [T][S] */
     int T, H, M, S, K, E;
@@ -176,128 +328,90 @@ struct GemmArgs {
     float *y, *ysh;           /* down outputs */
 };
 
-/* ---------------------------------------------------------- gate/up */
-template <int FMT>
-DEV void gu_tile(const GemmArgs &a, const uint8_t *wg, const uint8_t *wu, int nrows_out, int in_dim,
-                 const int *rowoff, _Float16 *out, int out_ld, int first, int rows, _Float16 *xs) {
-    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-    const int kg = lane >> 4, i = lane & 15;
-    const int r0 = blockIdx.y * NB + wv * 16;
-    const size_t rb = gemm_row_bytes(FMT, in_dim);
-    const uint8_t *rg = wg + (size_t)(r0 + i) * rb, *ru = wu + (size_t)(r0 + i) * rb;
-    f4v cg[2] = {{0, 0, 0, 0}, {0, 0, 0, 0}}, cu[2] = {{0, 0, 0, 0}, {0, 0, 0, 0}};
-    const int nsb = in_dim / 256;
-    SpanRaw ng = span_load<FMT>(rg, 0, kg), nu = span_load<FMT>(ru, 0, kg);
-    for (int sb = 0; sb < nsb; sb++) {
-        SpanRaw g = ng, u = nu;
-        __syncthreads();
-        stage_tile(xs, a.src, rowoff, a.H, sb * KC);
-        if (sb + 1 < nsb) {
-            ng = span_load<FMT>(rg, sb + 1, kg);
-            nu = span_load<FMT>(ru, sb + 1, kg);
-        }
-        __syncthreads();
+/* D layout: lane (i, kg) holds token 16t + i, rows r..r+3 (r = 4kg + block base) */
+struct GuEpi {
+    _Float16 *out;
+    int out_ld, first, rows;
+    MDEV void operator()(const f4v (&c)[2][TBMAX], int r, int tb) const {
+        const int i = threadIdx.x & 15;
 #pragma unroll
-        for (int s = 0; s < 8; s++) {
-            int ka, kb;
-            h8 ag = span_step<FMT>(g, s, kg, ka, kb);
-            h8 au = span_step<FMT>(u, s, kg, ka, kb);
+        for (int t = 0; t < TBMAX; t++) {
+            const int tok = t * 16 + i;
+            if (t >= tb || tok >= rows) continue;
+            h4 v;
 #pragma unroll
-            for (int tb = 0; tb < 2; tb++) {
-                h8 b = lds_b_frag(xs, tb * 16 + i, ka, kb);
-                cg[tb] = mfma(ag, b, cg[tb]);
-                cu[tb] = mfma(au, b, cu[tb]);
-            }
+            for (int q = 0; q < 4; q++) v[q] = (_Float16)(silu_f(c[0][t][q]) * c[1][t][q]);
+            *(h4 *)(out + (size_t)(first + tok) * out_ld + r) = v;
         }
     }
-    (void)nrows_out;
-#pragma unroll
-    for (int tb = 0; tb < 2; tb++) {
-        const int tok = tb * 16 + i;
-        if (tok >= rows) continue;
-        h4 v;
-#pragma unroll
-        for (int q = 0; q < 4; q++) v[q] = (_Float16)(silu_f(cg[tb][q]) * cu[tb][q]);
-        *(h4 *)(out + (size_t)(first + tok) * out_ld + r0 + 4 * kg) = v;
-    }
-}
+};
 
-__global__ __launch_bounds__(256) void k_gemm_gate_up(GemmArgs a) {
-    __shared__ _Float16 xs[TM * XS_LD];
-    __shared__ int rowoff[TM];
+struct DnEpi {
+    float *out;
+    int out_ld, first, rows;
+    MDEV void operator()(const f4v (&c)[1][TBMAX], int r, int tb) const {
+        const int i = threadIdx.x & 15;
+#pragma unroll
+        for (int t = 0; t < TBMAX; t++) {
+            const int tok = t * 16 + i;
+            if (t >= tb || tok >= rows) continue;
+            *(f4v *)(out + (size_t)(first + tok) * out_ld + r) = c[0][t];
+        }
+    }
+};
+
+/* row blocks per wave and weight stages in flight per wave */
+#ifndef GU_DEPTH
+#define GU_DEPTH 4 /* Q8_0 (shared expert) spans are larger: depth 2 */
+#endif
+#ifndef DN_DEPTH
+#define DN_DEPTH 4
+#endif
+#define GU_RPW 1
+#define DN_RPW 4
+
+template <int SFMT, int NST>
+__global__ __launch_bounds__(WAVES * 64) void k_gemm_gate_up(GemmArgs a) {
+    __shared__ __attribute__((aligned(16))) _Float16 xs[2 * TILE * BLD];
+    __shared__ int rowoff[TILE];
     const uint32_t nt = a.tiles[0];
     if (blockIdx.x >= nt) return;
     const uint32_t e = a.tiles[1 + 3 * blockIdx.x], first = a.tiles[2 + 3 * blockIdx.x],
                    rows = a.tiles[3 + 3 * blockIdx.x];
     const bool sh = e == (uint32_t)a.E;
-    const int nout = sh ? a.S : a.M;
-    if (blockIdx.y * NB >= (unsigned)nout) return;
-    if (threadIdx.x < TM) {
-        int t = -1;
-        if (threadIdx.x < rows)
-            t = sh ? (int)(first + threadIdx.x) : (int)(a.pairs[first + threadIdx.x] / (uint32_t)a.K);
-        rowoff[threadIdx.x] = t;
+    if (blockIdx.y * (WAVES * 16 * GU_RPW) >= (unsigned)(sh ? a.S : a.M)) return;
+    if (threadIdx.x < TILE) { /* rows past the tile repeat the first row */
+        const uint32_t q = threadIdx.x < rows ? threadIdx.x : 0;
+        rowoff[threadIdx.x] = sh ? (int)(first + q) : (int)(a.pairs[first + q] / (uint32_t)a.K);
     }
+    __syncthreads();
     if (sh) {
-        if (a.sh_fmt == FQ8) gu_tile<FQ8>(a, a.sh_a, a.sh_b, a.S, a.H, rowoff, a.act_sh, a.S, first, rows, xs);
-        else gu_tile<FQ4K>(a, a.sh_a, a.sh_b, a.S, a.H, rowoff, a.act_sh, a.S, first, rows, xs);
+        const GuEpi epi{a.act_sh, a.S, (int)first, (int)rows};
+        tile_run<SFMT, 2, GU_RPW, (SFMT == FQ8 ? 2 : GU_DEPTH), NST>(a.sh_a, a.sh_b, a.H, a.src, a.H, rowoff, (int)rows, xs, epi);
     } else {
-        gu_tile<FQ4K>(a, a.wa + (size_t)e * a.stride_a, a.wb + (size_t)e * a.stride_b, a.M, a.H, rowoff,
-                      a.act, a.M, first, rows, xs);
+        const GuEpi epi{a.act, a.M, (int)first, (int)rows};
+        tile_run<FQ4K, 2, GU_RPW, GU_DEPTH, NST>(a.wa + (size_t)e * a.stride_a, a.wb + (size_t)e * a.stride_b, a.H, a.src,
+                                  a.H, rowoff, (int)rows, xs, epi);
     }
 }
 
-/* ------------------------------------------------------------- down */
-template <int FMT>
-DEV void down_tile(const uint8_t *w, int in_dim, const _Float16 *src, int ld, const int *rowoff,
-                   float *out, int out_ld, int first, int rows, _Float16 *xs) {
-    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-    const int kg = lane >> 4, i = lane & 15;
-    const int r0 = blockIdx.y * NB + wv * 16;
-    const size_t rb = gemm_row_bytes(FMT, in_dim);
-    const uint8_t *rw = w + (size_t)(r0 + i) * rb;
-    f4v c[2] = {{0, 0, 0, 0}, {0, 0, 0, 0}};
-    const int nsb = in_dim / 256;
-    SpanRaw nx = span_load<FMT>(rw, 0, kg);
-    for (int sb = 0; sb < nsb; sb++) {
-        SpanRaw r = nx;
-        __syncthreads();
-        stage_tile(xs, src, rowoff, ld, sb * KC);
-        if (sb + 1 < nsb) nx = span_load<FMT>(rw, sb + 1, kg);
-        __syncthreads();
-#pragma unroll
-        for (int s = 0; s < 8; s++) {
-            int ka, kb;
-            h8 aw = span_step<FMT>(r, s, kg, ka, kb);
-#pragma unroll
-            for (int tb = 0; tb < 2; tb++) c[tb] = mfma(aw, lds_b_frag(xs, tb * 16 + i, ka, kb), c[tb]);
-        }
-    }
-#pragma unroll
-    for (int tb = 0; tb < 2; tb++) {
-        const int tok = tb * 16 + i;
-        if (tok >= rows) continue;
-        *(f4v *)(out + (size_t)(first + tok) * out_ld + r0 + 4 * kg) = c[tb];
-    }
-}
-
-__global__ __launch_bounds__(256) void k_gemm_down(GemmArgs a) {
-    __shared__ _Float16 xs[TM * XS_LD];
-    __shared__ int rowoff[TM];
+template <int EFMT, int SFMT, int NST>
+__global__ __launch_bounds__(WAVES * 64) void k_gemm_down(GemmArgs a) {
+    __shared__ __attribute__((aligned(16))) _Float16 xs[2 * TILE * BLD];
+    __shared__ int rowoff[TILE];
     const uint32_t nt = a.tiles[0];
     if (blockIdx.x >= nt) return;
     const uint32_t e = a.tiles[1 + 3 * blockIdx.x], first = a.tiles[2 + 3 * blockIdx.x],
                    rows = a.tiles[3 + 3 * blockIdx.x];
     const bool sh = e == (uint32_t)a.E;
-    if (threadIdx.x < TM) rowoff[threadIdx.x] = threadIdx.x < rows ? (int)(first + threadIdx.x) : -1;
+    if (threadIdx.x < TILE) rowoff[threadIdx.x] = (int)(first + (threadIdx.x < rows ? threadIdx.x : 0));
+    __syncthreads();
     if (sh) {
-        if (a.sh_fmt == FQ8) down_tile<FQ8>(a.sh_a, a.S, a.src_sh, a.S, rowoff, a.ysh, a.H, first, rows, xs);
-        else if (a.sh_fmt == FQ6K) down_tile<FQ6K>(a.sh_a, a.S, a.src_sh, a.S, rowoff, a.ysh, a.H, first, rows, xs);
-        else down_tile<FQ4K>(a.sh_a, a.S, a.src_sh, a.S, rowoff, a.ysh, a.H, first, rows, xs);
+        const DnEpi epi{a.ysh, a.H, (int)first, (int)rows};
+        tile_run<SFMT, 1, DN_RPW, DN_DEPTH, NST>(a.sh_a, nullptr, a.S, a.src_sh, a.S, rowoff, (int)rows, xs, epi);
     } else {
-        const uint8_t *w = a.wa + (size_t)e * a.stride_a;
-        if (a.fmt == FQ6K) down_tile<FQ6K>(w, a.M, a.src, a.M, rowoff, a.y, a.H, first, rows, xs);
-        else down_tile<FQ4K>(w, a.M, a.src, a.M, rowoff, a.y, a.H, first, rows, xs);
+        const DnEpi epi{a.y, a.H, (int)first, (int)rows};
+        tile_run<EFMT, 1, DN_RPW, DN_DEPTH, NST>(a.wa + (size_t)e * a.stride_a, nullptr, a.M, a.src, a.M, rowoff, (int)rows, xs, epi);
     }
 }
 
@@ -305,29 +419,52 @@ __global__ __launch_bounds__(256) void k_gemm_down(GemmArgs a) {
 int launch_gemm_gate_up(const ExpertSide &ex, const SharedSide &sh, const _Float16 *x16, int T, int H,
                         int M, int K, int E, const uint32_t *tiles, int n_tiles_max,
                         const uint32_t *pairs, _Float16 *act, _Float16 *act_sh, hipStream_t s) {
-    if (H % 256 || M % NB || (sh.gate && sh.S % NB) || ex.gate_fmt != FQ4K) return -2;
+    const int NB = WAVES * 16 * GU_RPW;
+    if ((H / KC * GU_RPW) % GU_DEPTH) return -2;
+    if (H % KCH || M % NB || (sh.gate && sh.S % NB) || ex.gate_fmt != FQ4K) return -2;
     if (sh.gate && sh.gate_fmt != FQ4K && sh.gate_fmt != FQ8) return -2;
     GemmArgs a = {};
-    a.wa = ex.gate; a.wb = ex.up; a.stride_a = ex.gate_stride; a.stride_b = ex.up_stride; a.fmt = FQ4K;
-    a.sh_a = sh.gate; a.sh_b = sh.up; a.sh_fmt = sh.gate_fmt;
+    a.wa = ex.gate; a.wb = ex.up; a.stride_a = ex.gate_stride; a.stride_b = ex.up_stride;
+    a.sh_a = sh.gate; a.sh_b = sh.up;
     a.src = x16; a.T = T; a.H = H; a.M = M; a.S = sh.gate ? sh.S : 0; a.K = K; a.E = E;
     a.tiles = tiles; a.pairs = pairs; a.act = act; a.act_sh = act_sh;
-    const int nby = (M > a.S ? M : a.S) / NB;
-    hipLaunchKernelGGL(k_gemm_gate_up, dim3(n_tiles_max, nby), dim3(256), 0, s, a);
+    const dim3 grid(n_tiles_max, (M > a.S ? M : a.S) / NB), block(WAVES * 64);
+    const bool q8 = sh.gate && sh.gate_fmt == FQ8;
+    /* compile-time stage count for the common hidden size (Q4_K shared
+     * expert); other shapes take the generic loop */
+    if (q8) hipLaunchKernelGGL((k_gemm_gate_up<FQ8, 0>), grid, block, 0, s, a);
+    else if (H == 2048) hipLaunchKernelGGL((k_gemm_gate_up<FQ4K, 16>), grid, block, 0, s, a);
+    else hipLaunchKernelGGL((k_gemm_gate_up<FQ4K, 0>), grid, block, 0, s, a);
     return hipGetLastError() == hipSuccess ? 0 : -3;
 }
 
 int launch_gemm_down(const ExpertSide &ex, const SharedSide &sh, const _Float16 *act,
-                     const _Float16 *act_sh, int T, int H, int M, int K, int E, const uint32_t *tiles,
-                     int n_tiles_max, float *y, float *ysh, hipStream_t s) {
-    if (H % NB || M % 256 || (sh.gate && sh.S % 256)) return -2;
+                     const _Float16 *act_sh, int T, int H, int M, int K, int E,
+                     const uint32_t *tiles, int n_tiles_max, float *y, float *ysh, hipStream_t s) {
+    const int NB = WAVES * 16 * DN_RPW;
+    if ((M / KC * DN_RPW) % DN_DEPTH || (sh.gate && (sh.S / KC * DN_RPW) % DN_DEPTH)) return -2;
+    /* all of a tile's activations stay resident: in_dim <= 2 chunks */
+    if (H % NB || M % KCH || M > 2 * KCH || (sh.gate && (sh.S % KCH || sh.S > 2 * KCH))) return -2;
     if (ex.down_fmt != FQ4K && ex.down_fmt != FQ6K) return -2;
-    if (sh.gate && sh.down_fmt != FQ4K && sh.down_fmt != FQ6K && sh.down_fmt != FQ8) return -2;
+    const int sf = sh.gate ? sh.down_fmt : FQ4K;
+    if (sf != FQ4K && sf != FQ6K && sf != FQ8) return -2;
     GemmArgs a = {};
-    a.wa = ex.down; a.stride_a = ex.down_stride; a.fmt = ex.down_fmt;
-    a.sh_a = sh.gate ? sh.down : nullptr; a.sh_fmt = sh.down_fmt;
+    a.wa = ex.down; a.stride_a = ex.down_stride;
+    a.sh_a = sh.gate ? sh.down : nullptr;
     a.src = act; a.src_sh = act_sh; a.T = T; a.H = H; a.M = M; a.S = sh.gate ? sh.S : 0; a.K = K; a.E = E;
     a.tiles = tiles; a.y = y; a.ysh = ysh;
-    hipLaunchKernelGGL(k_gemm_down, dim3(n_tiles_max, H / NB), dim3(256), 0, s, a);
+    const dim3 grid(n_tiles_max, H / NB), block(WAVES * 64);
+    /* generic unit loop (a compile-time stage count spills here) */
+#define DN_LAUNCH(EF, SF) hipLaunchKernelGGL((k_gemm_down<EF, SF, 0>), grid, block, 0, s, a)
+    if (ex.down_fmt == FQ4K) {
+        if (sf == FQ4K) DN_LAUNCH(FQ4K, FQ4K);
+        else if (sf == FQ6K) DN_LAUNCH(FQ4K, FQ6K);
+        else DN_LAUNCH(FQ4K, FQ8);
+    } else {
+        if (sf == FQ4K) DN_LAUNCH(FQ6K, FQ4K);
+        else if (sf == FQ6K) DN_LAUNCH(FQ6K, FQ6K);
+        else DN_LAUNCH(FQ6K, FQ8);
+    }
+#undef DN_LAUNCH
     return hipGetLastError() == hipSuccess ? 0 : -3;
 }
