@@ -84,31 +84,45 @@ struct Span<FQ4K> {
         hdr = ld_u4(p);
         q = ld_u4(p + 16 + 16 * (kg + 4 * (j & 1)));
     }
-    h2 d, scl, ncl, sch, nch, mbl, mbh;
+    h2 d, sc, nc, mb; /* (lo, hi) sub-block pairs: sc = (sl, sh/16), nc = (-1024 sl, -64 sh), mb = -(dmin m) */
     MDEV void prepare(int j, int kg) {
         /* the first half-block never reads hdr.w: consume it here so its
          * register is not recycled (a write-after-write wait on the load
          * still in flight) before this unit */
         asm volatile("" ::"v"(hdr.w));
-        uint32_t sl, sh, ml, mh;
-        q4k_scale_min(hdr, (kg + 4 * (j & 1)) >> 1, sl, sh, ml, mh);
-        const float dmin = f16_bits_to_f32(hdr.x >> 16);
+        /* 6-bit scale/min pairs of sub-blocks 2g, 2g+1 (g = 2(j&1) + kg/2),
+         * packed as (lo | hi << 16): bytes 2hb, 2hb+1 of the scale and min
+         * words, plus for g >= 2 the 4-bit parts from byte 8+hb / 10+hb
+         * (inference/src/format.m:41-64) */
+        const uint32_t hb = (uint32_t)kg >> 1, sel = 0x0C010C00u + hb * 0x00020002u;
+        uint32_t s2, m2;
+        if ((j & 1) == 0) {
+            s2 = __builtin_amdgcn_perm(0u, hdr.y, sel) & 0x003F003Fu;
+            m2 = __builtin_amdgcn_perm(0u, hdr.z, sel) & 0x003F003Fu;
+        } else {
+            const uint32_t sp = (hdr.w >> (8 * hb)) & 0xFFu, mp = (hdr.w >> (8 * hb + 16)) & 0xFFu;
+            s2 = ((sp | (sp << 12)) & 0x000F000Fu) | ((__builtin_amdgcn_perm(0u, hdr.y, sel) >> 2) & 0x00300030u);
+            m2 = ((mp | (mp << 12)) & 0x000F000Fu) | ((__builtin_amdgcn_perm(0u, hdr.z, sel) >> 2) & 0x00300030u);
+        }
+        const h2 bias = {(_Float16)1024.0f, (_Float16)1024.0f};
+        const h2 S = or_bias(s2) - bias, M = or_bias(m2) - bias; /* exact small integers */
+        sc = S * h2{(_Float16)1.0f, (_Float16)0.0625f};
+        nc = S * h2{(_Float16)-1024.0f, (_Float16)-64.0f};
+        const _Float16 dmin = __builtin_bit_cast(_Float16, (uint16_t)(hdr.x >> 16));
+        mb = M * h2{-dmin, -dmin}; /* RN(dmin m), as fp16 of the exact fp32 product */
         d = splat(__builtin_bit_cast(_Float16, (uint16_t)(hdr.x & 0xFFFFu)));
-        scl = splat((_Float16)(float)sl);
-        ncl = splat((_Float16)(-1024.0f * (float)sl));
-        sch = splat((_Float16)((float)sh * 0.0625f));
-        nch = splat((_Float16)(-64.0f * (float)sh));
-        mbl = splat((_Float16)(-(dmin * (float)ml)));
-        mbh = splat((_Float16)(-(dmin * (float)mh)));
     }
     /* k order of the result: l, l+2, l+1, l+3, l+32, l+34, l+33, l+35 */
     MDEV h8 frag(int s) const {
-        const uint32_t w = u4_at(q, s), w8 = w >> 8;
-        const h2 t0 = hfma(or_bias(w & 0x000F000Fu), scl, ncl);
-        const h2 t1 = hfma(or_bias(w8 & 0x000F000Fu), scl, ncl);
-        const h2 t2 = hfma(or_bias(w & 0x00F000F0u), sch, nch);
-        const h2 t3 = hfma(or_bias(w8 & 0x00F000F0u), sch, nch);
-        return cat4(hfma(t0, d, mbl), hfma(t1, d, mbl), hfma(t2, d, mbh), hfma(t3, d, mbh));
+        const uint32_t w = u4_at(q, s);
+        /* bytes 1 and 3 under the 0x64 exponent byte: (0x64 b1, 0x64 b3) */
+        const uint32_t p13 = __builtin_amdgcn_perm(0x64646464u, w, 0x04030401u);
+        const h2 t0 = hfma(or_bias(w & 0x000F000Fu), splat(sc.x), splat(nc.x));
+        const h2 t1 = hfma(as_h2(p13 & 0xFF0FFF0Fu), splat(sc.x), splat(nc.x));
+        const h2 t2 = hfma(or_bias(w & 0x00F000F0u), splat(sc.y), splat(nc.y));
+        const h2 t3 = hfma(as_h2(p13 & 0xFFF0FFF0u), splat(sc.y), splat(nc.y));
+        return cat4(hfma(t0, d, splat(mb.x)), hfma(t1, d, splat(mb.x)), hfma(t2, d, splat(mb.y)),
+                    hfma(t3, d, splat(mb.y)));
     }
 };
 
