@@ -47,7 +47,7 @@ struct orome_hip_ctx {
     /* scratch */
     float *logits, *w, *sgl, *y, *ysh, *xnorm;
     int32_t *idx;
-    uint32_t *offsets, *pairs, *pos, *list, *counter, *tiles;
+    uint32_t *offsets, *pairs, *pos, *list, *counter, *tiles, *dcount;
     _Float16 *x16, *act, *act_sh;
     void *arena;
     size_t arena_bytes;
@@ -94,6 +94,7 @@ extern "C" orome_hip_ctx *orome_hip_create(const ModelConfig *cfg, int max_token
         {(void **)&c->offsets, (E + 1) * 4},    {(void **)&c->pairs, T * K * 4},
         {(void **)&c->pos, T * K * 4},          {(void **)&c->list, (2 * E + 2) * 4},
         {(void **)&c->counter, 256},            {(void **)&c->tiles, (1 + 3 * ntile) * 4},
+        {(void **)&c->dcount, (size_t)dispatch_blocks((int)T) * E * 4},
         {(void **)&c->x16, T * H * 2},          {(void **)&c->act, T * K * M * 2},
         {(void **)&c->act_sh, T * (S ? S : 1) * 2}, {(void **)&c->y, T * K * H * 4},
         {(void **)&c->ysh, T * H * 4},          {(void **)&c->xnorm, T * H * 4},
@@ -314,7 +315,7 @@ extern "C" int orome_moe_forward(orome_hip_ctx *c, const ModelConfig *cfg, const
         TLAUNCH(c, ST_ROUTE, launch_route_logits(a, s), "router logits");
         TLAUNCH(c, ST_TOPK, launch_topk(a, s), "top-k");
         const int tile_m = GEMM_TILE_TOKENS;
-        TLAUNCH(c, ST_DISPATCH, launch_dispatch(a, c->tiles, tile_m, S ? 1 : 0, s), "dispatch");
+        TLAUNCH(c, ST_DISPATCH, launch_dispatch(a, c->tiles, tile_m, S ? 1 : 0, c->dcount, s), "dispatch");
         TLAUNCH(c, ST_STAGE, launch_to_f16(x, T, H, c->x16, s), "fp16 staging");
         const int ntiles = (T * K) / tile_m + E + (S ? (T + tile_m - 1) / tile_m : 0);
         TLAUNCH(c, ST_GATE_UP, launch_gemm_gate_up(ex, sh, c->x16, T, H, M, K, E, c->tiles, ntiles, c->pairs, c->act,

@@ -46,7 +46,9 @@ struct SharedSide {
 int launch_route_small(const RouteArgs &a, hipStream_t s);
 int launch_route_logits(const RouteArgs &a, hipStream_t s);
 int launch_topk(const RouteArgs &a, hipStream_t s);
-int launch_dispatch(const RouteArgs &a, uint32_t *tiles, int tile_m, int has_shared, hipStream_t s);
+int dispatch_blocks(int T); /* rows of the dispatch count scratch ([rows][E] words) */
+int launch_dispatch(const RouteArgs &a, uint32_t *tiles, int tile_m, int has_shared, uint32_t *cnt,
+                    hipStream_t s);
 
 /* decode gate/up; with route_in_block the top-k + dispatch of the call is
  * folded in (every block selects; block 0 publishes the routing outputs in

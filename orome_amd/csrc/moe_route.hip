@@ -78,50 +78,63 @@ __global__ __launch_bounds__(256) void k_topk_dispatch_small(RouteArgs a) {
     topk_dispatch_block<EPL, false>(a);
 }
 
-/* Large-batch router logits: a block computes 16 rows x 8 tokens; each wave
- * 4 rows x 8 tokens with the canonical per-logit order. */
+/* Large-batch router logits: a block computes 32 rows (expert rows, then the
+ * shared-gate row E) x 8 tokens, so the 2 MB router matrix is what gets
+ * re-read (from L2) rather than the activations; each wave 8 rows x 8
+ * tokens, lane L
+ * accumulating k = 256 i + 4 L + c in (i, c) order with fma from zero. */
 __global__ __launch_bounds__(256) void k_route_logits(RouteArgs a) {
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int E = a.E, H = a.H, T = a.T;
-    const int r0 = blockIdx.x * 16 + wv * 4, t0 = blockIdx.y * 8;
-    float acc[4][8];
-    const float *wr[4];
+    const int r0 = blockIdx.x * 32 + wv * 8, t0 = blockIdx.y * 8;
+    const float *wr[8];
 #pragma unroll
-    for (int r = 0; r < 4; r++) {
-        int row = r0 + r;
+    for (int r = 0; r < 8; r++) {
+        const int row = r0 + r;
         wr[r] = row < E ? a.W + (size_t)row * H : (row == E ? a.wsg : nullptr);
-#pragma unroll
-        for (int t = 0; t < 8; t++) acc[r][t] = 0.0f;
     }
     const int nt = min(8, T - t0);
+    float acc[64]; /* output o = 8 r + t */
+#pragma unroll
+    for (int o = 0; o < 64; o++) acc[o] = 0.0f;
     for (int i = 0; i < H / 256; i++) {
         f4 xv[8];
 #pragma unroll
         for (int t = 0; t < 8; t++)
             xv[t] = t < nt ? *(const f4 *)(a.x + (size_t)(t0 + t) * H + 256 * i + 4 * lane) : f4{0, 0, 0, 0};
 #pragma unroll
-        for (int r = 0; r < 4; r++) {
-            if (!wr[r]) continue;
-            f4 w = *(const f4 *)(wr[r] + 256 * i + 4 * lane);
+        for (int r = 0; r < 8; r++) {
+            const f4 w = wr[r] ? *(const f4 *)(wr[r] + 256 * i + 4 * lane) : f4{0, 0, 0, 0};
 #pragma unroll
             for (int t = 0; t < 8; t++) {
-                acc[r][t] = __builtin_fmaf(w.x, xv[t].x, acc[r][t]);
-                acc[r][t] = __builtin_fmaf(w.y, xv[t].y, acc[r][t]);
-                acc[r][t] = __builtin_fmaf(w.z, xv[t].z, acc[r][t]);
-                acc[r][t] = __builtin_fmaf(w.w, xv[t].w, acc[r][t]);
+                float &c = acc[8 * r + t];
+                c = __builtin_fmaf(w.x, xv[t].x, c);
+                c = __builtin_fmaf(w.y, xv[t].y, c);
+                c = __builtin_fmaf(w.z, xv[t].z, c);
+                c = __builtin_fmaf(w.w, xv[t].w, c);
             }
         }
     }
+    /* Butterfly reduce-scatter over the 64 lanes: at stage s lanes L and
+     * L ^ 2^s add the partial sums of the half of their outputs that L keeps
+     * (bit s of L picks the half).  Each add joins the subtree sums of lanes
+     * [L0, L0 + 2^s) and [L0 + 2^s, L0 + 2^(s+1)), so every output is summed
+     * in the canonical contiguous balanced tree; lane L ends with output
+     * bitreverse6(L). */
 #pragma unroll
-    for (int r = 0; r < 4; r++) {
-        int row = r0 + r;
-        if (row > E) continue;
+    for (int st = 0; st < 6; st++) {
+        const int half = 32 >> st;
+        const bool hi = (lane >> st) & 1;
 #pragma unroll
-        for (int t = 0; t < 8; t++) {
-            float s = wave_sum_canon(acc[r][t]);
-            if (lane == 0 && t < nt) a.logits[(size_t)(t0 + t) * (E + 1) + row] = s;
+        for (int o = 0; o < half; o++) {
+            const float send = hi ? acc[o] : acc[o + half];
+            const float keep = hi ? acc[o + half] : acc[o];
+            acc[o] = keep + __shfl_xor(send, 1 << st, 64);
         }
     }
+    const int o = (int)(__builtin_bitreverse32((uint32_t)lane) >> 26);
+    const int row = r0 + (o >> 3), tok = t0 + (o & 7);
+    if (row <= E && tok < T) a.logits[(size_t)tok * (E + 1) + row] = acc[0];
 }
 
 /* Large-batch selection: one wave per token. */
@@ -133,9 +146,51 @@ __global__ __launch_bounds__(256) void k_topk(RouteArgs a) {
                    a.w + t * a.K, a.sgl + t, nullptr);
 }
 
-/* Block-wide exclusive scan of three counters per expert (one thread per
- * expert, E <= DSP_THREADS), Hillis-Steele over LDS. */
+/* Dispatch for any T, in three launches over blocks of DSP_TOK tokens.  A
+ * pair p = t*K + k goes to position offsets[e] + (number of earlier tokens
+ * that picked e): a stable counting sort by expert (tokens pick distinct
+ * experts, so token order is pair order inside an expert).
+ *  1. count:   per block, an LDS token-membership mask per expert
+ *              (DSP_TOK bits) and its popcount -> cnt[block][e].
+ *  2. scan:    one block: per expert an exclusive scan of cnt over blocks
+ *              (in place) and the total; block scans of the totals give the
+ *              offsets, active-expert ranks and GEMM tile offsets; then the
+ *              active list and the tile list (expert, first row, rows), tiles
+ *              of tile_m rows, the shared expert (id E) over tokens 0..T-1.
+ *  3. scatter: per block, the same masks; a pair's rank is its expert's
+ *              offset + the block's base + the popcount of the mask below
+ *              its token. */
+#define DSP_TOK 256
+#define DSP_WORDS (DSP_TOK / 32)
 #define DSP_THREADS 1024
+
+DEV void dispatch_masks(const RouteArgs &a, uint32_t *mask, int ek[OROME_MAXK]) {
+    const int E = a.E, K = a.K, tid = threadIdx.x, t = blockIdx.x * DSP_TOK + tid;
+    for (int i = tid; i < E * DSP_WORDS; i += DSP_TOK) mask[i] = 0;
+#pragma unroll
+    for (int k = 0; k < OROME_MAXK; k++)
+        if (k < K) ek[k] = t < a.T ? a.idx[t * K + k] : -1;
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < OROME_MAXK; k++)
+        if (k < K && ek[k] >= 0) atomicOr(&mask[ek[k] * DSP_WORDS + (tid >> 5)], 1u << (tid & 31));
+    __syncthreads();
+}
+
+__global__ __launch_bounds__(DSP_TOK) void k_dispatch_count(RouteArgs a, uint32_t *cnt) {
+    extern __shared__ uint32_t mask[]; /* E * DSP_WORDS */
+    int ek[OROME_MAXK];
+    dispatch_masks(a, mask, ek);
+    for (int e = threadIdx.x; e < a.E; e += DSP_TOK) {
+        uint32_t c = 0;
+#pragma unroll
+        for (int w = 0; w < DSP_WORDS; w++) c += __popc(mask[e * DSP_WORDS + w]);
+        cnt[(size_t)blockIdx.x * a.E + e] = c;
+    }
+}
+
+/* Block-wide inclusive scan of three counters per expert (one thread per
+ * expert, E <= DSP_THREADS), Hillis-Steele over LDS. */
 DEV void block_scan3(uint32_t *a, uint32_t *b, uint32_t *c, int n) {
     const int tid = threadIdx.x;
     for (int off = 1; off < n; off <<= 1) {
@@ -147,34 +202,21 @@ DEV void block_scan3(uint32_t *a, uint32_t *b, uint32_t *c, int n) {
     }
 }
 
-/* Dispatch for any T (one block of 1024 threads):
- *  1. LDS histogram of the T*K expert ids; block scans give the offsets, the
- *     active-expert ranks and the GEMM tile offsets.
- *  2. Stable scatter in chunks of 1024 tokens: each expert keeps a 1024-bit
- *     membership mask of the chunk's tokens, so a pair's rank inside its
- *     expert is the popcount of the mask below its token, plus the count
- *     carried from earlier chunks.
- *  3. Active-expert list and GEMM tile list (expert, first row, rows), tiles
- *     of tile_m rows; the shared expert (id E) covers tokens 0..T-1. */
-__global__ __launch_bounds__(DSP_THREADS) void k_dispatch(RouteArgs a, uint32_t *tiles, int tile_m,
-                                                          int has_shared) {
-    extern __shared__ uint32_t lds[];
-    const int E = a.E, K = a.K, T = a.T, tid = threadIdx.x;
-    uint32_t *hist = lds;                   /* E */
-    uint32_t *offs = hist + E;              /* E (inclusive scan of hist) */
-    uint32_t *arank = offs + E;             /* E (inclusive scan of active) */
-    uint32_t *toff = arank + E;             /* E (inclusive scan of tile counts) */
-    uint32_t *cursor = toff + E;            /* E */
-    uint32_t *mask = cursor + E;            /* E * 32 */
-    uint32_t *wpre = mask + (size_t)E * 32; /* E * 32 */
-    for (int e = tid; e < E; e += DSP_THREADS) { hist[e] = 0; cursor[e] = 0; }
-    __syncthreads();
-    for (int p = tid; p < T * K; p += DSP_THREADS) atomicAdd(&hist[a.idx[p]], 1u);
-    __syncthreads();
+__global__ __launch_bounds__(DSP_THREADS) void k_dispatch_scan(RouteArgs a, uint32_t *cnt, int G,
+                                                               uint32_t *tiles, int tile_m, int has_shared) {
+    __shared__ uint32_t hist[DSP_THREADS], offs[DSP_THREADS], arank[DSP_THREADS], toff[DSP_THREADS];
+    const int E = a.E, T = a.T, tid = threadIdx.x;
     if (tid < E) {
-        offs[tid] = hist[tid];
-        arank[tid] = hist[tid] != 0;
-        toff[tid] = (hist[tid] + tile_m - 1) / tile_m;
+        uint32_t run = 0;
+        for (int g = 0; g < G; g++) {
+            const uint32_t c = cnt[(size_t)g * E + tid];
+            cnt[(size_t)g * E + tid] = run;
+            run += c;
+        }
+        hist[tid] = run;
+        offs[tid] = run;
+        arank[tid] = run != 0;
+        toff[tid] = (run + tile_m - 1) / tile_m;
     }
     __syncthreads();
     block_scan3(offs, arank, toff, E);
@@ -211,46 +253,33 @@ __global__ __launch_bounds__(DSP_THREADS) void k_dispatch(RouteArgs a, uint32_t 
             tiles[3 + 3 * (nt + j)] = (uint32_t)min(tile_m, T - j * tile_m);
         }
     }
-    for (int base = 0; base < T; base += 1024) {
-        for (int i = tid; i < E * 32; i += DSP_THREADS) mask[i] = 0;
-        __syncthreads();
-        const int t = base + tid;
-        const bool live = t < T;
-        int ek[OROME_MAXK];
+}
+
+__global__ __launch_bounds__(DSP_TOK) void k_dispatch_scatter(RouteArgs a, const uint32_t *base) {
+    extern __shared__ uint32_t mask[]; /* E * DSP_WORDS, then E * DSP_WORDS word prefixes */
+    uint32_t *wpre = mask + a.E * DSP_WORDS;
+    int ek[OROME_MAXK];
+    dispatch_masks(a, mask, ek);
+    const int E = a.E, K = a.K, tid = threadIdx.x, t = blockIdx.x * DSP_TOK + tid;
+    for (int e = tid; e < E; e += DSP_TOK) {
+        uint32_t run = a.offsets[e] + base[(size_t)blockIdx.x * E + e];
 #pragma unroll
-        for (int k = 0; k < OROME_MAXK; k++)
-            if (k < K) ek[k] = live ? a.idx[t * K + k] : 0;
-        if (live)
-#pragma unroll
-            for (int k = 0; k < OROME_MAXK; k++)
-                if (k < K) atomicOr(&mask[ek[k] * 32 + (tid >> 5)], 1u << (tid & 31));
-        __syncthreads();
-        for (int i = tid; i < E * 32; i += DSP_THREADS) {
-            /* prefix popcount over the 32 words of one expert: word w of
-             * expert e sums words 0..w-1 (32 lanes of a wave share e) */
-            const int e = i >> 5, w = i & 31;
-            uint32_t s = 0;
-            for (int v = 0; v < w; v++) s += __popc(mask[e * 32 + v]);
-            wpre[i] = s;
+        for (int w = 0; w < DSP_WORDS; w++) {
+            wpre[e * DSP_WORDS + w] = run;
+            run += __popc(mask[e * DSP_WORDS + w]);
         }
-        __syncthreads();
-        if (live)
-#pragma unroll
-            for (int k = 0; k < OROME_MAXK; k++)
-                if (k < K) {
-                    const int e = ek[k];
-                    const uint32_t wd = mask[e * 32 + (tid >> 5)];
-                    const uint32_t rank = cursor[e] + wpre[e * 32 + (tid >> 5)] + __popc(wd & ((1u << (tid & 31)) - 1u));
-                    const uint32_t pos = offs[e] - hist[e] + rank;
-                    const uint32_t p = (uint32_t)(t * K + k);
-                    a.pairs[pos] = p;
-                    a.pos[p] = pos;
-                }
-        __syncthreads();
-        for (int e = tid; e < E; e += DSP_THREADS)
-            cursor[e] += wpre[e * 32 + 31] + __popc(mask[e * 32 + 31]);
-        __syncthreads();
     }
+    __syncthreads();
+    const uint32_t below = (1u << (tid & 31)) - 1u;
+#pragma unroll
+    for (int k = 0; k < OROME_MAXK; k++)
+        if (k < K && ek[k] >= 0) {
+            const int i = ek[k] * DSP_WORDS + (tid >> 5);
+            const uint32_t pos = wpre[i] + __popc(mask[i] & below);
+            const uint32_t p = (uint32_t)(t * K + k);
+            a.pairs[pos] = p;
+            a.pos[p] = pos;
+        }
 }
 
 /* RMSNorm (inference/src/shaders.metal:128-149) with the canonical sum of
@@ -324,7 +353,7 @@ int launch_topk_dispatch_small(const RouteArgs &a, hipStream_t s) {
 
 int launch_route_logits(const RouteArgs &a, hipStream_t s) {
     if (a.H % 256) return -2;
-    dim3 grid((a.E + 1 + 15) / 16, (a.T + 7) / 8);
+    dim3 grid((a.E + 1 + 31) / 32, (a.T + 7) / 8);
     hipLaunchKernelGGL(k_route_logits, grid, dim3(256), 0, s, a);
     return hipGetLastError() == hipSuccess ? 0 : -3;
 }
@@ -335,10 +364,16 @@ int launch_topk(const RouteArgs &a, hipStream_t s) {
     return hipGetLastError() == hipSuccess ? 0 : -3;
 }
 
-int launch_dispatch(const RouteArgs &a, uint32_t *tiles, int tile_m, int has_shared, hipStream_t s) {
-    size_t lds = sizeof(uint32_t) * ((size_t)a.E * 5 + (size_t)a.E * 64);
-    if (lds > 160 * 1024 || a.E > DSP_THREADS) return -2;
-    hipLaunchKernelGGL(k_dispatch, dim3(1), dim3(DSP_THREADS), lds, s, a, tiles, tile_m, has_shared);
+int dispatch_blocks(int T) { return (T + DSP_TOK - 1) / DSP_TOK; }
+
+int launch_dispatch(const RouteArgs &a, uint32_t *tiles, int tile_m, int has_shared, uint32_t *cnt,
+                    hipStream_t s) {
+    const size_t lds = sizeof(uint32_t) * (size_t)a.E * DSP_WORDS * 2;
+    if (lds > 64 * 1024 || a.E > DSP_THREADS || a.K > OROME_MAXK) return -2;
+    const int G = dispatch_blocks(a.T);
+    hipLaunchKernelGGL(k_dispatch_count, dim3(G), dim3(DSP_TOK), lds / 2, s, a, cnt);
+    hipLaunchKernelGGL(k_dispatch_scan, dim3(1), dim3(DSP_THREADS), 0, s, a, cnt, G, tiles, tile_m, has_shared);
+    hipLaunchKernelGGL(k_dispatch_scatter, dim3(G), dim3(DSP_TOK), lds, s, a, (const uint32_t *)cnt);
     return hipGetLastError() == hipSuccess ? 0 : -3;
 }
 
