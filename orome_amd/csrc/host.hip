@@ -42,12 +42,14 @@ enum { ST_NORM, ST_ROUTE, ST_TOPK, ST_DISPATCH, ST_STAGE, ST_GATE_UP, ST_DOWN, S
 struct orome_hip_ctx {
     int device;
     hipStream_t stream;
+    hipStream_t side;        /* second stream: the big-tile GEMM list runs beside the small one */
+    hipEvent_t fork, join;
     ModelConfig cfg;
     int tmax, kmax, path;
     /* scratch */
     float *logits, *w, *sgl, *y, *ysh, *xnorm;
     int32_t *idx;
-    uint32_t *offsets, *pairs, *pos, *list, *counter, *tiles, *dcount;
+    uint32_t *offsets, *pairs, *pos, *list, *counter, *tiles, *tiles_b, *dcount;
     _Float16 *x16, *act, *act_sh;
     void *arena;
     size_t arena_bytes;
@@ -84,16 +86,25 @@ extern "C" orome_hip_ctx *orome_hip_create(const ModelConfig *cfg, int max_token
         free(c);
         return NULL;
     }
+    if (hipStreamCreateWithFlags(&c->side, hipStreamNonBlocking) != hipSuccess ||
+        hipEventCreateWithFlags(&c->fork, hipEventDisableTiming) != hipSuccess ||
+        hipEventCreateWithFlags(&c->join, hipEventDisableTiming) != hipSuccess) {
+        orome_fail(OROME_EHIP, "orome_hip_create: side stream creation failed");
+        (void)hipStreamDestroy(c->stream);
+        free(c);
+        return NULL;
+    }
     const size_t T = (size_t)max_tokens, E = (size_t)cfg->num_experts, K = (size_t)c->kmax,
                  H = (size_t)cfg->hidden_dim, M = (size_t)cfg->moe_intermediate,
                  S = (size_t)(cfg->shared_intermediate > 0 ? cfg->shared_intermediate : 0);
-    const size_t ntile = (T * K) / GEMM_TILE_TOKENS + E + T / GEMM_TILE_TOKENS + 2;
+    const size_t ntile_s = E + T / GEMM_TILE_SMALL + 2, ntile_b = (T * K) / GEMM_TILE_BIG + E + T / GEMM_TILE_BIG + 2;
     struct { void **p; size_t bytes; } parts[] = {
         {(void **)&c->logits, T * (E + 1) * 4}, {(void **)&c->idx, T * K * 4},
         {(void **)&c->w, T * K * 4},           {(void **)&c->sgl, T * 4},
         {(void **)&c->offsets, (E + 1) * 4},    {(void **)&c->pairs, T * K * 4},
         {(void **)&c->pos, T * K * 4},          {(void **)&c->list, (2 * E + 2) * 4},
-        {(void **)&c->counter, 256},            {(void **)&c->tiles, (1 + 3 * ntile) * 4},
+        {(void **)&c->counter, 256},            {(void **)&c->tiles, (1 + 3 * ntile_s) * 4},
+        {(void **)&c->tiles_b, (1 + 3 * ntile_b) * 4},
         {(void **)&c->dcount, (size_t)dispatch_blocks((int)T) * E * 4},
         {(void **)&c->x16, T * H * 2},          {(void **)&c->act, T * K * M * 2},
         {(void **)&c->act_sh, T * (S ? S : 1) * 2}, {(void **)&c->y, T * K * H * 4},
@@ -103,6 +114,7 @@ extern "C" orome_hip_ctx *orome_hip_create(const ModelConfig *cfg, int max_token
     for (auto &p : parts) total += (p.bytes + 255) / 256 * 256;
     if (hipMalloc(&c->arena, total) != hipSuccess) {
         orome_fail(OROME_ENOMEM, "orome_hip_create: scratch arena of %zu bytes", total);
+        (void)hipStreamDestroy(c->side);
         (void)hipStreamDestroy(c->stream);
         free(c);
         return NULL;
@@ -118,6 +130,7 @@ extern "C" orome_hip_ctx *orome_hip_create(const ModelConfig *cfg, int max_token
     if (hipMemset(c->arena, 0, total) != hipSuccess || hipDeviceSynchronize() != hipSuccess) {
         orome_fail(OROME_EHIP, "orome_hip_create: scratch clear failed");
         (void)hipFree(c->arena);
+        (void)hipStreamDestroy(c->side);
         (void)hipStreamDestroy(c->stream);
         free(c);
         return NULL;
@@ -137,8 +150,12 @@ extern "C" void orome_hip_destroy(orome_hip_ctx *c) {
     if (!c) return;
     (void)hipSetDevice(c->device);
     (void)hipStreamSynchronize(c->stream);
+    (void)hipStreamSynchronize(c->side);
     free_timing(c);
     (void)hipFree(c->arena);
+    (void)hipEventDestroy(c->fork);
+    (void)hipEventDestroy(c->join);
+    (void)hipStreamDestroy(c->side);
     (void)hipStreamDestroy(c->stream);
     free(c);
 }
@@ -314,16 +331,41 @@ extern "C" int orome_moe_forward(orome_hip_ctx *c, const ModelConfig *cfg, const
     } else {
         TLAUNCH(c, ST_ROUTE, launch_route_logits(a, s), "router logits");
         TLAUNCH(c, ST_TOPK, launch_topk(a, s), "top-k");
-        const int tile_m = GEMM_TILE_TOKENS;
-        TLAUNCH(c, ST_DISPATCH, launch_dispatch(a, c->tiles, tile_m, S ? 1 : 0, c->dcount, s), "dispatch");
+        TLAUNCH(c, ST_DISPATCH, launch_dispatch(a, c->tiles, c->tiles_b, S ? 1 : 0, c->dcount, s), "dispatch");
         TLAUNCH(c, ST_STAGE, launch_to_f16(x, T, H, c->x16, s), "fp16 staging");
-        const int ntiles = (T * K) / tile_m + E + (S ? (T + tile_m - 1) / tile_m : 0);
-        TLAUNCH(c, ST_GATE_UP, launch_gemm_gate_up(ex, sh, c->x16, T, H, M, K, E, c->tiles, ntiles, c->pairs, c->act,
-                                   c->act_sh, s),
-               "grouped gate/up");
-        TLAUNCH(c, ST_DOWN, launch_gemm_down(ex, sh, c->act, c->act_sh, T, H, M, K, E, c->tiles, ntiles, c->y,
-                                c->ysh, s),
-               "grouped down");
+        /* one launch per tile list (grid sized for the most tiles it can hold) */
+        const bool sh_small = (long)T * K <= (long)GEMM_TILE_SMALL * E;
+        const int ns_max = E + (S && sh_small ? (T + GEMM_TILE_SMALL - 1) / GEMM_TILE_SMALL : 0),
+                  nb_max = (T * K) / GEMM_TILE_BIG + E + (S && !sh_small ? (T + GEMM_TILE_BIG - 1) / GEMM_TILE_BIG : 0);
+        auto gate_up = [&](int tm, hipStream_t st) {
+            return tm == GEMM_TILE_SMALL
+                       ? launch_gemm_gate_up(ex, sh, c->x16, T, H, M, K, E, tm, c->tiles, ns_max, c->pairs, c->act,
+                                             c->act_sh, st)
+                       : launch_gemm_gate_up(ex, sh, c->x16, T, H, M, K, E, tm, c->tiles_b, nb_max, c->pairs, c->act,
+                                             c->act_sh, st);
+        };
+        auto down = [&](int tm, hipStream_t st) {
+            return tm == GEMM_TILE_SMALL
+                       ? launch_gemm_down(ex, sh, c->act, c->act_sh, T, H, M, K, E, tm, c->tiles, ns_max, c->y,
+                                          c->ysh, st)
+                       : launch_gemm_down(ex, sh, c->act, c->act_sh, T, H, M, K, E, tm, c->tiles_b, nb_max, c->y,
+                                          c->ysh, st);
+        };
+        if (c->timing) { /* per-stage timing: both lists in order on one stream */
+            TLAUNCH(c, ST_GATE_UP, (gate_up(GEMM_TILE_SMALL, s) ? -3 : gate_up(GEMM_TILE_BIG, s)), "grouped gate/up");
+            TLAUNCH(c, ST_DOWN, (down(GEMM_TILE_SMALL, s) ? -3 : down(GEMM_TILE_BIG, s)), "grouped down");
+        } else {
+            /* the lists touch disjoint rows of act and y: the big-tile list
+             * runs on the side stream, overlapping the small one's tail */
+            HIP_OK(hipEventRecord(c->fork, s), OROME_EHIP);
+            HIP_OK(hipStreamWaitEvent(c->side, c->fork, 0), OROME_EHIP);
+            LAUNCH(gate_up(GEMM_TILE_BIG, c->side), "grouped gate/up (big tiles)");
+            LAUNCH(down(GEMM_TILE_BIG, c->side), "grouped down (big tiles)");
+            LAUNCH(gate_up(GEMM_TILE_SMALL, s), "grouped gate/up (small tiles)");
+            LAUNCH(down(GEMM_TILE_SMALL, s), "grouped down (small tiles)");
+            HIP_OK(hipEventRecord(c->join, c->side), OROME_EHIP);
+            HIP_OK(hipStreamWaitEvent(s, c->join, 0), OROME_EHIP);
+        }
         TLAUNCH(c, ST_COMBINE, launch_combine(c->y, c->ysh, c->pos, c->w, c->sgl, S ? 1 : 0, h_in, h_out, T, H, K, s),
                "combine");
     }

@@ -47,7 +47,7 @@ int launch_route_small(const RouteArgs &a, hipStream_t s);
 int launch_route_logits(const RouteArgs &a, hipStream_t s);
 int launch_topk(const RouteArgs &a, hipStream_t s);
 int dispatch_blocks(int T); /* rows of the dispatch count scratch ([rows][E] words) */
-int launch_dispatch(const RouteArgs &a, uint32_t *tiles, int tile_m, int has_shared, uint32_t *cnt,
+int launch_dispatch(const RouteArgs &a, uint32_t *tiles_s, uint32_t *tiles_b, int has_shared, uint32_t *cnt,
                     hipStream_t s);
 
 /* decode gate/up; with route_in_block the top-k + dispatch of the call is
@@ -70,10 +70,10 @@ int launch_dequant(int fmt, const uint8_t *src, uint32_t rows, uint32_t n, float
 /* prefill (MFMA) path */
 int launch_to_f16(const float *x, int T, int H, _Float16 *x16, hipStream_t s);
 int launch_gemm_gate_up(const ExpertSide &ex, const SharedSide &sh, const _Float16 *x16, int T,
-                        int H, int M, int K, int E, const uint32_t *tiles, int n_tiles_max,
+                        int H, int M, int K, int E, int tile_m, const uint32_t *tiles, int n_tiles_max,
                         const uint32_t *pairs, _Float16 *act, _Float16 *act_sh, hipStream_t s);
 int launch_gemm_down(const ExpertSide &ex, const SharedSide &sh, const _Float16 *act,
-                     const _Float16 *act_sh, int T, int H, int M, int K, int E,
+                     const _Float16 *act_sh, int T, int H, int M, int K, int E, int tile_m,
                      const uint32_t *tiles, int n_tiles_max, float *y, float *ysh,
                      hipStream_t s);
 int launch_combine(const float *y, const float *ysh, const uint32_t *pos, const float *w,
@@ -82,6 +82,9 @@ int launch_combine(const float *y, const float *ysh, const uint32_t *pos, const 
 
 /* tile list for the grouped GEMM: tiles[0] = count, then (expert, first, rows)
  * triples; expert == E denotes the shared expert over all T tokens */
-#ifndef GEMM_TILE_TOKENS
-#define GEMM_TILE_TOKENS 96
-#endif
+/* two tile lists per call: experts with <= GEMM_TILE_SMALL rows (one small
+ * tile each) and the rest in tiles of GEMM_TILE_BIG rows; the shared expert
+ * joins the small list when T*K <= GEMM_TILE_SMALL*E.  Capacities: small
+ * E + T/SMALL + 1, big T*K/BIG + E + T/BIG + 1. */
+#define GEMM_TILE_SMALL 32
+#define GEMM_TILE_BIG 96

@@ -1,16 +1,17 @@
 /*
  * moe_gemm.hip -- prefill-path grouped expert GEMMs on the matrix cores.
  *
- * Work list: the dispatch kernel emits tiles (expert, first row, rows <= GEMM_TILE_TOKENS)
+ * Work list: the dispatch kernel emits two tile lists (expert, first row,
+ * rows <= GEMM_TILE_SMALL or GEMM_TILE_BIG), each launched with its tile size,
  * over the expert-sorted pair list; the shared expert is expert E over the
  * token order.  One block computes one tile x NB output rows:
  *   gate/up  D[row][token] = W_{gate,up}[e][row] . x16[token]      (K = H)
  *   down     y[pos][row]   = W_down[e][row]    . act[pos]         (K = M)
  * with v_mfma_f32_16x16x32_f16 (A = 16 weight rows x 32 k, B = 32 k x 16
- * tokens, fp32 accumulate).  Each of the 4 waves owns 2 x 16 weight rows (of
- * gate and of up for the first GEMM) for all TB = ceil(rows/16) token blocks
- * of the tile, so one dequantised A fragment feeds TB matrix instructions and
- * one B fragment read from LDS feeds 2 (down) or 4 (gate/up).
+ * tokens, fp32 accumulate).  Each of the 8 waves owns RPW blocks of 16
+ * weight rows (of gate and of up for the first GEMM, one block; of down,
+ * four) for all TB = ceil(rows/16) token blocks of the tile, so one
+ * dequantised A fragment feeds TB matrix instructions.
  *
  * Weights are dequantised straight into A fragments with packed fp16
  * arithmetic on exactly factored terms (q arrives as the exact fp16 1024+q by
@@ -40,8 +41,6 @@ typedef float f4v __attribute__((ext_vector_type(4)));
 #define KC 128                          /* k per stage (one A fragment set) */
 #define KCH 256                         /* k per LDS activation chunk */
 #define BLD (KCH + 8)                   /* chunk row pitch (halves) */
-#define TILE GEMM_TILE_TOKENS           /* tokens per tile */
-#define TBMAX (TILE / 16)
 
 DEV size_t gemm_row_bytes(int fmt, int n) {
     return fmt == FQ4K ? (size_t)(n / 256) * 144 : fmt == FQ6K ? (size_t)(n / 256) * 210 : (size_t)(n / 32) * 34;
@@ -187,15 +186,16 @@ DEV f4v mfma(h8 a, h8 b, f4v c) { return __builtin_amdgcn_mfma_f32_16x16x32_f16(
  * halves (132 dwords: 16 rows x 16 bytes per lane group hit distinct banks),
  * each 128-k half in the fragment order of FMT.  A thread's vector n covers
  * token 16n + tid/32, k 8 (tid%32) .. +7.  Every thread loads and stores all
- * TBMAX vectors (rows past the tile read a valid row and are zeroed by a
+ * TBM vectors (rows past the tile read a valid row and are zeroed by a
  * select): the loads stay straight-line code, so the compiler's wait counts
  * for the weight prefetch ring stay exact. */
+template <int TBM>
 struct Chunk {
-    u4 v[TBMAX];
+    u4 v[TBM];
     MDEV void fetch(const _Float16 *src, const int *rowoff, int ld, int k0) {
         const int cc = (threadIdx.x & 31) * 8;
 #pragma unroll
-        for (int n = 0; n < TBMAX; n++)
+        for (int n = 0; n < TBM; n++)
             v[n] = ld_u4((const uint8_t *)(src + (size_t)rowoff[16 * n + (threadIdx.x >> 5)] * ld + k0 + cc));
     }
     /* the zero select for rows past the tile happens here, not at the load,
@@ -205,7 +205,7 @@ struct Chunk {
         const int col = threadIdx.x & 31, half = col >> 4, c0 = (col & 15) * 2;
         const int p0 = half * KC + frag_pos<FMT>(c0), p1 = half * KC + frag_pos<FMT>(c0 + 1);
 #pragma unroll
-        for (int n = 0; n < TBMAX; n++) {
+        for (int n = 0; n < TBM; n++) {
             const int t = 16 * n + (threadIdx.x >> 5);
             _Float16 *row = xs + t * BLD;
             const u4 x = t < rows ? v[n] : u4{0, 0, 0, 0};
@@ -228,7 +228,7 @@ struct Chunk {
  * chunks (256 k) sit in two LDS buffers: with <= 2 chunks both stay resident
  * (one barrier in all); with more, chunk c+2 is written into c's buffer
  * after the barrier that ends chunk c (RPW must be 1 then). */
-template <int FMT, int NMAT, int RPW, int DEPTH, int NST, typename Epi>
+template <int FMT, int NMAT, int RPW, int DEPTH, int NST, int TBM, typename Epi>
 DEV void tile_run(const uint8_t *w0, const uint8_t *w1, int in_dim, const _Float16 *src, int ld,
                   const int *rowoff, int rows, _Float16 *xs, const Epi &epi) {
     const int tb = (rows + 15) >> 4;
@@ -256,21 +256,21 @@ DEV void tile_run(const uint8_t *w0, const uint8_t *w1, int in_dim, const _Float
         }
     }
 
-    Chunk ch;
+    Chunk<TBM> ch;
     ch.fetch(src, rowoff, ld, 0);
-    ch.store<FMT>(xs, rows);
+    ch.template store<FMT>(xs, rows);
     if (nch > 1) {
         ch.fetch(src, rowoff, ld, KCH);
-        ch.store<FMT>(xs + TILE * BLD, rows);
+        ch.template store<FMT>(xs + TBM * 16 * BLD, rows);
     }
     if (nch > 2) ch.fetch(src, rowoff, ld, 2 * KCH);
     __syncthreads();
 
-    f4v c[NMAT][TBMAX];
+    f4v c[NMAT][TBM];
 #pragma unroll
     for (int m = 0; m < NMAT; m++)
 #pragma unroll
-        for (int t = 0; t < TBMAX; t++) c[m][t] = f4v{0, 0, 0, 0};
+        for (int t = 0; t < TBM; t++) c[m][t] = f4v{0, 0, 0, 0};
 
 #pragma unroll
     for (int u0 = 0; u0 < U; u0 += DEPTH) {
@@ -294,7 +294,7 @@ DEV void tile_run(const uint8_t *w0, const uint8_t *w1, int in_dim, const _Float
 #pragma unroll
                 for (int m = 0; m < NMAT; m++) ring[d][m].load((m ? rw1 : rw0) + (size_t)rb2 * 16 * rbytes, j2, kg);
             }
-            const _Float16 *bp = xs + ((j >> 1) & 1) * (TILE * BLD) + (j & 1) * KC + i * BLD + kg * 8;
+            const _Float16 *bp = xs + ((j >> 1) & 1) * (TBM * 16 * BLD) + (j & 1) * KC + i * BLD + kg * 8;
 #pragma unroll
             for (int s = 0; s < 4; s++) {
                 h8 a[NMAT];
@@ -302,26 +302,26 @@ DEV void tile_run(const uint8_t *w0, const uint8_t *w1, int in_dim, const _Float
                 for (int m = 0; m < NMAT; m++) a[m] = cur[m].frag(s);
                 /* B reads for every token block (rows past the tile hold
                  * zeros): straight-line LDS traffic the scheduler can hoist */
-                h8 b[TBMAX];
+                h8 b[TBM];
 #pragma unroll
-                for (int t = 0; t < TBMAX; t++) b[t] = *(const h8 *)(bp + t * 16 * BLD + s * 32);
+                for (int t = 0; t < TBM; t++) b[t] = *(const h8 *)(bp + t * 16 * BLD + s * 32);
 #pragma unroll
-                for (int t = 0; t < TBMAX; t++)
+                for (int t = 0; t < TBM; t++)
                     if (t < tb) {
 #pragma unroll
                         for (int m = 0; m < NMAT; m++) c[m][t] = mfma(a[m], b[t], c[m][t]);
                     }
             }
             if (j == nst - 1) {
-                epi(c, rbase + rb * 16 + 4 * kg, tb);
+                epi.template operator()<TBM>(c, rbase + rb * 16 + 4 * kg, tb);
 #pragma unroll
                 for (int m = 0; m < NMAT; m++)
 #pragma unroll
-                    for (int t = 0; t < TBMAX; t++) c[m][t] = f4v{0, 0, 0, 0};
+                    for (int t = 0; t < TBM; t++) c[m][t] = f4v{0, 0, 0, 0};
             }
             if (nch > 2 && (j & 1) && (j >> 1) + 2 < nch) {
                 __syncthreads();
-                ch.store<FMT>(xs + ((j >> 1) & 1) * (TILE * BLD), rows);
+                ch.template store<FMT>(xs + ((j >> 1) & 1) * (TBM * 16 * BLD), rows);
                 if ((j >> 1) + 3 < nch) ch.fetch(src, rowoff, ld, ((j >> 1) + 3) * KCH);
             } else if (nch > 2 && (j & 1) && (j >> 1) + 1 < nch) {
                 __syncthreads(); /* chunk c+1 was stored before the previous barrier */
@@ -346,10 +346,11 @@ struct GemmArgs {
 struct GuEpi {
     _Float16 *out;
     int out_ld, first, rows;
-    MDEV void operator()(const f4v (&c)[2][TBMAX], int r, int tb) const {
+    template <int TBM>
+    MDEV void operator()(const f4v (&c)[2][TBM], int r, int tb) const {
         const int i = threadIdx.x & 15;
 #pragma unroll
-        for (int t = 0; t < TBMAX; t++) {
+        for (int t = 0; t < TBM; t++) {
             const int tok = t * 16 + i;
             if (t >= tb || tok >= rows) continue;
             h4 v;
@@ -363,10 +364,11 @@ struct GuEpi {
 struct DnEpi {
     float *out;
     int out_ld, first, rows;
-    MDEV void operator()(const f4v (&c)[1][TBMAX], int r, int tb) const {
+    template <int TBM>
+    MDEV void operator()(const f4v (&c)[1][TBM], int r, int tb) const {
         const int i = threadIdx.x & 15;
 #pragma unroll
-        for (int t = 0; t < TBMAX; t++) {
+        for (int t = 0; t < TBM; t++) {
             const int tok = t * 16 + i;
             if (t >= tb || tok >= rows) continue;
             *(f4v *)(out + (size_t)(first + tok) * out_ld + r) = c[0][t];
@@ -384,54 +386,54 @@ struct DnEpi {
 #define GU_RPW 1
 #define DN_RPW 4
 
-template <int SFMT, int NST>
+template <int SFMT, int NST, int TBM>
 __global__ __launch_bounds__(WAVES * 64) void k_gemm_gate_up(GemmArgs a) {
-    __shared__ __attribute__((aligned(16))) _Float16 xs[2 * TILE * BLD];
-    __shared__ int rowoff[TILE];
+    __shared__ __attribute__((aligned(16))) _Float16 xs[2 * TBM * 16 * BLD];
+    __shared__ int rowoff[TBM * 16];
     const uint32_t nt = a.tiles[0];
     if (blockIdx.x >= nt) return;
     const uint32_t e = a.tiles[1 + 3 * blockIdx.x], first = a.tiles[2 + 3 * blockIdx.x],
                    rows = a.tiles[3 + 3 * blockIdx.x];
     const bool sh = e == (uint32_t)a.E;
     if (blockIdx.y * (WAVES * 16 * GU_RPW) >= (unsigned)(sh ? a.S : a.M)) return;
-    if (threadIdx.x < TILE) { /* rows past the tile repeat the first row */
+    if (threadIdx.x < TBM * 16) { /* rows past the tile repeat the first row */
         const uint32_t q = threadIdx.x < rows ? threadIdx.x : 0;
         rowoff[threadIdx.x] = sh ? (int)(first + q) : (int)(a.pairs[first + q] / (uint32_t)a.K);
     }
     __syncthreads();
     if (sh) {
         const GuEpi epi{a.act_sh, a.S, (int)first, (int)rows};
-        tile_run<SFMT, 2, GU_RPW, (SFMT == FQ8 ? 2 : GU_DEPTH), NST>(a.sh_a, a.sh_b, a.H, a.src, a.H, rowoff, (int)rows, xs, epi);
+        tile_run<SFMT, 2, GU_RPW, (SFMT == FQ8 ? 2 : GU_DEPTH), NST, TBM>(a.sh_a, a.sh_b, a.H, a.src, a.H, rowoff, (int)rows, xs, epi);
     } else {
         const GuEpi epi{a.act, a.M, (int)first, (int)rows};
-        tile_run<FQ4K, 2, GU_RPW, GU_DEPTH, NST>(a.wa + (size_t)e * a.stride_a, a.wb + (size_t)e * a.stride_b, a.H, a.src,
+        tile_run<FQ4K, 2, GU_RPW, GU_DEPTH, NST, TBM>(a.wa + (size_t)e * a.stride_a, a.wb + (size_t)e * a.stride_b, a.H, a.src,
                                   a.H, rowoff, (int)rows, xs, epi);
     }
 }
 
-template <int EFMT, int SFMT, int NST>
+template <int EFMT, int SFMT, int NST, int TBM>
 __global__ __launch_bounds__(WAVES * 64) void k_gemm_down(GemmArgs a) {
-    __shared__ __attribute__((aligned(16))) _Float16 xs[2 * TILE * BLD];
-    __shared__ int rowoff[TILE];
+    __shared__ __attribute__((aligned(16))) _Float16 xs[2 * TBM * 16 * BLD];
+    __shared__ int rowoff[TBM * 16];
     const uint32_t nt = a.tiles[0];
     if (blockIdx.x >= nt) return;
     const uint32_t e = a.tiles[1 + 3 * blockIdx.x], first = a.tiles[2 + 3 * blockIdx.x],
                    rows = a.tiles[3 + 3 * blockIdx.x];
     const bool sh = e == (uint32_t)a.E;
-    if (threadIdx.x < TILE) rowoff[threadIdx.x] = (int)(first + (threadIdx.x < rows ? threadIdx.x : 0));
+    if (threadIdx.x < TBM * 16) rowoff[threadIdx.x] = (int)(first + (threadIdx.x < rows ? threadIdx.x : 0));
     __syncthreads();
     if (sh) {
         const DnEpi epi{a.ysh, a.H, (int)first, (int)rows};
-        tile_run<SFMT, 1, DN_RPW, DN_DEPTH, NST>(a.sh_a, nullptr, a.S, a.src_sh, a.S, rowoff, (int)rows, xs, epi);
+        tile_run<SFMT, 1, DN_RPW, DN_DEPTH, NST, TBM>(a.sh_a, nullptr, a.S, a.src_sh, a.S, rowoff, (int)rows, xs, epi);
     } else {
         const DnEpi epi{a.y, a.H, (int)first, (int)rows};
-        tile_run<EFMT, 1, DN_RPW, DN_DEPTH, NST>(a.wa + (size_t)e * a.stride_a, nullptr, a.M, a.src, a.M, rowoff, (int)rows, xs, epi);
+        tile_run<EFMT, 1, DN_RPW, DN_DEPTH, NST, TBM>(a.wa + (size_t)e * a.stride_a, nullptr, a.M, a.src, a.M, rowoff, (int)rows, xs, epi);
     }
 }
 
 /* ------------------------------------------------------------ launch */
 int launch_gemm_gate_up(const ExpertSide &ex, const SharedSide &sh, const _Float16 *x16, int T, int H,
-                        int M, int K, int E, const uint32_t *tiles, int n_tiles_max,
+                        int M, int K, int E, int tile_m, const uint32_t *tiles, int n_tiles_max,
                         const uint32_t *pairs, _Float16 *act, _Float16 *act_sh, hipStream_t s) {
     const int NB = WAVES * 16 * GU_RPW;
     if ((H / KC * GU_RPW) % GU_DEPTH) return -2;
@@ -444,16 +446,23 @@ int launch_gemm_gate_up(const ExpertSide &ex, const SharedSide &sh, const _Float
     a.tiles = tiles; a.pairs = pairs; a.act = act; a.act_sh = act_sh;
     const dim3 grid(n_tiles_max, (M > a.S ? M : a.S) / NB), block(WAVES * 64);
     const bool q8 = sh.gate && sh.gate_fmt == FQ8;
+    if (tile_m != GEMM_TILE_SMALL && tile_m != GEMM_TILE_BIG) return -2;
     /* compile-time stage count for the common hidden size (Q4_K shared
      * expert); other shapes take the generic loop */
-    if (q8) hipLaunchKernelGGL((k_gemm_gate_up<FQ8, 0>), grid, block, 0, s, a);
-    else if (H == 2048) hipLaunchKernelGGL((k_gemm_gate_up<FQ4K, 16>), grid, block, 0, s, a);
-    else hipLaunchKernelGGL((k_gemm_gate_up<FQ4K, 0>), grid, block, 0, s, a);
+#define GU_LAUNCH(SF, NS)                                                                    \
+    do {                                                                                     \
+        if (tile_m == GEMM_TILE_SMALL) hipLaunchKernelGGL((k_gemm_gate_up<SF, NS, GEMM_TILE_SMALL / 16>), grid, block, 0, s, a); \
+        else hipLaunchKernelGGL((k_gemm_gate_up<SF, NS, GEMM_TILE_BIG / 16>), grid, block, 0, s, a);              \
+    } while (0)
+    if (q8) GU_LAUNCH(FQ8, 0);
+    else if (H == 2048) GU_LAUNCH(FQ4K, 16);
+    else GU_LAUNCH(FQ4K, 0);
+#undef GU_LAUNCH
     return hipGetLastError() == hipSuccess ? 0 : -3;
 }
 
 int launch_gemm_down(const ExpertSide &ex, const SharedSide &sh, const _Float16 *act,
-                     const _Float16 *act_sh, int T, int H, int M, int K, int E,
+                     const _Float16 *act_sh, int T, int H, int M, int K, int E, int tile_m,
                      const uint32_t *tiles, int n_tiles_max, float *y, float *ysh, hipStream_t s) {
     const int NB = WAVES * 16 * DN_RPW;
     if ((M / KC * DN_RPW) % DN_DEPTH || (sh.gate && (sh.S / KC * DN_RPW) % DN_DEPTH)) return -2;
@@ -469,7 +478,12 @@ int launch_gemm_down(const ExpertSide &ex, const SharedSide &sh, const _Float16 
     a.tiles = tiles; a.y = y; a.ysh = ysh;
     const dim3 grid(n_tiles_max, H / NB), block(WAVES * 64);
     /* generic unit loop (a compile-time stage count spills here) */
-#define DN_LAUNCH(EF, SF) hipLaunchKernelGGL((k_gemm_down<EF, SF, 0>), grid, block, 0, s, a)
+    if (tile_m != GEMM_TILE_SMALL && tile_m != GEMM_TILE_BIG) return -2;
+#define DN_LAUNCH(EF, SF)                                                                    \
+    do {                                                                                     \
+        if (tile_m == GEMM_TILE_SMALL) hipLaunchKernelGGL((k_gemm_down<EF, SF, 0, GEMM_TILE_SMALL / 16>), grid, block, 0, s, a); \
+        else hipLaunchKernelGGL((k_gemm_down<EF, SF, 0, GEMM_TILE_BIG / 16>), grid, block, 0, s, a);              \
+    } while (0)
     if (ex.down_fmt == FQ4K) {
         if (sf == FQ4K) DN_LAUNCH(FQ4K, FQ4K);
         else if (sf == FQ6K) DN_LAUNCH(FQ4K, FQ6K);

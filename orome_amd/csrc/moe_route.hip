@@ -155,8 +155,11 @@ __global__ __launch_bounds__(256) void k_topk(RouteArgs a) {
  *  2. scan:    one block: per expert an exclusive scan of cnt over blocks
  *              (in place) and the total; block scans of the totals give the
  *              offsets, active-expert ranks and GEMM tile offsets; then the
- *              active list and the tile list (expert, first row, rows), tiles
- *              of tile_m rows, the shared expert (id E) over tokens 0..T-1.
+ *              active list and two GEMM tile lists (expert, first row, rows):
+ *              experts with <= GEMM_TILE_SMALL rows get one small tile, the
+ *              others tiles of GEMM_TILE_BIG rows; the shared expert (id E)
+ *              covers tokens 0..T-1 in small tiles when the average expert
+ *              has <= GEMM_TILE_SMALL rows, else in big ones.
  *  3. scatter: per block, the same masks; a pair's rank is its expert's
  *              offset + the block's base + the popcount of the mask below
  *              its token. */
@@ -189,22 +192,36 @@ __global__ __launch_bounds__(DSP_TOK) void k_dispatch_count(RouteArgs a, uint32_
     }
 }
 
-/* Block-wide inclusive scan of three counters per expert (one thread per
+/* Block-wide inclusive scan of four counters per expert (one thread per
  * expert, E <= DSP_THREADS), Hillis-Steele over LDS. */
-DEV void block_scan3(uint32_t *a, uint32_t *b, uint32_t *c, int n) {
+DEV void block_scan4(uint32_t *a, uint32_t *b, uint32_t *c, uint32_t *d, int n) {
     const int tid = threadIdx.x;
     for (int off = 1; off < n; off <<= 1) {
-        uint32_t va = 0, vb = 0, vc = 0;
-        if (tid < n && tid >= off) { va = a[tid - off]; vb = b[tid - off]; vc = c[tid - off]; }
+        uint32_t va = 0, vb = 0, vc = 0, vd = 0;
+        if (tid < n && tid >= off) { va = a[tid - off]; vb = b[tid - off]; vc = c[tid - off]; vd = d[tid - off]; }
         __syncthreads();
-        if (tid < n && tid >= off) { a[tid] += va; b[tid] += vb; c[tid] += vc; }
+        if (tid < n && tid >= off) { a[tid] += va; b[tid] += vb; c[tid] += vc; d[tid] += vd; }
         __syncthreads();
     }
 }
 
+/* Tiles of one expert: rows <= GEMM_TILE_SMALL -> one small tile, else
+ * ceil(rows / GEMM_TILE_BIG) big tiles. */
+DEV uint32_t n_small_tiles(uint32_t c) { return c != 0 && c <= GEMM_TILE_SMALL; }
+DEV uint32_t n_big_tiles(uint32_t c) { return c > GEMM_TILE_SMALL ? (c + GEMM_TILE_BIG - 1) / GEMM_TILE_BIG : 0; }
+DEV void put_tiles(uint32_t *list, uint32_t t0, uint32_t e, uint32_t first, uint32_t c, uint32_t tm) {
+    for (uint32_t j = 0; j * tm < c; j++) {
+        list[1 + 3 * (t0 + j)] = e;
+        list[2 + 3 * (t0 + j)] = first + j * tm;
+        list[3 + 3 * (t0 + j)] = min(tm, c - j * tm);
+    }
+}
+
 __global__ __launch_bounds__(DSP_THREADS) void k_dispatch_scan(RouteArgs a, uint32_t *cnt, int G,
-                                                               uint32_t *tiles, int tile_m, int has_shared) {
-    __shared__ uint32_t hist[DSP_THREADS], offs[DSP_THREADS], arank[DSP_THREADS], toff[DSP_THREADS];
+                                                               uint32_t *tiles_s, uint32_t *tiles_b,
+                                                               int has_shared) {
+    __shared__ uint32_t hist[DSP_THREADS], offs[DSP_THREADS], arank[DSP_THREADS], ts[DSP_THREADS],
+        tbg[DSP_THREADS];
     const int E = a.E, T = a.T, tid = threadIdx.x;
     if (tid < E) {
         uint32_t run = 0;
@@ -216,10 +233,11 @@ __global__ __launch_bounds__(DSP_THREADS) void k_dispatch_scan(RouteArgs a, uint
         hist[tid] = run;
         offs[tid] = run;
         arank[tid] = run != 0;
-        toff[tid] = (run + tile_m - 1) / tile_m;
+        ts[tid] = n_small_tiles(run);
+        tbg[tid] = n_big_tiles(run);
     }
     __syncthreads();
-    block_scan3(offs, arank, toff, E);
+    block_scan4(offs, arank, ts, tbg, E);
     /* inclusive -> exclusive views: ex(x)[e] = x[e] - own */
     if (tid < E) {
         const uint32_t c = hist[tid];
@@ -229,29 +247,23 @@ __global__ __launch_bounds__(DSP_THREADS) void k_dispatch_scan(RouteArgs a, uint
             const uint32_t r = arank[tid] - 1;
             ACT_E(a.list, r) = (uint32_t)tid;
             ACT_OFF(a.list, E, r) = o;
-            const uint32_t nt = (c + tile_m - 1) / tile_m, t0 = toff[tid] - nt;
-            for (uint32_t j = 0; j < nt; j++) {
-                tiles[1 + 3 * (t0 + j)] = (uint32_t)tid;
-                tiles[2 + 3 * (t0 + j)] = o + j * tile_m;
-                tiles[3 + 3 * (t0 + j)] = min((uint32_t)tile_m, c - j * tile_m);
-            }
+            if (c <= GEMM_TILE_SMALL) put_tiles(tiles_s, ts[tid] - 1, (uint32_t)tid, o, c, GEMM_TILE_SMALL);
+            else put_tiles(tiles_b, tbg[tid] - n_big_tiles(c), (uint32_t)tid, o, c, GEMM_TILE_BIG);
         }
     }
     if (tid == 0) {
-        const uint32_t n_act = arank[E - 1], nt = toff[E - 1];
+        const uint32_t n_act = arank[E - 1], ns = ts[E - 1], nb = tbg[E - 1], Tu = (uint32_t)T;
         a.offsets[E] = offs[E - 1];
         ACT_N(a.list) = n_act;
         ACT_OFF(a.list, E, n_act) = offs[E - 1];
-        const uint32_t nsh = has_shared ? (uint32_t)((T + tile_m - 1) / tile_m) : 0;
-        tiles[0] = nt + nsh;
-    }
-    if (has_shared) {
-        const uint32_t nt = toff[E - 1];
-        for (int j = tid; j * tile_m < T; j += DSP_THREADS) {
-            tiles[1 + 3 * (nt + j)] = (uint32_t)E;
-            tiles[2 + 3 * (nt + j)] = (uint32_t)(j * tile_m);
-            tiles[3 + 3 * (nt + j)] = (uint32_t)min(tile_m, T - j * tile_m);
-        }
+        /* the shared expert (id E) over tokens 0..T-1, in the list that holds
+         * most of the routed work (a lone list of shared tiles would run as
+         * a tail after the other launch) */
+        const bool sm = (size_t)T * a.K <= (size_t)GEMM_TILE_SMALL * E;
+        const uint32_t tm = sm ? GEMM_TILE_SMALL : GEMM_TILE_BIG, nsh = has_shared ? (Tu + tm - 1) / tm : 0;
+        if (has_shared) put_tiles(sm ? tiles_s : tiles_b, sm ? ns : nb, (uint32_t)E, 0, Tu, tm);
+        tiles_s[0] = ns + (sm ? nsh : 0);
+        tiles_b[0] = nb + (sm ? 0 : nsh);
     }
 }
 
@@ -366,13 +378,13 @@ int launch_topk(const RouteArgs &a, hipStream_t s) {
 
 int dispatch_blocks(int T) { return (T + DSP_TOK - 1) / DSP_TOK; }
 
-int launch_dispatch(const RouteArgs &a, uint32_t *tiles, int tile_m, int has_shared, uint32_t *cnt,
+int launch_dispatch(const RouteArgs &a, uint32_t *tiles_s, uint32_t *tiles_b, int has_shared, uint32_t *cnt,
                     hipStream_t s) {
     const size_t lds = sizeof(uint32_t) * (size_t)a.E * DSP_WORDS * 2;
     if (lds > 64 * 1024 || a.E > DSP_THREADS || a.K > OROME_MAXK) return -2;
     const int G = dispatch_blocks(a.T);
     hipLaunchKernelGGL(k_dispatch_count, dim3(G), dim3(DSP_TOK), lds / 2, s, a, cnt);
-    hipLaunchKernelGGL(k_dispatch_scan, dim3(1), dim3(DSP_THREADS), 0, s, a, cnt, G, tiles, tile_m, has_shared);
+    hipLaunchKernelGGL(k_dispatch_scan, dim3(1), dim3(DSP_THREADS), 0, s, a, cnt, G, tiles_s, tiles_b, has_shared);
     hipLaunchKernelGGL(k_dispatch_scatter, dim3(G), dim3(DSP_TOK), lds, s, a, (const uint32_t *)cnt);
     return hipGetLastError() == hipSuccess ? 0 : -3;
 }
