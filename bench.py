@@ -61,11 +61,25 @@ def main():
     ap.add_argument("--config", default="0", choices=sorted(CONFIGS))
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="run only a plain device-to-device copy of MIB MiB (5 times), the known-size "
+                         "kernel that scales rocprofv3 FETCH_SIZE / WRITE_SIZE to bytes")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU only (the MoE path is single-GPU; "
               "expert-parallel sharding is design-only). Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
+
+    if args.copy_calibration:
+        import torch
+        n = args.copy_calibration << 20
+        src = torch.empty(n, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes_per_launch": n, "launches": 5}))
+        return
 
     import orome_amd
     from orome_amd import _lib
