@@ -24,6 +24,7 @@ typedef uint32_t u4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u2 __attribute__((ext_vector_type(2)));
 
 #define DEV static __device__ __forceinline__
+#define MDEV __device__ __forceinline__ /* member functions */
 
 DEV h2 as_h2(uint32_t v) { return __builtin_bit_cast(h2, v); }
 DEV uint32_t as_u32(h2 v) { return __builtin_bit_cast(uint32_t, v); }

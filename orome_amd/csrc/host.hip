@@ -324,10 +324,18 @@ extern "C" int orome_moe_forward(orome_hip_ctx *c, const ModelConfig *cfg, const
         if (!fold) TLAUNCH(c, ST_TOPK, launch_topk_dispatch_small(a, s), "top-k + dispatch");
         TLAUNCH(c, ST_GATE_UP, launch_gemv_gate_up(ex, sh, a, fold, x, T, H, M, K, E, c->act, c->act_sh, s),
                 "gemv gate/up");
-        TLAUNCH(c, ST_DOWN, launch_gemv_down(ex, sh, c->act, c->act_sh, T, H, M, K, E, c->list, c->y, c->ysh, s),
-                "gemv down");
-        TLAUNCH(c, ST_COMBINE, launch_combine(c->y, c->ysh, c->pos, c->w, c->sgl, S ? 1 : 0, h_in, h_out, T, H, K, s),
-                "combine");
+        /* one token: down and combine in one kernel when the shape allows */
+        const bool dc1 = T == 1 && K <= 8 && M == 512 && (!S || S == 512);
+        if (dc1) {
+            TLAUNCH(c, ST_DOWN, launch_gemv_down_combine1(ex, sh, a, c->act, c->act_sh, H, M, K, h_in, h_out, s),
+                    "gemv down + combine");
+        } else {
+            TLAUNCH(c, ST_DOWN, launch_gemv_down(ex, sh, c->act, c->act_sh, T, H, M, K, E, c->list, c->y, c->ysh, s),
+                    "gemv down");
+            TLAUNCH(c, ST_COMBINE,
+                    launch_combine(c->y, c->ysh, c->pos, c->w, c->sgl, S ? 1 : 0, h_in, h_out, T, H, K, s),
+                    "combine");
+        }
     } else {
         TLAUNCH(c, ST_ROUTE, launch_route_logits(a, s), "router logits");
         TLAUNCH(c, ST_TOPK, launch_topk(a, s), "top-k");

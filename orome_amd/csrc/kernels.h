@@ -62,6 +62,11 @@ int launch_gemv_down(const ExpertSide &ex, const SharedSide &sh, const _Float16 
                      const _Float16 *act_sh, int T, int H, int M, int K, int E, const uint32_t *list,
                      float *y, float *ysh, hipStream_t s);
 
+/* T = 1: down of all K routed slots and the shared slot, combined into h_out
+ * (K <= 8, M = S = 512); returns -2 when the shape is not covered */
+int launch_gemv_down_combine1(const ExpertSide &ex, const SharedSide &sh, const RouteArgs &ra,
+                              const _Float16 *act, const _Float16 *act_sh, int H, int M, int K,
+                              const float *h_in, float *h_out, hipStream_t s);
 int launch_delay(uint32_t usec, hipStream_t s);
 int launch_rmsnorm(const float *h, const float *w, int T, int H, float eps, float *x, hipStream_t s);
 int launch_dequant(int fmt, const uint8_t *src, uint32_t rows, uint32_t n, float *out32,

@@ -36,7 +36,6 @@ enum { FQ4K = 0, FQ6K = 2, FQ8 = 3 };
 
 typedef float f4v __attribute__((ext_vector_type(4)));
 
-#define MDEV __device__ __forceinline__ /* member functions */
 #define WAVES 8                         /* waves per block */
 #define KC 128                          /* k per stage (one A fragment set) */
 #define KCH 256                         /* k per LDS activation chunk */

@@ -239,7 +239,9 @@ DEV void gu_body(const GUArgs &a, const uint8_t *gbase, const uint8_t *ubase, in
                     (_Float16)(silu_f(red[(i * 2) * 16 + j]) * red[(i * 2 + 1) * 16 + j]);
 }
 
-#define GU_RPW 4
+#ifndef GU_RPW
+#define GU_RPW 2
+#endif
 /* Decode gate/up with the routing folded in: routed blocks select the
  * experts themselves from the router logits (block 0 publishes the routing
  * for the down kernel); shared-expert blocks start at once. */
@@ -397,6 +399,90 @@ __global__ __launch_bounds__(128) void k_gemv_down(DownArgs a) {
     }
 }
 
+/* One-token down + combine.  For T = 1 every routed expert holds one pair,
+ * so a block of 8 output rows can take all K routed slots and the shared
+ * slot itself and write h_out directly (k_combine's order: h_in + sum_k
+ * w_k y_k, then + sigmoid(s) y_shared), with no y round trip and one launch
+ * fewer.  Raw weight chunks of every slot are loaded before any is used, so
+ * all of a lane's loads are in flight together.  in_dim = 512: one chunk
+ * per lane (16 lanes per row). */
+#define DC_K 8
+template <int FMT>
+struct DnRaw;
+template <>
+struct DnRaw<FQ4K> {
+    Q4Raw r;
+    MDEV void load(const uint8_t *row, int c) { r = q4_load(row, c); }
+    MDEV float dot(int c, const _Float16 *x) const {
+        int klo;
+        q4_pos(c, klo);
+        h2 xl[8], xh[8];
+        load_h8(x + klo, xl);
+        load_h8(x + klo + 8, xl + 4);
+        load_h8(x + klo + 32, xh);
+        load_h8(x + klo + 40, xh + 4);
+        return q4_dot(r, c, xl, xh, hsum(xl, 8), hsum(xh, 8));
+    }
+};
+template <>
+struct DnRaw<FQ6K> {
+    Q6Raw r;
+    MDEV void load(const uint8_t *row, int c) { r = q6_load(row, c); }
+    MDEV float dot(int c, const _Float16 *x) const {
+        int k0;
+        q6_pos(c, k0);
+        h2 xv[16];
+#pragma unroll
+        for (int gq = 0; gq < 4; gq++) load_h8(x + k0 + 32 * gq, xv + 4 * gq);
+        return q6_dot(r, c, xv);
+    }
+};
+template <>
+struct DnRaw<FQ8> {
+    Q8Raw r;
+    MDEV void load(const uint8_t *row, int c) { r = q8_load(row, c); }
+    MDEV float dot(int c, const _Float16 *x) const {
+        h2 xv[16];
+#pragma unroll
+        for (int gq = 0; gq < 4; gq++) load_h8(x + c * 32 + 8 * gq, xv + 4 * gq);
+        return q8_dot(r, xv);
+    }
+};
+
+template <int EFMT, int SFMT>
+__global__ __launch_bounds__(128) void k_gemv_down_combine1(DownArgs a, RouteArgs ra, const float *h_in,
+                                                            float *h_out) {
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int cl = lane & 15, r = blockIdx.x * 8 + wv * 4 + (lane >> 4);
+    const int K = a.K;
+    const size_t rb = row_bytes(EFMT, a.M);
+    DnRaw<EFMT> raw[DC_K];
+    const _Float16 *xr[DC_K];
+#pragma unroll
+    for (int k = 0; k < DC_K; k++) {
+        const int kk = k < K ? k : K - 1;
+        const int e = ra.idx[kk];
+        raw[k].load(a.down + (size_t)e * a.down_stride + (size_t)r * rb, cl);
+        xr[k] = a.act + (size_t)ra.pos[kk] * a.M;
+    }
+    DnRaw<SFMT> rsh;
+    const bool has_sh = a.sh_down != nullptr;
+    if (has_sh) rsh.load(a.sh_down + (size_t)r * row_bytes(SFMT, a.S), cl);
+    float y[DC_K];
+#pragma unroll
+    for (int k = 0; k < DC_K; k++) y[k] = row_sum16(raw[k].dot(cl, xr[k]));
+    const float ysh = has_sh ? row_sum16(rsh.dot(cl, a.act_sh)) : 0.0f;
+    if (cl == 0) {
+        float moe = 0.0f;
+#pragma unroll
+        for (int k = 0; k < DC_K; k++)
+            if (k < K) moe += ra.w[k] * y[k];
+        float o = (h_in ? h_in[r] : 0.0f) + moe;
+        if (has_sh) o = o + sigmoid_f(ra.sgl[0]) * ysh;
+        h_out[r] = o;
+    }
+}
+
 /* ------------------------------------------------------------ launch */
 
 static int epl_of(int E) { return E <= 64 ? 1 : E <= 128 ? 2 : E <= 256 ? 4 : E <= 512 ? 8 : E <= 1024 ? 16 : 0; }
@@ -456,5 +542,30 @@ int launch_gemv_down(const ExpertSide &ex, const SharedSide &sh, const _Float16 
         case 4: hipLaunchKernelGGL(k_gemv_down<4>, grid, dim3(128), 0, s, a); break;
         default: hipLaunchKernelGGL(k_gemv_down<8>, grid, dim3(128), 0, s, a); break;
     }
+    return hipGetLastError() == hipSuccess ? 0 : -3;
+}
+
+int launch_gemv_down_combine1(const ExpertSide &ex, const SharedSide &sh, const RouteArgs &ra,
+                              const _Float16 *act, const _Float16 *act_sh, int H, int M, int K,
+                              const float *h_in, float *h_out, hipStream_t s) {
+    if (K < 1 || K > DC_K || H % 8 || M != 512 || (sh.gate && sh.S != 512)) return -2;
+    if (ex.down_fmt != FQ4K && ex.down_fmt != FQ6K) return -2;
+    const int sf = sh.gate ? sh.down_fmt : FQ4K;
+    if (sf != FQ4K && sf != FQ6K && sf != FQ8) return -2;
+    DownArgs a = {};
+    a.down = ex.down; a.down_stride = ex.down_stride; a.fmt = ex.down_fmt;
+    a.sh_down = sh.gate ? sh.down : nullptr; a.sh_fmt = sf; a.S = sh.gate ? sh.S : 0;
+    a.act = act; a.act_sh = act_sh; a.T = 1; a.H = H; a.M = M; a.K = K;
+#define DC_LAUNCH(EF, SF) hipLaunchKernelGGL((k_gemv_down_combine1<EF, SF>), dim3(H / 8), dim3(128), 0, s, a, ra, h_in, h_out)
+    if (ex.down_fmt == FQ4K) {
+        if (sf == FQ4K) DC_LAUNCH(FQ4K, FQ4K);
+        else if (sf == FQ6K) DC_LAUNCH(FQ4K, FQ6K);
+        else DC_LAUNCH(FQ4K, FQ8);
+    } else {
+        if (sf == FQ4K) DC_LAUNCH(FQ6K, FQ4K);
+        else if (sf == FQ6K) DC_LAUNCH(FQ6K, FQ6K);
+        else DC_LAUNCH(FQ6K, FQ8);
+    }
+#undef DC_LAUNCH
     return hipGetLastError() == hipSuccess ? 0 : -3;
 }

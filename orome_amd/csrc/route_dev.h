@@ -48,16 +48,22 @@ DEV uint64_t wave_max64(uint64_t m) {
 template <int EPL, bool COH = false>
 DEV void wave_topk(const float *l, const float *bias, int E, int K, int lane, int32_t *idx_out,
                    float *w_out, float *sgl_out, int *e_out) {
+    /* all loads first and unconditional (index clamped, then masked), so
+     * they are in flight together instead of one round trip each */
+    float v[EPL], bv[EPL];
+#pragma unroll
+    for (int j = 0; j < EPL; j++) {
+        const int e = min(lane + 64 * j, E - 1);
+        v[j] = COH ? ld_coh(l + e) : l[e];
+    }
+    if (bias)
+#pragma unroll
+        for (int j = 0; j < EPL; j++) bv[j] = bias[min(lane + 64 * j, E - 1)];
     uint64_t key[EPL];
 #pragma unroll
     for (int j = 0; j < EPL; j++) {
-        int e = lane + 64 * j;
-        key[j] = 0;
-        if (e < E) {
-            float v = COH ? ld_coh(l + e) : l[e];
-            if (bias) v = v + bias[e];
-            key[j] = route_key(v, e);
-        }
+        const int e = lane + 64 * j;
+        key[j] = e < E ? route_key(bias ? v[j] + bv[j] : v[j], e) : 0;
     }
     float vals[OROME_MAXK];
     int ids[OROME_MAXK];
@@ -95,53 +101,92 @@ DEV void wave_topk(const float *l, const float *bias, int E, int K, int lane, in
     }
 }
 
+/* Block-wide exclusive scan of one 32-bit value per thread (256 threads):
+ * wave inclusive scans by shuffles, then the four wave totals.  Returns the
+ * exclusive prefix; *total receives the block sum. */
+DEV uint32_t block_excl_scan256(uint32_t v, uint32_t *wsum /* LDS [4] */, uint32_t *total) {
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    uint32_t inc = v;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const uint32_t o = (uint32_t)__shfl_up((int)inc, off, 64);
+        if (lane >= off) inc += o;
+    }
+    if (lane == 63) wsum[wv] = inc;
+    __syncthreads();
+    uint32_t base = 0;
+    for (int w = 0; w < wv; w++) base += wsum[w];
+    *total = wsum[0] + wsum[1] + wsum[2] + wsum[3];
+    return base + inc - v;
+}
+
 /* Small-batch selection and dispatch (T*K <= 256) by one block of 256
  * threads: a wave per token for the top-k, then the stable counting sort of
- * the T*K pairs by ranking each pair against all others. */
+ * the T*K pairs by expert.  Each expert keeps an LDS membership mask over
+ * the pairs (8 words); its popcount is the expert's count, a block scan of
+ * the counts gives the offsets and the active-expert ranks, and a pair's
+ * rank inside its expert is the popcount of the mask below it. */
 template <int EPL, bool COH>
 DEV void topk_dispatch_block(const RouteArgs &a) {
-    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-    const int E = a.E, T = a.T, K = a.K;
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, tid = threadIdx.x;
+    const int E = a.E, T = a.T, K = a.K, NP = T * K;
     __shared__ int s_e[256];
-    __shared__ int s_head[256];
+    __shared__ uint32_t mask[64 * EPL * 8]; /* experts (< 64 EPL) x 8 words of pair bits */
+    __shared__ uint32_t eoff[64 * EPL];
+    __shared__ uint32_t wsum[4];
+    for (int i = tid; i < 64 * EPL * 8; i += 256) mask[i] = 0;
     for (int t = wv; t < T; t += 4)
         wave_topk<EPL, COH>(a.logits + (size_t)t * (E + 1), a.bias, E, K, lane, a.idx + t * K,
                             a.w + t * K, a.sgl + t, s_e + t * K);
     __syncthreads();
-    const int NP = T * K, p = threadIdx.x;
-    int e = 0, less = 0, before = 0;
-    if (p < NP) {
-        e = s_e[p];
-        for (int q = 0; q < NP; q++) {
-            int eq = s_e[q];
-            less += eq < e;
-            before += (q < p) & (eq == e);
-        }
-        uint32_t pos = (uint32_t)(less + before);
-        a.pairs[pos] = (uint32_t)p;
-        a.pos[p] = pos;
-        s_head[p] = before == 0;
-    }
+    if (tid < NP) atomicOr(&mask[s_e[tid] * 8 + (tid >> 5)], 1u << (tid & 31));
     __syncthreads();
-    if (p < NP && s_head[p]) {
-        int rank = 0;
-        for (int q = 0; q < NP; q++) rank += s_head[q] & (s_e[q] < e);
-        ACT_E(a.list, rank) = (uint32_t)e;
-        ACT_OFF(a.list, E, rank) = (uint32_t)less;
+    /* thread tid owns experts [tid*EPT, tid*EPT + EPT), EPT = EPL/4 (E <= 64 EPL) */
+    constexpr int EPT = EPL >= 4 ? EPL / 4 : 1;
+    uint32_t cnt[EPT], packed = 0;
+#pragma unroll
+    for (int j = 0; j < EPT; j++) {
+        const int e = tid * EPT + j;
+        uint32_t c = 0;
+        if (e < E)
+#pragma unroll
+            for (int w = 0; w < 8; w++) c += __popc(mask[e * 8 + w]);
+        cnt[j] = c;
+        packed += (c << 16) | (c != 0); /* count <= 256 in the high half, active count low */
     }
-    if (threadIdx.x == 0) {
-        int n = 0;
-        for (int q = 0; q < NP; q++) n += s_head[q];
-        ACT_N(a.list) = (uint32_t)n;
+    uint32_t total;
+    const uint32_t ex = block_excl_scan256(packed, wsum, &total);
+    uint32_t off = ex >> 16, rank = ex & 0xFFFFu;
+#pragma unroll
+    for (int j = 0; j < EPT; j++) {
+        const int e = tid * EPT + j;
+        if (e < E) {
+            eoff[e] = off;
+            a.offsets[e] = off;
+            if (cnt[j]) {
+                ACT_E(a.list, rank) = (uint32_t)e;
+                ACT_OFF(a.list, E, rank) = off;
+                rank++;
+            }
+            off += cnt[j];
+        }
+    }
+    if (tid == 0) {
+        const uint32_t n = total & 0xFFFFu;
+        a.offsets[E] = (uint32_t)NP;
+        ACT_N(a.list) = n;
         ACT_OFF(a.list, E, n) = (uint32_t)NP;
     }
-    for (int ee = threadIdx.x; ee <= E; ee += 256) {
-        int c = 0;
-        for (int q = 0; q < NP; q++) c += s_e[q] < ee;
-        a.offsets[ee] = (uint32_t)c;
+    __syncthreads();
+    if (tid < NP) {
+        const int e = s_e[tid], wd = tid >> 5;
+        uint32_t r = __popc(mask[e * 8 + wd] & ((1u << (tid & 31)) - 1u));
+        for (int w = 0; w < wd; w++) r += __popc(mask[e * 8 + w]);
+        const uint32_t pos = eoff[e] + r;
+        a.pairs[pos] = (uint32_t)tid;
+        a.pos[tid] = pos;
     }
 }
-
 
 /* Block-local routing for T*K <= 256 by one block of 256 threads: the
  * top-k of every token and the dispatch of its pairs, all in LDS.  With
