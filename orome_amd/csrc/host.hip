@@ -254,10 +254,13 @@ static int launch_rc(int rc, const char *what) {
         }                                                                                  \
     } while (0)
 
-extern "C" int orome_moe_forward(orome_hip_ctx *c, const ModelConfig *cfg, const ExpertLayerRef *elr,
-                                 const LayerTensorCache *lt, const float *x, const float *h_in,
-                                 float *h_out, int T, int K) {
-    if (!c || !cfg || !elr || !lt || !x || !h_out)
+/* The MoE block on x (or, with norm_h, on RMSNorm(norm_h) * bf16(norm_w),
+ * which the small-batch router computes itself and the large-batch path
+ * computes in a separate kernel first). */
+static int forward_impl(orome_hip_ctx *c, const ModelConfig *cfg, const ExpertLayerRef *elr,
+                        const LayerTensorCache *lt, const float *x, const float *h_in, float *h_out, int T,
+                        int K, const float *norm_h, const float *norm_w) {
+    if (!c || !cfg || !elr || !lt || !(x || norm_h) || !h_out)
         return orome_fail(OROME_EINVAL, "orome_moe_forward: NULL argument");
     const int H = cfg->hidden_dim, E = cfg->num_experts, M = cfg->moe_intermediate;
     if (H != c->cfg.hidden_dim || E != c->cfg.num_experts || M != c->cfg.moe_intermediate ||
@@ -311,10 +314,21 @@ extern "C" int orome_moe_forward(orome_hip_ctx *c, const ModelConfig *cfg, const
     a.logits = c->logits; a.idx = c->idx; a.w = c->w; a.sgl = c->sgl;
     a.offsets = c->offsets; a.pairs = c->pairs; a.pos = c->pos; a.list = c->list;
     a.counter = c->counter;
+    a.norm_h = NULL; a.norm_w = NULL; a.norm_eps = cfg->rms_norm_eps; a.xnorm = c->xnorm;
 
     int path = c->path;
     if (path == OROME_PATH_AUTO) path = T <= 8 ? OROME_PATH_GEMV : OROME_PATH_MFMA;
     hipStream_t s = c->stream;
+    if (norm_h) {
+        if (path == OROME_PATH_GEMV) { /* the router kernel normalises and writes xnorm */
+            a.norm_h = norm_h;
+            a.norm_w = norm_w;
+        } else {
+            TLAUNCH(c, ST_NORM, launch_rmsnorm(norm_h, norm_w, T, H, cfg->rms_norm_eps, c->xnorm, s), "rmsnorm");
+        }
+        x = c->xnorm;
+        a.x = x;
+    }
     if (path == OROME_PATH_GEMV) {
         if (T > 8) return orome_fail(OROME_EUNSUPPORTED, "GEMV path handles T <= 8 (T=%d)", T);
         TLAUNCH(c, ST_ROUTE, launch_route_small(a, s), "router logits");
@@ -382,6 +396,13 @@ extern "C" int orome_moe_forward(orome_hip_ctx *c, const ModelConfig *cfg, const
     return OROME_OK;
 }
 
+extern "C" int orome_moe_forward(orome_hip_ctx *c, const ModelConfig *cfg, const ExpertLayerRef *elr,
+                                 const LayerTensorCache *lt, const float *x, const float *h_in,
+                                 float *h_out, int T, int K) {
+    if (!x) return orome_fail(OROME_EINVAL, "orome_moe_forward: NULL argument");
+    return forward_impl(c, cfg, elr, lt, x, h_in, h_out, T, K, NULL, NULL);
+}
+
 extern "C" int orome_moe_layer_forward(orome_hip_ctx *c, const ModelConfig *cfg,
                                        const ExpertLayerRef *elr, const LayerTensorCache *lt,
                                        float *h, int T, int K) {
@@ -391,8 +412,7 @@ extern "C" int orome_moe_layer_forward(orome_hip_ctx *c, const ModelConfig *cfg,
     const float *nw = lt->post_norm.buffer && lt->post_norm.format == QFMT_F32
                           ? (const float *)dev_addr(lt->post_norm.buffer, lt->post_norm.offset)
                           : NULL;
-    TLAUNCH(c, ST_NORM, launch_rmsnorm(h, nw, T, cfg->hidden_dim, cfg->rms_norm_eps, c->xnorm, c->stream), "rmsnorm");
-    return orome_moe_forward(c, cfg, elr, lt, c->xnorm, h, h, T, K);
+    return forward_impl(c, cfg, elr, lt, NULL, h, h, T, K, h, nw);
 }
 
 extern "C" int orome_moe_stack_forward(orome_hip_ctx *c, const ModelConfig *cfg,

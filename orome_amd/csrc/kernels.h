@@ -29,6 +29,12 @@ struct RouteArgs {
     uint32_t *pos;       /* [T*K] sorted position of pair p */
     uint32_t *list;      /* active list, 2E+2 entries */
     uint32_t *counter;   /* one zeroed word, returned to zero by the kernel */
+    /* fused RMSNorm (small-batch router only): when norm_h is set, x is
+     * RMSNorm(norm_h) * bf16(norm_w) computed in the router kernel, which
+     * also writes it to xnorm for the later kernels */
+    const float *norm_h, *norm_w;
+    float norm_eps;
+    float *xnorm;
 };
 
 struct ExpertSide {

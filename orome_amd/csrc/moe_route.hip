@@ -51,8 +51,64 @@ DEV void canon_dots(const float *wrow, const float *x, int T, int H, int lane, f
     }
 }
 
+/* As canon_dots, with x = RMSNorm(h) computed in place (RMSNorm of
+ * inference/src/shaders.metal:128-149, the same arithmetic and canonical sum
+ * of squares as k_rmsnorm, so x is bit-identical to that kernel's output);
+ * write_x stores x for the later kernels. */
+template <int TMAX>
+DEV void canon_dots_norm(const float *wrow, const RouteArgs &a, int lane, bool write_x, float *acc) {
+    const int NI = a.H / 256, H = a.H, T = a.T;
+    f4 wv[CANON_NI], nw[CANON_NI];
+#pragma unroll
+    for (int i = 0; i < CANON_NI; i++)
+        if (i < NI) {
+            wv[i] = wrow ? *(const f4 *)(wrow + 256 * i + 4 * lane) : f4{0, 0, 0, 0};
+            const f4 w = a.norm_w ? *(const f4 *)(a.norm_w + 256 * i + 4 * lane) : f4{1, 1, 1, 1};
+            nw[i] = f4{__builtin_bit_cast(float, __builtin_bit_cast(uint32_t, w.x) & 0xFFFF0000u),
+                       __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, w.y) & 0xFFFF0000u),
+                       __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, w.z) & 0xFFFF0000u),
+                       __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, w.w) & 0xFFFF0000u)};
+        }
+#pragma unroll
+    for (int t = 0; t < TMAX; t++) {
+        acc[t] = 0.0f;
+        if (t < T) {
+            f4 hv[CANON_NI];
+#pragma unroll
+            for (int i = 0; i < CANON_NI; i++)
+                if (i < NI) hv[i] = *(const f4 *)(a.norm_h + (size_t)t * H + 256 * i + 4 * lane);
+            float ss = 0.0f;
+#pragma unroll
+            for (int i = 0; i < CANON_NI; i++)
+                if (i < NI) {
+                    ss = __builtin_fmaf(hv[i].x, hv[i].x, ss);
+                    ss = __builtin_fmaf(hv[i].y, hv[i].y, ss);
+                    ss = __builtin_fmaf(hv[i].z, hv[i].z, ss);
+                    ss = __builtin_fmaf(hv[i].w, hv[i].w, ss);
+                }
+            ss = wave_sum_canon(ss);
+            const float scale = 1.0f / sqrtf(ss / (float)H + a.norm_eps);
+            float d = 0.0f;
+#pragma unroll
+            for (int i = 0; i < CANON_NI; i++)
+                if (i < NI) {
+                    const f4 x = {(hv[i].x * scale) * nw[i].x, (hv[i].y * scale) * nw[i].y,
+                                  (hv[i].z * scale) * nw[i].z, (hv[i].w * scale) * nw[i].w};
+                    if (write_x) *(f4 *)(a.xnorm + (size_t)t * H + 256 * i + 4 * lane) = x;
+                    d = __builtin_fmaf(wv[i].x, x.x, d);
+                    d = __builtin_fmaf(wv[i].y, x.y, d);
+                    d = __builtin_fmaf(wv[i].z, x.z, d);
+                    d = __builtin_fmaf(wv[i].w, x.w, d);
+                }
+            acc[t] = wave_sum_canon(d);
+        }
+    }
+}
+
 /* Small-batch router logits (T <= 16): every wave computes one router row
- * (or the shared-gate row) for all tokens. */
+ * (or the shared-gate row) for all tokens; with NORM, x is RMSNorm(norm_h)
+ * and the row-0 wave also writes it out. */
+template <bool NORM>
 __global__ __launch_bounds__(256) void k_route_small(RouteArgs a) {
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int row = blockIdx.x * 4 + wv;
@@ -60,7 +116,9 @@ __global__ __launch_bounds__(256) void k_route_small(RouteArgs a) {
     if (row > E) return;
     const float *wr = row < E ? a.W + (size_t)row * H : a.wsg;
     float acc[16];
-    if (wr) {
+    if (NORM) {
+        canon_dots_norm<16>(wr, a, lane, row == 0, acc);
+    } else if (wr) {
         canon_dots<16>(wr, a.x, T, H, lane, acc);
     } else {
 #pragma unroll
@@ -353,7 +411,8 @@ static int epl_for(int E) {
 
 int launch_route_small(const RouteArgs &a, hipStream_t s) {
     if (a.T < 1 || a.T > 16 || a.T * a.K > 256 || a.H % 256 || a.H > 4096) return -2;
-    hipLaunchKernelGGL(k_route_small, dim3((a.E + 1 + 3) / 4), dim3(256), 0, s, a);
+    if (a.norm_h) hipLaunchKernelGGL(k_route_small<true>, dim3((a.E + 1 + 3) / 4), dim3(256), 0, s, a);
+    else hipLaunchKernelGGL(k_route_small<false>, dim3((a.E + 1 + 3) / 4), dim3(256), 0, s, a);
     return hipGetLastError() == hipSuccess ? 0 : -3;
 }
 
