@@ -106,8 +106,9 @@ extern "C" orome_hip_ctx *orome_hip_create(const ModelConfig *cfg, int max_token
         {(void **)&c->counter, 256},            {(void **)&c->tiles, (1 + 3 * ntile_s) * 4},
         {(void **)&c->tiles_b, (1 + 3 * ntile_b) * 4},
         {(void **)&c->dcount, (size_t)dispatch_blocks((int)T) * E * 4},
-        {(void **)&c->x16, T * H * 2},          {(void **)&c->act, T * K * M * 2},
-        {(void **)&c->act_sh, T * (S ? S : 1) * 2}, {(void **)&c->y, T * K * H * 4},
+        /* one extra all-zero row each (index tmax, tmax*kmax, tmax) */
+        {(void **)&c->x16, (T + 1) * H * 2},    {(void **)&c->act, (T * K + 1) * M * 2},
+        {(void **)&c->act_sh, (T + 1) * (S ? S : 1) * 2}, {(void **)&c->y, T * K * H * 4},
         {(void **)&c->ysh, T * H * 4},          {(void **)&c->xnorm, T * H * 4},
     };
     size_t total = 0;
@@ -361,16 +362,16 @@ static int forward_impl(orome_hip_ctx *c, const ModelConfig *cfg, const ExpertLa
                   nb_max = (T * K) / GEMM_TILE_BIG + E + (S && !sh_small ? (T + GEMM_TILE_BIG - 1) / GEMM_TILE_BIG : 0);
         auto gate_up = [&](int tm, hipStream_t st) {
             return tm == GEMM_TILE_SMALL
-                       ? launch_gemm_gate_up(ex, sh, c->x16, T, H, M, K, E, tm, c->tiles, ns_max, c->pairs, c->act,
+                       ? launch_gemm_gate_up(ex, sh, c->x16, c->tmax, T, H, M, K, E, tm, c->tiles, ns_max, c->pairs, c->act,
                                              c->act_sh, st)
-                       : launch_gemm_gate_up(ex, sh, c->x16, T, H, M, K, E, tm, c->tiles_b, nb_max, c->pairs, c->act,
+                       : launch_gemm_gate_up(ex, sh, c->x16, c->tmax, T, H, M, K, E, tm, c->tiles_b, nb_max, c->pairs, c->act,
                                              c->act_sh, st);
         };
         auto down = [&](int tm, hipStream_t st) {
             return tm == GEMM_TILE_SMALL
-                       ? launch_gemm_down(ex, sh, c->act, c->act_sh, T, H, M, K, E, tm, c->tiles, ns_max, c->y,
+                       ? launch_gemm_down(ex, sh, c->act, c->act_sh, c->tmax * c->kmax, c->tmax, T, H, M, K, E, tm, c->tiles, ns_max, c->y,
                                           c->ysh, st)
-                       : launch_gemm_down(ex, sh, c->act, c->act_sh, T, H, M, K, E, tm, c->tiles_b, nb_max, c->y,
+                       : launch_gemm_down(ex, sh, c->act, c->act_sh, c->tmax * c->kmax, c->tmax, T, H, M, K, E, tm, c->tiles_b, nb_max, c->y,
                                           c->ysh, st);
         };
         if (c->timing) { /* per-stage timing: both lists in order on one stream */

@@ -78,13 +78,15 @@ int launch_rmsnorm(const float *h, const float *w, int T, int H, float eps, floa
 int launch_dequant(int fmt, const uint8_t *src, uint32_t rows, uint32_t n, float *out32,
                    _Float16 *out16, hipStream_t s);
 
-/* prefill (MFMA) path */
+/* prefill (MFMA) path; x16 is written (0,2,1,3) within each 4-group */
 int launch_to_f16(const float *x, int T, int H, _Float16 *x16, hipStream_t s);
-int launch_gemm_gate_up(const ExpertSide &ex, const SharedSide &sh, const _Float16 *x16, int T,
+/* x16, act and act_sh rows are stored (0,2,1,3) within each 4-group; zrow /
+ * zrow_sh name an all-zero row of the activation source(s) */
+int launch_gemm_gate_up(const ExpertSide &ex, const SharedSide &sh, const _Float16 *x16, int zrow, int T,
                         int H, int M, int K, int E, int tile_m, const uint32_t *tiles, int n_tiles_max,
                         const uint32_t *pairs, _Float16 *act, _Float16 *act_sh, hipStream_t s);
 int launch_gemm_down(const ExpertSide &ex, const SharedSide &sh, const _Float16 *act,
-                     const _Float16 *act_sh, int T, int H, int M, int K, int E, int tile_m,
+                     const _Float16 *act_sh, int zrow, int zrow_sh, int T, int H, int M, int K, int E, int tile_m,
                      const uint32_t *tiles, int n_tiles_max, float *y, float *ysh,
                      hipStream_t s);
 int launch_combine(const float *y, const float *ysh, const uint32_t *pos, const float *w,

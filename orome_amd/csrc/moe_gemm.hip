@@ -49,11 +49,28 @@ DEV h2 splat(_Float16 v) { return h2{v, v}; }
 DEV h2 hfma(h2 a, h2 b, h2 c) { return __builtin_elementwise_fma(a, b, c); }
 DEV h2 or_bias(uint32_t v) { return as_h2(v | 0x64006400u); }
 DEV h8 cat4(h2 a, h2 b, h2 c, h2 d) { return h8{a.x, a.y, b.x, b.y, c.x, c.y, d.x, d.y}; }
+/* exact fp16 pairs (q0, q2) and (q1, q3) of four 6-bit (minus 32) or int8
+ * quants: the (0,2,1,3) order every activation row is stored in */
+DEV void q6_h2_0213(uint32_t ql, uint32_t qh, int shift, int qshift, h2 &p02, h2 &p13) {
+    const uint32_t v = ((ql >> shift) & 0x0F0F0F0Fu) | (((qh >> qshift) & 0x03030303u) << 4);
+    const h2 bias = {(_Float16)1056.0f, (_Float16)1056.0f};
+    p02 = as_h2(__builtin_amdgcn_perm(0x64646464u, v, 0x04020400u)) - bias;
+    p13 = as_h2(__builtin_amdgcn_perm(0x64646464u, v, 0x04030401u)) - bias;
+}
+DEV void q8_h2_0213(uint32_t w, h2 &p02, h2 &p13) {
+    const uint32_t v = w ^ 0x80808080u;
+    const h2 bias = {(_Float16)1152.0f, (_Float16)1152.0f};
+    p02 = as_h2(__builtin_amdgcn_perm(0x64646464u, v, 0x04020400u)) - bias;
+    p13 = as_h2(__builtin_amdgcn_perm(0x64646464u, v, 0x04030401u)) - bias;
+}
 
 /* ------------------------------------------------- k order in LDS */
 /* Position (halves) inside a stage row of the 4 k values [4c, 4c+4), i.e. of
  * fragment (s, kg) elements j0..j0+3.  Mirrors the lane -> k mapping of each
- * Span below; Q4_K groups are additionally stored in (0,2,1,3) order. */
+ * Span below.  Activation rows (x16, act, act_sh) are kept in global memory
+ * with every 4-group stored (0,2,1,3) -- the order the Q4_K nibble split
+ * yields; the Q6_K and Q8_0 spans produce the same order -- so a 4-group is
+ * copied into LDS unchanged. */
 template <int FMT>
 DEV int frag_pos(int c) {
     if (FMT == FQ4K) { /* lane kg, step s: k = 64(kg>>1) + 16(kg&1) + 4s (+32 high nibbles) */
@@ -146,12 +163,13 @@ struct Span<FQ6K> {
         scl = splat((_Float16)(float)(int8_t)((sc8.x >> (8 * b)) & 0xFF));
         sch = splat((_Float16)(float)(int8_t)((sc8.y >> (8 * b)) & 0xFF));
     }
+    /* k order of the result: l, l+2, l+1, l+3, then the same 64 further */
     MDEV h8 frag(int s) const {
         const uint32_t a = u4_at(ql, s), b = u4_at(qh, s);
-        h2 p01, p23, r01, r23;
-        q6_h2(a, b, 0, odd2, p01, p23);
-        q6_h2(a, b, 4, 4 + odd2, r01, r23);
-        return cat4((p01 * scl) * d, (p23 * scl) * d, (r01 * sch) * d, (r23 * sch) * d);
+        h2 p02, p13, r02, r13;
+        q6_h2_0213(a, b, 0, odd2, p02, p13);
+        q6_h2_0213(a, b, 4, 4 + odd2, r02, r13);
+        return cat4((p02 * scl) * d, (p13 * scl) * d, (r02 * sch) * d, (r13 * sch) * d);
     }
 };
 
@@ -171,10 +189,10 @@ struct Span<FQ8> {
     MDEV void prepare(int, int) {}
     MDEV h8 frag(int s) const {
         const h2 d = splat(__builtin_bit_cast(_Float16, (uint16_t)(dd[s] & 0xFFFFu)));
-        h2 p01, p23, p45, p67;
-        q8_h2(qv[s].x, p01, p23);
-        q8_h2(qv[s].y, p45, p67);
-        return cat4(p01 * d, p23 * d, p45 * d, p67 * d);
+        h2 p02, p13, p46, p57; /* k order l, l+2, l+1, l+3, l+4, l+6, l+5, l+7 */
+        q8_h2_0213(qv[s].x, p02, p13);
+        q8_h2_0213(qv[s].y, p46, p57);
+        return cat4(p02 * d, p13 * d, p46 * d, p57 * d);
     }
 };
 
@@ -185,9 +203,9 @@ DEV f4v mfma(h8 a, h8 b, f4v c) { return __builtin_amdgcn_mfma_f32_16x16x32_f16(
  * halves (132 dwords: 16 rows x 16 bytes per lane group hit distinct banks),
  * each 128-k half in the fragment order of FMT.  A thread's vector n covers
  * token 16n + tid/32, k 8 (tid%32) .. +7.  Every thread loads and stores all
- * TBM vectors (rows past the tile read a valid row and are zeroed by a
- * select): the loads stay straight-line code, so the compiler's wait counts
- * for the weight prefetch ring stay exact. */
+ * TBM vectors: rows past the tile read an all-zero row, so the code stays
+ * straight-line (exact wait counts for the weight ring) and needs no
+ * select. */
 template <int TBM>
 struct Chunk {
     u4 v[TBM];
@@ -197,24 +215,15 @@ struct Chunk {
         for (int n = 0; n < TBM; n++)
             v[n] = ld_u4((const uint8_t *)(src + (size_t)rowoff[16 * n + (threadIdx.x >> 5)] * ld + k0 + cc));
     }
-    /* the zero select for rows past the tile happens here, not at the load,
-     * so nothing waits on the fetch before the chunk is due */
     template <int FMT>
-    MDEV void store(_Float16 *xs, int rows) const {
+    MDEV void store(_Float16 *xs) const {
         const int col = threadIdx.x & 31, half = col >> 4, c0 = (col & 15) * 2;
         const int p0 = half * KC + frag_pos<FMT>(c0), p1 = half * KC + frag_pos<FMT>(c0 + 1);
 #pragma unroll
         for (int n = 0; n < TBM; n++) {
-            const int t = 16 * n + (threadIdx.x >> 5);
-            _Float16 *row = xs + t * BLD;
-            const u4 x = t < rows ? v[n] : u4{0, 0, 0, 0};
-            u2 g0 = {x.x, x.y}, g1 = {x.z, x.w};
-            if (FMT == FQ4K) { /* (x0,x1),(x2,x3) -> (x0,x2),(x1,x3) */
-                g0 = u2{__builtin_amdgcn_perm(g0.y, g0.x, 0x05040100u), __builtin_amdgcn_perm(g0.y, g0.x, 0x07060302u)};
-                g1 = u2{__builtin_amdgcn_perm(g1.y, g1.x, 0x05040100u), __builtin_amdgcn_perm(g1.y, g1.x, 0x07060302u)};
-            }
-            *(u2 *)(row + p0) = g0;
-            *(u2 *)(row + p1) = g1;
+            _Float16 *row = xs + (16 * n + (threadIdx.x >> 5)) * BLD;
+            *(u2 *)(row + p0) = u2{v[n].x, v[n].y};
+            *(u2 *)(row + p1) = u2{v[n].z, v[n].w};
         }
     }
 };
@@ -257,10 +266,10 @@ DEV void tile_run(const uint8_t *w0, const uint8_t *w1, int in_dim, const _Float
 
     Chunk<TBM> ch;
     ch.fetch(src, rowoff, ld, 0);
-    ch.template store<FMT>(xs, rows);
+    ch.template store<FMT>(xs);
     if (nch > 1) {
         ch.fetch(src, rowoff, ld, KCH);
-        ch.template store<FMT>(xs + TBM * 16 * BLD, rows);
+        ch.template store<FMT>(xs + TBM * 16 * BLD);
     }
     if (nch > 2) ch.fetch(src, rowoff, ld, 2 * KCH);
     __syncthreads();
@@ -304,12 +313,13 @@ DEV void tile_run(const uint8_t *w0, const uint8_t *w1, int in_dim, const _Float
                 h8 b[TBM];
 #pragma unroll
                 for (int t = 0; t < TBM; t++) b[t] = *(const h8 *)(bp + t * 16 * BLD + s * 32);
+                /* every token block, also past the tile (zero rows): no
+                 * branches between the matrix instructions, so the scheduler
+                 * can interleave them with the next step's dequant */
 #pragma unroll
                 for (int t = 0; t < TBM; t++)
-                    if (t < tb) {
 #pragma unroll
-                        for (int m = 0; m < NMAT; m++) c[m][t] = mfma(a[m], b[t], c[m][t]);
-                    }
+                    for (int m = 0; m < NMAT; m++) c[m][t] = mfma(a[m], b[t], c[m][t]);
             }
             if (j == nst - 1) {
                 epi.template operator()<TBM>(c, rbase + rb * 16 + 4 * kg, tb);
@@ -320,7 +330,7 @@ DEV void tile_run(const uint8_t *w0, const uint8_t *w1, int in_dim, const _Float
             }
             if (nch > 2 && (j & 1) && (j >> 1) + 2 < nch) {
                 __syncthreads();
-                ch.template store<FMT>(xs + ((j >> 1) & 1) * (TBM * 16 * BLD), rows);
+                ch.template store<FMT>(xs + ((j >> 1) & 1) * (TBM * 16 * BLD));
                 if ((j >> 1) + 3 < nch) ch.fetch(src, rowoff, ld, ((j >> 1) + 3) * KCH);
             } else if (nch > 2 && (j & 1) && (j >> 1) + 1 < nch) {
                 __syncthreads(); /* chunk c+1 was stored before the previous barrier */
@@ -336,6 +346,7 @@ struct GemmArgs {
     const _Float16 *src;      /* x16 [T][H] (gate/up) or act [pairs][M] (down) */
     const _Float16 *src_sh;   /* down: act_sh [T][S] */
     int T, H, M, S, K, E;
+    int zrow, zrow_sh;        /* all-zero rows of src / src_sh (rows past a tile read them) */
     const uint32_t *tiles, *pairs;
     _Float16 *act, *act_sh;   /* gate/up outputs */
     float *y, *ysh;           /* down outputs */
@@ -352,9 +363,9 @@ struct GuEpi {
         for (int t = 0; t < TBM; t++) {
             const int tok = t * 16 + i;
             if (t >= tb || tok >= rows) continue;
-            h4 v;
+            h4 v; /* act rows are stored (0,2,1,3) within each 4-group */
 #pragma unroll
-            for (int q = 0; q < 4; q++) v[q] = (_Float16)(silu_f(c[0][t][q]) * c[1][t][q]);
+            for (int q = 0; q < 4; q++) v[(q & 1) * 2 + (q >> 1)] = (_Float16)(silu_f(c[0][t][q]) * c[1][t][q]);
             *(h4 *)(out + (size_t)(first + tok) * out_ld + r) = v;
         }
     }
@@ -395,9 +406,9 @@ __global__ __launch_bounds__(WAVES * 64) void k_gemm_gate_up(GemmArgs a) {
                    rows = a.tiles[3 + 3 * blockIdx.x];
     const bool sh = e == (uint32_t)a.E;
     if (blockIdx.y * (WAVES * 16 * GU_RPW) >= (unsigned)(sh ? a.S : a.M)) return;
-    if (threadIdx.x < TBM * 16) { /* rows past the tile repeat the first row */
-        const uint32_t q = threadIdx.x < rows ? threadIdx.x : 0;
-        rowoff[threadIdx.x] = sh ? (int)(first + q) : (int)(a.pairs[first + q] / (uint32_t)a.K);
+    if (threadIdx.x < TBM * 16) { /* rows past the tile read the zero row */
+        const uint32_t q = threadIdx.x;
+        rowoff[threadIdx.x] = q >= rows ? a.zrow : sh ? (int)(first + q) : (int)(a.pairs[first + q] / (uint32_t)a.K);
     }
     __syncthreads();
     if (sh) {
@@ -419,7 +430,8 @@ __global__ __launch_bounds__(WAVES * 64) void k_gemm_down(GemmArgs a) {
     const uint32_t e = a.tiles[1 + 3 * blockIdx.x], first = a.tiles[2 + 3 * blockIdx.x],
                    rows = a.tiles[3 + 3 * blockIdx.x];
     const bool sh = e == (uint32_t)a.E;
-    if (threadIdx.x < TBM * 16) rowoff[threadIdx.x] = (int)(first + (threadIdx.x < rows ? threadIdx.x : 0));
+    if (threadIdx.x < TBM * 16)
+        rowoff[threadIdx.x] = threadIdx.x < rows ? (int)(first + threadIdx.x) : (sh ? a.zrow_sh : a.zrow);
     __syncthreads();
     if (sh) {
         const DnEpi epi{a.ysh, a.H, (int)first, (int)rows};
@@ -431,8 +443,8 @@ __global__ __launch_bounds__(WAVES * 64) void k_gemm_down(GemmArgs a) {
 }
 
 /* ------------------------------------------------------------ launch */
-int launch_gemm_gate_up(const ExpertSide &ex, const SharedSide &sh, const _Float16 *x16, int T, int H,
-                        int M, int K, int E, int tile_m, const uint32_t *tiles, int n_tiles_max,
+int launch_gemm_gate_up(const ExpertSide &ex, const SharedSide &sh, const _Float16 *x16, int zrow, int T,
+                        int H, int M, int K, int E, int tile_m, const uint32_t *tiles, int n_tiles_max,
                         const uint32_t *pairs, _Float16 *act, _Float16 *act_sh, hipStream_t s) {
     const int NB = WAVES * 16 * GU_RPW;
     if ((H / KC * GU_RPW) % GU_DEPTH) return -2;
@@ -442,6 +454,7 @@ int launch_gemm_gate_up(const ExpertSide &ex, const SharedSide &sh, const _Float
     a.wa = ex.gate; a.wb = ex.up; a.stride_a = ex.gate_stride; a.stride_b = ex.up_stride;
     a.sh_a = sh.gate; a.sh_b = sh.up;
     a.src = x16; a.T = T; a.H = H; a.M = M; a.S = sh.gate ? sh.S : 0; a.K = K; a.E = E;
+    a.zrow = zrow; a.zrow_sh = zrow;
     a.tiles = tiles; a.pairs = pairs; a.act = act; a.act_sh = act_sh;
     const dim3 grid(n_tiles_max, (M > a.S ? M : a.S) / NB), block(WAVES * 64);
     const bool q8 = sh.gate && sh.gate_fmt == FQ8;
@@ -461,7 +474,7 @@ int launch_gemm_gate_up(const ExpertSide &ex, const SharedSide &sh, const _Float
 }
 
 int launch_gemm_down(const ExpertSide &ex, const SharedSide &sh, const _Float16 *act,
-                     const _Float16 *act_sh, int T, int H, int M, int K, int E, int tile_m,
+                     const _Float16 *act_sh, int zrow, int zrow_sh, int T, int H, int M, int K, int E, int tile_m,
                      const uint32_t *tiles, int n_tiles_max, float *y, float *ysh, hipStream_t s) {
     const int NB = WAVES * 16 * DN_RPW;
     if ((M / KC * DN_RPW) % DN_DEPTH || (sh.gate && (sh.S / KC * DN_RPW) % DN_DEPTH)) return -2;
@@ -474,6 +487,7 @@ int launch_gemm_down(const ExpertSide &ex, const SharedSide &sh, const _Float16 
     a.wa = ex.down; a.stride_a = ex.down_stride;
     a.sh_a = sh.gate ? sh.down : nullptr;
     a.src = act; a.src_sh = act_sh; a.T = T; a.H = H; a.M = M; a.S = sh.gate ? sh.S : 0; a.K = K; a.E = E;
+    a.zrow = zrow; a.zrow_sh = zrow_sh;
     a.tiles = tiles; a.y = y; a.ysh = ysh;
     const dim3 grid(n_tiles_max, H / NB), block(WAVES * 64);
     /* generic unit loop (a compile-time stage count spills here) */

@@ -72,12 +72,13 @@ int launch_dequant(int fmt, const uint8_t *src, uint32_t rows, uint32_t n, float
     return hipGetLastError() == hipSuccess ? 0 : -3;
 }
 
-/* x fp32 -> fp16 RNE (the reference's half(x) staging) */
+/* x fp32 -> fp16 RNE (the reference's half(x) staging), each 4-group stored
+ * (0,2,1,3) for the grouped GEMMs; n is a multiple of 4 */
 __global__ void k_to_f16(const float *x, size_t n, _Float16 *o) {
     size_t i = ((size_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
     if (i + 4 <= n) {
         f4 v = *(const f4 *)(x + i);
-        h4 h = {(_Float16)v.x, (_Float16)v.y, (_Float16)v.z, (_Float16)v.w};
+        h4 h = {(_Float16)v.x, (_Float16)v.z, (_Float16)v.y, (_Float16)v.w}; /* (0,2,1,3) */
         *(h4 *)(o + i) = h;
     } else {
         for (; i < n; i++) o[i] = (_Float16)x[i];
