@@ -230,7 +230,7 @@ struct Chunk {
 
 /* ------------------------------------------------------------- tile */
 /* One block: WAVES waves, wave w owns RPW row blocks of 16 rows (rows
- * blockIdx.y*NB + (w*RPW + rb)*16 ..) of NMAT matrices (gate+up, or down).
+ * yb*NB + (w*RPW + rb)*16 ..) of NMAT matrices (gate+up, or down).
  * A wave walks units u = (rb, stage j) in order, stage j = 128 k; weight
  * bytes for unit u+DEPTH are in flight while unit u computes.  Activation
  * chunks (256 k) sit in two LDS buffers: with <= 2 chunks both stay resident
@@ -238,7 +238,7 @@ struct Chunk {
  * after the barrier that ends chunk c (RPW must be 1 then). */
 template <int FMT, int NMAT, int RPW, int DEPTH, int NST, int TBM, typename Epi>
 DEV void tile_run(const uint8_t *w0, const uint8_t *w1, int in_dim, const _Float16 *src, int ld,
-                  const int *rowoff, int rows, _Float16 *xs, const Epi &epi) {
+                  const int *rowoff, int rows, int yb, _Float16 *xs, const Epi &epi) {
     const int tb = (rows + 15) >> 4;
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int kg = lane >> 4, i = lane & 15;
@@ -247,7 +247,7 @@ DEV void tile_run(const uint8_t *w0, const uint8_t *w1, int in_dim, const _Float
      * completely and the prefetch ring never crosses a loop back-edge (where
      * the register copies would wait for every load in flight) */
     const int nst = NST ? NST : in_dim / KC, nch = nst / 2, U = RPW * nst;
-    const int rbase = blockIdx.y * (WAVES * 16 * RPW) + wv * 16 * RPW;
+    const int rbase = yb * (WAVES * 16 * RPW) + wv * 16 * RPW;
     const uint8_t *rw0 = w0 + (size_t)(rbase + i) * rbytes;
     const uint8_t *rw1 = NMAT > 1 ? w1 + (size_t)(rbase + i) * rbytes : nullptr;
 
@@ -339,6 +339,15 @@ DEV void tile_run(const uint8_t *w0, const uint8_t *w1, int in_dim, const _Float
     }
 }
 
+/* Block -> (tile, row block).  Work-groups go to the 8 XCDs round-robin by
+ * linear id, so the NYB row blocks of one tile are given ids 8 apart: same
+ * XCD (one L2 for the tile's gathered activation rows) and dispatched close
+ * together.  The grid holds ceil(tiles/8)*8*NYB blocks. */
+DEV void block_tile(int nyb, int &tile, int &yb) {
+    const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
+    tile = (slot / nyb) * 8 + xcd;
+    yb = slot % nyb;
+}
 struct GemmArgs {
     const uint8_t *wa, *wb;   /* gate/up (wb NULL for down) of expert 0 */
     size_t stride_a, stride_b;
@@ -347,6 +356,7 @@ struct GemmArgs {
     const _Float16 *src_sh;   /* down: act_sh [T][S] */
     int T, H, M, S, K, E;
     int zrow, zrow_sh;        /* all-zero rows of src / src_sh (rows past a tile read them) */
+    int nyb;                  /* row blocks per tile */
     const uint32_t *tiles, *pairs;
     _Float16 *act, *act_sh;   /* gate/up outputs */
     float *y, *ysh;           /* down outputs */
@@ -400,12 +410,13 @@ template <int SFMT, int NST, int TBM>
 __global__ __launch_bounds__(WAVES * 64) void k_gemm_gate_up(GemmArgs a) {
     __shared__ __attribute__((aligned(16))) _Float16 xs[2 * TBM * 16 * BLD];
     __shared__ int rowoff[TBM * 16];
+    int ti, yb;
+    block_tile(a.nyb, ti, yb);
     const uint32_t nt = a.tiles[0];
-    if (blockIdx.x >= nt) return;
-    const uint32_t e = a.tiles[1 + 3 * blockIdx.x], first = a.tiles[2 + 3 * blockIdx.x],
-                   rows = a.tiles[3 + 3 * blockIdx.x];
+    if ((uint32_t)ti >= nt) return;
+    const uint32_t e = a.tiles[1 + 3 * ti], first = a.tiles[2 + 3 * ti], rows = a.tiles[3 + 3 * ti];
     const bool sh = e == (uint32_t)a.E;
-    if (blockIdx.y * (WAVES * 16 * GU_RPW) >= (unsigned)(sh ? a.S : a.M)) return;
+    if (yb * (WAVES * 16 * GU_RPW) >= (sh ? a.S : a.M)) return;
     if (threadIdx.x < TBM * 16) { /* rows past the tile read the zero row */
         const uint32_t q = threadIdx.x;
         rowoff[threadIdx.x] = q >= rows ? a.zrow : sh ? (int)(first + q) : (int)(a.pairs[first + q] / (uint32_t)a.K);
@@ -413,11 +424,11 @@ __global__ __launch_bounds__(WAVES * 64) void k_gemm_gate_up(GemmArgs a) {
     __syncthreads();
     if (sh) {
         const GuEpi epi{a.act_sh, a.S, (int)first, (int)rows};
-        tile_run<SFMT, 2, GU_RPW, (SFMT == FQ8 ? 2 : GU_DEPTH), NST, TBM>(a.sh_a, a.sh_b, a.H, a.src, a.H, rowoff, (int)rows, xs, epi);
+        tile_run<SFMT, 2, GU_RPW, (SFMT == FQ8 ? 2 : GU_DEPTH), NST, TBM>(a.sh_a, a.sh_b, a.H, a.src, a.H, rowoff, (int)rows, yb, xs, epi);
     } else {
         const GuEpi epi{a.act, a.M, (int)first, (int)rows};
         tile_run<FQ4K, 2, GU_RPW, GU_DEPTH, NST, TBM>(a.wa + (size_t)e * a.stride_a, a.wb + (size_t)e * a.stride_b, a.H, a.src,
-                                  a.H, rowoff, (int)rows, xs, epi);
+                                  a.H, rowoff, (int)rows, yb, xs, epi);
     }
 }
 
@@ -425,20 +436,21 @@ template <int EFMT, int SFMT, int NST, int TBM>
 __global__ __launch_bounds__(WAVES * 64) void k_gemm_down(GemmArgs a) {
     __shared__ __attribute__((aligned(16))) _Float16 xs[2 * TBM * 16 * BLD];
     __shared__ int rowoff[TBM * 16];
+    int ti, yb;
+    block_tile(a.nyb, ti, yb);
     const uint32_t nt = a.tiles[0];
-    if (blockIdx.x >= nt) return;
-    const uint32_t e = a.tiles[1 + 3 * blockIdx.x], first = a.tiles[2 + 3 * blockIdx.x],
-                   rows = a.tiles[3 + 3 * blockIdx.x];
+    if ((uint32_t)ti >= nt) return;
+    const uint32_t e = a.tiles[1 + 3 * ti], first = a.tiles[2 + 3 * ti], rows = a.tiles[3 + 3 * ti];
     const bool sh = e == (uint32_t)a.E;
     if (threadIdx.x < TBM * 16)
         rowoff[threadIdx.x] = threadIdx.x < rows ? (int)(first + threadIdx.x) : (sh ? a.zrow_sh : a.zrow);
     __syncthreads();
     if (sh) {
         const DnEpi epi{a.ysh, a.H, (int)first, (int)rows};
-        tile_run<SFMT, 1, DN_RPW, DN_DEPTH, NST, TBM>(a.sh_a, nullptr, a.S, a.src_sh, a.S, rowoff, (int)rows, xs, epi);
+        tile_run<SFMT, 1, DN_RPW, DN_DEPTH, NST, TBM>(a.sh_a, nullptr, a.S, a.src_sh, a.S, rowoff, (int)rows, yb, xs, epi);
     } else {
         const DnEpi epi{a.y, a.H, (int)first, (int)rows};
-        tile_run<EFMT, 1, DN_RPW, DN_DEPTH, NST, TBM>(a.wa + (size_t)e * a.stride_a, nullptr, a.M, a.src, a.M, rowoff, (int)rows, xs, epi);
+        tile_run<EFMT, 1, DN_RPW, DN_DEPTH, NST, TBM>(a.wa + (size_t)e * a.stride_a, nullptr, a.M, a.src, a.M, rowoff, (int)rows, yb, xs, epi);
     }
 }
 
@@ -456,7 +468,8 @@ int launch_gemm_gate_up(const ExpertSide &ex, const SharedSide &sh, const _Float
     a.src = x16; a.T = T; a.H = H; a.M = M; a.S = sh.gate ? sh.S : 0; a.K = K; a.E = E;
     a.zrow = zrow; a.zrow_sh = zrow;
     a.tiles = tiles; a.pairs = pairs; a.act = act; a.act_sh = act_sh;
-    const dim3 grid(n_tiles_max, (M > a.S ? M : a.S) / NB), block(WAVES * 64);
+    a.nyb = (M > a.S ? M : a.S) / NB;
+    const dim3 grid((unsigned)((n_tiles_max + 7) / 8 * 8 * a.nyb)), block(WAVES * 64);
     const bool q8 = sh.gate && sh.gate_fmt == FQ8;
     if (tile_m != GEMM_TILE_SMALL && tile_m != GEMM_TILE_BIG) return -2;
     /* compile-time stage count for the common hidden size (Q4_K shared
@@ -489,7 +502,8 @@ int launch_gemm_down(const ExpertSide &ex, const SharedSide &sh, const _Float16 
     a.src = act; a.src_sh = act_sh; a.T = T; a.H = H; a.M = M; a.S = sh.gate ? sh.S : 0; a.K = K; a.E = E;
     a.zrow = zrow; a.zrow_sh = zrow_sh;
     a.tiles = tiles; a.y = y; a.ysh = ysh;
-    const dim3 grid(n_tiles_max, H / NB), block(WAVES * 64);
+    a.nyb = H / NB;
+    const dim3 grid((unsigned)((n_tiles_max + 7) / 8 * 8 * a.nyb)), block(WAVES * 64);
     /* generic unit loop (a compile-time stage count spills here) */
     if (tile_m != GEMM_TILE_SMALL && tile_m != GEMM_TILE_BIG) return -2;
 #define DN_LAUNCH(EF, SF)                                                                    \
