@@ -27,6 +27,7 @@
 #include "kernels.h"
 #include "route_dev.h"
 
+
 enum { FQ4K = 0, FQ5K = 1, FQ6K = 2, FQ8 = 3 };
 
 DEV size_t row_bytes(int fmt, int n) {
@@ -239,6 +240,27 @@ DEV void gu_body(const GUArgs &a, const uint8_t *gbase, const uint8_t *ubase, in
                     (_Float16)(silu_f(red[(i * 2) * 16 + j]) * red[(i * 2 + 1) * 16 + j]);
 }
 
+/* One token, H = 2048 (one 32-weight chunk per lane): x arrives already
+ * converted (loaded before the routing), so only the weight bytes are
+ * waited for once the experts are known.  Same sums as gu_body. */
+template <int RPW>
+DEV void gu_body1(const GUArgs &a, const uint8_t *gbase, const uint8_t *ubase, int r0, const h2 *xl,
+                  const h2 *xh, float Xl, float Xh, _Float16 *out, int lane) {
+    const size_t rb = row_bytes(FQ4K, a.H);
+    Q4Raw g[RPW], u[RPW];
+#pragma unroll
+    for (int i = 0; i < RPW; i++) {
+        g[i] = q4_load(gbase + (size_t)(r0 + i) * rb, lane);
+        u[i] = q4_load(ubase + (size_t)(r0 + i) * rb, lane);
+    }
+#pragma unroll
+    for (int i = 0; i < RPW; i++) {
+        const float pg = wave_sum_fast(q4_dot(g[i], lane, xl, xh, Xl, Xh));
+        const float pu = wave_sum_fast(q4_dot(u[i], lane, xl, xh, Xl, Xh));
+        if (lane == 0) out[r0 + i] = (_Float16)(silu_f(pg) * pu);
+    }
+}
+
 #ifndef GU_RPW
 #define GU_RPW 2
 #endif
@@ -285,6 +307,122 @@ __global__ __launch_bounds__(256) void k_gemv_gate_up(GUArgs a, RouteArgs ra) {
             gu_body<GU_RPW, FQ8>(a, a.sh_gate, a.sh_up, r0, a.T, tok, a.act_sh, a.S, lane, red);
         else
             gu_body<GU_RPW, FQ4K>(a, a.sh_gate, a.sh_up, r0, a.T, tok, a.act_sh, a.S, lane, red);
+    }
+}
+
+/* One-token gate/up with the routing folded in (H = 2048, E <= 64 EPL).
+ * Every wave selects the experts itself (no separate routing kernel, no
+ * barrier), and the waves of the block for selection rank u issue their
+ * weight loads for expert ids[u] as soon as round u has named it; the
+ * remaining rounds, the expert's sorted position (the number of smaller
+ * selected ids: its act row) and, in block 0, the published routing overlap
+ * those loads.  Selection and softmax restate softmax_topk_route
+ * (inference/src/shaders.metal:1141-1234) exactly as wave_topk does. */
+template <int EPL>
+__global__ __launch_bounds__(256) void k_gemv_gate_up1(GUArgs a, RouteArgs ra) {
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int rows_blk = 4 * GU_RPW, b = blockIdx.x;
+    const int E = a.E, K = a.K;
+    int klo;
+    q4_pos(lane, klo);
+    h2 xl[8], xh[8];
+    const float Xl = load_x16_f32(a.x + klo, xl), Xh = load_x16_f32(a.x + klo + 32, xh);
+    if (b >= a.routed_blocks) { /* shared expert (Q4_K): needs no routing */
+        const int r0 = (b - a.routed_blocks) * rows_blk + wv * GU_RPW;
+        gu_body1<GU_RPW>(a, a.sh_gate, a.sh_up, r0, xl, xh, Xl, Xh, a.act_sh, lane);
+        return;
+    }
+    const int bpe = a.M / rows_blk, u = b / bpe, r0 = (b % bpe) * rows_blk + wv * GU_RPW;
+    const size_t rb = row_bytes(FQ4K, a.H);
+
+    const float *l = ra.logits;
+    float v[EPL], bv[EPL];
+#pragma unroll
+    for (int j = 0; j < EPL; j++) v[j] = l[min(lane * EPL + j, E - 1)];
+    const float sg = l[E];
+    if (ra.bias)
+#pragma unroll
+        for (int j = 0; j < EPL; j++) bv[j] = ra.bias[min(lane * EPL + j, E - 1)];
+    uint32_t key[EPL];
+    int kj[EPL];
+#pragma unroll
+    for (int j = 0; j < EPL; j++) {
+        key[j] = lane * EPL + j < E ? route_ord(ra.bias ? v[j] + bv[j] : v[j]) : 0u;
+        kj[j] = j;
+    }
+#pragma unroll
+    for (int pass = 0; pass < EPL; pass++)
+#pragma unroll
+        for (int j = pass & 1; j + 1 < EPL; j += 2)
+            if (key[j + 1] > key[j]) {
+                const uint32_t tk = key[j]; key[j] = key[j + 1]; key[j + 1] = tk;
+                const int tj = kj[j]; kj[j] = kj[j + 1]; kj[j + 1] = tj;
+            }
+    /* lane k keeps the k-th winner */
+    int myid = 0, eu = 0;
+    float myval = 0.0f, v0 = 0.0f;
+    Q4Raw g[GU_RPW], w2[GU_RPW];
+    /* a rolled loop: each wave runs these rounds once */
+#pragma unroll 1
+    for (int k = 0; k < K; k++) {
+        const uint32_t m = wave_max_u32(key[0]);
+        const int wl = (int)__builtin_ctzll(__ballot(key[0] == m));
+        const int id = wl * EPL + __builtin_amdgcn_readlane(kj[0], wl);
+        const float val = ord_value(m);
+        if (lane == k) { myid = id; myval = val; }
+        if (k == 0) v0 = val;
+        if (lane == wl) {
+#pragma unroll
+            for (int j = 0; j + 1 < EPL; j++) { key[j] = key[j + 1]; kj[j] = kj[j + 1]; }
+            key[EPL - 1] = 0u;
+        }
+        if (k == u) {
+            eu = id;
+            const uint8_t *gb = a.gate + (size_t)eu * a.gate_stride, *ub = a.up + (size_t)eu * a.up_stride;
+#pragma unroll
+            for (int i = 0; i < GU_RPW; i++) {
+                g[i] = q4_load(gb + (size_t)(r0 + i) * rb, lane);
+                w2[i] = q4_load(ub + (size_t)(r0 + i) * rb, lane);
+            }
+        }
+    }
+    const int rank = __popcll(__ballot(lane < K && myid < eu));
+    if (b == 0 && wv == 0) { /* publish the call's routing for the down kernel */
+        const float tw = lane < K ? expf(myval - v0) : 0.0f;
+        float sum = 0.0f;
+#pragma unroll 1
+        for (int k = 0; k < K; k++)
+            sum += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, tw), k));
+        const float inv = sum > 0.0f ? 1.0f / sum : 0.0f;
+        int rkk = 0;
+#pragma unroll 1
+        for (int k = 0; k < K; k++) rkk += __builtin_amdgcn_readlane(myid, k) < myid;
+        if (lane < K) {
+            ra.idx[lane] = myid;
+            ra.w[lane] = tw * inv;
+            ra.pairs[rkk] = (uint32_t)lane;
+            ra.pos[lane] = (uint32_t)rkk;
+            ACT_E(ra.list, rkk) = (uint32_t)myid;
+            ACT_OFF(ra.list, E, rkk) = (uint32_t)rkk;
+        }
+        if (lane == 0) {
+            ra.sgl[0] = sg;
+            ACT_N(ra.list) = (uint32_t)K;
+            ACT_OFF(ra.list, E, K) = (uint32_t)K;
+        }
+        for (int ee = lane; ee <= E; ee += 64) {
+            int c = 0;
+#pragma unroll 1
+            for (int k = 0; k < K; k++) c += __builtin_amdgcn_readlane(myid, k) < ee;
+            ra.offsets[ee] = (uint32_t)c;
+        }
+    }
+    _Float16 *out = a.act + (size_t)rank * a.M;
+#pragma unroll
+    for (int i = 0; i < GU_RPW; i++) {
+        const float pg = wave_sum_fast(q4_dot(g[i], lane, xl, xh, Xl, Xh));
+        const float pu = wave_sum_fast(q4_dot(w2[i], lane, xl, xh, Xl, Xh));
+        if (lane == 0) out[r0 + i] = (_Float16)(silu_f(pg) * pu);
     }
 }
 
@@ -502,6 +640,18 @@ int launch_gemv_gate_up(const ExpertSide &ex, const SharedSide &sh, const RouteA
     const int umax = T * K < E ? T * K : E;
     a.routed_blocks = umax * (M / rows_blk);
     const int blocks = a.routed_blocks + (sh.gate ? sh.S / rows_blk : 0);
+    if (route_in_block && T == 1 && H == 2048 && (!sh.gate || sh.gate_fmt == FQ4K)) {
+#define GU1_LAUNCH(EPLV) hipLaunchKernelGGL((k_gemv_gate_up1<EPLV>), dim3(blocks), dim3(256), 0, s, a, ra)
+        switch (epl_of(E)) {
+            case 1: GU1_LAUNCH(1); break;
+            case 2: GU1_LAUNCH(2); break;
+            case 4: GU1_LAUNCH(4); break;
+            case 8: GU1_LAUNCH(8); break;
+            default: GU1_LAUNCH(16); break;
+        }
+#undef GU1_LAUNCH
+        return hipGetLastError() == hipSuccess ? 0 : -3;
+    }
 #define GU_LAUNCH(EPLV)                                                                          \
     do {                                                                                          \
         if (route_in_block)                                                                       \

@@ -12,93 +12,110 @@
 #include "kernels.h"
 
 /* -------------------------------------------------------- key helpers */
-DEV uint64_t route_key(float v, int e) {
-    if (v == 0.0f) v = 0.0f; /* -0 and +0 tie by index, as in IEEE compare */
-    uint32_t b = __builtin_bit_cast(uint32_t, v);
-    uint32_t ord = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
-    return ((uint64_t)ord << 32) | (uint64_t)(0xFFFFFFFFu - (uint32_t)e);
+/* Order-preserving 32-bit image of a float (larger float -> larger key);
+ * -0 is folded into +0 so the two tie, as in an IEEE compare.  Key 0 (the
+ * image of one NaN pattern, outside the contract) marks taken or absent
+ * entries. */
+DEV uint32_t route_ord(float v) {
+    if (v == 0.0f) v = 0.0f;
+    const uint32_t b = __builtin_bit_cast(uint32_t, v);
+    return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
 }
-DEV float key_value(uint64_t k) {
-    uint32_t ord = (uint32_t)(k >> 32);
-    uint32_t b = (ord & 0x80000000u) ? (ord & 0x7FFFFFFFu) : ~ord;
+DEV float ord_value(uint32_t ord) {
+    const uint32_t b = (ord & 0x80000000u) ? (ord & 0x7FFFFFFFu) : ~ord;
     return __builtin_bit_cast(float, b);
 }
-DEV int key_expert(uint64_t k) { return (int)(0xFFFFFFFFu - (uint32_t)k); }
 
-template <int CTRL>
-DEV uint64_t dpp64(uint64_t v) {
-    return ((uint64_t)dppu<CTRL>((uint32_t)(v >> 32)) << 32) | dppu<CTRL>((uint32_t)v);
-}
-DEV uint64_t max64(uint64_t a, uint64_t b) { return a > b ? a : b; }
-DEV uint64_t readlane64(uint64_t v, int l) {
-    return ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(v >> 32), l) << 32) |
-           (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, l);
-}
-/* wave64 maximum of a 64-bit key (DPP within rows, then the four row maxima) */
-DEV uint64_t wave_max64(uint64_t m) {
-    m = max64(m, dpp64<DPP_XOR1>(m));
-    m = max64(m, dpp64<DPP_XOR2>(m));
-    m = max64(m, dpp64<DPP_HALF_MIRROR>(m));
-    m = max64(m, dpp64<DPP_MIRROR>(m));
-    return max64(max64(readlane64(m, 0), readlane64(m, 16)), max64(readlane64(m, 32), readlane64(m, 48)));
+/* wave64 maximum of a 32-bit key, returned wave-uniform: DPP maxima within
+ * rows of 16 lanes, then the four row maxima */
+DEV uint32_t wave_max_u32(uint32_t m) {
+    m = max(m, dppu<DPP_XOR1>(m));
+    m = max(m, dppu<DPP_XOR2>(m));
+    m = max(m, dppu<DPP_HALF_MIRROR>(m));
+    m = max(m, dppu<DPP_MIRROR>(m));
+    const uint32_t a = (uint32_t)__builtin_amdgcn_readlane((int)m, 0), b = (uint32_t)__builtin_amdgcn_readlane((int)m, 16);
+    const uint32_t c = (uint32_t)__builtin_amdgcn_readlane((int)m, 32), d = (uint32_t)__builtin_amdgcn_readlane((int)m, 48);
+    return max(max(a, b), max(c, d));
 }
 
-/* One token's top-K on one wave.  Lane 0 writes idx/w/sgl; e_out (LDS, may be
- * NULL) receives the K expert ids. */
+/* One token's top-K on one wave.  Lane L owns the EPL consecutive experts
+ * EPL*L .. EPL*L + EPL-1, so lane order is expert order.  Each lane first
+ * sorts its keys (adjacent compare-exchanges that swap only on a strictly
+ * larger right-hand key, hence stable: equal keys keep index order); a
+ * round then takes the wave maximum of the lanes' heads and the lowest lane
+ * holding it -- the lowest expert index among equal values (strict '>' of
+ * shaders.metal:1164-1190) -- and that lane pops its head.  All round state
+ * except the lane's list is wave-uniform (scalar registers), and the rounds
+ * form a rolled loop (each wave runs them once: unrolled, every round would
+ * be fetched cold).  Lane k < K ends with the k-th expert and its softmax
+ * weight (softmax over the winners, summed in k order as the reference's
+ * loop does); lanes < K write idx_out/w_out/e_out (each may be NULL) and
+ * lane 0 the shared-gate logit. */
+struct TopkLane {
+    int id;
+    float w;
+};
 template <int EPL, bool COH = false>
-DEV void wave_topk(const float *l, const float *bias, int E, int K, int lane, int32_t *idx_out,
-                   float *w_out, float *sgl_out, int *e_out) {
+DEV TopkLane wave_topk(const float *l, const float *bias, int E, int K, int lane, int32_t *idx_out,
+                       float *w_out, float *sgl_out, int *e_out) {
     /* all loads first and unconditional (index clamped, then masked), so
      * they are in flight together instead of one round trip each */
     float v[EPL], bv[EPL];
 #pragma unroll
     for (int j = 0; j < EPL; j++) {
-        const int e = min(lane + 64 * j, E - 1);
+        const int e = min(lane * EPL + j, E - 1);
         v[j] = COH ? ld_coh(l + e) : l[e];
     }
+    const float sg = COH ? ld_coh(l + E) : l[E];
     if (bias)
 #pragma unroll
-        for (int j = 0; j < EPL; j++) bv[j] = bias[min(lane + 64 * j, E - 1)];
-    uint64_t key[EPL];
+        for (int j = 0; j < EPL; j++) bv[j] = bias[min(lane * EPL + j, E - 1)];
+    uint32_t key[EPL];
+    int kj[EPL];
 #pragma unroll
     for (int j = 0; j < EPL; j++) {
-        const int e = lane + 64 * j;
-        key[j] = e < E ? route_key(bias ? v[j] + bv[j] : v[j], e) : 0;
+        key[j] = lane * EPL + j < E ? route_ord(bias ? v[j] + bv[j] : v[j]) : 0u;
+        kj[j] = j;
     }
-    float vals[OROME_MAXK];
-    int ids[OROME_MAXK];
+    /* odd-even transposition sort, descending */
 #pragma unroll
-    for (int k = 0; k < OROME_MAXK; k++) {
-        if (k < K) {
-            uint64_t m = key[0];
+    for (int pass = 0; pass < EPL; pass++)
 #pragma unroll
-            for (int j = 1; j < EPL; j++) m = key[j] > m ? key[j] : m;
-            m = wave_max64(m);
+        for (int j = pass & 1; j + 1 < EPL; j += 2)
+            if (key[j + 1] > key[j]) {
+                const uint32_t tk = key[j]; key[j] = key[j + 1]; key[j + 1] = tk;
+                const int tj = kj[j]; kj[j] = kj[j + 1]; kj[j + 1] = tj;
+            }
+    int id = 0;
+    float val = 0.0f, v0 = 0.0f;
+#pragma unroll 1
+    for (int k = 0; k < K; k++) {
+        const uint32_t m = wave_max_u32(key[0]);
+        const int wl = (int)__builtin_ctzll(__ballot(key[0] == m));
+        const int e = wl * EPL + __builtin_amdgcn_readlane(kj[0], wl);
+        const float vk = ord_value(m);
+        if (lane == k) { id = e; val = vk; }
+        if (k == 0) v0 = vk;
+        if (lane == wl) {
 #pragma unroll
-            for (int j = 0; j < EPL; j++)
-                if (key[j] == m) key[j] = 0;
-            vals[k] = key_value(m);
-            ids[k] = key_expert(m);
+            for (int j = 0; j + 1 < EPL; j++) { key[j] = key[j + 1]; kj[j] = kj[j + 1]; }
+            key[EPL - 1] = 0u;
         }
     }
-    if (lane == 0) {
-        float mx = vals[0], sum = 0.0f, tw[OROME_MAXK];
-#pragma unroll
-        for (int k = 0; k < OROME_MAXK; k++)
-            if (k < K) {
-                tw[k] = expf(vals[k] - mx);
-                sum += tw[k];
-            }
-        float inv = sum > 0.0f ? 1.0f / sum : 0.0f;
-#pragma unroll
-        for (int k = 0; k < OROME_MAXK; k++)
-            if (k < K) {
-                idx_out[k] = ids[k];
-                w_out[k] = tw[k] * inv;
-                if (e_out) e_out[k] = ids[k];
-            }
-        *sgl_out = COH ? ld_coh(l + E) : l[E];
+    const float tw = lane < K ? expf(val - v0) : 0.0f;
+    float sum = 0.0f;
+#pragma unroll 1
+    for (int k = 0; k < K; k++)
+        sum += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, tw), k));
+    const float inv = sum > 0.0f ? 1.0f / sum : 0.0f;
+    const float w = tw * inv;
+    if (lane < K) {
+        if (idx_out) idx_out[lane] = id;
+        if (w_out) w_out[lane] = w;
+        if (e_out) e_out[lane] = id;
     }
+    if (lane == 0 && sgl_out) *sgl_out = sg;
+    return TopkLane{id, w};
 }
 
 /* Block-wide exclusive scan of one 32-bit value per thread (256 threads):
