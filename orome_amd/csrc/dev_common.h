@@ -25,6 +25,12 @@ typedef uint32_t u2 __attribute__((ext_vector_type(2)));
 
 #define DEV static __device__ __forceinline__
 #define MDEV __device__ __forceinline__ /* member functions */
+#ifdef OROME_TRACE
+extern __device__ unsigned long long g_trace[65536 * 8];
+#define TSTAMP(i) do { if ((threadIdx.x & 63) == 0 && blockIdx.x < 65536) g_trace[blockIdx.x * 8 + (i)] = __builtin_amdgcn_s_memrealtime() | ((unsigned long long)(threadIdx.x >> 6) << 60); } while (0)
+#else
+#define TSTAMP(i) do {} while (0)
+#endif
 
 DEV h2 as_h2(uint32_t v) { return __builtin_bit_cast(h2, v); }
 DEV uint32_t as_u32(h2 v) { return __builtin_bit_cast(uint32_t, v); }
@@ -148,6 +154,20 @@ DEV void q4_nibbles_h2(uint32_t w, h2 &lo01, h2 &lo23, h2 &hi01, h2 &hi23) {
     lo23 = as_h2(__builtin_amdgcn_perm(0x64646464u, lo, 0x05030402u)) - bias;
     hi01 = as_h2(__builtin_amdgcn_perm(0x64646464u, hi, 0x05010400u)) - bias;
     hi23 = as_h2(__builtin_amdgcn_perm(0x64646464u, hi, 0x05030402u)) - bias;
+}
+
+/* Biased exact fp16 images of the eight 4-bit quants of a dword (bytes =
+ * positions l..l+3), in the pair order (l, l+2), (l+1, l+3):
+ * lo = 1024 + q_lo, hi = 1024 + 16 q_hi (the nibbles OR-ed under the 0x64
+ * exponent byte; five instructions).  With S = sum of (image * x) over a
+ * sub-block and X = sum of x, sum q_lo x = S_lo - 1024 X and
+ * sum q_hi x = (S_hi - 1024 X) / 16. */
+DEV void q4_bias_h2(uint32_t w, h2 &l02, h2 &l13, h2 &h02, h2 &h13) {
+    const uint32_t p13 = __builtin_amdgcn_perm(0x64646464u, w, 0x04030401u);
+    l02 = as_h2((w & 0x000F000Fu) | 0x64006400u);
+    l13 = as_h2(p13 & 0xFF0FFF0Fu);
+    h02 = as_h2((w & 0x00F000F0u) | 0x64006400u);
+    h13 = as_h2(p13 & 0xFFF0FFF0u);
 }
 
 /* --------------------------------------------------------------- Q6_K */

@@ -26,6 +26,12 @@
 #include "dev_common.h"
 #include "kernels.h"
 #include "route_dev.h"
+#ifdef OROME_TRACE
+__device__ unsigned long long g_trace[65536 * 8];
+extern "C" __attribute__((visibility("default"))) int orome_trace_fetch(unsigned long long *h) {
+    return (int)hipMemcpyFromSymbol(h, HIP_SYMBOL(g_trace), sizeof(g_trace));
+}
+#endif
 
 
 enum { FQ4K = 0, FQ5K = 1, FQ6K = 2, FQ8 = 3 };
@@ -426,6 +432,226 @@ __global__ __launch_bounds__(256) void k_gemv_gate_up1(GUArgs a, RouteArgs ra) {
     }
 }
 
+/* Batched gate/up, 2 <= T <= 8, H = 2048, Q4_K.  One 16-lane DPP row per
+ * weight row: lane cl owns chunks 4cl..4cl+3 of the row (64 contiguous
+ * quant bytes, one super-block header, sub-block pairs 2(cl&1) and
+ * 2(cl&1)+1, k = 128cl .. 128cl+127), so a row's sum is one 16-lane DPP
+ * reduction.  A block = 4 waves over GB_ITER tiles of 16 rows (gate and up)
+ * of one slot -- an active expert, or the shared expert over all T tokens
+ * (the shared slot's blocks come first in the grid: they carry the most
+ * tokens) -- with a two-deep weight ring: tile i+1's bytes are in flight
+ * while tile i computes.  The slot's tokens are staged once in LDS as fp16
+ * (half(x), as the reference stages it) with the sums of each 16
+ * consecutive rounded values (the Q4_K min term).  ROUTE: the block selects
+ * and dispatches itself (route_block_lds); else it reads the routing written
+ * by k_topk_dispatch_small in one round trip. */
+#define GB_ROWS 16
+#define GB_ITER 4
+/* LDS: per token, 16 segments of 128 k (lane cl reads segment cl) padded to
+ * GB_SEG halves, and per segment the 8 sums padded to GB_SUM floats, so the
+ * 16 lanes of a row hit distinct banks */
+#define GB_SEG 136
+#define GB_SUM 12
+#define GB_TOK_BYTES (16 * GB_SEG * 2 + 16 * GB_SUM * 4 + GB_ROWS * GB_ITER * 2)
+struct GbTile {
+    u4 hg, hu, qg[4], qu[4];
+    MDEV void load(const uint8_t *pg, const uint8_t *pu, int cl) {
+        hg = ld_u4(pg);
+        hu = ld_u4(pu);
+#pragma unroll
+        for (int p = 0; p < 4; p++) {
+            qg[p] = ld_u4(pg + 16 + 64 * (cl & 1) + 16 * p);
+            qu[p] = ld_u4(pu + 16 + 64 * (cl & 1) + 16 * p);
+        }
+    }
+};
+/* One tile: 4 rows per wave (one per DPP row) of gate and up, every token
+ * of the slot; results (act = silu(gate) * up, fp16) go to obuf[j][row].
+ * Quant dwords become biased exact fp16 images (q4_bias_h2) and meet x,
+ * which sits in LDS in the matching (0,2,1,3) order.  Per sub-block pair g
+ * (scales a = d sc, mins b = dmin m) and token:
+ *   a_lo (S_lo - 1024 X_lo) + a_hi (S_hi - 1024 X_hi) / 16 - b_lo X_lo - b_hi X_hi
+ * folded as  a_lo S_lo + (a_hi/16) S_hi - (1024 a_lo + b_lo) X_lo - (64 a_hi + b_hi) X_hi. */
+DEV void gb_tile(const GbTile &tl, int it, int cl, int q, int wv, int n, const _Float16 *xs, const float *xsum,
+                 _Float16 *obuf) {
+    float A[2][4], B[2][4]; /* [g][gate lo, gate hi, up lo, up hi] */
+#pragma unroll
+    for (int g = 0; g < 2; g++) {
+        const Q4Affine fg = q4k_affine(tl.hg, 2 * (cl & 1) + g), fu = q4k_affine(tl.hu, 2 * (cl & 1) + g);
+        A[g][0] = fg.a_lo; A[g][1] = fg.a_hi * 0.0625f; A[g][2] = fu.a_lo; A[g][3] = fu.a_hi * 0.0625f;
+        B[g][0] = fmaf(1024.0f, fg.a_lo, fg.b_lo); B[g][1] = fmaf(64.0f, fg.a_hi, fg.b_hi);
+        B[g][2] = fmaf(1024.0f, fu.a_lo, fu.b_lo); B[g][3] = fmaf(64.0f, fu.a_hi, fu.b_hi);
+    }
+    const int rr = it * GB_ROWS + wv * 4 + q;
+#pragma unroll 1
+    for (int j = 0; j < n; j++) {
+        const _Float16 *xj = xs + (size_t)j * (16 * GB_SEG) + cl * GB_SEG;
+        const float *sj = xsum + j * (16 * GB_SUM) + cl * GB_SUM;
+        float cg = 0.0f, cu = 0.0f;
+#pragma unroll
+        for (int g = 0; g < 2; g++) {
+            float gl = 0.0f, gh = 0.0f, ul = 0.0f, uh = 0.0f;
+#pragma unroll
+            for (int c = 0; c < 2; c++) {
+                h2 xl[8], xh[8];
+                load_h8<true>(xj + g * 64 + c * 16, xl);
+                load_h8<true>(xj + g * 64 + c * 16 + 8, xl + 4);
+                load_h8<true>(xj + g * 64 + 32 + c * 16, xh);
+                load_h8<true>(xj + g * 64 + 32 + c * 16 + 8, xh + 4);
+                const u4 wq = tl.qg[2 * g + c], uq = tl.qu[2 * g + c];
+                uint32_t gw[4] = {wq.x, wq.y, wq.z, wq.w}, uw[4] = {uq.x, uq.y, uq.z, uq.w};
+#pragma unroll
+                for (int d = 0; d < 4; d++) {
+                    /* opaque per token: keeps the split inside the token loop
+                     * instead of hoisting 128 registers of it */
+                    asm volatile("" : "+v"(gw[d]), "+v"(uw[d]));
+                    h2 l02, l13, h02, h13;
+                    q4_bias_h2(gw[d], l02, l13, h02, h13);
+                    gl = dot2(l02, xl[2 * d], gl);
+                    gl = dot2(l13, xl[2 * d + 1], gl);
+                    gh = dot2(h02, xh[2 * d], gh);
+                    gh = dot2(h13, xh[2 * d + 1], gh);
+                    q4_bias_h2(uw[d], l02, l13, h02, h13);
+                    ul = dot2(l02, xl[2 * d], ul);
+                    ul = dot2(l13, xl[2 * d + 1], ul);
+                    uh = dot2(h02, xh[2 * d], uh);
+                    uh = dot2(h13, xh[2 * d + 1], uh);
+                }
+            }
+            const float Xl = sj[4 * g] + sj[4 * g + 1], Xh = sj[4 * g + 2] + sj[4 * g + 3];
+            cg += (A[g][0] * gl + A[g][1] * gh) - (B[g][0] * Xl + B[g][1] * Xh);
+            cu += (A[g][2] * ul + A[g][3] * uh) - (B[g][2] * Xl + B[g][3] * Xh);
+        }
+        const float tg = row_sum16(cg), tu = row_sum16(cu);
+        if (cl == 0) obuf[j * (GB_ROWS * GB_ITER) + rr] = (_Float16)(silu_f(tg) * tu);
+    }
+}
+
+/* The slot's tiles through a two-deep weight ring (t0 holds tile 0 on entry). */
+DEV void gb_run(GbTile &t0, GbTile &t1, const uint8_t *wg, const uint8_t *wu, size_t tile_step, int ntile, int cl,
+                int q, int wv, int n, const _Float16 *xs, const float *xsum, _Float16 *obuf) {
+#pragma unroll 1
+    for (int it = 0; it < ntile; it += 2) {
+        /* every load unconditional (clamped tile): a skipped load would
+         * leave the wait counts unknown and a tile would wait for every load
+         * in flight */
+        const int n1 = it + 1 < ntile ? it + 1 : it, n2 = it + 2 < ntile ? it + 2 : ntile - 1;
+        t1.load(wg + n1 * tile_step, wu + n1 * tile_step, cl);
+        gb_tile(t0, it, cl, q, wv, n, xs, xsum, obuf);
+        t0.load(wg + n2 * tile_step, wu + n2 * tile_step, cl);
+        if (it + 1 < ntile) gb_tile(t1, it + 1, cl, q, wv, n, xs, xsum, obuf);
+    }
+}
+
+template <int EPL, bool ROUTE>
+__global__ __launch_bounds__(256) void k_gemv_gu_b(GUArgs a, RouteArgs ra) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t gb_dyn[];
+    __shared__ RouteLds r;
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, tid = threadIdx.x;
+    const int cl = lane & 15, q = lane >> 4;
+    TSTAMP(0);
+    const int T = a.T, K = a.K, H = 2048;
+    _Float16 *xs = (_Float16 *)gb_dyn;
+    float *xsum = (float *)(gb_dyn + (size_t)T * 16 * GB_SEG * 2);
+    const int sh_blocks = a.S / GB_ROWS; /* one tile each: the shared slot carries all T tokens */
+    const int b = blockIdx.x;
+    const bool sh = b < sh_blocks;
+    const int bpe = a.M / (GB_ROWS * GB_ITER);
+    int n, s0 = 0, base;
+    int tk[8];
+    const uint8_t *wg, *wu;
+    if (!sh) {
+        const int br = b - sh_blocks, u = br / bpe;
+        base = (br % bpe) * (GB_ROWS * GB_ITER);
+        int e;
+        if constexpr (ROUTE) {
+            route_block_lds<EPL>(ra, r, br == 0);
+            if (u >= r.nact) return;
+            e = r.act_e[u];
+            s0 = r.act_off[u];
+            n = r.act_off[u + 1] - s0;
+#pragma unroll
+            for (int j = 0; j < 8; j++) tk[j] = j < n ? r.pairs[s0 + j] / K : 0;
+        } else {
+            const uint32_t nact = ACT_N(a.list);
+            const uint32_t eu = ACT_E(a.list, u), o0 = ACT_OFF(a.list, a.E, u), o1 = ACT_OFF(a.list, a.E, u + 1);
+            const uint32_t pr = lane < T * K ? a.pairs[lane] : 0u;
+            if ((uint32_t)u >= nact) return;
+            e = (int)eu;
+            s0 = (int)o0;
+            n = (int)(o1 - o0);
+#pragma unroll
+            for (int j = 0; j < 8; j++)
+                tk[j] = j < n ? (int)((uint32_t)__builtin_amdgcn_readlane((int)pr, s0 + j) / (uint32_t)K) : 0;
+        }
+        wg = a.gate + (size_t)e * a.gate_stride;
+        wu = a.up + (size_t)e * a.up_stride;
+    } else {
+        base = b * GB_ROWS;
+        n = T;
+#pragma unroll
+        for (int j = 0; j < 8; j++) tk[j] = j;
+        wg = a.sh_gate;
+        wu = a.sh_up;
+    }
+    const size_t rb = row_bytes(FQ4K, H);
+    const size_t wave_row = (size_t)(base + wv * 4 + q) * rb + (cl >> 1) * 144;
+    wg += wave_row;
+    wu += wave_row;
+    const size_t tile_step = (size_t)GB_ROWS * rb;
+    GbTile t0, t1;
+    TSTAMP(1);
+    t0.load(wg, wu, cl); /* weight bytes first */
+    /* stage the tokens: thread t converts x[tok][8t .. 8t+8), four tokens
+     * per pass; loads are unconditional (clamped token) so they stay in
+     * flight together */
+    const h2 one = {(_Float16)1.0f, (_Float16)1.0f};
+#pragma unroll
+    for (int j0 = 0; j0 < 8; j0 += 4) {
+        if (j0 < n) {
+            f4 xv[4][2];
+#pragma unroll
+            for (int jj = 0; jj < 4; jj++) {
+                const float *src = a.x + (size_t)tk[j0 + jj < n ? j0 + jj : j0] * H + 8 * tid;
+                xv[jj][0] = *(const f4 *)src;
+                xv[jj][1] = *(const f4 *)(src + 4);
+            }
+#pragma unroll
+            for (int jj = 0; jj < 4; jj++) {
+                const int j = j0 + jj;
+                h2 o[4] = {h2{(_Float16)xv[jj][0].x, (_Float16)xv[jj][0].y}, h2{(_Float16)xv[jj][0].z, (_Float16)xv[jj][0].w},
+                           h2{(_Float16)xv[jj][1].x, (_Float16)xv[jj][1].y}, h2{(_Float16)xv[jj][1].z, (_Float16)xv[jj][1].w}};
+                float s8 = 0.0f;
+#pragma unroll
+                for (int v = 0; v < 4; v++) s8 = dot2(o[v], one, s8);
+                const float s16 = s8 + dppf<DPP_XOR1>(s8);
+                if (j < n) { /* each 4-group stored (0,2,1,3) */
+                    const h2 p0 = {o[0].x, o[1].x}, p1 = {o[0].y, o[1].y}, p2 = {o[2].x, o[3].x}, p3 = {o[2].y, o[3].y};
+                    *(u4 *)(xs + (size_t)j * (16 * GB_SEG) + (tid >> 4) * GB_SEG + 8 * (tid & 15)) =
+                        u4{as_u32(p0), as_u32(p1), as_u32(p2), as_u32(p3)};
+                    if ((tid & 1) == 0) xsum[j * (16 * GB_SUM) + (tid >> 4) * GB_SUM + ((tid & 15) >> 1)] = s16;
+                }
+            }
+        }
+    }
+    __syncthreads();
+    TSTAMP(2);
+    /* outputs wait in LDS (no global stores between the ring's loads) */
+    _Float16 *obuf = xs + (size_t)T * 16 * GB_SEG + (size_t)T * 16 * GB_SUM * 2;
+    const int ntile = sh ? 1 : GB_ITER;
+    gb_run(t0, t1, wg, wu, tile_step, ntile, cl, q, wv, n, xs, xsum, obuf);
+    __syncthreads();
+    /* obuf[j][r] holds act for token j, block row r (GB_ITER * 16 rows) */
+    _Float16 *out = sh ? a.act_sh : a.act + (size_t)s0 * a.M;
+    const int ld = sh ? a.S : a.M;
+    for (int i = tid; i < n * GB_ROWS * GB_ITER; i += 256) {
+        if (sh && i % (GB_ROWS * GB_ITER) >= GB_ROWS) continue;
+        const int j = i / (GB_ROWS * GB_ITER), rr = i % (GB_ROWS * GB_ITER);
+        out[(size_t)j * ld + base + rr] = obuf[i];
+    }
+    TSTAMP(7);
+}
+
 /* =================================================================== */
 /* down.  One block = one active slot (routed expert or the shared expert) x
  * 8 output rows; each wave covers 4 rows with 16 lanes per row (a row pass
@@ -640,6 +866,28 @@ int launch_gemv_gate_up(const ExpertSide &ex, const SharedSide &sh, const RouteA
     const int umax = T * K < E ? T * K : E;
     a.routed_blocks = umax * (M / rows_blk);
     const int blocks = a.routed_blocks + (sh.gate ? sh.S / rows_blk : 0);
+    const int gb_rows = GB_ROWS * GB_ITER;
+    if (T >= 2 && T <= 8 && H == 2048 && M % gb_rows == 0 && (!sh.gate || (sh.gate_fmt == FQ4K && sh.S % gb_rows == 0))) {
+        a.routed_blocks = umax * (M / gb_rows);
+        const int gblocks = a.routed_blocks + (sh.gate ? sh.S / GB_ROWS : 0);
+        const size_t lds = (size_t)T * GB_TOK_BYTES;
+#define GB_LAUNCH(EPLV)                                                                                       \
+    do {                                                                                                      \
+        if (route_in_block)                                                                                   \
+            hipLaunchKernelGGL((k_gemv_gu_b<EPLV, true>), dim3(gblocks), dim3(256), lds, s, a, ra);           \
+        else                                                                                                  \
+            hipLaunchKernelGGL((k_gemv_gu_b<EPLV, false>), dim3(gblocks), dim3(256), lds, s, a, ra);          \
+    } while (0)
+        switch (epl_of(E)) {
+            case 1: GB_LAUNCH(1); break;
+            case 2: GB_LAUNCH(2); break;
+            case 4: GB_LAUNCH(4); break;
+            case 8: GB_LAUNCH(8); break;
+            default: GB_LAUNCH(16); break;
+        }
+#undef GB_LAUNCH
+        return hipGetLastError() == hipSuccess ? 0 : -3;
+    }
     if (route_in_block && T == 1 && H == 2048 && (!sh.gate || sh.gate_fmt == FQ4K)) {
 #define GU1_LAUNCH(EPLV) hipLaunchKernelGGL((k_gemv_gate_up1<EPLV>), dim3(blocks), dim3(256), 0, s, a, ra)
         switch (epl_of(E)) {
