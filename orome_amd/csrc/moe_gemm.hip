@@ -31,12 +31,26 @@
  */
 #include "dev_common.h"
 #include "kernels.h"
+#ifdef OROME_TRACE
+extern "C" __attribute__((visibility("default"))) int orome_trace_fetch_gemm(unsigned long long *h) {
+    return (int)hipMemcpyFromSymbol(h, HIP_SYMBOL(g_trace), sizeof(g_trace));
+}
+#endif
 
 enum { FQ4K = 0, FQ6K = 2, FQ8 = 3 };
 
 typedef float f4v __attribute__((ext_vector_type(4)));
 
-#define WAVES 8                         /* waves per block */
+/* Block shape per tile size.  Small tiles (<= 32 tokens: the HBM-bound
+ * regime) run 4-wave blocks with a 2-deep weight ring, so four waves share
+ * a SIMD; big tiles run 8-wave blocks with a 4-deep ring (their LDS tile
+ * allows one block per CU). */
+template <int TBM>
+struct Shape {
+    static constexpr int W = TBM <= 2 ? 4 : 8;     /* waves per block */
+    static constexpr int DEPTH = TBM <= 2 ? 2 : 4; /* weight stages in flight per wave */
+    static constexpr int CHV = 8 / W;              /* chunk vectors per token block and thread */
+};
 #define KC 128                          /* k per stage (one A fragment set) */
 #define KCH 256                         /* k per LDS activation chunk */
 #define BLD (KCH + 8)                   /* chunk row pitch (halves) */
@@ -130,11 +144,13 @@ struct Span<FQ4K> {
     /* k order of the result: l, l+2, l+1, l+3, l+32, l+34, l+33, l+35 */
     MDEV h8 frag(int s) const {
         const uint32_t w = u4_at(q, s);
-        /* bytes 1 and 3 under the 0x64 exponent byte: (0x64 b1, 0x64 b3) */
+        /* bytes 1 and 3 under the 0x64 exponent byte: (0x64 b1, 0x64 b3);
+         * bytes 0 and 2 masked and OR-ed under it in one three-input op
+         * (truth table 0xEA: (a & b) | c) */
         const uint32_t p13 = __builtin_amdgcn_perm(0x64646464u, w, 0x04030401u);
-        const h2 t0 = hfma(or_bias(w & 0x000F000Fu), splat(sc.x), splat(nc.x));
+        const h2 t0 = hfma(as_h2(__builtin_amdgcn_bitop3_b32(w, 0x000F000Fu, 0x64006400u, 0xEA)), splat(sc.x), splat(nc.x));
         const h2 t1 = hfma(as_h2(p13 & 0xFF0FFF0Fu), splat(sc.x), splat(nc.x));
-        const h2 t2 = hfma(or_bias(w & 0x00F000F0u), splat(sc.y), splat(nc.y));
+        const h2 t2 = hfma(as_h2(__builtin_amdgcn_bitop3_b32(w, 0x00F000F0u, 0x64006400u, 0xEA)), splat(sc.y), splat(nc.y));
         const h2 t3 = hfma(as_h2(p13 & 0xFFF0FFF0u), splat(sc.y), splat(nc.y));
         return cat4(hfma(t0, d, splat(mb.x)), hfma(t1, d, splat(mb.x)), hfma(t2, d, splat(mb.y)),
                     hfma(t3, d, splat(mb.y)));
@@ -208,20 +224,21 @@ DEV f4v mfma(h8 a, h8 b, f4v c) { return __builtin_amdgcn_mfma_f32_16x16x32_f16(
  * select. */
 template <int TBM>
 struct Chunk {
-    u4 v[TBM];
+    static constexpr int W = Shape<TBM>::W, CHV = Shape<TBM>::CHV;
+    u4 v[TBM * CHV];
     MDEV void fetch(const _Float16 *src, const int *rowoff, int ld, int k0) {
         const int cc = (threadIdx.x & 31) * 8;
 #pragma unroll
-        for (int n = 0; n < TBM; n++)
-            v[n] = ld_u4((const uint8_t *)(src + (size_t)rowoff[16 * n + (threadIdx.x >> 5)] * ld + k0 + cc));
+        for (int n = 0; n < TBM * CHV; n++)
+            v[n] = ld_u4((const uint8_t *)(src + (size_t)rowoff[(W * 2) * n + (threadIdx.x >> 5)] * ld + k0 + cc));
     }
     template <int FMT>
     MDEV void store(_Float16 *xs) const {
         const int col = threadIdx.x & 31, half = col >> 4, c0 = (col & 15) * 2;
         const int p0 = half * KC + frag_pos<FMT>(c0), p1 = half * KC + frag_pos<FMT>(c0 + 1);
 #pragma unroll
-        for (int n = 0; n < TBM; n++) {
-            _Float16 *row = xs + (16 * n + (threadIdx.x >> 5)) * BLD;
+        for (int n = 0; n < TBM * CHV; n++) {
+            _Float16 *row = xs + ((W * 2) * n + (threadIdx.x >> 5)) * BLD;
             *(u2 *)(row + p0) = u2{v[n].x, v[n].y};
             *(u2 *)(row + p1) = u2{v[n].z, v[n].w};
         }
@@ -229,7 +246,7 @@ struct Chunk {
 };
 
 /* ------------------------------------------------------------- tile */
-/* One block: WAVES waves, wave w owns RPW row blocks of 16 rows (rows
+/* One block: Shape<TBM>::W waves, wave w owns RPW row blocks of 16 rows (rows
  * yb*NB + (w*RPW + rb)*16 ..) of NMAT matrices (gate+up, or down).
  * A wave walks units u = (rb, stage j) in order, stage j = 128 k; weight
  * bytes for unit u+DEPTH are in flight while unit u computes.  Activation
@@ -247,7 +264,7 @@ DEV void tile_run(const uint8_t *w0, const uint8_t *w1, int in_dim, const _Float
      * completely and the prefetch ring never crosses a loop back-edge (where
      * the register copies would wait for every load in flight) */
     const int nst = NST ? NST : in_dim / KC, nch = nst / 2, U = RPW * nst;
-    const int rbase = yb * (WAVES * 16 * RPW) + wv * 16 * RPW;
+    const int rbase = yb * (Shape<TBM>::W * 16 * RPW) + wv * 16 * RPW;
     const uint8_t *rw0 = w0 + (size_t)(rbase + i) * rbytes;
     const uint8_t *rw1 = NMAT > 1 ? w1 + (size_t)(rbase + i) * rbytes : nullptr;
 
@@ -273,6 +290,7 @@ DEV void tile_run(const uint8_t *w0, const uint8_t *w1, int in_dim, const _Float
     }
     if (nch > 2) ch.fetch(src, rowoff, ld, 2 * KCH);
     __syncthreads();
+    if (threadIdx.x == 0) TSTAMP(1);
 
     f4v c[NMAT][TBM];
 #pragma unroll
@@ -307,20 +325,27 @@ DEV void tile_run(const uint8_t *w0, const uint8_t *w1, int in_dim, const _Float
             for (int s = 0; s < 4; s++) {
                 h8 a[NMAT];
 #pragma unroll
-                for (int m = 0; m < NMAT; m++) a[m] = cur[m].frag(s);
+                for (int m = 0; m < NMAT; m++) {
+                    a[m] = cur[m].frag(s);
+                }
                 /* B reads for every token block (rows past the tile hold
                  * zeros): straight-line LDS traffic the scheduler can hoist */
                 h8 b[TBM];
 #pragma unroll
-                for (int t = 0; t < TBM; t++) b[t] = *(const h8 *)(bp + t * 16 * BLD + s * 32);
+                for (int t = 0; t < TBM; t++) {
+                    b[t] = *(const h8 *)(bp + t * 16 * BLD + s * 32);
+                }
                 /* every token block, also past the tile (zero rows): no
                  * branches between the matrix instructions, so the scheduler
                  * can interleave them with the next step's dequant */
 #pragma unroll
                 for (int t = 0; t < TBM; t++)
 #pragma unroll
-                    for (int m = 0; m < NMAT; m++) c[m][t] = mfma(a[m], b[t], c[m][t]);
+                    for (int m = 0; m < NMAT; m++) {
+                        c[m][t] = mfma(a[m], b[t], c[m][t]);
+                    }
             }
+            if (threadIdx.x == 0 && (j & 3) == 3 && j < 16) TSTAMP(2 + (j >> 2));
             if (j == nst - 1) {
                 epi.template operator()<TBM>(c, rbase + rb * 16 + 4 * kg, tb);
 #pragma unroll
@@ -397,26 +422,21 @@ struct DnEpi {
 };
 
 /* row blocks per wave and weight stages in flight per wave */
-#ifndef GU_DEPTH
-#define GU_DEPTH 4 /* Q8_0 (shared expert) spans are larger: depth 2 */
-#endif
-#ifndef DN_DEPTH
-#define DN_DEPTH 4
-#endif
 #define GU_RPW 1
 #define DN_RPW 4
 
 template <int SFMT, int NST, int TBM>
-__global__ __launch_bounds__(WAVES * 64) void k_gemm_gate_up(GemmArgs a) {
+__global__ __launch_bounds__(Shape<TBM>::W * 64) void k_gemm_gate_up(GemmArgs a) {
     __shared__ __attribute__((aligned(16))) _Float16 xs[2 * TBM * 16 * BLD];
     __shared__ int rowoff[TBM * 16];
     int ti, yb;
     block_tile(a.nyb, ti, yb);
     const uint32_t nt = a.tiles[0];
     if ((uint32_t)ti >= nt) return;
+    if (threadIdx.x == 0) TSTAMP(0);
     const uint32_t e = a.tiles[1 + 3 * ti], first = a.tiles[2 + 3 * ti], rows = a.tiles[3 + 3 * ti];
     const bool sh = e == (uint32_t)a.E;
-    if (yb * (WAVES * 16 * GU_RPW) >= (sh ? a.S : a.M)) return;
+    if (yb * (Shape<TBM>::W * 16 * GU_RPW) >= (sh ? a.S : a.M)) return;
     if (threadIdx.x < TBM * 16) { /* rows past the tile read the zero row */
         const uint32_t q = threadIdx.x;
         rowoff[threadIdx.x] = q >= rows ? a.zrow : sh ? (int)(first + q) : (int)(a.pairs[first + q] / (uint32_t)a.K);
@@ -424,16 +444,17 @@ __global__ __launch_bounds__(WAVES * 64) void k_gemm_gate_up(GemmArgs a) {
     __syncthreads();
     if (sh) {
         const GuEpi epi{a.act_sh, a.S, (int)first, (int)rows};
-        tile_run<SFMT, 2, GU_RPW, (SFMT == FQ8 ? 2 : GU_DEPTH), NST, TBM>(a.sh_a, a.sh_b, a.H, a.src, a.H, rowoff, (int)rows, yb, xs, epi);
+        tile_run<SFMT, 2, GU_RPW, (SFMT == FQ8 ? 2 : Shape<TBM>::DEPTH), NST, TBM>(a.sh_a, a.sh_b, a.H, a.src, a.H, rowoff, (int)rows, yb, xs, epi);
     } else {
         const GuEpi epi{a.act, a.M, (int)first, (int)rows};
-        tile_run<FQ4K, 2, GU_RPW, GU_DEPTH, NST, TBM>(a.wa + (size_t)e * a.stride_a, a.wb + (size_t)e * a.stride_b, a.H, a.src,
+        tile_run<FQ4K, 2, GU_RPW, Shape<TBM>::DEPTH, NST, TBM>(a.wa + (size_t)e * a.stride_a, a.wb + (size_t)e * a.stride_b, a.H, a.src,
                                   a.H, rowoff, (int)rows, yb, xs, epi);
     }
+    if (threadIdx.x == 0) TSTAMP(6);
 }
 
 template <int EFMT, int SFMT, int NST, int TBM>
-__global__ __launch_bounds__(WAVES * 64) void k_gemm_down(GemmArgs a) {
+__global__ __launch_bounds__(Shape<TBM>::W * 64) void k_gemm_down(GemmArgs a) {
     __shared__ __attribute__((aligned(16))) _Float16 xs[2 * TBM * 16 * BLD];
     __shared__ int rowoff[TBM * 16];
     int ti, yb;
@@ -447,10 +468,10 @@ __global__ __launch_bounds__(WAVES * 64) void k_gemm_down(GemmArgs a) {
     __syncthreads();
     if (sh) {
         const DnEpi epi{a.ysh, a.H, (int)first, (int)rows};
-        tile_run<SFMT, 1, DN_RPW, DN_DEPTH, NST, TBM>(a.sh_a, nullptr, a.S, a.src_sh, a.S, rowoff, (int)rows, yb, xs, epi);
+        tile_run<SFMT, 1, DN_RPW, Shape<TBM>::DEPTH, NST, TBM>(a.sh_a, nullptr, a.S, a.src_sh, a.S, rowoff, (int)rows, yb, xs, epi);
     } else {
         const DnEpi epi{a.y, a.H, (int)first, (int)rows};
-        tile_run<EFMT, 1, DN_RPW, DN_DEPTH, NST, TBM>(a.wa + (size_t)e * a.stride_a, nullptr, a.M, a.src, a.M, rowoff, (int)rows, yb, xs, epi);
+        tile_run<EFMT, 1, DN_RPW, Shape<TBM>::DEPTH, NST, TBM>(a.wa + (size_t)e * a.stride_a, nullptr, a.M, a.src, a.M, rowoff, (int)rows, yb, xs, epi);
     }
 }
 
@@ -458,8 +479,9 @@ __global__ __launch_bounds__(WAVES * 64) void k_gemm_down(GemmArgs a) {
 int launch_gemm_gate_up(const ExpertSide &ex, const SharedSide &sh, const _Float16 *x16, int zrow, int T,
                         int H, int M, int K, int E, int tile_m, const uint32_t *tiles, int n_tiles_max,
                         const uint32_t *pairs, _Float16 *act, _Float16 *act_sh, hipStream_t s) {
-    const int NB = WAVES * 16 * GU_RPW;
-    if ((H / KC * GU_RPW) % GU_DEPTH) return -2;
+    const int W = tile_m == GEMM_TILE_SMALL ? Shape<GEMM_TILE_SMALL / 16>::W : Shape<GEMM_TILE_BIG / 16>::W;
+    const int NB = W * 16 * GU_RPW;
+    if ((H / KC * GU_RPW) % 4) return -2; /* every ring depth used divides the unit count */
     if (H % KCH || M % NB || (sh.gate && sh.S % NB) || ex.gate_fmt != FQ4K) return -2;
     if (sh.gate && sh.gate_fmt != FQ4K && sh.gate_fmt != FQ8) return -2;
     GemmArgs a = {};
@@ -469,7 +491,7 @@ int launch_gemm_gate_up(const ExpertSide &ex, const SharedSide &sh, const _Float
     a.zrow = zrow; a.zrow_sh = zrow;
     a.tiles = tiles; a.pairs = pairs; a.act = act; a.act_sh = act_sh;
     a.nyb = (M > a.S ? M : a.S) / NB;
-    const dim3 grid((unsigned)((n_tiles_max + 7) / 8 * 8 * a.nyb)), block(WAVES * 64);
+    const dim3 grid((unsigned)((n_tiles_max + 7) / 8 * 8 * a.nyb)), block(W * 64);
     const bool q8 = sh.gate && sh.gate_fmt == FQ8;
     if (tile_m != GEMM_TILE_SMALL && tile_m != GEMM_TILE_BIG) return -2;
     /* compile-time stage count for the common hidden size (Q4_K shared
@@ -489,8 +511,9 @@ int launch_gemm_gate_up(const ExpertSide &ex, const SharedSide &sh, const _Float
 int launch_gemm_down(const ExpertSide &ex, const SharedSide &sh, const _Float16 *act,
                      const _Float16 *act_sh, int zrow, int zrow_sh, int T, int H, int M, int K, int E, int tile_m,
                      const uint32_t *tiles, int n_tiles_max, float *y, float *ysh, hipStream_t s) {
-    const int NB = WAVES * 16 * DN_RPW;
-    if ((M / KC * DN_RPW) % DN_DEPTH || (sh.gate && (sh.S / KC * DN_RPW) % DN_DEPTH)) return -2;
+    const int W = tile_m == GEMM_TILE_SMALL ? Shape<GEMM_TILE_SMALL / 16>::W : Shape<GEMM_TILE_BIG / 16>::W;
+    const int NB = W * 16 * DN_RPW;
+    if ((M / KC * DN_RPW) % 4 || (sh.gate && (sh.S / KC * DN_RPW) % 4)) return -2;
     /* all of a tile's activations stay resident: in_dim <= 2 chunks */
     if (H % NB || M % KCH || M > 2 * KCH || (sh.gate && (sh.S % KCH || sh.S > 2 * KCH))) return -2;
     if (ex.down_fmt != FQ4K && ex.down_fmt != FQ6K) return -2;
@@ -503,7 +526,7 @@ int launch_gemm_down(const ExpertSide &ex, const SharedSide &sh, const _Float16 
     a.zrow = zrow; a.zrow_sh = zrow_sh;
     a.tiles = tiles; a.y = y; a.ysh = ysh;
     a.nyb = H / NB;
-    const dim3 grid((unsigned)((n_tiles_max + 7) / 8 * 8 * a.nyb)), block(WAVES * 64);
+    const dim3 grid((unsigned)((n_tiles_max + 7) / 8 * 8 * a.nyb)), block(W * 64);
     /* generic unit loop (a compile-time stage count spills here) */
     if (tile_m != GEMM_TILE_SMALL && tile_m != GEMM_TILE_BIG) return -2;
 #define DN_LAUNCH(EF, SF)                                                                    \

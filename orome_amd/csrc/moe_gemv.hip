@@ -27,7 +27,6 @@
 #include "kernels.h"
 #include "route_dev.h"
 #ifdef OROME_TRACE
-__device__ unsigned long long g_trace[65536 * 8];
 extern "C" __attribute__((visibility("default"))) int orome_trace_fetch(unsigned long long *h) {
     return (int)hipMemcpyFromSymbol(h, HIP_SYMBOL(g_trace), sizeof(g_trace));
 }
