@@ -53,7 +53,7 @@ struct Shape {
 };
 #define KC 128                          /* k per stage (one A fragment set) */
 #define KCH 256                         /* k per LDS activation chunk */
-#define BLD (KCH + 8)                   /* chunk row pitch (halves) */
+#define BLD (KCH + 16)                  /* chunk row pitch (halves): 544 bytes, B-fragment reads conflict-free */
 
 DEV size_t gemm_row_bytes(int fmt, int n) {
     return fmt == FQ4K ? (size_t)(n / 256) * 144 : fmt == FQ6K ? (size_t)(n / 256) * 210 : (size_t)(n / 32) * 34;
@@ -216,7 +216,8 @@ DEV f4v mfma(h8 a, h8 b, f4v c) { return __builtin_amdgcn_mfma_f32_16x16x32_f16(
 
 /* ------------------------------------------------------- B chunks */
 /* A chunk is KCH (256) k of the tile's token rows in LDS, row pitch BLD
- * halves (132 dwords: 16 rows x 16 bytes per lane group hit distinct banks),
+ * halves (136 dwords; measured conflict-free for the B-fragment reads, where
+ * a 132-dword pitch doubles the LDS cycles),
  * each 128-k half in the fragment order of FMT.  A thread's vector n covers
  * token 16n + tid/32, k 8 (tid%32) .. +7.  Every thread loads and stores all
  * TBM vectors: rows past the tile read an all-zero row, so the code stays
