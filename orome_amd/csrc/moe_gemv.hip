@@ -846,6 +846,91 @@ __global__ __launch_bounds__(128) void k_gemv_down_combine1(DownArgs a, RouteArg
     }
 }
 
+/* Activation values of chunk c of one token, loaded once and used for
+ * every weight row of the lane (the DnRaw<FMT> chunk layouts). */
+template <int FMT>
+struct DnX;
+template <>
+struct DnX<FQ4K> {
+    h2 xl[8], xh[8];
+    float Xl, Xh;
+    MDEV void load(int c, const _Float16 *x) {
+        int klo;
+        q4_pos(c, klo);
+        load_h8(x + klo, xl);
+        load_h8(x + klo + 8, xl + 4);
+        load_h8(x + klo + 32, xh);
+        load_h8(x + klo + 40, xh + 4);
+        Xl = hsum(xl, 8);
+        Xh = hsum(xh, 8);
+    }
+    MDEV float dot(const DnRaw<FQ4K> &r, int c) const { return q4_dot(r.r, c, xl, xh, Xl, Xh); }
+};
+template <>
+struct DnX<FQ6K> {
+    h2 x[16];
+    MDEV void load(int c, const _Float16 *xr) {
+        int k0;
+        q6_pos(c, k0);
+#pragma unroll
+        for (int gq = 0; gq < 4; gq++) load_h8(xr + k0 + 32 * gq, x + 4 * gq);
+    }
+    MDEV float dot(const DnRaw<FQ6K> &r, int c) const { return q6_dot(r.r, c, x); }
+};
+template <>
+struct DnX<FQ8> {
+    h2 x[16];
+    MDEV void load(int c, const _Float16 *xr) {
+#pragma unroll
+        for (int gq = 0; gq < 4; gq++) load_h8(xr + c * 32 + 8 * gq, x + 4 * gq);
+    }
+    MDEV float dot(const DnRaw<FQ8> &r, int) const { return q8_dot(r.r, x); }
+};
+
+/* Batched down (T <= 8, in_dim = 512): a block = 4 waves = 64 output rows of
+ * one slot (an active routed expert, or the shared expert over all T
+ * tokens, last); a 16-lane DPP row takes DB_R consecutive weight rows, lane
+ * cl chunk cl of each (all DB_R chunks loaded at once), and walks the slot's
+ * tokens with each token's activation chunk loaded once for all its rows.
+ * Same sums as k_gemv_down; results go to y[sorted position][H] and
+ * ysh[t][H]. */
+#ifndef DB_R
+#define DB_R 2
+#endif
+#define DB_ROWS (4 * 4 * DB_R)
+template <int FMT>
+DEV void db_run(const uint8_t *w, size_t rb, int r0, int cl, int n, const _Float16 *x0, int x_ld, float *out,
+                int H) {
+    DnRaw<FMT> raw[DB_R];
+#pragma unroll
+    for (int r = 0; r < DB_R; r++) raw[r].load(w + (size_t)(r0 + r) * rb, cl);
+#pragma unroll 1
+    for (int j = 0; j < n; j++) {
+        DnX<FMT> xv;
+        xv.load(cl, x0 + (size_t)j * x_ld);
+#pragma unroll
+        for (int r = 0; r < DB_R; r++) {
+            const float v = row_sum16(xv.dot(raw[r], cl));
+            if (cl == 0) out[(size_t)j * H + r0 + r] = v;
+        }
+    }
+}
+template <int EFMT, int SFMT>
+__global__ __launch_bounds__(256) void k_gemv_down_b(DownArgs a) {
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, cl = lane & 15, q = lane >> 4;
+    const int bps = a.H / DB_ROWS, u = blockIdx.x / bps;
+    const int r0 = (blockIdx.x % bps) * DB_ROWS + wv * (4 * DB_R) + q * DB_R;
+    const uint32_t nact = ACT_N(a.list), eu = ACT_E(a.list, u), o0 = ACT_OFF(a.list, a.E, u),
+                   o1 = ACT_OFF(a.list, a.E, u + 1);
+    const bool has_sh = a.sh_down != nullptr;
+    if ((uint32_t)u > nact || ((uint32_t)u == nact && !has_sh)) return;
+    if ((uint32_t)u == nact)
+        db_run<SFMT>(a.sh_down, row_bytes(SFMT, a.S), r0, cl, a.T, a.act_sh, a.S, a.ysh, a.H);
+    else
+        db_run<EFMT>(a.down + (size_t)eu * a.down_stride, row_bytes(EFMT, a.M), r0, cl, (int)(o1 - o0),
+                     a.act + (size_t)o0 * a.M, a.M, a.y + (size_t)o0 * a.H, a.H);
+}
+
 /* ------------------------------------------------------------ launch */
 
 static int epl_of(int E) { return E <= 64 ? 1 : E <= 128 ? 2 : E <= 256 ? 4 : E <= 512 ? 8 : E <= 1024 ? 16 : 0; }
@@ -932,6 +1017,22 @@ int launch_gemv_down(const ExpertSide &ex, const SharedSide &sh, const _Float16 
     a.act = act; a.act_sh = act_sh; a.T = T; a.H = H; a.M = M; a.K = K; a.E = E;
     a.list = list; a.y = y; a.ysh = ysh;
     const int umax = T * K < E ? T * K : E;
+    if (M == 512 && (!sh.gate || sh.S == 512) && H % DB_ROWS == 0) {
+        const dim3 g((unsigned)((umax + (sh.gate ? 1 : 0)) * (H / DB_ROWS)));
+        const int sf = sh.gate ? sh.down_fmt : FQ4K;
+#define DB_LAUNCH(EF, SF) hipLaunchKernelGGL((k_gemv_down_b<EF, SF>), g, dim3(256), 0, s, a)
+        if (ex.down_fmt == FQ4K) {
+            if (sf == FQ4K) DB_LAUNCH(FQ4K, FQ4K);
+            else if (sf == FQ6K) DB_LAUNCH(FQ4K, FQ6K);
+            else DB_LAUNCH(FQ4K, FQ8);
+        } else {
+            if (sf == FQ4K) DB_LAUNCH(FQ6K, FQ4K);
+            else if (sf == FQ6K) DB_LAUNCH(FQ6K, FQ6K);
+            else DB_LAUNCH(FQ6K, FQ8);
+        }
+#undef DB_LAUNCH
+        return hipGetLastError() == hipSuccess ? 0 : -3;
+    }
     dim3 grid((umax + (sh.gate ? 1 : 0)) * (H / 8));
     switch (NT) {
         case 1: hipLaunchKernelGGL(k_gemv_down<1>, grid, dim3(128), 0, s, a); break;
