@@ -98,7 +98,10 @@ DEV float group_sum(float v) {
     return row_sum16(v);
 }
 
-DEV float silu_f(float g) { return g / (1.0f + __expf(-g)); }
+/* SiLU with the hardware reciprocal (1 ulp) instead of the IEEE divide
+ * sequence: the result is rounded to fp16 right after, and g -> -inf still
+ * gives -0 (rcp(inf) = 0) */
+DEV float silu_f(float g) { return g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)); }
 DEV float sigmoid_f(float s) { return 1.0f / (1.0f + expf(-s)); }
 
 /* --------------------------------------------------------------- Q4_K */

@@ -29,6 +29,7 @@
  * activations and weight bytes are fetched to registers before the current
  * stage's matrix work.
  */
+#include <cstdlib>
 #include "dev_common.h"
 #include "kernels.h"
 #ifdef OROME_TRACE
@@ -426,6 +427,226 @@ struct DnEpi {
 #define GU_RPW 1
 #define DN_RPW 4
 
+/* --------------------------------------------------- persistent stream */
+/* A unit is one (tile, row block) of a tile list; uniform over the block. */
+struct UnitDesc {
+    int valid, sh, first, rows, yb;
+    uint32_t e;
+};
+
+/* The n-th unit of this block.  Units of tiles t = xcd (mod 8) go to the
+ * blocks of that XCD (work-groups are dealt to the 8 XCDs round-robin by
+ * linear id), so the row blocks of one tile share an L2 and run at about the
+ * same time; within an XCD, block `slot` takes units slot, slot + bpx, ... */
+DEV UnitDesc unit_desc(const uint32_t *tiles, int nyb, int E, int n) {
+    const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3, bpx = gridDim.x >> 3;
+    const int q = slot + n * bpx, ti = 8 * (q / nyb) + xcd;
+    /* the list is read-only here: constant address space, so the uniform
+     * reads are scalar loads and do not wait behind the weight loads */
+    typedef const __attribute__((address_space(4))) uint32_t cu32;
+    cu32 *tl = (cu32 *)(uintptr_t)tiles;
+    UnitDesc u;
+    u.valid = (uint32_t)ti < tl[0];
+    u.yb = q % nyb;
+    const int tc = u.valid ? ti : 0; /* entry 0 exists whenever the list is read */
+    u.e = u.valid ? tl[1 + 3 * tc] : 0u;
+    u.first = u.valid ? (int)tl[2 + 3 * tc] : 0;
+    u.rows = u.valid ? (int)tl[3 + 3 * tc] : 0;
+    u.sh = u.e == (uint32_t)E;
+    return u;
+}
+
+/* Persistent form of tile_run: the block walks its units back to back and
+ * the weight ring and the activation chunk stream run on across unit
+ * boundaries, so only the first unit waits for its loads.  Per unit the
+ * arithmetic is exactly tile_run's (same fragments, same MFMA order).
+ *   - weight stage u + DEPTH of unit n is unit n+1's stage u + DEPTH - U;
+ *   - global chunk C = n * nch + c sits in LDS buffer C & 1 (nch even); at
+ *     the barrier that ends chunk C, chunk C + 2 is stored and C + 3 fetched,
+ *     whichever unit they belong to;
+ *   - token row offsets of unit n sit in LDS slot n % 3, written at the start
+ *     of unit n - 2 (units past the end point every row at the zero row, so
+ *     loads and stores stay unconditional).
+ * P supplies the unit's weight and source pointers, row offsets and
+ * epilogue. */
+template <int FMT, int NMAT, int RPW, int DEPTH, int NST, int TBM, typename P>
+DEV void tile_stream(const P &pol, _Float16 *xs, int *rowoff) {
+    constexpr int W = Shape<TBM>::W, TR = TBM * 16, nst = NST, nch = NST / 2, U = RPW * NST;
+    static_assert(NST % 4 == 0 && U % DEPTH == 0 && (RPW == 1 || nch == 2), "stream shape");
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int kg = lane >> 4, i = lane & 15;
+    const size_t rbytes = gemm_row_bytes(FMT, pol.in_dim());
+#ifdef OROME_TRACE
+    const unsigned long long t_start = __builtin_amdgcn_s_memrealtime();
+#endif
+    UnitDesc cu = pol.desc(0), nu = pol.desc(1);
+    if (!cu.valid) return;
+    /* this lane's weight row in matrix m of unit u (row block 0, stage 0);
+     * a unit past the end reuses `other` (its loads are never consumed) */
+    auto wrow = [&](const UnitDesc &u, int m, const uint8_t *other) -> const uint8_t * {
+        return u.valid ? pol.weights(u, m) + (size_t)(u.yb * (W * 16 * RPW) + wv * 16 * RPW + i) * rbytes : other;
+    };
+    if (threadIdx.x < TR) {
+        rowoff[threadIdx.x] = pol.row_fin(cu, pol.row_raw(cu, (int)threadIdx.x));
+        rowoff[TR + threadIdx.x] = pol.row_fin(nu, pol.row_raw(nu, (int)threadIdx.x));
+    }
+    __syncthreads();
+
+    const uint8_t *cw[NMAT], *nw[NMAT];
+#pragma unroll
+    for (int m = 0; m < NMAT; m++) {
+        cw[m] = wrow(cu, m, nullptr);
+        nw[m] = wrow(nu, m, cw[m]);
+    }
+    Span<FMT> ring[DEPTH][NMAT];
+#pragma unroll
+    for (int d = 0; d < DEPTH; d++) {
+        const int rb = d / nst, j = d - rb * nst;
+#pragma unroll
+        for (int m = 0; m < NMAT; m++) {
+            ring[d][m].init(kg);
+            ring[d][m].load(cw[m] + (size_t)rb * 16 * rbytes, j, kg);
+        }
+    }
+    /* chunks 0, 1 of unit 0 into the two buffers, chunk 2 of the stream
+     * (unit 0's when nch > 2, else unit 1's chunk 0) into registers */
+    Chunk<TBM> ch;
+    ch.fetch(pol.src(cu), rowoff, pol.ld(), 0);
+    ch.template store<FMT>(xs);
+    ch.fetch(pol.src(cu), rowoff, pol.ld(), KCH);
+    ch.template store<FMT>(xs + TR * BLD);
+    if (nch > 2) ch.fetch(pol.src(cu), rowoff, pol.ld(), 2 * KCH);
+    else ch.fetch(pol.src(nu), rowoff + TR, pol.ld(), 0);
+    __syncthreads();
+
+    f4v c[NMAT][TBM];
+#pragma unroll
+    for (int m = 0; m < NMAT; m++)
+#pragma unroll
+        for (int t = 0; t < TBM; t++) c[m][t] = f4v{0, 0, 0, 0};
+
+    for (int n = 0;; n++) {
+        /* unit n + 2: its row offsets are read here (a global load for
+         * routed gate/up rows) and stored into LDS slot (n + 2) % 3 after the
+         * first barrier of this unit, so the load's wait comes stages later.
+         * That slot was last read by fetches issued in unit n - 1. */
+        const UnitDesc fu = pol.desc(n + 2);
+        const int s1 = (n + 1) % 3, s2 = (n + 2) % 3;
+        const uint32_t ro = threadIdx.x < TR ? pol.row_raw(fu, (int)threadIdx.x) : 0u;
+#pragma unroll
+        for (int u0 = 0; u0 < U; u0 += DEPTH) {
+#pragma unroll
+            for (int d = 0; d < DEPTH; d++) {
+                const int u = u0 + d;
+                const int rb = u / nst, j = u - rb * nst;
+                __builtin_amdgcn_sched_barrier(0);
+                asm volatile("" ::: "memory");
+                Span<FMT> cur[NMAT];
+#pragma unroll
+                for (int m = 0; m < NMAT; m++) {
+                    cur[m] = ring[d][m];
+                    cur[m].prepare(j, kg);
+                }
+                {
+                    /* stage u + DEPTH: of this unit, else of the next */
+                    const bool here = u + DEPTH < U;
+                    const int u2 = here ? u + DEPTH : u + DEPTH - U;
+                    const int rb2 = u2 / nst, j2 = u2 - rb2 * nst;
+#pragma unroll
+                    for (int m = 0; m < NMAT; m++) ring[d][m].load((here ? cw[m] : nw[m]) + (size_t)rb2 * 16 * rbytes, j2, kg);
+                }
+                const _Float16 *bp = xs + ((j >> 1) & 1) * (TR * BLD) + (j & 1) * KC + i * BLD + kg * 8;
+#pragma unroll
+                for (int s = 0; s < 4; s++) {
+                    h8 a[NMAT];
+#pragma unroll
+                    for (int m = 0; m < NMAT; m++) a[m] = cur[m].frag(s);
+                    h8 b[TBM];
+#pragma unroll
+                    for (int t = 0; t < TBM; t++) b[t] = *(const h8 *)(bp + t * 16 * BLD + s * 32);
+#pragma unroll
+                    for (int t = 0; t < TBM; t++)
+#pragma unroll
+                        for (int m = 0; m < NMAT; m++) c[m][t] = mfma(a[m], b[t], c[m][t]);
+                }
+                if (j == nst - 1) {
+                    pol.epilogue(cu, c, cu.yb * (W * 16 * RPW) + wv * 16 * RPW + rb * 16 + 4 * kg, (cu.rows + 15) >> 4);
+#pragma unroll
+                    for (int m = 0; m < NMAT; m++)
+#pragma unroll
+                        for (int t = 0; t < TBM; t++) c[m][t] = f4v{0, 0, 0, 0};
+                }
+                if (rb == RPW - 1 && (j & 1)) {
+                    /* end of chunk C = n nch + cc: store chunk C + 2 into
+                     * C's buffer, fetch chunk C + 3 (of unit n + off) */
+                    const int cc = j >> 1, c3 = cc + 3, off = c3 / nch;
+                    __syncthreads();
+                    if (cc == 0 && threadIdx.x < TR) rowoff[s2 * TR + threadIdx.x] = pol.row_fin(fu, ro);
+                    ch.template store<FMT>(xs + (cc & 1) * (TR * BLD));
+                    const UnitDesc &tu = off == 0 ? cu : off == 1 ? nu : fu;
+                    const int slot = off == 0 ? n % 3 : off == 1 ? s1 : s2;
+                    ch.fetch(pol.src(tu), rowoff + slot * TR, pol.ld(), (c3 % nch) * KCH);
+                }
+            }
+        }
+#ifdef OROME_TRACE
+        if (threadIdx.x == 0 && n < 7 && NMAT == 2) {
+            g_trace[blockIdx.x * 8 + 1 + n] = __builtin_amdgcn_s_memrealtime();
+            if (n == 0) g_trace[blockIdx.x * 8] = t_start;
+        }
+#endif
+        if (!nu.valid) break;
+        cu = nu;
+        nu = fu;
+#pragma unroll
+        for (int m = 0; m < NMAT; m++) {
+            cw[m] = nw[m];
+            nw[m] = wrow(nu, m, cw[m]);
+        }
+    }
+}
+
+struct GuPol {
+    const GemmArgs &a;
+    MDEV int in_dim() const { return a.H; }
+    MDEV int ld() const { return a.H; }
+    MDEV UnitDesc desc(int n) const { return unit_desc(a.tiles, a.nyb, a.E, n); }
+    MDEV const _Float16 *src(const UnitDesc &) const { return a.src; }
+    MDEV const uint8_t *weights(const UnitDesc &u, int m) const {
+        return u.sh ? (m ? a.sh_b : a.sh_a) : m ? a.wb + (size_t)u.e * a.stride_b : a.wa + (size_t)u.e * a.stride_a;
+    }
+    /* token row of tile row q in two steps (the pair load, then its use) */
+    MDEV uint32_t row_raw(const UnitDesc &u, int q) const {
+        if (!u.valid || q >= u.rows) return ~0u;
+        return u.sh ? (uint32_t)(u.first + q) : a.pairs[u.first + q];
+    }
+    MDEV int row_fin(const UnitDesc &u, uint32_t r) const {
+        return r == ~0u ? a.zrow : u.sh ? (int)r : (int)(r / (uint32_t)a.K);
+    }
+    template <int TBM>
+    MDEV void epilogue(const UnitDesc &u, const f4v (&c)[2][TBM], int r, int tb) const {
+        const GuEpi epi{u.sh ? a.act_sh : a.act, u.sh ? a.S : a.M, u.first, u.rows};
+        epi.template operator()<TBM>(c, r, tb);
+    }
+};
+
+struct DnPol {
+    const GemmArgs &a;
+    MDEV int in_dim() const { return a.M; }
+    MDEV int ld() const { return a.M; }
+    MDEV UnitDesc desc(int n) const { return unit_desc(a.tiles, a.nyb, a.E, n); }
+    MDEV const _Float16 *src(const UnitDesc &u) const { return u.sh ? a.src_sh : a.src; }
+    MDEV const uint8_t *weights(const UnitDesc &u, int) const { return u.sh ? a.sh_a : a.wa + (size_t)u.e * a.stride_a; }
+    MDEV uint32_t row_raw(const UnitDesc &u, int q) const { return !u.valid || q >= u.rows ? ~0u : (uint32_t)(u.first + q); }
+    MDEV int row_fin(const UnitDesc &u, uint32_t r) const { return r == ~0u ? (u.sh ? a.zrow_sh : a.zrow) : (int)r; }
+    template <int TBM>
+    MDEV void epilogue(const UnitDesc &u, const f4v (&c)[1][TBM], int r, int tb) const {
+        const DnEpi epi{u.sh ? a.ysh : a.y, a.H, u.first, u.rows};
+        epi.template operator()<TBM>(c, r, tb);
+    }
+};
+
+
 template <int SFMT, int NST, int TBM>
 __global__ __launch_bounds__(Shape<TBM>::W * 64) void k_gemm_gate_up(GemmArgs a) {
     __shared__ __attribute__((aligned(16))) _Float16 xs[2 * TBM * 16 * BLD];
@@ -476,6 +697,45 @@ __global__ __launch_bounds__(Shape<TBM>::W * 64) void k_gemm_down(GemmArgs a) {
     }
 }
 
+/* Persistent big-tile kernels: one block per CU walks its units (tile_stream).
+ * Shared expert in the routed format and of the routed width only. */
+#ifndef GEMM_PERSIST
+#define GEMM_PERSIST 1
+#endif
+template <int TBM>
+__global__ __launch_bounds__(Shape<TBM>::W * 64) void k_gemm_gate_up_p(GemmArgs a) {
+    __shared__ __attribute__((aligned(16))) _Float16 xs[2 * TBM * 16 * BLD];
+    __shared__ int rowoff[3 * TBM * 16];
+    tile_stream<FQ4K, 2, GU_RPW, Shape<TBM>::DEPTH, 16, TBM>(GuPol{a}, xs, rowoff);
+}
+
+template <int EFMT, int TBM>
+__global__ __launch_bounds__(Shape<TBM>::W * 64) void k_gemm_down_p(GemmArgs a) {
+    __shared__ __attribute__((aligned(16))) _Float16 xs[2 * TBM * 16 * BLD];
+    __shared__ int rowoff[3 * TBM * 16];
+    tile_stream<EFMT, 1, DN_RPW, Shape<TBM>::DEPTH, 4, TBM>(DnPol{a}, xs, rowoff);
+}
+
+/* Persistent grid: one block per CU, a multiple of the 8 XCDs.  The
+ * environment variable OROME_GEMM_PERSIST_BLOCKS overrides it (tests use a
+ * small grid to give every block many units); 0 selects the per-tile
+ * kernels. */
+static unsigned persist_blocks() {
+    static int n[64];
+    if (const char *env = getenv("OROME_GEMM_PERSIST_BLOCKS")) {
+        const long v = strtol(env, nullptr, 10);
+        return v <= 0 ? 0u : v < 8 ? 8u : (unsigned)(v / 8 * 8);
+    }
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (!n[dev]) {
+        int v = 0;
+        if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v < 8) v = 256;
+        n[dev] = v / 8 * 8;
+    }
+    return (unsigned)n[dev];
+}
+
 /* ------------------------------------------------------------ launch */
 int launch_gemm_gate_up(const ExpertSide &ex, const SharedSide &sh, const _Float16 *x16, int zrow, int T,
                         int H, int M, int K, int E, int tile_m, const uint32_t *tiles, int n_tiles_max,
@@ -494,6 +754,11 @@ int launch_gemm_gate_up(const ExpertSide &ex, const SharedSide &sh, const _Float
     a.nyb = (M > a.S ? M : a.S) / NB;
     const dim3 grid((unsigned)((n_tiles_max + 7) / 8 * 8 * a.nyb)), block(W * 64);
     const bool q8 = sh.gate && sh.gate_fmt == FQ8;
+    const unsigned pb = GEMM_PERSIST && tile_m == GEMM_TILE_BIG ? persist_blocks() : 0u;
+    if (pb && H == 2048 && (!sh.gate || (sh.gate_fmt == FQ4K && sh.S == M))) {
+        hipLaunchKernelGGL((k_gemm_gate_up_p<GEMM_TILE_BIG / 16>), dim3(pb), block, 0, s, a);
+        return hipGetLastError() == hipSuccess ? 0 : -3;
+    }
     if (tile_m != GEMM_TILE_SMALL && tile_m != GEMM_TILE_BIG) return -2;
     /* compile-time stage count for the common hidden size (Q4_K shared
      * expert); other shapes take the generic loop */
@@ -528,8 +793,14 @@ int launch_gemm_down(const ExpertSide &ex, const SharedSide &sh, const _Float16 
     a.tiles = tiles; a.y = y; a.ysh = ysh;
     a.nyb = H / NB;
     const dim3 grid((unsigned)((n_tiles_max + 7) / 8 * 8 * a.nyb)), block(W * 64);
-    /* generic unit loop (a compile-time stage count spills here) */
     if (tile_m != GEMM_TILE_SMALL && tile_m != GEMM_TILE_BIG) return -2;
+    const unsigned pb = GEMM_PERSIST && tile_m == GEMM_TILE_BIG ? persist_blocks() : 0u;
+    if (pb && M == 512 && (!sh.gate || (sf == ex.down_fmt && sh.S == M))) {
+        if (ex.down_fmt == FQ4K) hipLaunchKernelGGL((k_gemm_down_p<FQ4K, GEMM_TILE_BIG / 16>), dim3(pb), block, 0, s, a);
+        else hipLaunchKernelGGL((k_gemm_down_p<FQ6K, GEMM_TILE_BIG / 16>), dim3(pb), block, 0, s, a);
+        return hipGetLastError() == hipSuccess ? 0 : -3;
+    }
+    /* generic unit loop (a compile-time stage count spills here) */
 #define DN_LAUNCH(EF, SF)                                                                    \
     do {                                                                                     \
         if (tile_m == GEMM_TILE_SMALL) hipLaunchKernelGGL((k_gemm_down<EF, SF, 0, GEMM_TILE_SMALL / 16>), grid, block, 0, s, a); \

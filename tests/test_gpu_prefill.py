@@ -97,3 +97,43 @@ def test_prefill_matches_decode_path(base):
     b, db = base.run(0, x, h, path=_lib.OROME_PATH_MFMA)
     assert np.array_equal(da["idx"], db["idx"]) and np.array_equal(da["pairs"], db["pairs"])
     assert rel_l2(b - h, a - h) < TOL
+
+
+def test_persistent_gemm_bit_identical(base, monkeypatch):
+    """The persistent big-tile GEMMs (a block walks its (tile, row block)
+    units back to back; the weight ring and the activation chunks run on
+    across unit boundaries) compute every unit exactly as the per-tile
+    kernels do: outputs are bit-identical with the default grid, with the
+    per-tile kernels (OROME_GEMM_PERSIST_BLOCKS=0) and with an 8-block grid,
+    where each block walks ~140 units."""
+    banner("persistent GEMM vs per-tile, T=2048")
+    x, h = base.inputs(2048, seed=4096)
+    outs = {}
+    for blocks in (None, "0", "8"):
+        if blocks is None:
+            monkeypatch.delenv("OROME_GEMM_PERSIST_BLOCKS", raising=False)
+        else:
+            monkeypatch.setenv("OROME_GEMM_PERSIST_BLOCKS", blocks)
+        outs[blocks], _ = base.run(0, x, h, path=_lib.OROME_PATH_MFMA)
+    monkeypatch.delenv("OROME_GEMM_PERSIST_BLOCKS", raising=False)
+    assert np.array_equal(outs[None], outs["0"])
+    assert np.array_equal(outs["8"], outs["0"])
+    sel = np.arange(5, 2048, 64)
+    ref = base.om.forward(0, x[sel], h[sel])
+    assert rel_l2(outs[None][sel] - h[sel], ref - h[sel]) < TOL
+
+
+def test_persistent_gemm_zipf_q6k(monkeypatch):
+    """Skewed routing (a few experts with many tiles, many with none) and a
+    Q6_K down projection through a 16-block persistent grid, against the
+    oracle and bit-identical to the per-tile kernels."""
+    banner("persistent GEMM, Zipf T=512, Q6_K down")
+    p = Pair(max_tokens=512, down=14, shared_down=14, zipf=True, seed=35)
+    monkeypatch.setenv("OROME_GEMM_PERSIST_BLOCKS", "16")
+    out, _ = run_and_check(p, 512, seed=1512, path=_lib.OROME_PATH_MFMA)
+    monkeypatch.setenv("OROME_GEMM_PERSIST_BLOCKS", "0")
+    x, h = p.inputs(512, seed=1512)
+    ref, _ = p.run(0, x, h, path=_lib.OROME_PATH_MFMA)
+    monkeypatch.delenv("OROME_GEMM_PERSIST_BLOCKS", raising=False)
+    assert np.array_equal(out, ref)
+    p.gm.close()
