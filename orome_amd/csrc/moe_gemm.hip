@@ -461,23 +461,27 @@ DEV UnitDesc unit_desc(const uint32_t *tiles, int nyb, int E, int n) {
  * boundaries, so only the first unit waits for its loads.  Per unit the
  * arithmetic is exactly tile_run's (same fragments, same MFMA order).
  *   - weight stage u + DEPTH of unit n is unit n+1's stage u + DEPTH - U;
- *   - global chunk C = n * nch + c sits in LDS buffer C & 1 (nch even); at
- *     the barrier that ends chunk C, chunk C + 2 is stored and C + 3 fetched,
- *     whichever unit they belong to;
- *   - token row offsets of unit n sit in LDS slot n % 3, written at the start
- *     of unit n - 2 (units past the end point every row at the zero row, so
- *     loads and stores stay unconditional).
+ *   - global chunk C = n * nch + c sits in LDS buffer C % 3.  Before the
+ *     barrier that ends chunk C, chunk C + 2 is stored (its buffer held
+ *     C - 1, which every wave finished before the previous barrier) and
+ *     C + 3 fetched into registers, so nothing waits after the barrier and
+ *     chunk C + 1 is readable a whole chunk before it is used;
+ *   - B fragments are read one MFMA step ahead (across stages, chunks and
+ *     units), so the LDS latency hides behind the current step's work;
+ *   - token row offsets of unit n sit in LDS slot n % 3, written at the end
+ *     of unit n - 2's first chunk (units past the end point every row at the
+ *     zero row, so loads and stores stay unconditional).
  * P supplies the unit's weight and source pointers, row offsets and
  * epilogue. */
 template <int FMT, int NMAT, int RPW, int DEPTH, int NST, int TBM, typename P>
 DEV void tile_stream(const P &pol, _Float16 *xs, int *rowoff) {
-    constexpr int W = Shape<TBM>::W, TR = TBM * 16, nst = NST, nch = NST / 2, U = RPW * NST;
+    constexpr int W = Shape<TBM>::W, TR = TBM * 16, nst = NST, nch = NST / 2, U = RPW * NST, CB = TR * BLD;
     static_assert(NST % 4 == 0 && U % DEPTH == 0 && (RPW == 1 || nch == 2), "stream shape");
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int kg = lane >> 4, i = lane & 15;
     const size_t rbytes = gemm_row_bytes(FMT, pol.in_dim());
 #ifdef OROME_TRACE
-    const unsigned long long t_start = __builtin_amdgcn_s_memrealtime();
+    if (threadIdx.x == 0 && NMAT == 2) g_trace[blockIdx.x * 8] = __builtin_amdgcn_s_memrealtime();
 #endif
     UnitDesc cu = pol.desc(0), nu = pol.desc(1);
     if (!cu.valid) return;
@@ -508,16 +512,26 @@ DEV void tile_stream(const P &pol, _Float16 *xs, int *rowoff) {
             ring[d][m].load(cw[m] + (size_t)rb * 16 * rbytes, j, kg);
         }
     }
-    /* chunks 0, 1 of unit 0 into the two buffers, chunk 2 of the stream
-     * (unit 0's when nch > 2, else unit 1's chunk 0) into registers */
+    /* chunks 0, 1 of the stream into buffers 0, 1, chunk 2 (unit 0's when
+     * nch > 2, else unit 1's chunk 0) into registers */
     Chunk<TBM> ch;
     ch.fetch(pol.src(cu), rowoff, pol.ld(), 0);
     ch.template store<FMT>(xs);
     ch.fetch(pol.src(cu), rowoff, pol.ld(), KCH);
-    ch.template store<FMT>(xs + TR * BLD);
+    ch.template store<FMT>(xs + CB);
     if (nch > 2) ch.fetch(pol.src(cu), rowoff, pol.ld(), 2 * KCH);
     else ch.fetch(pol.src(nu), rowoff + TR, pol.ld(), 0);
     __syncthreads();
+
+    /* B fragment of token block t, step s of a stage whose chunk sits in
+     * buffer `buf` (j & 1 picks the chunk's 128-k half) */
+    const _Float16 *bl = xs + i * BLD + kg * 8;
+    auto bfrag = [&](int buf, int j, int s, int t) -> h8 {
+        return *(const h8 *)(bl + buf * CB + (j & 1) * KC + t * 16 * BLD + s * 32);
+    };
+    h8 b[TBM];
+#pragma unroll
+    for (int t = 0; t < TBM; t++) b[t] = bfrag(0, 0, 0, t);
 
     f4v c[NMAT][TBM];
 #pragma unroll
@@ -527,12 +541,13 @@ DEV void tile_stream(const P &pol, _Float16 *xs, int *rowoff) {
 
     for (int n = 0;; n++) {
         /* unit n + 2: its row offsets are read here (a global load for
-         * routed gate/up rows) and stored into LDS slot (n + 2) % 3 after the
-         * first barrier of this unit, so the load's wait comes stages later.
-         * That slot was last read by fetches issued in unit n - 1. */
+         * routed gate/up rows) and stored into LDS slot (n + 2) % 3 at the
+         * end of this unit's first chunk, so the load's wait comes stages
+         * later.  That slot was last read by fetches issued in unit n - 1. */
         const UnitDesc fu = pol.desc(n + 2);
         const int s1 = (n + 1) % 3, s2 = (n + 2) % 3;
         const uint32_t ro = threadIdx.x < TR ? pol.row_raw(fu, (int)threadIdx.x) : 0u;
+        const int bb = (n * nch) % 3; /* buffer of this unit's chunk 0 */
 #pragma unroll
         for (int u0 = 0; u0 < U; u0 += DEPTH) {
 #pragma unroll
@@ -555,19 +570,30 @@ DEV void tile_stream(const P &pol, _Float16 *xs, int *rowoff) {
 #pragma unroll
                     for (int m = 0; m < NMAT; m++) ring[d][m].load((here ? cw[m] : nw[m]) + (size_t)rb2 * 16 * rbytes, j2, kg);
                 }
-                const _Float16 *bp = xs + ((j >> 1) & 1) * (TR * BLD) + (j & 1) * KC + i * BLD + kg * 8;
+                /* the stage after this one: next row block or next unit
+                 * restart at stage 0, whose chunk 0 is this unit's (row
+                 * blocks) or the next unit's */
+                const int jn = j + 1 < nst ? j + 1 : 0;
+                const int cnext = j + 1 < nst ? (j + 1) >> 1 : rb + 1 < RPW ? 0 : nch;
+                const int bufc = (bb + (j >> 1)) % 3, bufn = (bb + cnext) % 3;
 #pragma unroll
                 for (int s = 0; s < 4; s++) {
+                    /* next step's B reads first, pinned above this step's
+                     * work (the scheduler would otherwise sink each read next
+                     * to its use and wait for it there) */
+                    h8 bn[TBM];
+#pragma unroll
+                    for (int t = 0; t < TBM; t++) bn[t] = s < 3 ? bfrag(bufc, j, s + 1, t) : bfrag(bufn, jn, 0, t);
+                    __builtin_amdgcn_sched_barrier(0);
                     h8 a[NMAT];
 #pragma unroll
                     for (int m = 0; m < NMAT; m++) a[m] = cur[m].frag(s);
-                    h8 b[TBM];
-#pragma unroll
-                    for (int t = 0; t < TBM; t++) b[t] = *(const h8 *)(bp + t * 16 * BLD + s * 32);
 #pragma unroll
                     for (int t = 0; t < TBM; t++)
 #pragma unroll
                         for (int m = 0; m < NMAT; m++) c[m][t] = mfma(a[m], b[t], c[m][t]);
+#pragma unroll
+                    for (int t = 0; t < TBM; t++) b[t] = bn[t];
                 }
                 if (j == nst - 1) {
                     pol.epilogue(cu, c, cu.yb * (W * 16 * RPW) + wv * 16 * RPW + rb * 16 + 4 * kg, (cu.rows + 15) >> 4);
@@ -577,23 +603,21 @@ DEV void tile_stream(const P &pol, _Float16 *xs, int *rowoff) {
                         for (int t = 0; t < TBM; t++) c[m][t] = f4v{0, 0, 0, 0};
                 }
                 if (rb == RPW - 1 && (j & 1)) {
-                    /* end of chunk C = n nch + cc: store chunk C + 2 into
-                     * C's buffer, fetch chunk C + 3 (of unit n + off) */
+                    /* end of chunk C = n nch + cc: store chunk C + 2, fetch
+                     * chunk C + 3 (of unit n + off), then the barrier */
                     const int cc = j >> 1, c3 = cc + 3, off = c3 / nch;
-                    __syncthreads();
                     if (cc == 0 && threadIdx.x < TR) rowoff[s2 * TR + threadIdx.x] = pol.row_fin(fu, ro);
-                    ch.template store<FMT>(xs + (cc & 1) * (TR * BLD));
+                    ch.template store<FMT>(xs + ((bb + cc + 2) % 3) * CB);
                     const UnitDesc &tu = off == 0 ? cu : off == 1 ? nu : fu;
                     const int slot = off == 0 ? n % 3 : off == 1 ? s1 : s2;
                     ch.fetch(pol.src(tu), rowoff + slot * TR, pol.ld(), (c3 % nch) * KCH);
+                    __syncthreads();
                 }
             }
         }
 #ifdef OROME_TRACE
-        if (threadIdx.x == 0 && n < 7 && NMAT == 2) {
-            g_trace[blockIdx.x * 8 + 1 + n] = __builtin_amdgcn_s_memrealtime();
-            if (n == 0) g_trace[blockIdx.x * 8] = t_start;
-        }
+        /* unit end times of the gate/up stream, per block (slot 0: start) */
+        if (threadIdx.x == 0 && n < 7 && NMAT == 2) g_trace[blockIdx.x * 8 + 1 + n] = __builtin_amdgcn_s_memrealtime();
 #endif
         if (!nu.valid) break;
         cu = nu;
@@ -704,14 +728,14 @@ __global__ __launch_bounds__(Shape<TBM>::W * 64) void k_gemm_down(GemmArgs a) {
 #endif
 template <int TBM>
 __global__ __launch_bounds__(Shape<TBM>::W * 64) void k_gemm_gate_up_p(GemmArgs a) {
-    __shared__ __attribute__((aligned(16))) _Float16 xs[2 * TBM * 16 * BLD];
+    __shared__ __attribute__((aligned(16))) _Float16 xs[3 * TBM * 16 * BLD];
     __shared__ int rowoff[3 * TBM * 16];
     tile_stream<FQ4K, 2, GU_RPW, Shape<TBM>::DEPTH, 16, TBM>(GuPol{a}, xs, rowoff);
 }
 
 template <int EFMT, int TBM>
 __global__ __launch_bounds__(Shape<TBM>::W * 64) void k_gemm_down_p(GemmArgs a) {
-    __shared__ __attribute__((aligned(16))) _Float16 xs[2 * TBM * 16 * BLD];
+    __shared__ __attribute__((aligned(16))) _Float16 xs[3 * TBM * 16 * BLD];
     __shared__ int rowoff[3 * TBM * 16];
     tile_stream<EFMT, 1, DN_RPW, Shape<TBM>::DEPTH, 4, TBM>(DnPol{a}, xs, rowoff);
 }
