@@ -95,7 +95,7 @@ def main():
     print("[bench] config %s (%s): %d synthetic layers, T=%d" % (args.config, cf["name"], L, T),
           file=sys.stderr, flush=True)
     img = orome_amd.synth_gguf(spec)
-    gm = orome_amd.MoEModel(image=img, max_tokens=max(T, 16))
+    gm = orome_amd.MoEModel(image=img, max_tokens=max(T, 16), pack=T > 8)
     ctx = gm.ctx
     stack = cf["mode"] == "stack"
     xs_h = [orome_amd.synth_normal(77, i, T * H).reshape(T, H) for i in range(NX)]

@@ -101,6 +101,8 @@ SIGNATURES = {
     "orome_hip_free": (I, [VP, VP]),
     "orome_hip_htod": (I, [VP, VP, VP, SZ]),
     "orome_hip_dtoh": (I, [VP, VP, VP, SZ]),
+    "orome_hip_pack_layer": (I, [VP, P(ModelConfig), P(ExpertLayerRef), P(LayerTensorCache)]),
+    "orome_hip_unpack_all": (I, [VP]),
     "format_provider_open_gguf": (P(FormatProvider), [P(GGUFFile), VP]),
     "format_provider_close": (None, [P(FormatProvider)]),
     "format_resolve_expert_layer": (ExpertLayerRef, [P(FormatProvider), I, U32]),

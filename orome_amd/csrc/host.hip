@@ -58,6 +58,18 @@ struct orome_hip_ctx {
     int timing, tcap;
     hipEvent_t *ev;          /* [N_STAGES][tcap][2] */
     int tcount[N_STAGES];
+    /* tile-major copies of registered layers' Q4_K expert matrices */
+    struct Pack *packs;
+    int npacks, pcap;
+};
+
+/* One registered layer: keyed by the routed gate and shared gate device
+ * addresses; the copies' addresses (NULL where a matrix was not repacked). */
+struct Pack {
+    const uint8_t *key, *sh_key;
+    void *mem;
+    const uint8_t *gate, *up, *down, *sgate, *sup, *sdown;
+    size_t gate_stride, down_stride;
 };
 
 static int set_dev(orome_hip_ctx *c) {
@@ -147,11 +159,14 @@ static void free_timing(orome_hip_ctx *c) {
     c->timing = 0;
 }
 
+extern "C" int orome_hip_unpack_all(orome_hip_ctx *c);
+
 extern "C" void orome_hip_destroy(orome_hip_ctx *c) {
     if (!c) return;
     (void)hipSetDevice(c->device);
     (void)hipStreamSynchronize(c->stream);
     (void)hipStreamSynchronize(c->side);
+    (void)orome_hip_unpack_all(c);
     free_timing(c);
     (void)hipFree(c->arena);
     (void)hipEventDestroy(c->fork);
@@ -225,6 +240,99 @@ static int kfmt(QuantFormat f) {
         case QFMT_GGUF_Q8_0: return 3;
         default: return -1;
     }
+}
+
+/* ------------------------------------------------- tile-major repacking */
+
+static const Pack *find_pack(const orome_hip_ctx *c, const uint8_t *gate, const uint8_t *sh_gate) {
+    for (int k = 0; k < c->npacks; k++)
+        if (c->packs[k].key == gate && c->packs[k].sh_key == sh_gate) return &c->packs[k];
+    return NULL;
+}
+
+extern "C" int orome_hip_pack_layer(orome_hip_ctx *c, const ModelConfig *cfg, const ExpertLayerRef *elr,
+                                    const LayerTensorCache *lt) {
+    if (!c || !cfg || !elr || !lt || !elr->buffer) return orome_fail(OROME_EINVAL, "orome_hip_pack_layer: NULL argument");
+    const int H = cfg->hidden_dim, E = cfg->num_experts, M = cfg->moe_intermediate;
+    if (H != c->cfg.hidden_dim || E != c->cfg.num_experts || M != c->cfg.moe_intermediate)
+        return orome_fail(OROME_EINVAL, "orome_hip_pack_layer: config differs from the context's");
+    if (elr->gate.format != QFMT_GGUF_Q4_K || elr->up.format != QFMT_GGUF_Q4_K || H % 256 || M % 256)
+        return orome_fail(OROME_EUNSUPPORTED, "orome_hip_pack_layer: routed gate/up must be Q4_K, H and M multiples of 256");
+    const int S = lt->shared_gate.buffer ? (int)lt->shared_gate.out_dim : 0;
+    /* gate/up are repacked with the shared expert's (Q4_K or absent); down
+     * likewise; anything else keeps the row-major path */
+    const bool sh_gu = S && lt->shared_gate.format == QFMT_GGUF_Q4_K && lt->shared_up.format == QFMT_GGUF_Q4_K;
+    if (S && !sh_gu) return OROME_OK;
+    if (S % 16 || (S && S % 256)) return OROME_OK;
+    const bool dn = elr->down.format == QFMT_GGUF_Q4_K && (!S || lt->shared_down.format == QFMT_GGUF_Q4_K);
+    const size_t gu = packed_q4k_bytes(M, H, E), dnb = dn ? packed_q4k_bytes(H, M, E) : 0,
+                 sgu = S ? packed_q4k_bytes(S, H, 1) : 0, sdn = S && dn ? packed_q4k_bytes(H, S, 1) : 0;
+    if (set_dev(c)) return OROME_EHIP;
+    const uint8_t *gate = dev_addr(elr->buffer, elr->gate.offset), *sh_gate = S ? dev_addr(lt->shared_gate.buffer, lt->shared_gate.offset) : NULL;
+    if (c->npacks == c->pcap) {
+        const int cap = c->pcap ? 2 * c->pcap : 64;
+        Pack *np = (Pack *)realloc(c->packs, (size_t)cap * sizeof(Pack));
+        if (!np) return orome_fail(OROME_ENOMEM, "orome_hip_pack_layer: registry");
+        c->packs = np;
+        c->pcap = cap;
+    }
+    Pack pk = {};
+    pk.key = gate;
+    pk.sh_key = sh_gate;
+    HIP_OK(hipMalloc(&pk.mem, 2 * gu + dnb + 2 * sgu + sdn), OROME_ENOMEM);
+    uint8_t *m = (uint8_t *)pk.mem;
+    int rc = 0;
+    pk.gate = m;
+    rc |= launch_pack_q4k(gate, m, M, H, E, elr->gate.expert_stride, c->stream);
+    m += gu;
+    pk.up = m;
+    rc |= launch_pack_q4k(dev_addr(elr->buffer, elr->up.offset), m, M, H, E, elr->up.expert_stride, c->stream);
+    m += gu;
+    pk.gate_stride = gu / E;
+    if (dn) {
+        pk.down = m;
+        rc |= launch_pack_q4k(dev_addr(elr->buffer, elr->down.offset), m, H, M, E, elr->down.expert_stride, c->stream);
+        m += dnb;
+        pk.down_stride = dnb / E;
+    }
+    if (S) {
+        pk.sgate = m;
+        rc |= launch_pack_q4k(sh_gate, m, S, H, 1, 0, c->stream);
+        m += sgu;
+        pk.sup = m;
+        rc |= launch_pack_q4k(dev_addr(lt->shared_up.buffer, lt->shared_up.offset), m, S, H, 1, 0, c->stream);
+        m += sgu;
+        if (dn) {
+            pk.sdown = m;
+            rc |= launch_pack_q4k(dev_addr(lt->shared_down.buffer, lt->shared_down.offset), m, H, S, 1, 0, c->stream);
+        }
+    }
+    if (rc || hipStreamSynchronize(c->stream) != hipSuccess) {
+        (void)hipFree(pk.mem);
+        return orome_fail(OROME_EHIP, "orome_hip_pack_layer: repack failed (%d)", rc);
+    }
+    for (int k = 0; k < c->npacks; k++) /* re-registration replaces */
+        if (c->packs[k].key == gate && c->packs[k].sh_key == sh_gate) {
+            (void)hipFree(c->packs[k].mem);
+            c->packs[k] = pk;
+            return OROME_OK;
+        }
+    c->packs[c->npacks++] = pk;
+    return OROME_OK;
+}
+
+extern "C" int orome_hip_unpack_all(orome_hip_ctx *c) {
+    if (!c) return orome_fail(OROME_EINVAL, "orome_hip_unpack_all: NULL ctx");
+    if (c->npacks) {
+        if (set_dev(c)) return OROME_EHIP;
+        (void)hipStreamSynchronize(c->stream);
+        (void)hipStreamSynchronize(c->side);
+        for (int k = 0; k < c->npacks; k++) (void)hipFree(c->packs[k].mem);
+    }
+    free(c->packs);
+    c->packs = NULL;
+    c->npacks = c->pcap = 0;
+    return OROME_OK;
 }
 
 static int launch_rc(int rc, const char *what) {
@@ -360,18 +468,41 @@ static int forward_impl(orome_hip_ctx *c, const ModelConfig *cfg, const ExpertLa
         const bool sh_small = (long)T * K <= (long)GEMM_TILE_SMALL * E;
         const int ns_max = E + (S && sh_small ? (T + GEMM_TILE_SMALL - 1) / GEMM_TILE_SMALL : 0),
                   nb_max = (T * K) / GEMM_TILE_BIG + E + (S && !sh_small ? (T + GEMM_TILE_BIG - 1) / GEMM_TILE_BIG : 0);
+        /* registered layers: the grouped GEMMs read the tile-major copies */
+        ExpertSide exm = ex;
+        SharedSide shm = sh;
+        if (const Pack *pk = find_pack(c, ex.gate, sh.gate)) {
+            exm.gate = pk->gate;
+            exm.up = pk->up;
+            exm.gate_stride = exm.up_stride = pk->gate_stride;
+            exm.gate_fmt = GEMM_FMT_Q4K_TILED;
+            if (S) {
+                shm.gate = pk->sgate;
+                shm.up = pk->sup;
+                shm.gate_fmt = GEMM_FMT_Q4K_TILED;
+            }
+            if (pk->down) {
+                exm.down = pk->down;
+                exm.down_stride = pk->down_stride;
+                exm.down_fmt = GEMM_FMT_Q4K_TILED;
+                if (S) {
+                    shm.down = pk->sdown;
+                    shm.down_fmt = GEMM_FMT_Q4K_TILED;
+                }
+            }
+        }
         auto gate_up = [&](int tm, hipStream_t st) {
             return tm == GEMM_TILE_SMALL
-                       ? launch_gemm_gate_up(ex, sh, c->x16, c->tmax, T, H, M, K, E, tm, c->tiles, ns_max, c->pairs, c->act,
+                       ? launch_gemm_gate_up(exm, shm, c->x16, c->tmax, T, H, M, K, E, tm, c->tiles, ns_max, c->pairs, c->act,
                                              c->act_sh, st)
-                       : launch_gemm_gate_up(ex, sh, c->x16, c->tmax, T, H, M, K, E, tm, c->tiles_b, nb_max, c->pairs, c->act,
+                       : launch_gemm_gate_up(exm, shm, c->x16, c->tmax, T, H, M, K, E, tm, c->tiles_b, nb_max, c->pairs, c->act,
                                              c->act_sh, st);
         };
         auto down = [&](int tm, hipStream_t st) {
             return tm == GEMM_TILE_SMALL
-                       ? launch_gemm_down(ex, sh, c->act, c->act_sh, c->tmax * c->kmax, c->tmax, T, H, M, K, E, tm, c->tiles, ns_max, c->y,
+                       ? launch_gemm_down(exm, shm, c->act, c->act_sh, c->tmax * c->kmax, c->tmax, T, H, M, K, E, tm, c->tiles, ns_max, c->y,
                                           c->ysh, st)
-                       : launch_gemm_down(ex, sh, c->act, c->act_sh, c->tmax * c->kmax, c->tmax, T, H, M, K, E, tm, c->tiles_b, nb_max, c->y,
+                       : launch_gemm_down(exm, shm, c->act, c->act_sh, c->tmax * c->kmax, c->tmax, T, H, M, K, E, tm, c->tiles_b, nb_max, c->y,
                                           c->ysh, st);
         };
         if (c->timing) { /* per-stage timing: both lists in order on one stream */

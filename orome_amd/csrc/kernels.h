@@ -89,6 +89,11 @@ int launch_gemm_down(const ExpertSide &ex, const SharedSide &sh, const _Float16 
                      const _Float16 *act_sh, int zrow, int zrow_sh, int T, int H, int M, int K, int E, int tile_m,
                      const uint32_t *tiles, int n_tiles_max, float *y, float *ysh,
                      hipStream_t s);
+/* tile-major repack of Q4_K expert matrices for the grouped GEMMs (format
+ * id 4 in ExpertSide / SharedSide) */
+enum { GEMM_FMT_Q4K_TILED = 4 };
+size_t packed_q4k_bytes(int R, int K, int E);
+int launch_pack_q4k(const uint8_t *src, uint8_t *dst, int R, int K, int E, size_t src_stride, hipStream_t s);
 int launch_combine(const float *y, const float *ysh, const uint32_t *pos, const float *w,
                    const float *sgl, int has_shared, const float *h_in, float *h_out, int T,
                    int H, int K, hipStream_t s);

@@ -38,7 +38,8 @@ extern "C" __attribute__((visibility("default"))) int orome_trace_fetch_gemm(uns
 }
 #endif
 
-enum { FQ4K = 0, FQ6K = 2, FQ8 = 3 };
+/* FQ4KT: Q4_K repacked tile-major (launch_pack_q4k), same values */
+enum { FQ4K = 0, FQ6K = 2, FQ8 = 3, FQ4KT = GEMM_FMT_Q4K_TILED };
 
 typedef float f4v __attribute__((ext_vector_type(4)));
 
@@ -57,7 +58,13 @@ struct Shape {
 #define BLD (KCH + 16)                  /* chunk row pitch (halves): 544 bytes, B-fragment reads conflict-free */
 
 DEV size_t gemm_row_bytes(int fmt, int n) {
-    return fmt == FQ4K ? (size_t)(n / 256) * 144 : fmt == FQ6K ? (size_t)(n / 256) * 210 : (size_t)(n / 32) * 34;
+    return fmt == FQ4K || fmt == FQ4KT ? (size_t)(n / 256) * 144 : fmt == FQ6K ? (size_t)(n / 256) * 210 : (size_t)(n / 32) * 34;
+}
+/* offset of lane row i of the 16-row block starting at row0: a row of its
+ * own, or (tile-major Q4_K) the block base plus the lane's 16-byte column */
+template <int FMT>
+DEV size_t lane_row(int row0, int i, size_t rbytes) {
+    return FMT == FQ4KT ? (size_t)row0 * rbytes + (size_t)i * 16 : (size_t)(row0 + i) * rbytes;
 }
 DEV uint32_t u4_at(u4 v, int i) { return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w; }
 DEV h2 splat(_Float16 v) { return h2{v, v}; }
@@ -88,7 +95,7 @@ DEV void q8_h2_0213(uint32_t w, h2 &p02, h2 &p13) {
  * copied into LDS unchanged. */
 template <int FMT>
 DEV int frag_pos(int c) {
-    if (FMT == FQ4K) { /* lane kg, step s: k = 64(kg>>1) + 16(kg&1) + 4s (+32 high nibbles) */
+    if (FMT == FQ4K || FMT == FQ4KT) { /* lane kg, step s: k = 64(kg>>1) + 16(kg&1) + 4s (+32 high nibbles) */
         const int g = c >> 4, r = c & 15, hi = r >> 3, rr = r & 7;
         return (((rr & 3) * 4 + 2 * g + (rr >> 2)) * 8) + 4 * hi;
     } else if (FMT == FQ6K) { /* k = 32(kg&1) + 16(kg>>1) + 4s (+64 high nibbles) */
@@ -155,6 +162,20 @@ struct Span<FQ4K> {
         const h2 t3 = hfma(as_h2(p13 & 0xFFF0FFF0u), splat(sc.y), splat(nc.y));
         return cat4(hfma(t0, d, splat(mb.x)), hfma(t1, d, splat(mb.x)), hfma(t2, d, splat(mb.y)),
                     hfma(t3, d, splat(mb.y)));
+    }
+};
+
+/* Tile-major Q4_K: per 16-row block and 256-wide super-block, 2304 bytes =
+ * the 16 rows' 16-byte headers (d, dmin, scales), then for each 128-k half
+ * the 64 lanes' 16 quant bytes in lane order (kg * 16 + i).  A wave's quant
+ * load is one contiguous 1 KB and its header load 256 B, where the row-major
+ * layout touches 16 rows 1152 B apart.  `p` is the block base plus 16 i. */
+template <>
+struct Span<FQ4KT> : Span<FQ4K> {
+    MDEV void load(const uint8_t *p, int j, int kg) {
+        const uint8_t *b = p + (size_t)(j >> 1) * 2304;
+        hdr = ld_u4(b);
+        q = ld_u4(b + 256 + (j & 1) * 1024 + kg * 256);
     }
 };
 
@@ -267,8 +288,8 @@ DEV void tile_run(const uint8_t *w0, const uint8_t *w1, int in_dim, const _Float
      * the register copies would wait for every load in flight) */
     const int nst = NST ? NST : in_dim / KC, nch = nst / 2, U = RPW * nst;
     const int rbase = yb * (Shape<TBM>::W * 16 * RPW) + wv * 16 * RPW;
-    const uint8_t *rw0 = w0 + (size_t)(rbase + i) * rbytes;
-    const uint8_t *rw1 = NMAT > 1 ? w1 + (size_t)(rbase + i) * rbytes : nullptr;
+    const uint8_t *rw0 = w0 + lane_row<FMT>(rbase, i, rbytes);
+    const uint8_t *rw1 = NMAT > 1 ? w1 + lane_row<FMT>(rbase, i, rbytes) : nullptr;
 
     /* U is a multiple of DEPTH (checked by the launchers); the last DEPTH
      * units reload unit U-1 instead of branching */
@@ -488,7 +509,7 @@ DEV void tile_stream(const P &pol, _Float16 *xs, int *rowoff) {
     /* this lane's weight row in matrix m of unit u (row block 0, stage 0);
      * a unit past the end reuses `other` (its loads are never consumed) */
     auto wrow = [&](const UnitDesc &u, int m, const uint8_t *other) -> const uint8_t * {
-        return u.valid ? pol.weights(u, m) + (size_t)(u.yb * (W * 16 * RPW) + wv * 16 * RPW + i) * rbytes : other;
+        return u.valid ? pol.weights(u, m) + lane_row<FMT>(u.yb * (W * 16 * RPW) + wv * 16 * RPW, i, rbytes) : other;
     };
     if (threadIdx.x < TR) {
         rowoff[threadIdx.x] = pol.row_fin(cu, pol.row_raw(cu, (int)threadIdx.x));
@@ -693,7 +714,8 @@ __global__ __launch_bounds__(Shape<TBM>::W * 64) void k_gemm_gate_up(GemmArgs a)
         tile_run<SFMT, 2, GU_RPW, (SFMT == FQ8 ? 2 : Shape<TBM>::DEPTH), NST, TBM>(a.sh_a, a.sh_b, a.H, a.src, a.H, rowoff, (int)rows, yb, xs, epi);
     } else {
         const GuEpi epi{a.act, a.M, (int)first, (int)rows};
-        tile_run<FQ4K, 2, GU_RPW, Shape<TBM>::DEPTH, NST, TBM>(a.wa + (size_t)e * a.stride_a, a.wb + (size_t)e * a.stride_b, a.H, a.src,
+        /* routed gate/up: Q4_K, tile-major exactly when the shared expert's is */
+        tile_run<(SFMT == FQ4KT ? FQ4KT : FQ4K), 2, GU_RPW, Shape<TBM>::DEPTH, NST, TBM>(a.wa + (size_t)e * a.stride_a, a.wb + (size_t)e * a.stride_b, a.H, a.src,
                                   a.H, rowoff, (int)rows, yb, xs, epi);
     }
     if (threadIdx.x == 0) TSTAMP(6);
@@ -726,11 +748,11 @@ __global__ __launch_bounds__(Shape<TBM>::W * 64) void k_gemm_down(GemmArgs a) {
 #ifndef GEMM_PERSIST
 #define GEMM_PERSIST 1
 #endif
-template <int TBM>
+template <int TBM, int GF>
 __global__ __launch_bounds__(Shape<TBM>::W * 64) void k_gemm_gate_up_p(GemmArgs a) {
     __shared__ __attribute__((aligned(16))) _Float16 xs[3 * TBM * 16 * BLD];
     __shared__ int rowoff[3 * TBM * 16];
-    tile_stream<FQ4K, 2, GU_RPW, Shape<TBM>::DEPTH, 16, TBM>(GuPol{a}, xs, rowoff);
+    tile_stream<GF, 2, GU_RPW, Shape<TBM>::DEPTH, 16, TBM>(GuPol{a}, xs, rowoff);
 }
 
 template <int EFMT, int TBM>
@@ -767,8 +789,9 @@ int launch_gemm_gate_up(const ExpertSide &ex, const SharedSide &sh, const _Float
     const int W = tile_m == GEMM_TILE_SMALL ? Shape<GEMM_TILE_SMALL / 16>::W : Shape<GEMM_TILE_BIG / 16>::W;
     const int NB = W * 16 * GU_RPW;
     if ((H / KC * GU_RPW) % 4) return -2; /* every ring depth used divides the unit count */
-    if (H % KCH || M % NB || (sh.gate && sh.S % NB) || ex.gate_fmt != FQ4K) return -2;
-    if (sh.gate && sh.gate_fmt != FQ4K && sh.gate_fmt != FQ8) return -2;
+    if (H % KCH || M % NB || (sh.gate && sh.S % NB) || (ex.gate_fmt != FQ4K && ex.gate_fmt != FQ4KT)) return -2;
+    const bool tiled = ex.gate_fmt == FQ4KT;
+    if (sh.gate && (tiled ? sh.gate_fmt != FQ4KT : sh.gate_fmt != FQ4K && sh.gate_fmt != FQ8)) return -2;
     GemmArgs a = {};
     a.wa = ex.gate; a.wb = ex.up; a.stride_a = ex.gate_stride; a.stride_b = ex.up_stride;
     a.sh_a = sh.gate; a.sh_b = sh.up;
@@ -779,8 +802,9 @@ int launch_gemm_gate_up(const ExpertSide &ex, const SharedSide &sh, const _Float
     const dim3 grid((unsigned)((n_tiles_max + 7) / 8 * 8 * a.nyb)), block(W * 64);
     const bool q8 = sh.gate && sh.gate_fmt == FQ8;
     const unsigned pb = GEMM_PERSIST && tile_m == GEMM_TILE_BIG ? persist_blocks() : 0u;
-    if (pb && H == 2048 && (!sh.gate || (sh.gate_fmt == FQ4K && sh.S == M))) {
-        hipLaunchKernelGGL((k_gemm_gate_up_p<GEMM_TILE_BIG / 16>), dim3(pb), block, 0, s, a);
+    if (pb && H == 2048 && (!sh.gate || (sh.gate_fmt == ex.gate_fmt && sh.S == M))) {
+        if (tiled) hipLaunchKernelGGL((k_gemm_gate_up_p<GEMM_TILE_BIG / 16, FQ4KT>), dim3(pb), block, 0, s, a);
+        else hipLaunchKernelGGL((k_gemm_gate_up_p<GEMM_TILE_BIG / 16, FQ4K>), dim3(pb), block, 0, s, a);
         return hipGetLastError() == hipSuccess ? 0 : -3;
     }
     if (tile_m != GEMM_TILE_SMALL && tile_m != GEMM_TILE_BIG) return -2;
@@ -791,7 +815,10 @@ int launch_gemm_gate_up(const ExpertSide &ex, const SharedSide &sh, const _Float
         if (tile_m == GEMM_TILE_SMALL) hipLaunchKernelGGL((k_gemm_gate_up<SF, NS, GEMM_TILE_SMALL / 16>), grid, block, 0, s, a); \
         else hipLaunchKernelGGL((k_gemm_gate_up<SF, NS, GEMM_TILE_BIG / 16>), grid, block, 0, s, a);              \
     } while (0)
-    if (q8) GU_LAUNCH(FQ8, 0);
+    if (tiled) {
+        if (H == 2048) GU_LAUNCH(FQ4KT, 16);
+        else GU_LAUNCH(FQ4KT, 0);
+    } else if (q8) GU_LAUNCH(FQ8, 0);
     else if (H == 2048) GU_LAUNCH(FQ4K, 16);
     else GU_LAUNCH(FQ4K, 0);
 #undef GU_LAUNCH
@@ -806,9 +833,10 @@ int launch_gemm_down(const ExpertSide &ex, const SharedSide &sh, const _Float16 
     if ((M / KC * DN_RPW) % 4 || (sh.gate && (sh.S / KC * DN_RPW) % 4)) return -2;
     /* all of a tile's activations stay resident: in_dim <= 2 chunks */
     if (H % NB || M % KCH || M > 2 * KCH || (sh.gate && (sh.S % KCH || sh.S > 2 * KCH))) return -2;
-    if (ex.down_fmt != FQ4K && ex.down_fmt != FQ6K) return -2;
-    const int sf = sh.gate ? sh.down_fmt : FQ4K;
-    if (sf != FQ4K && sf != FQ6K && sf != FQ8) return -2;
+    if (ex.down_fmt != FQ4K && ex.down_fmt != FQ6K && ex.down_fmt != FQ4KT) return -2;
+    /* tile-major routed down needs a tile-major shared down (or none) */
+    const int sf = sh.gate ? sh.down_fmt : ex.down_fmt == FQ4KT ? FQ4KT : FQ4K;
+    if (ex.down_fmt == FQ4KT ? sf != FQ4KT : sf != FQ4K && sf != FQ6K && sf != FQ8) return -2;
     GemmArgs a = {};
     a.wa = ex.down; a.stride_a = ex.down_stride;
     a.sh_a = sh.gate ? sh.down : nullptr;
@@ -821,6 +849,7 @@ int launch_gemm_down(const ExpertSide &ex, const SharedSide &sh, const _Float16 
     const unsigned pb = GEMM_PERSIST && tile_m == GEMM_TILE_BIG ? persist_blocks() : 0u;
     if (pb && M == 512 && (!sh.gate || (sf == ex.down_fmt && sh.S == M))) {
         if (ex.down_fmt == FQ4K) hipLaunchKernelGGL((k_gemm_down_p<FQ4K, GEMM_TILE_BIG / 16>), dim3(pb), block, 0, s, a);
+        else if (ex.down_fmt == FQ4KT) hipLaunchKernelGGL((k_gemm_down_p<FQ4KT, GEMM_TILE_BIG / 16>), dim3(pb), block, 0, s, a);
         else hipLaunchKernelGGL((k_gemm_down_p<FQ6K, GEMM_TILE_BIG / 16>), dim3(pb), block, 0, s, a);
         return hipGetLastError() == hipSuccess ? 0 : -3;
     }
@@ -830,7 +859,9 @@ int launch_gemm_down(const ExpertSide &ex, const SharedSide &sh, const _Float16 
         if (tile_m == GEMM_TILE_SMALL) hipLaunchKernelGGL((k_gemm_down<EF, SF, 0, GEMM_TILE_SMALL / 16>), grid, block, 0, s, a); \
         else hipLaunchKernelGGL((k_gemm_down<EF, SF, 0, GEMM_TILE_BIG / 16>), grid, block, 0, s, a);              \
     } while (0)
-    if (ex.down_fmt == FQ4K) {
+    if (ex.down_fmt == FQ4KT) {
+        DN_LAUNCH(FQ4KT, FQ4KT);
+    } else if (ex.down_fmt == FQ4K) {
         if (sf == FQ4K) DN_LAUNCH(FQ4K, FQ4K);
         else if (sf == FQ6K) DN_LAUNCH(FQ4K, FQ6K);
         else DN_LAUNCH(FQ4K, FQ8);
@@ -840,5 +871,39 @@ int launch_gemm_down(const ExpertSide &ex, const SharedSide &sh, const _Float16 
         else DN_LAUNCH(FQ6K, FQ8);
     }
 #undef DN_LAUNCH
+    return hipGetLastError() == hipSuccess ? 0 : -3;
+}
+
+/* ------------------------------------------------------------ repack */
+/* Q4_K matrices [R rows][K/256 super-blocks of 144 B] (matrix e at src +
+ * e * src_stride) into the tile-major layout of Span<FQ4KT>, densely (matrix
+ * e at dst + e * R * row bytes): tile (row block rb, super-block sb) at
+ * (rb * nsb + sb) * 2304, whose 16-byte piece o holds row o's header (o <
+ * 16) or, for o = 16 + 64 jj + 16 kg + i, bytes 16 + 16 (kg + 4 jj) .. +15
+ * of row i's super-block.  A byte permutation: dequantised values are
+ * unchanged. */
+__global__ __launch_bounds__(144) void k_pack_q4k(const uint8_t *src, uint8_t *dst, int R, int nsb, size_t src_stride) {
+    const int tile = blockIdx.x, e = blockIdx.y, rb = tile / nsb, sb = tile - rb * nsb, o = threadIdx.x;
+    const size_t rbytes = (size_t)nsb * 144;
+    const uint8_t *t0 = src + (size_t)e * src_stride + (size_t)rb * 16 * rbytes + (size_t)sb * 144;
+    int row, off;
+    if (o < 16) {
+        row = o;
+        off = 0;
+    } else {
+        const int qo = o - 16, jj = qo >> 6, ln = qo & 63;
+        row = ln & 15;
+        off = 16 + 16 * ((ln >> 4) + 4 * jj);
+    }
+    const u4 v = ld_u4(t0 + (size_t)row * rbytes + off);
+    *(u4 *)(dst + (size_t)e * R * rbytes + (size_t)tile * 2304 + (size_t)o * 16) = v;
+}
+
+size_t packed_q4k_bytes(int R, int K, int E) { return (size_t)E * R * (K / 256) * 144; }
+
+int launch_pack_q4k(const uint8_t *src, uint8_t *dst, int R, int K, int E, size_t src_stride, hipStream_t s) {
+    if (R % 16 || K % 256 || E < 1 || ((uintptr_t)src & 15) || ((uintptr_t)dst & 15) || (src_stride & 15)) return -2;
+    const int nsb = K / 256;
+    hipLaunchKernelGGL(k_pack_q4k, dim3((unsigned)(R / 16 * nsb), (unsigned)E), dim3(144), 0, s, src, dst, R, nsb, src_stride);
     return hipGetLastError() == hipSuccess ? 0 : -3;
 }

@@ -111,7 +111,10 @@ def make_spec(layers=1, H=2048, E=256, K=8, M=512, S=512, down=_lib.GGML_Q4_K,
 class MoEModel:
     """A GGUF MoE model resident in HBM (all layers), ready for forward calls."""
 
-    def __init__(self, image=None, path=None, max_tokens=16, device=0):
+    def __init__(self, image=None, path=None, max_tokens=16, device=0, pack=None):
+        """pack: register every layer's tile-major Q4_K copies for the MFMA
+        path (orome_hip_pack_layer); default when max_tokens > 8, the sizes
+        that take that path."""
         if (image is None) == (path is None):
             raise ValueError("give exactly one of image or path")
         self._image = image  # keep the host image alive while parsed
@@ -135,6 +138,16 @@ class MoEModel:
         if not self._cache:
             raise _lib.OromeError("build_tensor_cache_gguf failed")
         self.caches = C.cast(self._cache, C.POINTER(_lib.LayerTensorCache * L)).contents
+        if pack if pack is not None else max_tokens > 8:
+            self.pack_layers()
+
+    def pack_layers(self):
+        for l in range(self.cfg.num_layers):
+            check(lib.orome_hip_pack_layer(self.ctx.handle, C.byref(self.cfg), C.byref(self.elrs[l]),
+                                           C.byref(self.caches[l])), "orome_hip_pack_layer")
+
+    def unpack(self):
+        check(lib.orome_hip_unpack_all(self.ctx.handle), "orome_hip_unpack_all")
 
     @property
     def H(self):

@@ -137,3 +137,41 @@ def test_persistent_gemm_zipf_q6k(monkeypatch):
     monkeypatch.delenv("OROME_GEMM_PERSIST_BLOCKS", raising=False)
     assert np.array_equal(out, ref)
     p.gm.close()
+
+
+def test_tile_major_copies_bit_identical(base):
+    """orome_hip_pack_layer's tile-major copies hold the same Q4_K bytes in
+    another order, so the grouped GEMMs give bit-identical outputs with and
+    without them: T=100 (small and big tiles, per-tile kernels) and T=2048
+    (persistent kernels)."""
+    banner("tile-major copies vs row-major, T=100 and T=2048")
+    outs = {}
+    for T in (100, 2048):
+        x, h = base.inputs(T, seed=7000 + T)
+        packed, _ = base.run(0, x, h, path=_lib.OROME_PATH_MFMA)
+        base.gm.unpack()
+        try:
+            plain, _ = base.run(0, x, h, path=_lib.OROME_PATH_MFMA)
+        finally:
+            base.gm.pack_layers()
+        assert np.array_equal(packed, plain), "T=%d" % T
+        outs[T] = packed
+    sel = np.arange(3, 2048, 128)
+    x, h = base.inputs(2048, seed=9048)
+    ref = base.om.forward(0, x[sel], h[sel])
+    assert rel_l2(outs[2048][sel] - h[sel], ref - h[sel]) < TOL
+
+
+def test_tile_major_q6k_down_and_q8_shared():
+    """Layers whose down projection is Q6_K keep a row-major down (gate/up
+    still tile-major); layers with a Q8_0 shared expert are left row-major:
+    both match the oracle and their unpacked runs bit for bit."""
+    banner("tile-major copies: Q6_K down / Q8_0 shared")
+    for kw, T in ((dict(down=14, seed=36), 300), (dict(shared=8, seed=37), 64)):
+        p = Pair(max_tokens=T, **kw)
+        out, _ = run_and_check(p, T, seed=1700 + T, path=_lib.OROME_PATH_MFMA)
+        p.gm.unpack()
+        x, h = p.inputs(T, seed=1700 + T)
+        plain, _ = p.run(0, x, h, path=_lib.OROME_PATH_MFMA)
+        assert np.array_equal(out, plain)
+        p.gm.close()
