@@ -424,6 +424,7 @@ static int forward_impl(orome_hip_ctx *c, const ModelConfig *cfg, const ExpertLa
     a.offsets = c->offsets; a.pairs = c->pairs; a.pos = c->pos; a.list = c->list;
     a.counter = c->counter;
     a.norm_h = NULL; a.norm_w = NULL; a.norm_eps = cfg->rms_norm_eps; a.xnorm = c->xnorm;
+    a.x16 = NULL;
 
     int path = c->path;
     if (path == OROME_PATH_AUTO) path = T <= 8 ? OROME_PATH_GEMV : OROME_PATH_MFMA;
@@ -460,10 +461,11 @@ static int forward_impl(orome_hip_ctx *c, const ModelConfig *cfg, const ExpertLa
                     "combine");
         }
     } else {
-        TLAUNCH(c, ST_ROUTE, launch_route_logits(a, s), "router logits");
+        a.x16 = c->x16; /* the router writes the fp16 copy of x the GEMMs read */
+        TLAUNCH(c, ST_ROUTE, launch_route_logits(a, s), "router logits + fp16 staging");
+        a.x16 = NULL;
         TLAUNCH(c, ST_TOPK, launch_topk(a, s), "top-k");
         TLAUNCH(c, ST_DISPATCH, launch_dispatch(a, c->tiles, c->tiles_b, S ? 1 : 0, c->dcount, s), "dispatch");
-        TLAUNCH(c, ST_STAGE, launch_to_f16(x, T, H, c->x16, s), "fp16 staging");
         /* one launch per tile list (grid sized for the most tiles it can hold) */
         const bool sh_small = (long)T * K <= (long)GEMM_TILE_SMALL * E;
         const int ns_max = E + (S && sh_small ? (T + GEMM_TILE_SMALL - 1) / GEMM_TILE_SMALL : 0),

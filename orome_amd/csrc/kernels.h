@@ -21,6 +21,7 @@ struct RouteArgs {
     const float *x;      /* [T][H] */
     int T, E, H, K;
     float *logits;       /* [T][E+1] */
+    _Float16 *x16;       /* large-batch router: also writes x as fp16, (0,2,1,3) per 4-group (or NULL) */
     int32_t *idx;        /* [T][K] */
     float *w;            /* [T][K] */
     float *sgl;          /* [T] shared-gate logit */

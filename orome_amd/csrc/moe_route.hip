@@ -160,6 +160,16 @@ __global__ __launch_bounds__(256) void k_route_logits(RouteArgs a) {
 #pragma unroll
         for (int t = 0; t < 8; t++)
             xv[t] = t < nt ? *(const f4 *)(a.x + (size_t)(t0 + t) * H + 256 * i + 4 * lane) : f4{0, 0, 0, 0};
+        /* the first row group's blocks also stage x as fp16 for the grouped
+         * GEMMs (round to nearest even, each 4-group stored (0,2,1,3)): wave
+         * wv writes tokens wv and wv + 4 */
+        if (a.x16 && blockIdx.x == 0) {
+#pragma unroll
+            for (int t = 0; t < 8; t++)
+                if ((t & 3) == wv && t < nt)
+                    *(h4 *)(a.x16 + (size_t)(t0 + t) * H + 256 * i + 4 * lane) =
+                        h4{(_Float16)xv[t].x, (_Float16)xv[t].z, (_Float16)xv[t].y, (_Float16)xv[t].w};
+        }
 #pragma unroll
         for (int r = 0; r < 8; r++) {
             const f4 w = wr[r] ? *(const f4 *)(wr[r] + 256 * i + 4 * lane) : f4{0, 0, 0, 0};
