@@ -100,27 +100,29 @@ def test_prefill_matches_decode_path(base):
 
 
 def test_persistent_gemm_bit_identical(base, monkeypatch):
-    """The persistent big-tile GEMMs (a block walks its (tile, row block)
-    units back to back; the weight ring and the activation chunks run on
-    across unit boundaries) compute every unit exactly as the per-tile
-    kernels do: outputs are bit-identical with the default grid, with the
-    per-tile kernels (OROME_GEMM_PERSIST_BLOCKS=0) and with an 8-block grid,
-    where each block walks ~140 units."""
-    banner("persistent GEMM vs per-tile, T=2048")
-    x, h = base.inputs(2048, seed=4096)
-    outs = {}
-    for blocks in (None, "0", "8"):
-        if blocks is None:
-            monkeypatch.delenv("OROME_GEMM_PERSIST_BLOCKS", raising=False)
-        else:
-            monkeypatch.setenv("OROME_GEMM_PERSIST_BLOCKS", blocks)
-        outs[blocks], _ = base.run(0, x, h, path=_lib.OROME_PATH_MFMA)
-    monkeypatch.delenv("OROME_GEMM_PERSIST_BLOCKS", raising=False)
-    assert np.array_equal(outs[None], outs["0"])
-    assert np.array_equal(outs["8"], outs["0"])
-    sel = np.arange(5, 2048, 64)
-    ref = base.om.forward(0, x[sel], h[sel])
-    assert rel_l2(outs[None][sel] - h[sel], ref - h[sel]) < TOL
+    """The persistent GEMMs (a block walks its (tile, row block) units back to
+    back; the weight ring and the activation chunks run on across unit
+    boundaries) compute every unit exactly as the per-tile kernels do:
+    outputs are bit-identical with the default grid, with the per-tile
+    kernels (OROME_GEMM_PERSIST_BLOCKS=0) and with an 8-block grid, where
+    each block walks many units.  T=2048 runs the big-tile kernels, T=512
+    the small-tile down projection."""
+    for T in (512, 2048):
+        banner("persistent GEMM vs per-tile, T=%d" % T)
+        x, h = base.inputs(T, seed=4096 + T)
+        outs = {}
+        for blocks in (None, "0", "8"):
+            if blocks is None:
+                monkeypatch.delenv("OROME_GEMM_PERSIST_BLOCKS", raising=False)
+            else:
+                monkeypatch.setenv("OROME_GEMM_PERSIST_BLOCKS", blocks)
+            outs[blocks], _ = base.run(0, x, h, path=_lib.OROME_PATH_MFMA)
+        monkeypatch.delenv("OROME_GEMM_PERSIST_BLOCKS", raising=False)
+        assert np.array_equal(outs[None], outs["0"]), "T=%d" % T
+        assert np.array_equal(outs["8"], outs["0"]), "T=%d" % T
+        sel = np.arange(5, T, 64)
+        ref = base.om.forward(0, x[sel], h[sel])
+        assert rel_l2(outs[None][sel] - h[sel], ref - h[sel]) < TOL
 
 
 def test_persistent_gemm_zipf_q6k(monkeypatch):
