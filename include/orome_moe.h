@@ -178,13 +178,14 @@ int orome_hip_set_path(orome_hip_ctx *ctx, int path);
 /* Tile-major copies of a layer's Q4_K expert matrices for the MFMA path.  No
  * counterpart in the reference (its kernels read the GGUF blocks in place):
  * registering a layer declares its weights immutable while registered and
- * repacks the routed gate/up (and down, when Q4_K) and the shared expert's
- * Q4_K matrices into one allocation on the context's device (the same bytes
+ * repacks the routed gate/up (Q4_K) and down (Q4_K or Q6_K) and the shared
+ * expert's matrices into one allocation on the context's device (the same bytes
  * as the originals); orome_moe_forward then feeds the grouped GEMMs from the
  * copies, so each wave's weight load is one contiguous 1 KB.  Outputs are
  * bit-identical with and without.  Layers are keyed by the routed gate and
  * shared gate addresses; registering again replaces the copy; layers whose
- * shared expert is not Q4_K are left as they are (OROME_OK).
+ * shared gate/up is not Q4_K are left as they are (OROME_OK), and a down
+ * projection stays row-major when either side is Q8_0.
  * orome_hip_unpack_all frees every copy (orome_hip_destroy calls it). */
 int orome_hip_pack_layer(orome_hip_ctx *ctx, const ModelConfig *cfg, const ExpertLayerRef *layer,
                          const LayerTensorCache *lt);

@@ -70,6 +70,7 @@ struct Pack {
     void *mem;
     const uint8_t *gate, *up, *down, *sgate, *sup, *sdown;
     size_t gate_stride, down_stride;
+    int down_fmt, sdown_fmt; /* GEMM_FMT_Q4K_TILED or GEMM_FMT_Q6K_TILED */
 };
 
 static int set_dev(orome_hip_ctx *c) {
@@ -264,9 +265,14 @@ extern "C" int orome_hip_pack_layer(orome_hip_ctx *c, const ModelConfig *cfg, co
     const bool sh_gu = S && lt->shared_gate.format == QFMT_GGUF_Q4_K && lt->shared_up.format == QFMT_GGUF_Q4_K;
     if (S && !sh_gu) return OROME_OK;
     if (S % 16 || (S && S % 256)) return OROME_OK;
-    const bool dn = elr->down.format == QFMT_GGUF_Q4_K && (!S || lt->shared_down.format == QFMT_GGUF_Q4_K);
-    const size_t gu = packed_q4k_bytes(M, H, E), dnb = dn ? packed_q4k_bytes(H, M, E) : 0,
-                 sgu = S ? packed_q4k_bytes(S, H, 1) : 0, sdn = S && dn ? packed_q4k_bytes(H, S, 1) : 0;
+    /* down projections: Q4_K or Q6_K on both sides (or no shared expert) */
+    auto tileable = [](QuantFormat f) { return f == QFMT_GGUF_Q4_K || f == QFMT_GGUF_Q6_K; };
+    const bool dn = tileable(elr->down.format) && (!S || tileable(lt->shared_down.format));
+    const bool rq6 = elr->down.format == QFMT_GGUF_Q6_K, sq6 = S && lt->shared_down.format == QFMT_GGUF_Q6_K;
+    const size_t gu = packed_q4k_bytes(M, H, E),
+                 dnb = !dn ? 0 : rq6 ? packed_q6k_bytes(H, M, E) : packed_q4k_bytes(H, M, E),
+                 sgu = S ? packed_q4k_bytes(S, H, 1) : 0,
+                 sdn = !(S && dn) ? 0 : sq6 ? packed_q6k_bytes(H, S, 1) : packed_q4k_bytes(H, S, 1);
     if (set_dev(c)) return OROME_EHIP;
     const uint8_t *gate = dev_addr(elr->buffer, elr->gate.offset), *sh_gate = S ? dev_addr(lt->shared_gate.buffer, lt->shared_gate.offset) : NULL;
     if (c->npacks == c->pcap) {
@@ -291,7 +297,9 @@ extern "C" int orome_hip_pack_layer(orome_hip_ctx *c, const ModelConfig *cfg, co
     pk.gate_stride = gu / E;
     if (dn) {
         pk.down = m;
-        rc |= launch_pack_q4k(dev_addr(elr->buffer, elr->down.offset), m, H, M, E, elr->down.expert_stride, c->stream);
+        pk.down_fmt = rq6 ? GEMM_FMT_Q6K_TILED : GEMM_FMT_Q4K_TILED;
+        rc |= (rq6 ? launch_pack_q6k : launch_pack_q4k)(dev_addr(elr->buffer, elr->down.offset), m, H, M, E,
+                                                         elr->down.expert_stride, c->stream);
         m += dnb;
         pk.down_stride = dnb / E;
     }
@@ -304,7 +312,9 @@ extern "C" int orome_hip_pack_layer(orome_hip_ctx *c, const ModelConfig *cfg, co
         m += sgu;
         if (dn) {
             pk.sdown = m;
-            rc |= launch_pack_q4k(dev_addr(lt->shared_down.buffer, lt->shared_down.offset), m, H, S, 1, 0, c->stream);
+            pk.sdown_fmt = sq6 ? GEMM_FMT_Q6K_TILED : GEMM_FMT_Q4K_TILED;
+            rc |= (sq6 ? launch_pack_q6k : launch_pack_q4k)(dev_addr(lt->shared_down.buffer, lt->shared_down.offset), m,
+                                                             H, S, 1, 0, c->stream);
         }
     }
     if (rc || hipStreamSynchronize(c->stream) != hipSuccess) {
@@ -486,10 +496,10 @@ static int forward_impl(orome_hip_ctx *c, const ModelConfig *cfg, const ExpertLa
             if (pk->down) {
                 exm.down = pk->down;
                 exm.down_stride = pk->down_stride;
-                exm.down_fmt = GEMM_FMT_Q4K_TILED;
+                exm.down_fmt = pk->down_fmt;
                 if (S) {
                     shm.down = pk->sdown;
-                    shm.down_fmt = GEMM_FMT_Q4K_TILED;
+                    shm.down_fmt = pk->sdown_fmt;
                 }
             }
         }

@@ -92,9 +92,11 @@ int launch_gemm_down(const ExpertSide &ex, const SharedSide &sh, const _Float16 
                      hipStream_t s);
 /* tile-major repack of Q4_K expert matrices for the grouped GEMMs (format
  * id 4 in ExpertSide / SharedSide) */
-enum { GEMM_FMT_Q4K_TILED = 4 };
+enum { GEMM_FMT_Q4K_TILED = 4, GEMM_FMT_Q6K_TILED = 5 };
 size_t packed_q4k_bytes(int R, int K, int E);
 int launch_pack_q4k(const uint8_t *src, uint8_t *dst, int R, int K, int E, size_t src_stride, hipStream_t s);
+size_t packed_q6k_bytes(int R, int K, int E);
+int launch_pack_q6k(const uint8_t *src, uint8_t *dst, int R, int K, int E, size_t src_stride, hipStream_t s);
 int launch_combine(const float *y, const float *ysh, const uint32_t *pos, const float *w,
                    const float *sgl, int has_shared, const float *h_in, float *h_out, int T,
                    int H, int K, hipStream_t s);

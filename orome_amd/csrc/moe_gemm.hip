@@ -38,8 +38,9 @@ extern "C" __attribute__((visibility("default"))) int orome_trace_fetch_gemm(uns
 }
 #endif
 
-/* FQ4KT: Q4_K repacked tile-major (launch_pack_q4k), same values */
-enum { FQ4K = 0, FQ6K = 2, FQ8 = 3, FQ4KT = GEMM_FMT_Q4K_TILED };
+/* FQ4KT, FQ6KT: Q4_K / Q6_K repacked tile-major (launch_pack_q4k,
+ * launch_pack_q6k), same values */
+enum { FQ4K = 0, FQ6K = 2, FQ8 = 3, FQ4KT = GEMM_FMT_Q4K_TILED, FQ6KT = GEMM_FMT_Q6K_TILED };
 
 typedef float f4v __attribute__((ext_vector_type(4)));
 
@@ -58,13 +59,13 @@ struct Shape {
 #define BLD (KCH + 16)                  /* chunk row pitch (halves): 544 bytes, B-fragment reads conflict-free */
 
 DEV size_t gemm_row_bytes(int fmt, int n) {
-    return fmt == FQ4K || fmt == FQ4KT ? (size_t)(n / 256) * 144 : fmt == FQ6K ? (size_t)(n / 256) * 210 : (size_t)(n / 32) * 34;
+    return fmt == FQ4K || fmt == FQ4KT ? (size_t)(n / 256) * 144 : fmt == FQ6K || fmt == FQ6KT ? (size_t)(n / 256) * 210 : (size_t)(n / 32) * 34;
 }
 /* offset of lane row i of the 16-row block starting at row0: a row of its
  * own, or (tile-major Q4_K) the block base plus the lane's 16-byte column */
 template <int FMT>
 DEV size_t lane_row(int row0, int i, size_t rbytes) {
-    return FMT == FQ4KT ? (size_t)row0 * rbytes + (size_t)i * 16 : (size_t)(row0 + i) * rbytes;
+    return FMT == FQ4KT || FMT == FQ6KT ? (size_t)row0 * rbytes + (size_t)i * 16 : (size_t)(row0 + i) * rbytes;
 }
 DEV uint32_t u4_at(u4 v, int i) { return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w; }
 DEV h2 splat(_Float16 v) { return h2{v, v}; }
@@ -98,7 +99,7 @@ DEV int frag_pos(int c) {
     if (FMT == FQ4K || FMT == FQ4KT) { /* lane kg, step s: k = 64(kg>>1) + 16(kg&1) + 4s (+32 high nibbles) */
         const int g = c >> 4, r = c & 15, hi = r >> 3, rr = r & 7;
         return (((rr & 3) * 4 + 2 * g + (rr >> 2)) * 8) + 4 * hi;
-    } else if (FMT == FQ6K) { /* k = 32(kg&1) + 16(kg>>1) + 4s (+64 high nibbles) */
+    } else if (FMT == FQ6K || FMT == FQ6KT) { /* k = 32(kg&1) + 16(kg>>1) + 4s (+64 high nibbles) */
         const int hi = c >> 4, r = c & 15, odd = r >> 3, q = r & 7;
         return (((q & 3) * 4 + 2 * (q >> 2) + odd) * 8) + 4 * hi;
     } else { /* k = 32s + 8kg .. +7 */
@@ -208,6 +209,23 @@ struct Span<FQ6K> {
         q6_h2_0213(a, b, 0, odd2, p02, p13);
         q6_h2_0213(a, b, 4, 4 + odd2, r02, r13);
         return cat4((p02 * scl) * d, (p13 * scl) * d, (r02 * sch) * d, (r13 * sch) * d);
+    }
+};
+
+/* Tile-major Q6_K: per 16-row block and super-block, 3360 bytes (16 rows of
+ * 210) = for each 128-k half the 64 lanes' 16 low-bit bytes in lane order
+ * (kg * 16 + i), then for each half the high-bit bytes of lane groups
+ * (kg >> 1) * 16 + i, then each row's 16 scales, then the 16 rows' d.  All
+ * but d are aligned 16-, 8-byte loads.  `p` is the block base plus 16 i. */
+template <>
+struct Span<FQ6KT> : Span<FQ6K> {
+    MDEV void load(const uint8_t *p, int j, int kg) {
+        const uint8_t *b = p + (size_t)(j >> 1) * 3360;
+        const int h = j & 1, i = (int)(threadIdx.x & 15);
+        ql = ld_u4(b + h * 1024 + kg * 256);
+        qh = ld_u4(b + 2048 + h * 512 + (kg >> 1) * 256);
+        sc8 = *(const u2 *)(b + 3072 + h * 8);
+        dw = *(const uint16_t *)(b + 3328 - 14 * i);
     }
 };
 
@@ -846,10 +864,11 @@ int launch_gemm_down(const ExpertSide &ex, const SharedSide &sh, const _Float16 
     if ((M / KC * DN_RPW) % 4 || (sh.gate && (sh.S / KC * DN_RPW) % 4)) return -2;
     /* all of a tile's activations stay resident: in_dim <= 2 chunks */
     if (H % NB || M % KCH || M > 2 * KCH || (sh.gate && (sh.S % KCH || sh.S > 2 * KCH))) return -2;
-    if (ex.down_fmt != FQ4K && ex.down_fmt != FQ6K && ex.down_fmt != FQ4KT) return -2;
-    /* tile-major routed down needs a tile-major shared down (or none) */
-    const int sf = sh.gate ? sh.down_fmt : ex.down_fmt == FQ4KT ? FQ4KT : FQ4K;
-    if (ex.down_fmt == FQ4KT ? sf != FQ4KT : sf != FQ4K && sf != FQ6K && sf != FQ8) return -2;
+    const bool dtiled = ex.down_fmt == FQ4KT || ex.down_fmt == FQ6KT;
+    if (ex.down_fmt != FQ4K && ex.down_fmt != FQ6K && !dtiled) return -2;
+    /* a tile-major routed down needs a tile-major shared down (or none) */
+    const int sf = sh.gate ? sh.down_fmt : dtiled ? ex.down_fmt : FQ4K;
+    if (dtiled ? sf != FQ4KT && sf != FQ6KT : sf != FQ4K && sf != FQ6K && sf != FQ8) return -2;
     GemmArgs a = {};
     a.wa = ex.down; a.stride_a = ex.down_stride;
     a.sh_a = sh.gate ? sh.down : nullptr;
@@ -865,6 +884,7 @@ int launch_gemm_down(const ExpertSide &ex, const SharedSide &sh, const _Float16 
     do {                                                                                                              \
         if (ex.down_fmt == FQ4K) hipLaunchKernelGGL((k_gemm_down_p<FQ4K, TB>), dim3(pb), block, 0, s, a);               \
         else if (ex.down_fmt == FQ4KT) hipLaunchKernelGGL((k_gemm_down_p<FQ4KT, TB>), dim3(pb), block, 0, s, a);        \
+        else if (ex.down_fmt == FQ6KT) hipLaunchKernelGGL((k_gemm_down_p<FQ6KT, TB>), dim3(pb), block, 0, s, a);        \
         else hipLaunchKernelGGL((k_gemm_down_p<FQ6K, TB>), dim3(pb), block, 0, s, a);                                   \
     } while (0)
         if (tile_m == GEMM_TILE_BIG) DP_LAUNCH(GEMM_TILE_BIG / 16);
@@ -879,7 +899,11 @@ int launch_gemm_down(const ExpertSide &ex, const SharedSide &sh, const _Float16 
         else hipLaunchKernelGGL((k_gemm_down<EF, SF, 0, GEMM_TILE_BIG / 16>), grid, block, 0, s, a);              \
     } while (0)
     if (ex.down_fmt == FQ4KT) {
-        DN_LAUNCH(FQ4KT, FQ4KT);
+        if (sf == FQ4KT) DN_LAUNCH(FQ4KT, FQ4KT);
+        else DN_LAUNCH(FQ4KT, FQ6KT);
+    } else if (ex.down_fmt == FQ6KT) {
+        if (sf == FQ4KT) DN_LAUNCH(FQ6KT, FQ4KT);
+        else DN_LAUNCH(FQ6KT, FQ6KT);
     } else if (ex.down_fmt == FQ4K) {
         if (sf == FQ4K) DN_LAUNCH(FQ4K, FQ4K);
         else if (sf == FQ6K) DN_LAUNCH(FQ4K, FQ6K);
@@ -924,5 +948,50 @@ int launch_pack_q4k(const uint8_t *src, uint8_t *dst, int R, int K, int E, size_
     if (R % 16 || K % 256 || E < 1 || ((uintptr_t)src & 15) || ((uintptr_t)dst & 15) || (src_stride & 15)) return -2;
     const int nsb = K / 256;
     hipLaunchKernelGGL(k_pack_q4k, dim3((unsigned)(R / 16 * nsb), (unsigned)E), dim3(144), 0, s, src, dst, R, nsb, src_stride);
+    return hipGetLastError() == hipSuccess ? 0 : -3;
+}
+
+/* Q6_K matrices [R rows][K/256 super-blocks of 210 B] into the tile-major
+ * layout of Span<FQ6KT> (a byte permutation; source blocks are only 2-byte
+ * aligned, so the copy moves 16-bit words).  Output byte ob of tile (rb, sb):
+ *   ob < 2048: half h = ob / 1024, lane (kg, i): row i, byte h 64 + 32 (kg & 1) + 16 (kg >> 1) + ob % 16
+ *   ob < 3072: half h, group g = kg >> 1:  row i, byte 128 + h 32 + 16 g + ob % 16
+ *   ob < 3328: row i = (ob - 3072) / 16,     byte 192 + ob % 16
+ *   else:      row i = (ob - 3328) / 2,      byte 208 + ob % 2 */
+__global__ __launch_bounds__(256) void k_pack_q6k(const uint8_t *src, uint8_t *dst, int R, int nsb, size_t src_stride) {
+    const int tile = blockIdx.x, e = blockIdx.y, rb = tile / nsb, sb = tile - rb * nsb;
+    const size_t rbytes = (size_t)nsb * 210;
+    const uint8_t *t0 = src + (size_t)e * src_stride + (size_t)rb * 16 * rbytes + (size_t)sb * 210;
+    uint8_t *d0 = dst + (size_t)e * R * rbytes + (size_t)tile * 3360;
+    for (int w = threadIdx.x; w < 1680; w += 256) {
+        const int ob = 2 * w;
+        int row, byte;
+        if (ob < 2048) {
+            const int h = ob >> 10, ln = (ob & 1023) >> 4, kg = ln >> 4;
+            row = ln & 15;
+            byte = h * 64 + 32 * (kg & 1) + 16 * (kg >> 1) + (ob & 15);
+        } else if (ob < 3072) {
+            const int x = ob - 2048, h = x >> 9, idx = (x & 511) >> 4;
+            row = idx & 15;
+            byte = 128 + h * 32 + 16 * (idx >> 4) + (x & 15);
+        } else if (ob < 3328) {
+            const int x = ob - 3072;
+            row = x >> 4;
+            byte = 192 + (x & 15);
+        } else {
+            const int x = ob - 3328;
+            row = x >> 1;
+            byte = 208 + (x & 1);
+        }
+        *(uint16_t *)(d0 + ob) = *(const uint16_t *)(t0 + (size_t)row * rbytes + byte);
+    }
+}
+
+size_t packed_q6k_bytes(int R, int K, int E) { return (size_t)E * R * (K / 256) * 210; }
+
+int launch_pack_q6k(const uint8_t *src, uint8_t *dst, int R, int K, int E, size_t src_stride, hipStream_t s) {
+    if (R % 16 || K % 256 || E < 1 || ((uintptr_t)src & 1) || ((uintptr_t)dst & 15) || (src_stride & 1)) return -2;
+    const int nsb = K / 256;
+    hipLaunchKernelGGL(k_pack_q6k, dim3((unsigned)(R / 16 * nsb), (unsigned)E), dim3(256), 0, s, src, dst, R, nsb, src_stride);
     return hipGetLastError() == hipSuccess ? 0 : -3;
 }

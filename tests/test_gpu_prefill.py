@@ -165,11 +165,12 @@ def test_tile_major_copies_bit_identical(base):
 
 
 def test_tile_major_q6k_down_and_q8_shared():
-    """Layers whose down projection is Q6_K keep a row-major down (gate/up
-    still tile-major); layers with a Q8_0 shared expert are left row-major:
-    both match the oracle and their unpacked runs bit for bit."""
+    """Q6_K down projections get tile-major Q6_K copies (routed only, and
+    routed + shared); layers with a Q8_0 shared expert are left row-major.
+    Each matches the oracle and its unpacked run bit for bit."""
     banner("tile-major copies: Q6_K down / Q8_0 shared")
-    for kw, T in ((dict(down=14, seed=36), 300), (dict(shared=8, seed=37), 64)):
+    for kw, T in ((dict(down=14, seed=36), 300), (dict(down=14, shared_down=14, seed=38), 96),
+                  (dict(shared=8, seed=37), 64)):
         p = Pair(max_tokens=T, **kw)
         out, _ = run_and_check(p, T, seed=1700 + T, path=_lib.OROME_PATH_MFMA)
         p.gm.unpack()
