@@ -285,26 +285,13 @@ DEV void put_tiles(uint32_t *list, uint32_t t0, uint32_t e, uint32_t first, uint
     }
 }
 
-__global__ __launch_bounds__(DSP_THREADS) void k_dispatch_scan(RouteArgs a, uint32_t *cnt, int G,
-                                                               uint32_t *tiles_s, uint32_t *tiles_b,
-                                                               int has_shared) {
-    __shared__ uint32_t hist[DSP_THREADS], offs[DSP_THREADS], arank[DSP_THREADS], ts[DSP_THREADS],
-        tbg[DSP_THREADS];
+/* Given per-expert counts (hist, copied into offs), and offs/arank/ts/tbg
+ * filled with the counts, active flags and tile counts: scans them and
+ * writes offsets, the active list and the two GEMM tile lists (E <=
+ * blockDim.x; every thread of the block calls it). */
+DEV void dispatch_lists(const RouteArgs &a, const uint32_t *hist, uint32_t *offs, uint32_t *arank, uint32_t *ts,
+                        uint32_t *tbg, uint32_t *tiles_s, uint32_t *tiles_b, int has_shared) {
     const int E = a.E, T = a.T, tid = threadIdx.x;
-    if (tid < E) {
-        uint32_t run = 0;
-        for (int g = 0; g < G; g++) {
-            const uint32_t c = cnt[(size_t)g * E + tid];
-            cnt[(size_t)g * E + tid] = run;
-            run += c;
-        }
-        hist[tid] = run;
-        offs[tid] = run;
-        arank[tid] = run != 0;
-        ts[tid] = n_small_tiles(run);
-        tbg[tid] = n_big_tiles(run);
-    }
-    __syncthreads();
     block_scan4(offs, arank, ts, tbg, E);
     /* inclusive -> exclusive views: ex(x)[e] = x[e] - own */
     if (tid < E) {
@@ -335,6 +322,29 @@ __global__ __launch_bounds__(DSP_THREADS) void k_dispatch_scan(RouteArgs a, uint
     }
 }
 
+__global__ __launch_bounds__(DSP_THREADS) void k_dispatch_scan(RouteArgs a, uint32_t *cnt, int G,
+                                                               uint32_t *tiles_s, uint32_t *tiles_b,
+                                                               int has_shared) {
+    __shared__ uint32_t hist[DSP_THREADS], offs[DSP_THREADS], arank[DSP_THREADS], ts[DSP_THREADS],
+        tbg[DSP_THREADS];
+    const int E = a.E, T = a.T, tid = threadIdx.x;
+    if (tid < E) {
+        uint32_t run = 0;
+        for (int g = 0; g < G; g++) {
+            const uint32_t c = cnt[(size_t)g * E + tid];
+            cnt[(size_t)g * E + tid] = run;
+            run += c;
+        }
+        hist[tid] = run;
+        offs[tid] = run;
+        arank[tid] = run != 0;
+        ts[tid] = n_small_tiles(run);
+        tbg[tid] = n_big_tiles(run);
+    }
+    __syncthreads();
+    dispatch_lists(a, hist, offs, arank, ts, tbg, tiles_s, tiles_b, has_shared);
+}
+
 __global__ __launch_bounds__(DSP_TOK) void k_dispatch_scatter(RouteArgs a, const uint32_t *base) {
     extern __shared__ uint32_t mask[]; /* E * DSP_WORDS, then E * DSP_WORDS word prefixes */
     uint32_t *wpre = mask + a.E * DSP_WORDS;
@@ -357,6 +367,61 @@ __global__ __launch_bounds__(DSP_TOK) void k_dispatch_scatter(RouteArgs a, const
             const int i = ek[k] * DSP_WORDS + (tid >> 5);
             const uint32_t pos = wpre[i] + __popc(mask[i] & below);
             const uint32_t p = (uint32_t)(t * K + k);
+            a.pairs[pos] = p;
+            a.pos[p] = pos;
+        }
+}
+
+/* The same dispatch in one block for T <= DSP_THREADS tokens (one launch
+ * instead of three; the positions are identical): thread t sets its pairs'
+ * bits in the membership masks of its DSP_TOK-token sub-chunk; an expert's
+ * count is the popcount of its masks; offsets and lists follow as in
+ * k_dispatch_scan; a pair's position is its expert's offset + the counts of
+ * earlier sub-chunks + the popcount of its sub-chunk's mask below its token.
+ * LDS: masks and word prefixes for DSP1_SUB sub-chunks of up to 256 experts. */
+#define DSP1_SUB (DSP_THREADS / DSP_TOK)
+__global__ __launch_bounds__(DSP_THREADS) void k_dispatch_one(RouteArgs a, uint32_t *tiles_s, uint32_t *tiles_b,
+                                                              int has_shared) {
+    __shared__ uint32_t hist[DSP_THREADS], offs[DSP_THREADS], arank[DSP_THREADS], ts[DSP_THREADS],
+        tbg[DSP_THREADS];
+    __shared__ uint32_t mask[DSP1_SUB * 256 * DSP_WORDS], wpre[DSP1_SUB * 256 * DSP_WORDS];
+    const int E = a.E, K = a.K, T = a.T, tid = threadIdx.x;
+    const int sub = tid / DSP_TOK, tl = tid % DSP_TOK;
+    for (int i = tid; i < DSP1_SUB * E * DSP_WORDS; i += DSP_THREADS) mask[i] = 0;
+    __syncthreads();
+    int ek[OROME_MAXK];
+#pragma unroll
+    for (int k = 0; k < OROME_MAXK; k++)
+        if (k < K) {
+            ek[k] = tid < T ? a.idx[tid * K + k] : -1;
+            if (ek[k] >= 0) atomicOr(&mask[(sub * E + ek[k]) * DSP_WORDS + (tl >> 5)], 1u << (tl & 31));
+        }
+    __syncthreads();
+    if (tid < E) { /* word prefixes from 0, and the expert's count */
+        uint32_t run = 0;
+        for (int sc = 0; sc < DSP1_SUB; sc++)
+#pragma unroll
+            for (int w = 0; w < DSP_WORDS; w++) {
+                const int i = (sc * E + tid) * DSP_WORDS + w;
+                wpre[i] = run;
+                run += __popc(mask[i]);
+            }
+        hist[tid] = run;
+        offs[tid] = run;
+        arank[tid] = run != 0;
+        ts[tid] = n_small_tiles(run);
+        tbg[tid] = n_big_tiles(run);
+    }
+    __syncthreads();
+    dispatch_lists(a, hist, offs, arank, ts, tbg, tiles_s, tiles_b, has_shared);
+    __syncthreads();
+    const uint32_t below = (1u << (tl & 31)) - 1u;
+#pragma unroll
+    for (int k = 0; k < OROME_MAXK; k++)
+        if (k < K && ek[k] >= 0) {
+            const int e = ek[k], i = (sub * E + e) * DSP_WORDS + (tl >> 5);
+            const uint32_t pos = offs[e] - hist[e] + wpre[i] + __popc(mask[i] & below);
+            const uint32_t p = (uint32_t)(tid * K + k);
             a.pairs[pos] = p;
             a.pos[p] = pos;
         }
@@ -451,6 +516,13 @@ int launch_dispatch(const RouteArgs &a, uint32_t *tiles_s, uint32_t *tiles_b, in
                     hipStream_t s) {
     const size_t lds = sizeof(uint32_t) * (size_t)a.E * DSP_WORDS * 2;
     if (lds > 64 * 1024 || a.E > DSP_THREADS || a.K > OROME_MAXK) return -2;
+#ifndef DISPATCH_ONE
+#define DISPATCH_ONE 1
+#endif
+    if (DISPATCH_ONE && a.E <= 256 && a.T <= DSP_THREADS) {
+        hipLaunchKernelGGL(k_dispatch_one, dim3(1), dim3(DSP_THREADS), 0, s, a, tiles_s, tiles_b, has_shared);
+        return hipGetLastError() == hipSuccess ? 0 : -3;
+    }
     const int G = dispatch_blocks(a.T);
     hipLaunchKernelGGL(k_dispatch_count, dim3(G), dim3(DSP_TOK), lds / 2, s, a, cnt);
     hipLaunchKernelGGL(k_dispatch_scan, dim3(1), dim3(DSP_THREADS), 0, s, a, cnt, G, tiles_s, tiles_b, has_shared);
