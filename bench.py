@@ -171,6 +171,33 @@ def main():
                 for i in range(8)}
     restore()
 
+    # gate/up launch durations as a kernel trace reports them: every block of
+    # the gate/up kernels stamps its start and end (orome_hip_kernel_timing);
+    # a launch lasts from its first block's start to its last block's end
+    # (the big- and small-tile launches of the MFMA path together)
+    KTB = 16384
+    ktbuf = DeviceBuffer(ctx, KTB * 2 * 8)
+    zeros = np.zeros(KTB * 2, np.uint64)
+    check(lib.orome_hip_kernel_timing(ctx.handle, ktbuf.ptr, KTB), "kernel_timing")
+    spans, spans_big, spans_small = [], [], []
+    for i in range(40):
+        ktbuf.upload(zeros)
+        if stack:
+            gm.layer_forward(i % L, xs[i % NX], T)
+        else:
+            gm.forward(i % L, xs[i % NX], hs[i % NX], outs[i % 2], T)
+        ctx.sync()
+        v = ktbuf.download(np.uint64, (KTB, 2)).astype(np.int64)
+        ok = (v[:, 0] > 0) & (v[:, 1] > 0)
+        spans.append((v[ok, 1].max() - v[ok, 0].min()) * 0.01)  # 100 MHz ticks -> us
+        for part, lst in ((v[:KTB // 2], spans_big), (v[KTB // 2:], spans_small)):
+            okp = (part[:, 0] > 0) & (part[:, 1] > 0)
+            if okp.any():
+                lst.append((part[okp, 1].max() - part[okp, 0].min()) * 0.01)
+    check(lib.orome_hip_kernel_timing(ctx.handle, None, 0), "kernel_timing")
+    ktbuf.free()
+    restore()
+
     # algorithmic work per gate/up launch and per MoE layer
     nl = L if stack else 1
     n_q6 = sum(1 for l in range(L) if cf["spec"].get("q6k_every") and l % 4 == 3) if stack else 0
@@ -184,7 +211,7 @@ def main():
         layer_bytes += (q6k_bytes(H, M) - q4k_bytes(H, M)) * u_mean * n_q6 / L
     step_bytes = layer_bytes * nl
     step_flops = 2.0 * (rows * M * H * 3 + T * (E + 1) * H) * nl
-    gu_us = stage_us["gate_up"]
+    gu_us = float(np.mean(spans))
     gu_gbs = gu_bytes / (gu_us * 1e-6) / 1e9
     gu_tflops = gu_flops / (gu_us * 1e-6) / 1e12
     mfma_bound = T >= 2048
@@ -200,7 +227,11 @@ def main():
     if os.path.exists(tf):
         traffic = json.load(open(tf)).get("gate_up_hbm_bytes_per_launch")
     roof.update({"traffic": traffic, "algorithmic_bytes_per_launch": int(gu_bytes),
-                 "algorithmic_flops_per_launch": gu_flops, "avg_launch_us": gu_us,
+                 "algorithmic_flops_per_launch": gu_flops, "avg_launch_us": round(gu_us, 3),
+                 "timing": "per-block s_memrealtime stamps of 40 launches (first start to last end)",
+                 "event_us": stage_us["gate_up"],
+                 "big_tile_us": round(float(np.mean(spans_big)), 3) if spans_big else None,
+                 "small_tile_us": round(float(np.mean(spans_small)), 3) if spans_small and T > 8 else None,
                  "gbs": round(gu_gbs, 1), "tflops": round(gu_tflops, 2)})
 
     cpu = None

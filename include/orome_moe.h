@@ -191,6 +191,15 @@ int orome_hip_pack_layer(orome_hip_ctx *ctx, const ModelConfig *cfg, const Exper
                          const LayerTensorCache *lt);
 int orome_hip_unpack_all(orome_hip_ctx *ctx);
 
+/* Launch timing of the gate/up stage for measurement tools (no counterpart in
+ * the reference): with `stamps` set (device memory of 2 * blocks 64-bit words,
+ * or NULL to stop), each gate/up kernel block b writes its start and end time
+ * (s_memrealtime, 100 MHz) to stamps[2 b] and stamps[2 b + 1]; on the MFMA
+ * path the big-tile launch uses blocks [0, blocks/2) and the small-tile one
+ * [blocks/2, blocks).  A launch whose grid does not fit writes nothing.  The
+ * launch's duration is max(end) - min(start) over the blocks written. */
+int orome_hip_kernel_timing(orome_hip_ctx *ctx, unsigned long long *stamps, int blocks);
+
 /* Device memory plumbing on the context's device. */
 void *orome_hip_malloc(orome_hip_ctx *ctx, size_t bytes);
 int orome_hip_free(orome_hip_ctx *ctx, void *p);

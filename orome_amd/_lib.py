@@ -103,6 +103,7 @@ SIGNATURES = {
     "orome_hip_dtoh": (I, [VP, VP, VP, SZ]),
     "orome_hip_pack_layer": (I, [VP, P(ModelConfig), P(ExpertLayerRef), P(LayerTensorCache)]),
     "orome_hip_unpack_all": (I, [VP]),
+    "orome_hip_kernel_timing": (I, [VP, VP, I]),
     "format_provider_open_gguf": (P(FormatProvider), [P(GGUFFile), VP]),
     "format_provider_close": (None, [P(FormatProvider)]),
     "format_resolve_expert_layer": (ExpertLayerRef, [P(FormatProvider), I, U32]),

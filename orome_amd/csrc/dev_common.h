@@ -33,6 +33,21 @@ static __device__ unsigned long long g_trace[65536 * 8];
 #else
 #define TSTAMP(i) do {} while (0)
 #endif
+/* Optional per-block start/end stamps of a kernel launch (s_memrealtime,
+ * 100 MHz) into kt[2 b], kt[2 b + 1] for block b: the launch's duration is
+ * max(end) - min(start), the quantity a kernel trace reports.  kt NULL:
+ * nothing is written. */
+#define KT_BEGIN(kt)                                                                   \
+    do {                                                                               \
+        if ((kt) && threadIdx.x == 0) (kt)[2 * blockIdx.x] = __builtin_amdgcn_s_memrealtime(); \
+    } while (0)
+#define KT_END(kt)                                                                     \
+    do {                                                                               \
+        if (kt) {                                                                      \
+            __syncthreads();                                                           \
+            if (threadIdx.x == 0) (kt)[2 * blockIdx.x + 1] = __builtin_amdgcn_s_memrealtime(); \
+        }                                                                              \
+    } while (0)
 
 DEV h2 as_h2(uint32_t v) { return __builtin_bit_cast(h2, v); }
 DEV uint32_t as_u32(h2 v) { return __builtin_bit_cast(uint32_t, v); }

@@ -61,6 +61,9 @@ struct orome_hip_ctx {
     /* tile-major copies of registered layers' Q4_K expert matrices */
     struct Pack *packs;
     int npacks, pcap;
+    /* per-block stamps of the gate/up launches (orome_hip_kernel_timing) */
+    unsigned long long *kt;
+    int kt_blocks;
 };
 
 /* One registered layer: keyed by the routed gate and shared gate device
@@ -189,6 +192,13 @@ extern "C" int orome_hip_set_path(orome_hip_ctx *c, int path) {
     if (!c || path < OROME_PATH_AUTO || path > OROME_PATH_MFMA)
         return orome_fail(OROME_EINVAL, "orome_hip_set_path: bad argument");
     c->path = path;
+    return OROME_OK;
+}
+
+extern "C" int orome_hip_kernel_timing(orome_hip_ctx *c, unsigned long long *stamps, int blocks) {
+    if (!c || (stamps && blocks < 2)) return orome_fail(OROME_EINVAL, "orome_hip_kernel_timing: bad argument");
+    c->kt = stamps;
+    c->kt_blocks = stamps ? blocks : 0;
     return OROME_OK;
 }
 
@@ -456,7 +466,7 @@ static int forward_impl(orome_hip_ctx *c, const ModelConfig *cfg, const ExpertLa
          * (saves a launch); larger batches route once in a separate kernel */
         const int fold = T <= 2;
         if (!fold) TLAUNCH(c, ST_TOPK, launch_topk_dispatch_small(a, s), "top-k + dispatch");
-        TLAUNCH(c, ST_GATE_UP, launch_gemv_gate_up(ex, sh, a, fold, x, T, H, M, K, E, c->act, c->act_sh, s),
+        TLAUNCH(c, ST_GATE_UP, launch_gemv_gate_up(ex, sh, a, fold, x, T, H, M, K, E, c->act, c->act_sh, s, c->kt, c->kt_blocks),
                 "gemv gate/up");
         /* one token: down and combine in one kernel when the shape allows */
         const bool dc1 = T == 1 && K <= 8 && M == 512 && (!S || S == 512);
@@ -506,9 +516,9 @@ static int forward_impl(orome_hip_ctx *c, const ModelConfig *cfg, const ExpertLa
         auto gate_up = [&](int tm, hipStream_t st) {
             return tm == GEMM_TILE_SMALL
                        ? launch_gemm_gate_up(exm, shm, c->x16, c->tmax, T, H, M, K, E, tm, c->tiles, ns_max, c->pairs, c->act,
-                                             c->act_sh, st)
+                                             c->act_sh, st, c->kt ? c->kt + 2 * (c->kt_blocks / 2) : nullptr, c->kt_blocks / 2)
                        : launch_gemm_gate_up(exm, shm, c->x16, c->tmax, T, H, M, K, E, tm, c->tiles_b, nb_max, c->pairs, c->act,
-                                             c->act_sh, st);
+                                             c->act_sh, st, c->kt, c->kt_blocks / 2);
         };
         auto down = [&](int tm, hipStream_t st) {
             return tm == GEMM_TILE_SMALL

@@ -62,7 +62,7 @@ int launch_dispatch(const RouteArgs &a, uint32_t *tiles_s, uint32_t *tiles_b, in
  * `ra`), otherwise it reads the routing written by launch_topk_dispatch_small */
 int launch_gemv_gate_up(const ExpertSide &ex, const SharedSide &sh, const RouteArgs &ra, int route_in_block,
                         const float *x, int T, int H, int M, int K, int E, _Float16 *act, _Float16 *act_sh,
-                        hipStream_t s);
+                        hipStream_t s, unsigned long long *kt = nullptr, int kt_cap = 0);
 int launch_topk_dispatch_small(const RouteArgs &a, hipStream_t s);
 
 int launch_gemv_down(const ExpertSide &ex, const SharedSide &sh, const _Float16 *act,
@@ -85,7 +85,7 @@ int launch_to_f16(const float *x, int T, int H, _Float16 *x16, hipStream_t s);
  * zrow_sh name an all-zero row of the activation source(s) */
 int launch_gemm_gate_up(const ExpertSide &ex, const SharedSide &sh, const _Float16 *x16, int zrow, int T,
                         int H, int M, int K, int E, int tile_m, const uint32_t *tiles, int n_tiles_max,
-                        const uint32_t *pairs, _Float16 *act, _Float16 *act_sh, hipStream_t s);
+                        const uint32_t *pairs, _Float16 *act, _Float16 *act_sh, hipStream_t s, unsigned long long *kt = nullptr, int kt_cap = 0);
 int launch_gemm_down(const ExpertSide &ex, const SharedSide &sh, const _Float16 *act,
                      const _Float16 *act_sh, int zrow, int zrow_sh, int T, int H, int M, int K, int E, int tile_m,
                      const uint32_t *tiles, int n_tiles_max, float *y, float *ysh,

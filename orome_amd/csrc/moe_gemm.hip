@@ -425,6 +425,7 @@ struct GemmArgs {
     int nyb;                  /* row blocks per tile */
     const uint32_t *tiles, *pairs;
     _Float16 *act, *act_sh;   /* gate/up outputs */
+    unsigned long long *kt;   /* gate/up: per-block launch stamps (KT_BEGIN / KT_END) or NULL */
     float *y, *ysh;           /* down outputs */
 };
 
@@ -711,7 +712,7 @@ struct DnPol {
 
 
 template <int SFMT, int NST, int TBM>
-__global__ __launch_bounds__(Shape<TBM>::W * 64) void k_gemm_gate_up(GemmArgs a) {
+DEV void k_gemm_gate_up_body(GemmArgs a) {
     __shared__ __attribute__((aligned(16))) _Float16 xs[2 * TBM * 16 * BLD];
     __shared__ int rowoff[TBM * 16];
     int ti, yb;
@@ -737,6 +738,13 @@ __global__ __launch_bounds__(Shape<TBM>::W * 64) void k_gemm_gate_up(GemmArgs a)
                                   a.H, rowoff, (int)rows, yb, xs, epi);
     }
     if (threadIdx.x == 0) TSTAMP(6);
+}
+
+template <int SFMT, int NST, int TBM>
+__global__ __launch_bounds__(Shape<TBM>::W * 64) void k_gemm_gate_up(GemmArgs a) {
+    KT_BEGIN(a.kt);
+    k_gemm_gate_up_body<SFMT, NST, TBM>(a);
+    KT_END(a.kt);
 }
 
 template <int EFMT, int SFMT, int NST, int TBM>
@@ -775,10 +783,17 @@ __global__ __launch_bounds__(Shape<TBM>::W * 64) void k_gemm_down(GemmArgs a) {
 #define GEMM_PERSIST_SMALL_DN 2
 #endif
 template <int TBM, int GF>
-__global__ __launch_bounds__(Shape<TBM>::W * 64) void k_gemm_gate_up_p(GemmArgs a) {
+DEV void k_gemm_gate_up_p_body(GemmArgs a) {
     __shared__ __attribute__((aligned(16))) _Float16 xs[3 * TBM * 16 * BLD];
     __shared__ int rowoff[3 * TBM * 16];
     tile_stream<GF, 2, GU_RPW, Shape<TBM>::DEPTH, 16, TBM>(GuPol{a}, xs, rowoff);
+}
+
+template <int TBM, int GF>
+__global__ __launch_bounds__(Shape<TBM>::W * 64) void k_gemm_gate_up_p(GemmArgs a) {
+    KT_BEGIN(a.kt);
+    k_gemm_gate_up_p_body<TBM, GF>(a);
+    KT_END(a.kt);
 }
 
 template <int EFMT, int TBM>
@@ -811,7 +826,8 @@ static unsigned persist_blocks() {
 /* ------------------------------------------------------------ launch */
 int launch_gemm_gate_up(const ExpertSide &ex, const SharedSide &sh, const _Float16 *x16, int zrow, int T,
                         int H, int M, int K, int E, int tile_m, const uint32_t *tiles, int n_tiles_max,
-                        const uint32_t *pairs, _Float16 *act, _Float16 *act_sh, hipStream_t s) {
+                        const uint32_t *pairs, _Float16 *act, _Float16 *act_sh, hipStream_t s,
+                        unsigned long long *kt, int kt_cap) {
     const int W = tile_m == GEMM_TILE_SMALL ? Shape<GEMM_TILE_SMALL / 16>::W : Shape<GEMM_TILE_BIG / 16>::W;
     const int NB = W * 16 * GU_RPW;
     if ((H / KC * GU_RPW) % 4) return -2; /* every ring depth used divides the unit count */
@@ -828,7 +844,9 @@ int launch_gemm_gate_up(const ExpertSide &ex, const SharedSide &sh, const _Float
     const dim3 grid((unsigned)((n_tiles_max + 7) / 8 * 8 * a.nyb)), block(W * 64);
     const bool q8 = sh.gate && sh.gate_fmt == FQ8;
     const unsigned pb = !GEMM_PERSIST ? 0u : tile_m == GEMM_TILE_BIG ? persist_blocks() : GEMM_PERSIST_SMALL * persist_blocks();
+    a.kt = kt && (long)grid.x <= kt_cap ? kt : nullptr;
     if (pb && H == 2048 && (!sh.gate || (sh.gate_fmt == ex.gate_fmt && sh.S == M))) {
+        a.kt = kt && (long)pb <= kt_cap ? kt : nullptr;
         if (tile_m == GEMM_TILE_BIG) {
             if (tiled) hipLaunchKernelGGL((k_gemm_gate_up_p<GEMM_TILE_BIG / 16, FQ4KT>), dim3(pb), block, 0, s, a);
             else hipLaunchKernelGGL((k_gemm_gate_up_p<GEMM_TILE_BIG / 16, FQ4K>), dim3(pb), block, 0, s, a);

@@ -171,6 +171,7 @@ struct GUArgs {
     const uint32_t *list, *pairs;
     _Float16 *act, *act_sh;
     int routed_blocks;
+    unsigned long long *kt; /* per-block launch stamps (KT_BEGIN / KT_END) or NULL */
 };
 
 /* One wave: RPW gate rows and RPW up rows for the n tokens of a slot.  Raw
@@ -273,7 +274,7 @@ DEV void gu_body1(const GUArgs &a, const uint8_t *gbase, const uint8_t *ubase, i
  * experts themselves from the router logits (block 0 publishes the routing
  * for the down kernel); shared-expert blocks start at once. */
 template <int EPL, bool ROUTE>
-__global__ __launch_bounds__(256) void k_gemv_gate_up(GUArgs a, RouteArgs ra) {
+DEV void k_gemv_gate_up_body(GUArgs a, RouteArgs ra) {
     __shared__ float red_all[4][GU_RPW * 2 * 16];
     __shared__ int tok[16];
     __shared__ RouteLds r;
@@ -315,6 +316,13 @@ __global__ __launch_bounds__(256) void k_gemv_gate_up(GUArgs a, RouteArgs ra) {
     }
 }
 
+template <int EPL, bool ROUTE>
+__global__ __launch_bounds__(256) void k_gemv_gate_up(GUArgs a, RouteArgs ra) {
+    KT_BEGIN(a.kt);
+    k_gemv_gate_up_body<EPL, ROUTE>(a, ra);
+    KT_END(a.kt);
+}
+
 /* One-token gate/up with the routing folded in (H = 2048, E <= 64 EPL).
  * Every wave selects the experts itself (no separate routing kernel, no
  * barrier), and the waves of the block for selection rank u issue their
@@ -324,7 +332,7 @@ __global__ __launch_bounds__(256) void k_gemv_gate_up(GUArgs a, RouteArgs ra) {
  * those loads.  Selection and softmax restate softmax_topk_route
  * (inference/src/shaders.metal:1141-1234) exactly as wave_topk does. */
 template <int EPL>
-__global__ __launch_bounds__(256) void k_gemv_gate_up1(GUArgs a, RouteArgs ra) {
+DEV void k_gemv_gate_up1_body(GUArgs a, RouteArgs ra) {
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int rows_blk = 4 * GU_RPW, b = blockIdx.x;
     const int E = a.E, K = a.K;
@@ -429,6 +437,13 @@ __global__ __launch_bounds__(256) void k_gemv_gate_up1(GUArgs a, RouteArgs ra) {
         const float pu = wave_sum_fast(q4_dot(w2[i], lane, xl, xh, Xl, Xh));
         if (lane == 0) out[r0 + i] = (_Float16)(silu_f(pg) * pu);
     }
+}
+
+template <int EPL>
+__global__ __launch_bounds__(256) void k_gemv_gate_up1(GUArgs a, RouteArgs ra) {
+    KT_BEGIN(a.kt);
+    k_gemv_gate_up1_body<EPL>(a, ra);
+    KT_END(a.kt);
 }
 
 /* Batched gate/up, 2 <= T <= 8, H = 2048, Q4_K.  One 16-lane DPP row per
@@ -543,7 +558,7 @@ DEV void gb_run(GbTile &t0, GbTile &t1, const uint8_t *wg, const uint8_t *wu, si
 }
 
 template <int EPL, bool ROUTE>
-__global__ __launch_bounds__(256) void k_gemv_gu_b(GUArgs a, RouteArgs ra) {
+DEV void k_gemv_gu_b_body(GUArgs a, RouteArgs ra) {
     extern __shared__ __attribute__((aligned(16))) uint8_t gb_dyn[];
     __shared__ RouteLds r;
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, tid = threadIdx.x;
@@ -649,6 +664,13 @@ __global__ __launch_bounds__(256) void k_gemv_gu_b(GUArgs a, RouteArgs ra) {
         out[(size_t)j * ld + base + rr] = obuf[i];
     }
     TSTAMP(7);
+}
+
+template <int EPL, bool ROUTE>
+__global__ __launch_bounds__(256) void k_gemv_gu_b(GUArgs a, RouteArgs ra) {
+    KT_BEGIN(a.kt);
+    k_gemv_gu_b_body<EPL, ROUTE>(a, ra);
+    KT_END(a.kt);
 }
 
 /* =================================================================== */
@@ -937,7 +959,7 @@ static int epl_of(int E) { return E <= 64 ? 1 : E <= 128 ? 2 : E <= 256 ? 4 : E 
 
 int launch_gemv_gate_up(const ExpertSide &ex, const SharedSide &sh, const RouteArgs &ra, int route_in_block,
                         const float *x, int T, int H, int M, int K, int E, _Float16 *act, _Float16 *act_sh,
-                        hipStream_t s) {
+                        hipStream_t s, unsigned long long *kt, int kt_cap) {
     const int rows_blk = 4 * GU_RPW;
     if (T < 1 || T > 16 || T * K > 256 || H % 256 || ex.gate_fmt != FQ4K || !epl_of(E)) return -2;
     if (M % rows_blk || (sh.gate && sh.S % rows_blk)) return -2;
@@ -950,11 +972,13 @@ int launch_gemv_gate_up(const ExpertSide &ex, const SharedSide &sh, const RouteA
     const int umax = T * K < E ? T * K : E;
     a.routed_blocks = umax * (M / rows_blk);
     const int blocks = a.routed_blocks + (sh.gate ? sh.S / rows_blk : 0);
+    a.kt = kt && blocks <= kt_cap ? kt : nullptr;
     const int gb_rows = GB_ROWS * GB_ITER;
     if (T >= 2 && T <= 8 && H == 2048 && M % gb_rows == 0 && (!sh.gate || (sh.gate_fmt == FQ4K && sh.S % gb_rows == 0))) {
         a.routed_blocks = umax * (M / gb_rows);
         const int gblocks = a.routed_blocks + (sh.gate ? sh.S / GB_ROWS : 0);
         const size_t lds = (size_t)T * GB_TOK_BYTES;
+        a.kt = kt && gblocks <= kt_cap ? kt : nullptr;
 #define GB_LAUNCH(EPLV)                                                                                       \
     do {                                                                                                      \
         if (route_in_block)                                                                                   \
