@@ -234,3 +234,32 @@ def test_graph_replay_matches_eager(base):
         base.gm.forward(0, bufs[1][0], bufs[1][1], bufs[1][2], x.shape[0])
         ctx.sync()
     check(lib.orome_hip_graph_destroy(ex))
+
+
+@pytest.mark.parametrize("T", [1, 512])
+def test_kernel_timing_stamps(T):
+    """orome_hip_kernel_timing: every gate/up block writes a start and an end
+    stamp (end >= start, spans of a few microseconds up to milliseconds), and
+    the stamped launches compute bit-identical outputs."""
+    banner("gate/up launch stamps T=%d" % T)
+    p = Pair(max_tokens=T)
+    x, h = p.inputs(T, seed=300 + T)
+    ref, _ = p.run(0, x, h)
+    nb = 16384
+    buf = DeviceBuffer(p.ctx, nb * 2 * 8)
+    buf.upload(np.zeros(nb * 2, np.uint64))
+    check(lib.orome_hip_kernel_timing(p.ctx.handle, buf.ptr, nb), "kernel_timing")
+    try:
+        out, _ = p.run(0, x, h)
+    finally:
+        check(lib.orome_hip_kernel_timing(p.ctx.handle, None, 0), "kernel_timing")
+    v = buf.download(np.uint64, (nb, 2)).astype(np.int64)
+    buf.free()
+    ok = v[:, 0] > 0
+    assert ok.sum() > 0
+    assert np.all(v[ok, 1] >= v[ok, 0])
+    span_us = (v[ok, 1].max() - v[ok, 0].min()) * 0.01
+    print("T=%d blocks=%d span=%.2f us" % (T, ok.sum(), span_us))
+    assert 0.5 < span_us < 5000
+    assert np.array_equal(out, ref)
+    p.gm.close()
