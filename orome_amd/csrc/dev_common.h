@@ -82,6 +82,8 @@ DEV float row_sum16(float v) {
     return v;
 }
 
+/* canonical per-lane layouts cover H <= 256 CANON_NI (f4 per lane per 256) */
+#define CANON_NI 16
 /* Canonical wave64 sum: the xor butterfly 1,2,4,8,16,32 as seen by lane 0,
  * i.e. rows r0..r3 of 16 lanes reduced as above, then (r0+r1)+(r2+r3).
  * Every lane returns the same value.  This order is part of the router/norm

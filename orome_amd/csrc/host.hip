@@ -388,7 +388,8 @@ static int launch_rc(int rc, const char *what) {
  * computes in a separate kernel first). */
 static int forward_impl(orome_hip_ctx *c, const ModelConfig *cfg, const ExpertLayerRef *elr,
                         const LayerTensorCache *lt, const float *x, const float *h_in, float *h_out, int T,
-                        int K, const float *norm_h, const float *norm_w) {
+                        int K, const float *norm_h, const float *norm_w,
+                        const float *next_norm_w = NULL, int fuse_next_norm = 0, int pre_normed = 0) {
     if (!c || !cfg || !elr || !lt || !(x || norm_h) || !h_out)
         return orome_fail(OROME_EINVAL, "orome_moe_forward: NULL argument");
     const int H = cfg->hidden_dim, E = cfg->num_experts, M = cfg->moe_intermediate;
@@ -453,7 +454,7 @@ static int forward_impl(orome_hip_ctx *c, const ModelConfig *cfg, const ExpertLa
         if (path == OROME_PATH_GEMV) { /* the router kernel normalises and writes xnorm */
             a.norm_h = norm_h;
             a.norm_w = norm_w;
-        } else {
+        } else if (!pre_normed) { /* else the previous layer's combine wrote xnorm */
             TLAUNCH(c, ST_NORM, launch_rmsnorm(norm_h, norm_w, T, H, cfg->rms_norm_eps, c->xnorm, s), "rmsnorm");
         }
         x = c->xnorm;
@@ -542,8 +543,14 @@ static int forward_impl(orome_hip_ctx *c, const ModelConfig *cfg, const ExpertLa
             HIP_OK(hipEventRecord(c->join, c->side), OROME_EHIP);
             HIP_OK(hipStreamWaitEvent(s, c->join, 0), OROME_EHIP);
         }
-        TLAUNCH(c, ST_COMBINE, launch_combine(c->y, c->ysh, c->pos, c->w, c->sgl, S ? 1 : 0, h_in, h_out, T, H, K, s),
-               "combine");
+        if (fuse_next_norm) /* also the next layer's RMSNorm of h_out into xnorm */
+            TLAUNCH(c, ST_COMBINE,
+                    launch_combine_norm(c->y, c->ysh, c->pos, c->w, c->sgl, S ? 1 : 0, h_in, h_out, T, H, K, next_norm_w,
+                                        cfg->rms_norm_eps, c->xnorm, s),
+                    "combine + next RMSNorm");
+        else
+            TLAUNCH(c, ST_COMBINE, launch_combine(c->y, c->ysh, c->pos, c->w, c->sgl, S ? 1 : 0, h_in, h_out, T, H, K, s),
+                    "combine");
     }
     c->last_T = T;
     c->last_K = K;
@@ -573,8 +580,23 @@ extern "C" int orome_moe_stack_forward(orome_hip_ctx *c, const ModelConfig *cfg,
                                        const ExpertLayerRef *elrs, const LayerTensorCache *lts,
                                        int n_layers, float *h, int T, int K) {
     if (!elrs || !lts || n_layers < 0) return orome_fail(OROME_EINVAL, "orome_moe_stack_forward: bad arguments");
+    if (!c || !cfg || !h) return orome_fail(OROME_EINVAL, "orome_moe_stack_forward: NULL argument");
+    if (T < 1 || T > c->tmax) return orome_fail(OROME_EINVAL, "orome_moe_stack_forward: T=%d", T);
+    if (set_dev(c)) return OROME_EHIP;
+    /* on the MFMA path each layer's combine also computes the next layer's
+     * RMSNorm (same bits as the separate norm kernel), which then is skipped */
+    const int path = c->path == OROME_PATH_AUTO ? (T <= 8 ? OROME_PATH_GEMV : OROME_PATH_MFMA) : c->path;
+    const bool fuse = path == OROME_PATH_MFMA && cfg->hidden_dim % 512 == 0 && cfg->hidden_dim <= 4096;
+    auto norm_w = [&](int l) -> const float * {
+        return lts[l].post_norm.buffer && lts[l].post_norm.format == QFMT_F32
+                   ? (const float *)dev_addr(lts[l].post_norm.buffer, lts[l].post_norm.offset)
+                   : NULL;
+    };
     for (int l = 0; l < n_layers; l++) {
-        int rc = orome_moe_layer_forward(c, cfg, &elrs[l], &lts[l], h, T, K);
+        if (!lts[l].routing_gate.buffer) return orome_fail(OROME_EINVAL, "orome_moe_stack_forward: layer %d", l);
+        const bool next = fuse && l + 1 < n_layers;
+        int rc = forward_impl(c, cfg, &elrs[l], &lts[l], NULL, h, h, T, K, h, norm_w(l), next ? norm_w(l + 1) : NULL,
+                              next ? 1 : 0, fuse && l > 0 ? 1 : 0);
         if (rc) return rc;
     }
     return OROME_OK;

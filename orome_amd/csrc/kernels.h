@@ -97,6 +97,11 @@ size_t packed_q4k_bytes(int R, int K, int E);
 int launch_pack_q4k(const uint8_t *src, uint8_t *dst, int R, int K, int E, size_t src_stride, hipStream_t s);
 size_t packed_q6k_bytes(int R, int K, int E);
 int launch_pack_q6k(const uint8_t *src, uint8_t *dst, int R, int K, int E, size_t src_stride, hipStream_t s);
+/* prefill combine of one token per wave that also writes the next layer's
+ * RMSNorm of h_out into xnorm (nw: its weight, or NULL for ones) */
+int launch_combine_norm(const float *y, const float *ysh, const uint32_t *pos, const float *w, const float *sgl,
+                        int has_shared, const float *h_in, float *h_out, int T, int H, int K, const float *nw,
+                        float eps, float *xnorm, hipStream_t s);
 int launch_combine(const float *y, const float *ysh, const uint32_t *pos, const float *w,
                    const float *sgl, int has_shared, const float *h_in, float *h_out, int T,
                    int H, int K, hipStream_t s);

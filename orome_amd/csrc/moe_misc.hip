@@ -94,6 +94,26 @@ int launch_to_f16(const float *x, int T, int H, _Float16 *x16, hipStream_t s) {
 /* Prefill combine (moe_combine_copy_sq_k8, shaders.metal:1079-1135):
  *   h_out = (h_in + sum_k w_k y[pos(t,k)]) + sigmoid(s_t) * y_shared[t]
  * y holds expert outputs in expert-sorted pair order. 4 columns per thread. */
+/* one 4-column group of a token's combine (the order k_combine and
+ * k_combine_norm share) */
+DEV f4 combine4(const float *y, const float *ysh, const uint32_t (&pk)[OROME_MAXK], const f4 (&v)[OROME_MAXK],
+                const float *w, float g, int has_sh, const float *h_in, int t, int H, int K, int c) {
+    f4 moe = {0, 0, 0, 0};
+#pragma unroll
+    for (int k = 0; k < OROME_MAXK; k++)
+        if (k < K) {
+            const float wk = w[t * K + k];
+            moe.x += wk * v[k].x; moe.y += wk * v[k].y; moe.z += wk * v[k].z; moe.w += wk * v[k].w;
+        }
+    f4 base = h_in ? *(const f4 *)(h_in + (size_t)t * H + c) : f4{0, 0, 0, 0};
+    f4 o = {base.x + moe.x, base.y + moe.y, base.z + moe.z, base.w + moe.w};
+    if (has_sh) {
+        f4 sv = *(const f4 *)(ysh + (size_t)t * H + c);
+        o.x = o.x + g * sv.x; o.y = o.y + g * sv.y; o.z = o.z + g * sv.z; o.w = o.w + g * sv.w;
+    }
+    return o;
+}
+
 __global__ void k_combine(const float *y, const float *ysh, const uint32_t *pos, const float *w,
                           const float *sgl, int has_sh, const float *h_in, float *h_out, int T,
                           int H, int K) {
@@ -109,21 +129,104 @@ __global__ void k_combine(const float *y, const float *ysh, const uint32_t *pos,
 #pragma unroll
     for (int k = 0; k < OROME_MAXK; k++)
         if (k < K) v[k] = *(const f4 *)(y + (size_t)pk[k] * H + c);
-    f4 moe = {0, 0, 0, 0};
+    const float g = has_sh ? sigmoid_f(sgl[t]) : 0.0f;
+    *(f4 *)(h_out + (size_t)t * H + c) = combine4(y, ysh, pk, v, w, g, has_sh, h_in, t, H, K, c);
+}
+
+/* Prefill combine with the next layer's RMSNorm (k_rmsnorm's arithmetic)
+ * fused in: one block of NI / 2 waves per token; wave w combines columns
+ * 256 i + 4 L .. +3 (lane L) for i = w, w + NI / 2 with all of its loads
+ * issued together, stores h_out and keeps the values in LDS; wave 0 then
+ * forms the sum of squares in the canonical order (per lane over i, then
+ * the canonical wave sum), so xnorm is bit-identical to k_rmsnorm run on
+ * h_out, and every wave writes its columns of xnorm. */
+template <int CN_W>
+__global__ __launch_bounds__(64 * CN_W) void k_combine_norm(const float *y, const float *ysh, const uint32_t *pos,
+                                                             const float *w, const float *sgl, int has_sh,
+                                                             const float *h_in, float *h_out, int T, int H, int K,
+                                                             const float *nw, float eps, float *xnorm) {
+    __shared__ f4 ro[CANON_NI][64];
+    __shared__ float sc;
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, t = blockIdx.x;
+    const int NI = H / 256;
+    uint32_t pk[OROME_MAXK];
 #pragma unroll
     for (int k = 0; k < OROME_MAXK; k++)
-        if (k < K) {
-            const float wk = w[t * K + k];
-            moe.x += wk * v[k].x; moe.y += wk * v[k].y; moe.z += wk * v[k].z; moe.w += wk * v[k].w;
+        if (k < K) pk[k] = pos[t * K + k];
+    const float g = has_sh ? sigmoid_f(sgl[t]) : 0.0f;
+    constexpr int PW = 2; /* steps per wave: NI = 2 CN_W */
+    f4 v[PW][OROME_MAXK];
+#pragma unroll
+    for (int q = 0; q < PW; q++) {
+        const int i = wv + CN_W * q, c = 256 * i + 4 * lane;
+        if (i < NI) {
+#pragma unroll
+            for (int k = 0; k < OROME_MAXK; k++)
+                if (k < K) v[q][k] = *(const f4 *)(y + (size_t)pk[k] * H + c);
         }
-    f4 base = h_in ? *(const f4 *)(h_in + (size_t)t * H + c) : f4{0, 0, 0, 0};
-    f4 o = {base.x + moe.x, base.y + moe.y, base.z + moe.z, base.w + moe.w};
-    if (has_sh) {
-        const float g = sigmoid_f(sgl[t]);
-        f4 sv = *(const f4 *)(ysh + (size_t)t * H + c);
-        o.x = o.x + g * sv.x; o.y = o.y + g * sv.y; o.z = o.z + g * sv.z; o.w = o.w + g * sv.w;
     }
-    *(f4 *)(h_out + (size_t)t * H + c) = o;
+#pragma unroll
+    for (int q = 0; q < PW; q++) {
+        const int i = wv + CN_W * q, c = 256 * i + 4 * lane;
+        if (i < NI) {
+            const f4 o = combine4(y, ysh, pk, v[q], w, g, has_sh, h_in, t, H, K, c);
+            *(f4 *)(h_out + (size_t)t * H + c) = o;
+            ro[i][lane] = o;
+        }
+    }
+    __syncthreads();
+    if (wv == 0) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int i = 0; i < CANON_NI; i++)
+            if (i < NI) {
+                const f4 o = ro[i][lane];
+                acc = __builtin_fmaf(o.x, o.x, acc);
+                acc = __builtin_fmaf(o.y, o.y, acc);
+                acc = __builtin_fmaf(o.z, o.z, acc);
+                acc = __builtin_fmaf(o.w, o.w, acc);
+            }
+        const float ss = wave_sum_canon(acc);
+        if (lane == 0) sc = 1.0f / sqrtf(ss / (float)H + eps);
+    }
+    __syncthreads();
+    const float scale = sc;
+#pragma unroll
+    for (int q = 0; q < PW; q++) {
+        const int i = wv + CN_W * q, j = 256 * i + 4 * lane;
+        if (i < NI) {
+            const f4 o = ro[i][lane];
+            const f4 wq = nw ? *(const f4 *)(nw + j) : f4{1, 1, 1, 1};
+            f4 r;
+            r.x = (o.x * scale) * __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, wq.x) & 0xFFFF0000u);
+            r.y = (o.y * scale) * __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, wq.y) & 0xFFFF0000u);
+            r.z = (o.z * scale) * __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, wq.z) & 0xFFFF0000u);
+            r.w = (o.w * scale) * __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, wq.w) & 0xFFFF0000u);
+            *(f4 *)(xnorm + (size_t)t * H + j) = r;
+        }
+    }
+}
+
+int launch_combine_norm(const float *y, const float *ysh, const uint32_t *pos, const float *w, const float *sgl,
+                        int has_shared, const float *h_in, float *h_out, int T, int H, int K, const float *nw,
+                        float eps, float *xnorm, hipStream_t s) {
+    const int NI = H / 256;
+    if (H % 512 || NI > 2 * 8 || NI > CANON_NI) return -2;
+#define CN_LAUNCH(CW)                                                                                           \
+    hipLaunchKernelGGL(k_combine_norm<CW>, dim3((unsigned)T), dim3(64 * CW), 0, s, y, ysh, pos, w, sgl, has_shared, \
+                       h_in, h_out, T, H, K, nw, eps, xnorm)
+    switch (NI / 2) {
+        case 1: CN_LAUNCH(1); break;
+        case 2: CN_LAUNCH(2); break;
+        case 3: CN_LAUNCH(3); break;
+        case 4: CN_LAUNCH(4); break;
+        case 5: CN_LAUNCH(5); break;
+        case 6: CN_LAUNCH(6); break;
+        case 7: CN_LAUNCH(7); break;
+        default: CN_LAUNCH(8); break;
+    }
+#undef CN_LAUNCH
+    return hipGetLastError() == hipSuccess ? 0 : -3;
 }
 
 int launch_combine(const float *y, const float *ysh, const uint32_t *pos, const float *w,

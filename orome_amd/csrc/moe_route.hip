@@ -19,9 +19,8 @@
 
 #include "route_dev.h"
 
-/* canonical dot of one wave over H (H % 256 == 0, H <= 4096), for up to
- * TMAX tokens; all loads of a row are issued before the multiply-adds */
-#define CANON_NI 16
+/* canonical dot of one wave over H (H % 256 == 0, H <= 256 CANON_NI), for
+ * up to TMAX tokens; all loads of a row are issued before the multiply-adds */
 template <int TMAX>
 DEV void canon_dots(const float *wrow, const float *x, int T, int H, int lane, float *acc) {
     const int NI = H / 256;

@@ -202,6 +202,34 @@ def test_layer_forward_and_stack():
     p.gm.close()
 
 
+def test_stack_prefill_fused_norm():
+    """On the MFMA path the stack fuses each layer's combine with the next
+    layer's RMSNorm: three layers at T=100 equal three separate layer calls
+    bit for bit, and the last layer's logits (computed from the fused norm)
+    equal the oracle's on the same input."""
+    banner("stack forward with fused next-layer RMSNorm, 3 layers, T=100")
+    p = Pair(max_tokens=100, layers=3, q6k_every=2, seed=19, centered=True)
+    T = 100
+    h0 = (orome_amd.synth_normal(19, 3, T * p.H) * 4).reshape(T, p.H)
+    dh = DeviceBuffer.from_array(p.ctx, h0)
+    for l in range(3):
+        p.gm.layer_forward(l, dh, T)
+        if l == 1:
+            p.ctx.sync()
+            h_in_last = dh.download(np.float32, (T, p.H))
+    p.ctx.sync()
+    want = dh.download(np.float32, (T, p.H))
+    dh2 = DeviceBuffer.from_array(p.ctx, h0)
+    p.gm.stack_forward(dh2, T)
+    p.ctx.sync()
+    assert np.array_equal(dh2.download(np.float32, (T, p.H)), want)
+    dbg = p.gm.debug_outputs(T)
+    xn = p.om.rmsnorm(2, h_in_last)
+    _, rdbg = p.om.forward(2, xn, h_in_last, debug=True)
+    assert np.array_equal(dbg["logits"].view(np.uint32), rdbg["logits"].view(np.uint32))
+    p.gm.close()
+
+
 def test_graph_replay_matches_eager(base):
     """Capture three forwards in a HIP graph, replay it several times with eager
     work and synchronisations in between, and check every replay."""
