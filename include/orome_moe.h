@@ -185,7 +185,15 @@ int orome_hip_set_path(orome_hip_ctx *ctx, int path);
  * bit-identical with and without.  Layers are keyed by the routed gate and
  * shared gate addresses; registering again replaces the copy; layers whose
  * shared gate/up is not Q4_K are left as they are (OROME_OK), and a down
- * projection stays row-major when either side is Q8_0.
+ * projection stays row-major when either side is Q8_0.  With an F32 router the
+ * copy also holds the router as fp16 rows (one power-of-two scale each) and
+ * row-norm bounds: above 8 tokens a registered layer is routed in two passes
+ * (approximate logits on the matrix cores, then the canonical fp32 logits of
+ * the experts that can win), which selects exactly the experts, order and
+ * weights of the one-pass router; the debug logits output then holds the
+ * canonical values for those candidates and the approximation (within its
+ * proven bound) elsewhere.  OROME_ROUTE_EXACT=1 in the environment keeps the
+ * one-pass router.
  * orome_hip_unpack_all frees every copy (orome_hip_destroy calls it). */
 int orome_hip_pack_layer(orome_hip_ctx *ctx, const ModelConfig *cfg, const ExpertLayerRef *layer,
                          const LayerTensorCache *lt);

@@ -74,6 +74,10 @@ struct Pack {
     const uint8_t *gate, *up, *down, *sgate, *sup, *sdown;
     size_t gate_stride, down_stride;
     int down_fmt, sdown_fmt; /* GEMM_FMT_Q4K_TILED or GEMM_FMT_Q6K_TILED */
+    /* router copy for the two-pass large-batch router (r16 NULL: none) */
+    const float *rkey;
+    _Float16 *r16;
+    float *rscale, *rnorm;
 };
 
 static int set_dev(orome_hip_ctx *c) {
@@ -255,6 +259,13 @@ static int kfmt(QuantFormat f) {
 
 /* ------------------------------------------------- tile-major repacking */
 
+/* OROME_ROUTE_EXACT=1 keeps the one-pass canonical router on registered
+ * layers too (the two routers select identically; this is for comparing them). */
+static bool route_exact_only() {
+    const char *v = getenv("OROME_ROUTE_EXACT");
+    return v && v[0] == '1';
+}
+
 static const Pack *find_pack(const orome_hip_ctx *c, const uint8_t *gate, const uint8_t *sh_gate) {
     for (int k = 0; k < c->npacks; k++)
         if (c->packs[k].key == gate && c->packs[k].sh_key == sh_gate) return &c->packs[k];
@@ -295,9 +306,20 @@ extern "C" int orome_hip_pack_layer(orome_hip_ctx *c, const ModelConfig *cfg, co
     Pack pk = {};
     pk.key = gate;
     pk.sh_key = sh_gate;
-    HIP_OK(hipMalloc(&pk.mem, 2 * gu + dnb + 2 * sgu + sdn), OROME_ENOMEM);
+    /* router copy (fp32 router only): fp16 rows, scales, norms */
+    const bool rt = lt->routing_gate.buffer && lt->routing_gate.format == QFMT_F32 && H % 128 == 0;
+    const size_t rb16 = rt ? ((size_t)E * H * 2 + 255) / 256 * 256 : 0, rbf = rt ? ((size_t)E * 4 + 255) / 256 * 256 : 0;
+    const size_t body = (2 * gu + dnb + 2 * sgu + sdn + 255) / 256 * 256;
+    HIP_OK(hipMalloc(&pk.mem, body + rb16 + 2 * rbf), OROME_ENOMEM);
     uint8_t *m = (uint8_t *)pk.mem;
     int rc = 0;
+    if (rt) {
+        pk.rkey = (const float *)dev_addr(lt->routing_gate.buffer, lt->routing_gate.offset);
+        pk.r16 = (_Float16 *)(m + body);
+        pk.rscale = (float *)(m + body + rb16);
+        pk.rnorm = (float *)(m + body + rb16 + rbf);
+        rc |= launch_pack_router(pk.rkey, E, H, pk.r16, pk.rscale, pk.rnorm, c->stream);
+    }
     pk.gate = m;
     rc |= launch_pack_q4k(gate, m, M, H, E, elr->gate.expert_stride, c->stream);
     m += gu;
@@ -446,6 +468,7 @@ static int forward_impl(orome_hip_ctx *c, const ModelConfig *cfg, const ExpertLa
     a.counter = c->counter;
     a.norm_h = NULL; a.norm_w = NULL; a.norm_eps = cfg->rms_norm_eps; a.xnorm = c->xnorm;
     a.x16 = NULL;
+    a.W16 = NULL; a.wscale = NULL; a.wnorm = NULL; a.eps_c1 = a.eps_c2 = 0.0f;
 
     int path = c->path;
     if (path == OROME_PATH_AUTO) path = T <= 8 ? OROME_PATH_GEMV : OROME_PATH_MFMA;
@@ -483,9 +506,22 @@ static int forward_impl(orome_hip_ctx *c, const ModelConfig *cfg, const ExpertLa
         }
     } else {
         a.x16 = c->x16; /* the router writes the fp16 copy of x the GEMMs read */
-        TLAUNCH(c, ST_ROUTE, launch_route_logits(a, s), "router logits + fp16 staging");
-        a.x16 = NULL;
-        TLAUNCH(c, ST_TOPK, launch_topk(a, s), "top-k");
+        const Pack *rpk = find_pack(c, ex.gate, sh.gate);
+        if (rpk && rpk->r16 && rpk->rkey == a.W && H <= 4096 && K <= 64 && !route_exact_only()) {
+            /* registered layer: approximate logits on the matrix cores, then
+             * the canonical logits of the experts that can win */
+            a.W16 = rpk->r16;
+            a.wscale = rpk->rscale;
+            a.wnorm = rpk->rnorm;
+            route_eps_coeffs(H, &a.eps_c1, &a.eps_c2);
+            TLAUNCH(c, ST_ROUTE, launch_route_approx(a, s), "router logits (matrix cores) + fp16 staging");
+            a.x16 = NULL;
+            TLAUNCH(c, ST_TOPK, launch_topk_exact(a, s), "top-k with canonical recomputation");
+        } else {
+            TLAUNCH(c, ST_ROUTE, launch_route_logits(a, s), "router logits + fp16 staging");
+            a.x16 = NULL;
+            TLAUNCH(c, ST_TOPK, launch_topk(a, s), "top-k");
+        }
         TLAUNCH(c, ST_DISPATCH, launch_dispatch(a, c->tiles, c->tiles_b, S ? 1 : 0, c->dcount, s), "dispatch");
         /* one launch per tile list (grid sized for the most tiles it can hold) */
         const bool sh_small = (long)T * K <= (long)GEMM_TILE_SMALL * E;

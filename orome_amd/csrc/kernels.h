@@ -36,6 +36,12 @@ struct RouteArgs {
     const float *norm_h, *norm_w;
     float norm_eps;
     float *xnorm;
+    /* two-pass large-batch router (launch_route_approx + launch_topk_exact):
+     * W16[e] = fp16(W[e] * 2^s_e), wscale[e] = 2^-s_e, wnorm[e] >= ||W[e]||_2
+     * (from launch_pack_router); eps_c1/eps_c2 from route_eps_coeffs */
+    const _Float16 *W16;
+    const float *wscale, *wnorm;
+    float eps_c1, eps_c2;
 };
 
 struct ExpertSide {
@@ -53,6 +59,10 @@ struct SharedSide {
 int launch_route_small(const RouteArgs &a, hipStream_t s);
 int launch_route_logits(const RouteArgs &a, hipStream_t s);
 int launch_topk(const RouteArgs &a, hipStream_t s);
+int launch_route_approx(const RouteArgs &a, hipStream_t s);
+int launch_topk_exact(const RouteArgs &a, hipStream_t s);
+int launch_pack_router(const float *W, int E, int H, _Float16 *W16, float *wscale, float *wnorm, hipStream_t s);
+void route_eps_coeffs(int H, float *c1, float *c2);
 int dispatch_blocks(int T); /* rows of the dispatch count scratch ([rows][E] words) */
 int launch_dispatch(const RouteArgs &a, uint32_t *tiles_s, uint32_t *tiles_b, int has_shared, uint32_t *cnt,
                     hipStream_t s);

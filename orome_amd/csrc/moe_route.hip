@@ -10,14 +10,19 @@
  *   the selected experts identical.
  * Selection restates softmax_topk_route (shaders.metal:1141-1234): K rounds
  * of argmax, ties to the lower expert index, softmax over the K winners.
- * It runs as a wave64 max over 64-bit keys (order-preserving float bits,
- * then the complemented index), so one reduction settles value and tie.
+ * A round is a wave64 max over order-preserving 32-bit images of the values;
+ * the lowest lane holding the maximum settles ties.
  * Dispatch is a stable counting sort of pairs p = t*K + k by expert.
  */
 #include "dev_common.h"
 #include "kernels.h"
 
 #include "route_dev.h"
+#ifdef OROME_TRACE
+extern "C" __attribute__((visibility("default"))) int orome_trace_fetch_route(unsigned long long *h) {
+    return (int)hipMemcpyFromSymbol(h, HIP_SYMBOL(g_trace), sizeof(g_trace));
+}
+#endif
 
 /* canonical dot of one wave over H (H % 256 == 0, H <= 256 CANON_NI), for
  * up to TMAX tokens; all loads of a row are issued before the multiply-adds */
@@ -211,6 +216,358 @@ __global__ __launch_bounds__(256) void k_topk(RouteArgs a) {
     if (t >= a.T) return;
     wave_topk<EPL>(a.logits + (size_t)t * (a.E + 1), a.bias, a.E, a.K, lane, a.idx + t * a.K,
                    a.w + t * a.K, a.sgl + t, nullptr);
+}
+
+/* ------------------------------------------------ two-pass large-batch router
+ * The selection needs the canonical logits only where they decide it.  Pass 1
+ * computes every logit approximately on the matrix cores; pass 2 brackets
+ * each canonical logit C(t,e) by the approximation A(t,e) +- eps(t,e),
+ * recomputes in the canonical order exactly the experts whose upper bound
+ * reaches the K-th largest lower bound (the only ones that can be among the K
+ * winners), and selects among those with the unchanged rounds.  The winners,
+ * their order, the weights and the shared-gate logit are therefore those of
+ * the canonical router bit for bit; a non-candidate's logit stays the
+ * approximation, within eps of the canonical value.
+ *
+ * The bound.  A = 2^-s_e * sum_i fp16(x_i) fp16(2^s_e w_i) with the products
+ * exact in fp32 and the sum accumulated in fp32 (any order).  Per element,
+ * |fp16(v) - v| <= 2^-11 |v| + 2^-14 (the second term also covers inputs the
+ * hardware would treat as zero); 2^s_e puts the row's largest |w| in
+ * [2^14, 2^15), so w's absolute term is below 2^-28 max|w_e|.  Summing, with
+ * sum |w_i x_i| <= |w||x| and sum |w_i| <= sqrt(H) |w|, and the accumulation
+ * error of both sums (gamma_H with u = 2^-23 for the matrix cores, u = 2^-24
+ * for the canonical fma chain) gives
+ *   |A - C| <= |w| (c1' |x| + 2^-14 sqrt(H)),
+ *   c1' = 2^-10 + 2^-21 + 2^-28 sqrt(H) + 2 gamma_H(2^-23).
+ * route_eps_coeffs returns 9/8 of these coefficients.  wnorm[e] >= |w_e| is
+ * rounded up at pack time and |x| is rounded up in pass 2; a non-finite
+ * approximation or bound makes the expert a candidate. */
+
+/* W16/wscale/wnorm for one router matrix: a block per row. */
+__global__ __launch_bounds__(256) void k_pack_router(const float *W, int H, _Float16 *W16, float *wscale,
+                                                      float *wnorm) {
+    const int e = blockIdx.x;
+    const float *row = W + (size_t)e * H;
+    __shared__ float smax[4];
+    __shared__ double ssq[4];
+    float m = 0.0f;
+    double q = 0.0;
+    bool bad = false;
+    for (int i = threadIdx.x; i < H; i += 256) {
+        const float v = row[i];
+        bad |= !__builtin_isfinite(v);
+        m = fmaxf(m, fabsf(v));
+        q += (double)v * (double)v;
+    }
+    for (int o = 32; o; o >>= 1) {
+        m = fmaxf(m, __shfl_xor(m, o, 64));
+        q += __shfl_xor(q, o, 64);
+    }
+    const int anybad = __syncthreads_or(bad);
+    if ((threadIdx.x & 63) == 0) { smax[threadIdx.x >> 6] = m; ssq[threadIdx.x >> 6] = q; }
+    __syncthreads();
+    m = fmaxf(fmaxf(smax[0], smax[1]), fmaxf(smax[2], smax[3]));
+    q = (ssq[0] + ssq[1]) + (ssq[2] + ssq[3]);
+    int sh = 0; /* 2^sh * m in [2^14, 2^15) */
+    bool unbounded = anybad;
+    if (m > 0.0f && !anybad) {
+        int ex;
+        (void)frexpf(m, &ex); /* m = f * 2^ex, f in [0.5, 1) */
+        sh = 15 - ex;
+        if (sh > 126 || sh < -126) { /* outside the bound's assumptions: always a candidate */
+            sh = sh > 126 ? 126 : -126;
+            unbounded = true;
+        }
+    }
+    const float sc = ldexpf(1.0f, sh);
+    for (int i = threadIdx.x; i < H; i += 256) W16[(size_t)e * H + i] = (_Float16)(row[i] * sc);
+    if (threadIdx.x == 0) {
+        wscale[e] = ldexpf(1.0f, -sh);
+        /* sqrt in double, then one float step up: an upper bound of |w| */
+        const float n = (float)sqrt(q);
+        wnorm[e] = unbounded ? __builtin_inff() : nextafterf(n, __builtin_inff()) * (1.0f + 0x1p-20f);
+    }
+}
+
+#ifdef OROME_TRACE
+/* phase stamps kept in registers and written once at the end (a store in
+ * flight would delay the loads' waits that follow it) */
+#define RSTAMP(i) unsigned long long rst_##i = __builtin_amdgcn_s_memrealtime()
+#define RSTAMP_FLUSH(n)                                                                             \
+    do {                                                                                           \
+        if (lane == 0) {                                                                           \
+            unsigned long long *g = g_trace + ((n) + blockIdx.x) * 8;                              \
+            g[0] = rst_0; g[1] = rst_1; g[2] = rst_2; g[3] = rst_3; g[4] = rst_4; g[5] = rst_5;    \
+        }                                                                                          \
+    } while (0)
+#else
+#define RSTAMP(i) do {} while (0)
+#define RSTAMP_FLUSH(n) do {} while (0)
+#endif
+
+/* Pass 1: a block of NW waves computes 16*TTS tokens x 16*TES experts
+ * (v_mfma_f32_16x16x32_f16, tokens as A rows, experts as B columns).  Wave w
+ * covers k in [w H/NW, (w+1) H/NW) in chunks of S steps of 32; a chunk's
+ * loads are all issued before its first MFMA.  The NW partial tiles are
+ * summed through LDS in wave order.  The blocks of the first expert tile also
+ * stage x as fp16 for the grouped GEMMs (round to nearest even, each 4-group
+ * stored (0,2,1,3)). */
+template <int TTS, int TES, int NW, int S>
+__global__ __launch_bounds__(64 * NW) void k_route_approx(RouteArgs a) {
+    /* the wave index is uniform: say so, or the k loop is compiled divergent */
+    const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int E = a.E, H = a.H, T = a.T;
+    RSTAMP(0);
+    const int e0 = blockIdx.x * (16 * TES), t0 = blockIdx.y * (16 * TTS);
+    const int r = lane & 15, kq = (lane >> 4) * 8;
+    const float *xr[TTS];
+    bool stage[TTS];
+#pragma unroll
+    for (int ts = 0; ts < TTS; ts++) {
+        const int t = t0 + ts * 16 + r;
+        xr[ts] = a.x + (size_t)min(t, T - 1) * H + kq;
+        stage[ts] = a.x16 && blockIdx.x == 0 && t < T;
+    }
+    const _Float16 *wr[TES];
+#pragma unroll
+    for (int es = 0; es < TES; es++) wr[es] = a.W16 + (size_t)min(e0 + es * 16 + r, E - 1) * H + kq;
+    f4 acc[TTS][TES];
+#pragma unroll
+    for (int ts = 0; ts < TTS; ts++)
+#pragma unroll
+        for (int es = 0; es < TES; es++) acc[ts][es] = f4{0, 0, 0, 0};
+    const int kw = H / NW, kb = wv * kw, ke = kb + kw;
+    f4 xa[S][TTS][2];
+    h8 B[S][TES];
+    /* loads unconditional (k clamped into the range; a clamped step is not
+     * used): a load under a branch makes the compiler wait for it */
+    auto load = [&](int k0) {
+#pragma unroll
+        for (int st = 0; st < S; st++) {
+            const int k = min(k0 + 32 * st, ke - 32);
+#pragma unroll
+            for (int ts = 0; ts < TTS; ts++) {
+                xa[st][ts][0] = *(const f4 *)(xr[ts] + k);
+                xa[st][ts][1] = *(const f4 *)(xr[ts] + k + 4);
+            }
+#pragma unroll
+            for (int es = 0; es < TES; es++) B[st][es] = *(const h8 *)(wr[es] + k);
+        }
+    };
+    auto compute = [&](int k0) {
+        h8 A[S][TTS];
+#pragma unroll
+        for (int st = 0; st < S; st++) {
+            const int k = k0 + 32 * st;
+            if (k < ke) {
+#pragma unroll
+                for (int ts = 0; ts < TTS; ts++) {
+                    const f4 lo = xa[st][ts][0], hi = xa[st][ts][1];
+                    A[st][ts] = h8{(_Float16)lo.x, (_Float16)lo.y, (_Float16)lo.z, (_Float16)lo.w,
+                                   (_Float16)hi.x, (_Float16)hi.y, (_Float16)hi.z, (_Float16)hi.w};
+#pragma unroll
+                    for (int es = 0; es < TES; es++)
+                        acc[ts][es] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[st][ts], B[st][es], acc[ts][es], 0, 0, 0);
+                }
+            }
+        }
+        /* staging stores after the chunk's last load is consumed: stores
+         * share the load counter, so earlier ones would hold up the waits */
+#pragma unroll
+        for (int st = 0; st < S; st++) {
+            const int k = k0 + 32 * st;
+#pragma unroll
+            for (int ts = 0; ts < TTS; ts++)
+                if (stage[ts] && k < ke) {
+                    const h8 v = A[st][ts];
+                    _Float16 *d = a.x16 + (xr[ts] - a.x) + k;
+                    *(h4 *)d = h4{v[0], v[2], v[1], v[3]};
+                    *(h4 *)(d + 4) = h4{v[4], v[6], v[5], v[7]};
+                }
+        }
+    };
+    load(kb);
+    /* the output scales of this thread's slots o = threadIdx.x + 64 NW j,
+     * issued behind the first chunk's loads */
+    constexpr int NO = (TTS * TES * 4 * 64 + 64 * NW - 1) / (64 * NW);
+    float osc[NO];
+#pragma unroll
+    for (int j = 0; j < NO; j++) {
+        const int o = threadIdx.x + 64 * NW * j, slot = o >> 6;
+        osc[j] = a.wscale[min(e0 + ((slot >> 2) % TES) * 16 + (o & 15), E - 1)];
+    }
+    RSTAMP(1);
+    compute(kb);
+    for (int k0 = kb + 32 * S; k0 < ke; k0 += 32 * S) {
+        load(k0);
+        compute(k0);
+    }
+    RSTAMP(2);
+    __shared__ float red[NW][TTS * TES * 4][64];
+#pragma unroll
+    for (int ts = 0; ts < TTS; ts++)
+#pragma unroll
+        for (int es = 0; es < TES; es++)
+#pragma unroll
+            for (int v = 0; v < 4; v++) red[wv][(ts * TES + es) * 4 + v][lane] = acc[ts][es][v];
+    __syncthreads();
+    RSTAMP(3);
+#pragma unroll
+    for (int j = 0; j < NO; j++) {
+        const int o = threadIdx.x + 64 * NW * j;
+        if (o >= TTS * TES * 4 * 64) break;
+        const int slot = o >> 6, ln = o & 63;
+        float sum = red[0][slot][ln];
+#pragma unroll
+        for (int w = 1; w < NW; w++) sum += red[w][slot][ln];
+        const int ts = slot / (TES * 4), es = (slot >> 2) % TES, v = slot & 3;
+        const int t = t0 + ts * 16 + 4 * (ln >> 4) + v, e = e0 + es * 16 + (ln & 15);
+        if (t < T && e < E) a.logits[(size_t)t * (E + 1) + e] = sum * osc[j];
+    }
+    RSTAMP(4);
+    RSTAMP(5);
+    if (blockIdx.y == 0 && wv == 0) RSTAMP_FLUSH(60000);
+}
+
+/* Pass 2: WPT waves per token (the lane layout of wave_topk).  Every wave of
+ * a token computes the bounds, the K-th largest lower bound and the candidate
+ * list; the candidates (the shared-gate row first) are recomputed NB = 32/NI
+ * rows at a time, batch i by wave i % WPT, with all loads of a batch in
+ * flight together; the exact values meet in LDS and the token's first wave
+ * selects.  NI >= H / 256. */
+template <int EPL, int NI, int WPT>
+__global__ __launch_bounds__(256) void k_topk_exact(RouteArgs a) {
+    constexpr int NB = 32 / NI, TPB = 4 / WPT;
+    __shared__ float exv[TPB][64 * EPL + 1];
+    __shared__ int clist[4][64 * EPL + 1];
+    const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int tw = wv % WPT, tb = wv / WPT;
+    const int t = blockIdx.x * TPB + tb;
+    const bool live = t < a.T;
+    const int E = a.E, H = a.H, K = a.K, ni = H / 256;
+    RSTAMP(0);
+    float *lrow = a.logits + (size_t)min(t, a.T - 1) * (E + 1);
+    const float *xrow = a.x + (size_t)min(t, a.T - 1) * H;
+    /* every load unconditional (indices clamped, values masked where used):
+     * a load under a branch makes the compiler wait for it */
+    f4 xv[NI];
+#pragma unroll
+    for (int i = 0; i < NI; i++) xv[i] = *(const f4 *)(xrow + 256 * min(i, ni - 1) + 4 * lane);
+#pragma unroll
+    for (int i = 0; i < NI; i++)
+        if (i >= ni) xv[i] = f4{0, 0, 0, 0};
+    float v[EPL], bv[EPL], rn[EPL];
+    const float *bias = a.bias ? a.bias : a.wnorm;
+#pragma unroll
+    for (int j = 0; j < EPL; j++) {
+        const int e = min(lane * EPL + j, E - 1);
+        v[j] = lrow[e];
+        rn[j] = a.wnorm[e];
+        bv[j] = bias[e];
+    }
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NI; i++) {
+        ss = __builtin_fmaf(xv[i].x, xv[i].x, ss);
+        ss = __builtin_fmaf(xv[i].y, xv[i].y, ss);
+        ss = __builtin_fmaf(xv[i].z, xv[i].z, ss);
+        ss = __builtin_fmaf(xv[i].w, xv[i].w, ss);
+    }
+    /* |x| rounded up: the fp32 sum of squares is within H 2^-24 of itself */
+    const float xn = sqrtf(wave_sum_fast(ss)) * (1.0f + 0x1p-10f);
+    RSTAMP(1);
+    /* lower bounds (as keys) and upper bounds of the selection values */
+    uint32_t lo[EPL];
+    float hi[EPL];
+#pragma unroll
+    for (int j = 0; j < EPL; j++) {
+        const float eps = rn[j] * __builtin_fmaf(a.eps_c1, xn, a.eps_c2);
+        float l = v[j] - eps, h = v[j] + eps;
+        if (a.bias) { l += bv[j]; h += bv[j]; }
+        const bool known = __builtin_isfinite(v[j]) && __builtin_isfinite(eps);
+        if (!known || !(l == l)) l = -__builtin_inff();
+        if (!known || !(h == h)) h = __builtin_inff();
+        lo[j] = lane * EPL + j < E ? route_ord(l) : 0u;
+        hi[j] = h;
+    }
+    /* the K-th largest lower bound */
+#pragma unroll
+    for (int pass = 0; pass < EPL; pass++)
+#pragma unroll
+        for (int j = pass & 1; j + 1 < EPL; j += 2)
+            if (lo[j + 1] > lo[j]) { const uint32_t tk = lo[j]; lo[j] = lo[j + 1]; lo[j + 1] = tk; }
+    uint32_t m = 0u;
+#pragma unroll 1
+    for (int k = 0; k < K; k++) {
+        m = wave_max_u32(lo[0]);
+        const int wl = (int)__builtin_ctzll(__ballot(lo[0] == m));
+        if (lane == wl) {
+#pragma unroll
+            for (int j = 0; j + 1 < EPL; j++) lo[j] = lo[j + 1];
+            lo[EPL - 1] = 0u;
+        }
+    }
+    const float L = ord_value(m);
+    RSTAMP(2);
+    bool cand[EPL];
+    /* the candidate list (the shared-gate row E first), in this wave's own
+     * LDS slot: position = rows before it in (j, lane) order */
+    int nc = a.wsg ? 1 : 0;
+#pragma unroll
+    for (int j = 0; j < EPL; j++) {
+        cand[j] = lane * EPL + j < E && !(hi[j] < L);
+        const uint64_t mk = __ballot(cand[j]);
+        const int below = (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(mk >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mk, 0u));
+        if (cand[j]) clist[wv][nc + below] = lane * EPL + j;
+        nc += (int)__builtin_popcountll(mk);
+    }
+    if (a.wsg && lane == 0) clist[wv][0] = E;
+    __builtin_amdgcn_wave_barrier();
+    /* canonical recomputation, NB rows a batch, batch i by wave i % WPT */
+    for (int base = tw * NB; live && base < nc; base += WPT * NB) {
+        int ids[NB];
+#pragma unroll
+        for (int b = 0; b < NB; b++)
+            ids[b] = base + b < nc ? __builtin_amdgcn_readfirstlane(clist[wv][base + b]) : -1;
+        f4 w[NB][NI];
+#pragma unroll
+        for (int b = 0; b < NB; b++) {
+            const float *row = ids[b] == E ? a.wsg : a.W + (size_t)max(ids[b], 0) * H;
+#pragma unroll
+            for (int i = 0; i < NI; i++) w[b][i] = *(const f4 *)(row + 256 * min(i, ni - 1) + 4 * lane);
+        }
+#pragma unroll
+        for (int b = 0; b < NB; b++) {
+            if (ids[b] < 0) break;
+            float d = 0.0f;
+#pragma unroll
+            for (int i = 0; i < NI; i++)
+                if (i < ni) {
+                    d = __builtin_fmaf(w[b][i].x, xv[i].x, d);
+                    d = __builtin_fmaf(w[b][i].y, xv[i].y, d);
+                    d = __builtin_fmaf(w[b][i].z, xv[i].z, d);
+                    d = __builtin_fmaf(w[b][i].w, xv[i].w, d);
+                }
+            d = wave_sum_canon(d);
+            if (lane == 0) exv[tb][ids[b]] = d;
+        }
+    }
+    RSTAMP(3);
+    if (WPT > 1) __syncthreads();
+    if (!live || tw != 0) return;
+    RSTAMP(4);
+    const float sg = a.wsg ? exv[tb][E] : 0.0f;
+    uint32_t key[EPL];
+#pragma unroll
+    for (int j = 0; j < EPL; j++) {
+        if (cand[j]) v[j] = exv[tb][lane * EPL + j];
+        key[j] = cand[j] ? route_ord(a.bias ? v[j] + bv[j] : v[j]) : 0u;
+        if (lane * EPL + j < E) lrow[lane * EPL + j] = v[j];
+    }
+    if (lane == 0) lrow[E] = sg;
+    wave_topk_keys<EPL>(key, sg, K, lane, a.idx + t * K, a.w + t * K, a.sgl + t, nullptr);
+    RSTAMP(5);
+    RSTAMP_FLUSH(0);
 }
 
 /* Dispatch for any T, in three launches over blocks of DSP_TOK tokens.  A
@@ -506,6 +863,62 @@ int launch_route_logits(const RouteArgs &a, hipStream_t s) {
 int launch_topk(const RouteArgs &a, hipStream_t s) {
     dim3 grid((a.T + 3) / 4);
     EPL_SWITCH(a.E, k_topk, grid, dim3(256), 0, s, a);
+    return hipGetLastError() == hipSuccess ? 0 : -3;
+}
+
+void route_eps_coeffs(int H, float *c1, float *c2) {
+    const double u = 0x1p-23, g = H * u / (1.0 - H * u);
+    /* 9/8: room for the rounding of the bound arithmetic itself (eps, the
+     * bounds and the norms: a few ulps, against eps >= 2^-10 |w||x|) */
+    *c1 = (float)(1.125 * (0x1p-10 + 0x1p-21 + 0x1p-28 * sqrt((double)H) + 2.0 * g));
+    *c2 = (float)(1.125 * 0x1p-14 * sqrt((double)H));
+}
+
+int launch_pack_router(const float *W, int E, int H, _Float16 *W16, float *wscale, float *wnorm, hipStream_t s) {
+    if (E < 1 || H < 1) return -2;
+    hipLaunchKernelGGL(k_pack_router, dim3(E), dim3(256), 0, s, W, H, W16, wscale, wnorm);
+    return hipGetLastError() == hipSuccess ? 0 : -3;
+}
+
+/* Tile shapes (measured): up to 1024 tokens, 16 tokens x 32 experts and 8
+ * waves per block (blocks for every CU); beyond, 32 x 64 and 4 waves (the
+ * fewest bytes moved per logit). */
+int launch_route_approx(const RouteArgs &a, hipStream_t s) {
+    if (!a.W16 || !a.wscale || a.H % 256 || a.T < 1) return -2;
+    if (a.T <= 1024)
+        hipLaunchKernelGGL((k_route_approx<1, 2, 8, 8>), dim3((a.E + 31) / 32, (a.T + 15) / 16), dim3(512), 0, s, a);
+    else
+        hipLaunchKernelGGL((k_route_approx<2, 4, 4, 4>), dim3((a.E + 63) / 64, (a.T + 31) / 32), dim3(256), 0, s, a);
+    return hipGetLastError() == hipSuccess ? 0 : -3;
+}
+
+int launch_topk_exact(const RouteArgs &a, hipStream_t s) {
+    if (!a.wnorm || a.H % 256 || a.H > 4096 || a.K > 64 || a.K > a.E) return -2;
+    const int ni = a.H / 256;
+    /* up to 1024 tokens a token's candidates spread over 4 waves (more waves
+     * in flight); beyond, one wave per token already fills the chip */
+    const int wpt = a.T <= 1024 ? 4 : 1;
+    const dim3 grid((a.T * wpt + 3) / 4);
+#define TKX(NIV, WPTV)                                                                                   \
+    switch (epl_for(a.E)) {                                                                              \
+        case 1: hipLaunchKernelGGL((k_topk_exact<1, NIV, WPTV>), grid, dim3(256), 0, s, a); break;   \
+        case 2: hipLaunchKernelGGL((k_topk_exact<2, NIV, WPTV>), grid, dim3(256), 0, s, a); break;   \
+        case 4: hipLaunchKernelGGL((k_topk_exact<4, NIV, WPTV>), grid, dim3(256), 0, s, a); break;   \
+        case 8: hipLaunchKernelGGL((k_topk_exact<8, NIV, WPTV>), grid, dim3(256), 0, s, a); break;   \
+        case 16: hipLaunchKernelGGL((k_topk_exact<16, NIV, WPTV>), grid, dim3(256), 0, s, a); break; \
+        default: return -2;                                                                              \
+    }
+#define TKW(NIV)                      \
+    do {                              \
+        if (wpt == 4) { TKX(NIV, 4) } \
+        else { TKX(NIV, 1) }          \
+    } while (0)
+    if (ni <= 2) TKW(2);
+    else if (ni <= 4) TKW(4);
+    else if (ni <= 8) TKW(8);
+    else TKW(16);
+#undef TKW
+#undef TKX
     return hipGetLastError() == hipSuccess ? 0 : -3;
 }
 

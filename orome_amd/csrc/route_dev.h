@@ -3,9 +3,9 @@
  *
  * Selection restates softmax_topk_route (inference/src/shaders.metal:
  * 1141-1234): K rounds of argmax, ties to the lower expert index, softmax over
- * the K winners.  It runs as a wave64 max over 64-bit keys (order-preserving
- * float bits, then the complemented index), so one reduction settles value
- * and tie.  Dispatch is a stable counting sort of pairs p = t*K + k by expert.
+ * the K winners.  A round is a wave64 max over order-preserving 32-bit images
+ * of the values; the lowest lane holding the maximum (lane order is expert
+ * order) settles ties.
  */
 #pragma once
 #include "dev_common.h"
@@ -55,6 +55,9 @@ struct TopkLane {
     int id;
     float w;
 };
+template <int EPL>
+DEV TopkLane wave_topk_keys(uint32_t *key, float sg, int K, int lane, int32_t *idx_out, float *w_out,
+                            float *sgl_out, int *e_out);
 template <int EPL, bool COH = false>
 DEV TopkLane wave_topk(const float *l, const float *bias, int E, int K, int lane, int32_t *idx_out,
                        float *w_out, float *sgl_out, int *e_out) {
@@ -71,12 +74,18 @@ DEV TopkLane wave_topk(const float *l, const float *bias, int E, int K, int lane
 #pragma unroll
         for (int j = 0; j < EPL; j++) bv[j] = bias[min(lane * EPL + j, E - 1)];
     uint32_t key[EPL];
+#pragma unroll
+    for (int j = 0; j < EPL; j++) key[j] = lane * EPL + j < E ? route_ord(bias ? v[j] + bv[j] : v[j]) : 0u;
+    return wave_topk_keys<EPL>(key, sg, K, lane, idx_out, w_out, sgl_out, e_out);
+}
+
+/* The selection of wave_topk from the lanes' keys (key 0: not eligible). */
+template <int EPL>
+DEV TopkLane wave_topk_keys(uint32_t *key, float sg, int K, int lane, int32_t *idx_out, float *w_out,
+                            float *sgl_out, int *e_out) {
     int kj[EPL];
 #pragma unroll
-    for (int j = 0; j < EPL; j++) {
-        key[j] = lane * EPL + j < E ? route_ord(bias ? v[j] + bv[j] : v[j]) : 0u;
-        kj[j] = j;
-    }
+    for (int j = 0; j < EPL; j++) kj[j] = j;
     /* odd-even transposition sort, descending */
 #pragma unroll
     for (int pass = 0; pass < EPL; pass++)

@@ -27,11 +27,14 @@ def rel_l2(a, b):
 class Pair:
     """A synthetic model resident on the GPU plus its oracle view."""
 
-    def __init__(self, max_tokens=64, **kw):
+    def __init__(self, max_tokens=64, mutate=None, **kw):
+        """mutate(img, om): edits the host image (e.g. router rows) before upload."""
         args = dict(layers=1, H=2048, E=256, K=8, M=512, S=512, seed=0)
         args.update(kw)
         self.img = orome_amd.synth_gguf(orome_amd.make_spec(**args))
         self.om = O.OracleModel(self.img)
+        if mutate:
+            mutate(self.img, self.om)
         self.gm = orome_amd.MoEModel(image=self.img, max_tokens=max_tokens)
         self.ctx = self.gm.ctx
         self.H = self.gm.H
@@ -57,6 +60,21 @@ class Pair:
 def base():
     banner("build base model H=2048 E=256 K=8 M=512 S=512 (Q4_K)")
     return Pair()
+
+
+def assert_logits(dbg, rdbg):
+    """Router logits against the oracle.  The winners' logits and the shared-gate
+    logit are bit-exact on every path.  The two-pass large-batch router
+    recomputes canonically only the experts that can win, so any other logit
+    is an fp16 matrix-core approximation of the canonical value: it is checked
+    against a tolerance far below the kernel's own error bound."""
+    got, ref = dbg["logits"], rdbg["logits"]
+    rows = np.arange(ref.shape[0])[:, None]
+    win = rdbg["idx"]
+    assert np.array_equal(got[rows, win].view(np.uint32), ref[rows, win].view(np.uint32)), "winner logits"
+    assert np.array_equal(got[:, -1].view(np.uint32), ref[:, -1].view(np.uint32)), "shared-gate logit"
+    scale = 1.0 + np.abs(ref).max(axis=1, keepdims=True)
+    assert np.all(np.abs(got - ref) <= 5e-3 * scale), "approximate logits"
 
 
 def check_routing(p, x, dbg, K, bias=None):
@@ -226,7 +244,8 @@ def test_stack_prefill_fused_norm():
     dbg = p.gm.debug_outputs(T)
     xn = p.om.rmsnorm(2, h_in_last)
     _, rdbg = p.om.forward(2, xn, h_in_last, debug=True)
-    assert np.array_equal(dbg["logits"].view(np.uint32), rdbg["logits"].view(np.uint32))
+    assert np.array_equal(dbg["idx"], rdbg["idx"])
+    assert_logits(dbg, rdbg)
     p.gm.close()
 
 
