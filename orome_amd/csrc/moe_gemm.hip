@@ -423,6 +423,7 @@ struct GemmArgs {
     int T, H, M, S, K, E;
     int zrow, zrow_sh;        /* all-zero rows of src / src_sh (rows past a tile read them) */
     int nyb;                  /* row blocks per tile */
+    int uwin;                 /* tiles walked: all (0), the last uwin (> 0) or all but the last -uwin (< 0) */
     const uint32_t *tiles, *pairs;
     _Float16 *act, *act_sh;   /* gate/up outputs */
     unsigned long long *kt;   /* gate/up: per-block launch stamps (KT_BEGIN / KT_END) or NULL */
@@ -478,17 +479,26 @@ struct UnitDesc {
  * blocks of that XCD (work-groups are dealt to the 8 XCDs round-robin by
  * linear id), so the row blocks of one tile share an L2 and run at about the
  * same time; within an XCD, block `slot` takes units slot, slot + bpx, ... */
-DEV UnitDesc unit_desc(const uint32_t *tiles, int nyb, int E, int n) {
+DEV UnitDesc unit_desc(const uint32_t *tiles, int nyb, int E, int n, int uwin) {
     const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3, bpx = gridDim.x >> 3;
     const int q = slot + n * bpx, ti = 8 * (q / nyb) + xcd;
     /* the list is read-only here: constant address space, so the uniform
      * reads are scalar loads and do not wait behind the weight loads */
     typedef const __attribute__((address_space(4))) uint32_t cu32;
     cu32 *tl = (cu32 *)(uintptr_t)tiles;
+    /* the window of tiles walked (the shared expert's tiles end the list) */
+    const uint32_t nall = tl[0];
+    uint32_t base = 0, cnt = nall;
+    if (uwin > 0) {
+        cnt = nall < (uint32_t)uwin ? nall : (uint32_t)uwin;
+        base = nall - cnt;
+    } else if (uwin < 0) {
+        cnt = nall > (uint32_t)-uwin ? nall - (uint32_t)-uwin : 0u;
+    }
     UnitDesc u;
-    u.valid = (uint32_t)ti < tl[0];
+    u.valid = (uint32_t)ti < cnt;
     u.yb = q % nyb;
-    const int tc = u.valid ? ti : 0; /* entry 0 exists whenever the list is read */
+    const int tc = u.valid ? (int)base + ti : 0; /* entry 0 exists whenever the list is read */
     u.e = u.valid ? tl[1 + 3 * tc] : 0u;
     u.first = u.valid ? (int)tl[2 + 3 * tc] : 0;
     u.rows = u.valid ? (int)tl[3 + 3 * tc] : 0;
@@ -674,7 +684,7 @@ struct GuPol {
     const GemmArgs &a;
     MDEV int in_dim() const { return a.H; }
     MDEV int ld() const { return a.H; }
-    MDEV UnitDesc desc(int n) const { return unit_desc(a.tiles, a.nyb, a.E, n); }
+    MDEV UnitDesc desc(int n) const { return unit_desc(a.tiles, a.nyb, a.E, n, a.uwin); }
     MDEV const _Float16 *src(const UnitDesc &) const { return a.src; }
     MDEV const uint8_t *weights(const UnitDesc &u, int m) const {
         return u.sh ? (m ? a.sh_b : a.sh_a) : m ? a.wb + (size_t)u.e * a.stride_b : a.wa + (size_t)u.e * a.stride_a;
@@ -698,7 +708,7 @@ struct DnPol {
     const GemmArgs &a;
     MDEV int in_dim() const { return a.M; }
     MDEV int ld() const { return a.M; }
-    MDEV UnitDesc desc(int n) const { return unit_desc(a.tiles, a.nyb, a.E, n); }
+    MDEV UnitDesc desc(int n) const { return unit_desc(a.tiles, a.nyb, a.E, n, a.uwin); }
     MDEV const _Float16 *src(const UnitDesc &u) const { return u.sh ? a.src_sh : a.src; }
     MDEV const uint8_t *weights(const UnitDesc &u, int) const { return u.sh ? a.sh_a : a.wa + (size_t)u.e * a.stride_a; }
     MDEV uint32_t row_raw(const UnitDesc &u, int q) const { return !u.valid || q >= u.rows ? ~0u : (uint32_t)(u.first + q); }
@@ -897,16 +907,35 @@ int launch_gemm_down(const ExpertSide &ex, const SharedSide &sh, const _Float16 
     const dim3 grid((unsigned)((n_tiles_max + 7) / 8 * 8 * a.nyb)), block(W * 64);
     if (tile_m != GEMM_TILE_SMALL && tile_m != GEMM_TILE_BIG) return -2;
     const unsigned pb = !GEMM_PERSIST ? 0u : tile_m == GEMM_TILE_BIG ? persist_blocks() : GEMM_PERSIST_SMALL_DN * persist_blocks();
-    if (pb && M == 512 && (!sh.gate || (sf == ex.down_fmt && sh.S == M))) {
-#define DP_LAUNCH(TB)                                                                                                 \
+    /* the shared expert's tiles end the list that holds most of the routed
+     * work (as the dispatch builds it); nsh of them here */
+    const bool sh_small = (size_t)T * K <= (size_t)GEMM_TILE_SMALL * E;
+    const int nsh = sh.gate && (tile_m == GEMM_TILE_SMALL) == sh_small ? (T + tile_m - 1) / tile_m : 0;
+    const bool mixed = nsh && sf != ex.down_fmt;
+    const bool two_tiled = (ex.down_fmt == FQ4KT || ex.down_fmt == FQ6KT) && (sf == FQ4KT || sf == FQ6KT);
+    if (pb && M == 512 && (!nsh || sh.S == M) && (!mixed || two_tiled)) {
+#define DP_LAUNCH(F, TB, ARGS)                                                                                        \
     do {                                                                                                              \
-        if (ex.down_fmt == FQ4K) hipLaunchKernelGGL((k_gemm_down_p<FQ4K, TB>), dim3(pb), block, 0, s, a);               \
-        else if (ex.down_fmt == FQ4KT) hipLaunchKernelGGL((k_gemm_down_p<FQ4KT, TB>), dim3(pb), block, 0, s, a);        \
-        else if (ex.down_fmt == FQ6KT) hipLaunchKernelGGL((k_gemm_down_p<FQ6KT, TB>), dim3(pb), block, 0, s, a);        \
-        else hipLaunchKernelGGL((k_gemm_down_p<FQ6K, TB>), dim3(pb), block, 0, s, a);                                   \
+        if ((F) == FQ4K) hipLaunchKernelGGL((k_gemm_down_p<FQ4K, TB>), dim3(pb), block, 0, s, ARGS);                    \
+        else if ((F) == FQ4KT) hipLaunchKernelGGL((k_gemm_down_p<FQ4KT, TB>), dim3(pb), block, 0, s, ARGS);             \
+        else if ((F) == FQ6KT) hipLaunchKernelGGL((k_gemm_down_p<FQ6KT, TB>), dim3(pb), block, 0, s, ARGS);             \
+        else hipLaunchKernelGGL((k_gemm_down_p<FQ6K, TB>), dim3(pb), block, 0, s, ARGS);                                \
     } while (0)
-        if (tile_m == GEMM_TILE_BIG) DP_LAUNCH(GEMM_TILE_BIG / 16);
-        else DP_LAUNCH(GEMM_TILE_SMALL / 16);
+#define DP_TILE(F, ARGS)                                                        \
+    do {                                                                        \
+        if (tile_m == GEMM_TILE_BIG) DP_LAUNCH(F, GEMM_TILE_BIG / 16, ARGS);     \
+        else DP_LAUNCH(F, GEMM_TILE_SMALL / 16, ARGS);                           \
+    } while (0)
+        if (!mixed) {
+            DP_TILE(ex.down_fmt, a);
+        } else { /* routed and shared down differ in format: one walk each */
+            GemmArgs ar = a, as = a;
+            ar.uwin = -nsh;
+            as.uwin = nsh;
+            DP_TILE(ex.down_fmt, ar);
+            DP_TILE(sf, as);
+        }
+#undef DP_TILE
 #undef DP_LAUNCH
         return hipGetLastError() == hipSuccess ? 0 : -3;
     }

@@ -125,12 +125,14 @@ def test_persistent_gemm_bit_identical(base, monkeypatch):
         assert rel_l2(outs[None][sel] - h[sel], ref - h[sel]) < TOL
 
 
-def test_persistent_gemm_zipf_q6k(monkeypatch):
+@pytest.mark.parametrize("shared_down", [14, 12])
+def test_persistent_gemm_zipf_q6k(monkeypatch, shared_down):
     """Skewed routing (a few experts with many tiles, many with none) and a
     Q6_K down projection through a 16-block persistent grid, against the
-    oracle and bit-identical to the per-tile kernels."""
-    banner("persistent GEMM, Zipf T=512, Q6_K down")
-    p = Pair(max_tokens=512, down=14, shared_down=14, zipf=True, seed=35)
+    oracle and bit-identical to the per-tile kernels.  With a Q4_K shared
+    down the routed and shared tiles are walked by two launches."""
+    banner("persistent GEMM, Zipf T=512, Q6_K down, shared down type %d" % shared_down)
+    p = Pair(max_tokens=512, down=14, shared_down=shared_down, zipf=True, seed=35)
     monkeypatch.setenv("OROME_GEMM_PERSIST_BLOCKS", "16")
     out, _ = run_and_check(p, 512, seed=1512, path=_lib.OROME_PATH_MFMA)
     monkeypatch.setenv("OROME_GEMM_PERSIST_BLOCKS", "0")
@@ -236,3 +238,21 @@ def test_two_pass_router_matches_one_pass(base, monkeypatch, T):
     out1, dbg1 = base.run(0, x, h)
     _same_routing(dbg, dbg1)
     assert np.array_equal(out, out1)
+
+
+def test_persistent_down_mixed_formats_2048(monkeypatch):
+    """Q6_K routed down with a Q4_K shared down at T=2048 (the shared tiles
+    then end the big-tile list): the two persistent walks equal the per-tile
+    kernels bit for bit, and a token sample matches the oracle."""
+    banner("persistent down, Q6_K routed + Q4_K shared, T=2048")
+    p = Pair(max_tokens=2048, down=14, shared_down=12, seed=36)
+    x, h = p.inputs(2048, seed=2036)
+    out, _ = p.run(0, x, h, path=_lib.OROME_PATH_MFMA)
+    monkeypatch.setenv("OROME_GEMM_PERSIST_BLOCKS", "0")
+    ref1, _ = p.run(0, x, h, path=_lib.OROME_PATH_MFMA)
+    monkeypatch.delenv("OROME_GEMM_PERSIST_BLOCKS", raising=False)
+    assert np.array_equal(out, ref1)
+    sel = np.arange(0, 2048, 32)
+    ref = p.om.forward(0, x[sel], h[sel])
+    assert rel_l2(out[sel] - h[sel], ref - h[sel]) < TOL
+    p.gm.close()
