@@ -95,42 +95,59 @@ int launch_to_f16(const float *x, int T, int H, _Float16 *x16, hipStream_t s) {
  *   h_out = (h_in + sum_k w_k y[pos(t,k)]) + sigmoid(s_t) * y_shared[t]
  * y holds expert outputs in expert-sorted pair order. 4 columns per thread. */
 /* one 4-column group of a token's combine (the order k_combine and
- * k_combine_norm share) */
-DEV f4 combine4(const float *y, const float *ysh, const uint32_t (&pk)[OROME_MAXK], const f4 (&v)[OROME_MAXK],
-                const float *w, float g, int has_sh, const float *h_in, int t, int H, int K, int c) {
+ * k_combine_norm share); v/wk hold the K expert rows and weights, base the
+ * h_in columns (0 without h_in), sv the shared expert's columns */
+template <int KM>
+DEV f4 combine4(const f4 (&v)[KM], const float (&wk)[KM], int K, f4 base, f4 sv, float g, int has_sh) {
     f4 moe = {0, 0, 0, 0};
 #pragma unroll
-    for (int k = 0; k < OROME_MAXK; k++)
+    for (int k = 0; k < KM; k++)
         if (k < K) {
-            const float wk = w[t * K + k];
-            moe.x += wk * v[k].x; moe.y += wk * v[k].y; moe.z += wk * v[k].z; moe.w += wk * v[k].w;
+            moe.x += wk[k] * v[k].x; moe.y += wk[k] * v[k].y; moe.z += wk[k] * v[k].z; moe.w += wk[k] * v[k].w;
         }
-    f4 base = h_in ? *(const f4 *)(h_in + (size_t)t * H + c) : f4{0, 0, 0, 0};
     f4 o = {base.x + moe.x, base.y + moe.y, base.z + moe.z, base.w + moe.w};
     if (has_sh) {
-        f4 sv = *(const f4 *)(ysh + (size_t)t * H + c);
         o.x = o.x + g * sv.x; o.y = o.y + g * sv.y; o.z = o.z + g * sv.z; o.w = o.w + g * sv.w;
     }
     return o;
 }
 
+/* A token's pair positions and weights (uniform loads, index clamped to
+ * K - 1 past K: every load is unconditional, so none is waited for alone). */
+template <int KM>
+DEV void combine_pairs(const uint32_t *pos, const float *w, int t, int K, uint32_t (&pk)[KM], float (&wk)[KM]) {
+#pragma unroll
+    for (int k = 0; k < KM; k++) {
+        const int kc = min(k, K - 1);
+        pk[k] = pos[t * K + kc];
+        wk[k] = w[t * K + kc];
+    }
+    /* hold the weights here, beside the positions the row addresses wait for
+     * anyway (left alone, the scheduler reloads them after the rows arrive) */
+#pragma unroll
+    for (int k = 0; k < KM; k++) asm volatile("" : : "s"(wk[k]));
+}
+
+template <int KM>
 __global__ void k_combine(const float *y, const float *ysh, const uint32_t *pos, const float *w,
                           const float *sgl, int has_sh, const float *h_in, float *h_out, int T,
                           int H, int K) {
     const int t = blockIdx.y;
-    const int c = (blockIdx.x * blockDim.x + threadIdx.x) * 4;
-    if (c >= H) return;
-    /* all pair positions first, then all expert rows in flight together */
-    uint32_t pk[OROME_MAXK];
-    f4 v[OROME_MAXK];
+    const int c = min((int)(blockIdx.x * blockDim.x + threadIdx.x) * 4, H - 4);
+    const bool live = (int)(blockIdx.x * blockDim.x + threadIdx.x) * 4 < H;
+    uint32_t pk[KM];
+    float wk[KM];
+    combine_pairs<KM>(pos, w, t, K, pk, wk);
+    const float sgt = sgl[t];
+    /* all rows in flight together */
+    f4 v[KM];
 #pragma unroll
-    for (int k = 0; k < OROME_MAXK; k++)
-        if (k < K) pk[k] = pos[t * K + k];
-#pragma unroll
-    for (int k = 0; k < OROME_MAXK; k++)
-        if (k < K) v[k] = *(const f4 *)(y + (size_t)pk[k] * H + c);
-    const float g = has_sh ? sigmoid_f(sgl[t]) : 0.0f;
-    *(f4 *)(h_out + (size_t)t * H + c) = combine4(y, ysh, pk, v, w, g, has_sh, h_in, t, H, K, c);
+    for (int k = 0; k < KM; k++) v[k] = *(const f4 *)(y + (size_t)pk[k] * H + c);
+    const f4 hb = *(const f4 *)((h_in ? h_in : y) + (size_t)t * H + c);
+    const f4 sv = *(const f4 *)((has_sh ? ysh : y) + (size_t)t * H + c);
+    const float g = has_sh ? sigmoid_f(sgt) : 0.0f;
+    const f4 o = combine4<KM>(v, wk, K, h_in ? hb : f4{0, 0, 0, 0}, sv, g, has_sh);
+    if (live) *(f4 *)(h_out + (size_t)t * H + c) = o;
 }
 
 /* Prefill combine with the next layer's RMSNorm (k_rmsnorm's arithmetic)
@@ -140,7 +157,7 @@ __global__ void k_combine(const float *y, const float *ysh, const uint32_t *pos,
  * forms the sum of squares in the canonical order (per lane over i, then
  * the canonical wave sum), so xnorm is bit-identical to k_rmsnorm run on
  * h_out, and every wave writes its columns of xnorm. */
-template <int CN_W>
+template <int CN_W, int KM>
 __global__ __launch_bounds__(64 * CN_W) void k_combine_norm(const float *y, const float *ysh, const uint32_t *pos,
                                                              const float *w, const float *sgl, int has_sh,
                                                              const float *h_in, float *h_out, int T, int H, int K,
@@ -149,27 +166,27 @@ __global__ __launch_bounds__(64 * CN_W) void k_combine_norm(const float *y, cons
     __shared__ float sc;
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, t = blockIdx.x;
     const int NI = H / 256;
-    uint32_t pk[OROME_MAXK];
-#pragma unroll
-    for (int k = 0; k < OROME_MAXK; k++)
-        if (k < K) pk[k] = pos[t * K + k];
-    const float g = has_sh ? sigmoid_f(sgl[t]) : 0.0f;
+    uint32_t pk[KM];
+    float wk[KM];
+    combine_pairs<KM>(pos, w, t, K, pk, wk);
+    const float sgt = sgl[t];
     constexpr int PW = 2; /* steps per wave: NI = 2 CN_W */
-    f4 v[PW][OROME_MAXK];
+    f4 v[PW][KM], hb[PW], sv[PW], wq[PW];
 #pragma unroll
     for (int q = 0; q < PW; q++) {
-        const int i = wv + CN_W * q, c = 256 * i + 4 * lane;
-        if (i < NI) {
+        const int i = min(wv + CN_W * q, NI - 1), c = 256 * i + 4 * lane;
 #pragma unroll
-            for (int k = 0; k < OROME_MAXK; k++)
-                if (k < K) v[q][k] = *(const f4 *)(y + (size_t)pk[k] * H + c);
-        }
+        for (int k = 0; k < KM; k++) v[q][k] = *(const f4 *)(y + (size_t)pk[k] * H + c);
+        hb[q] = *(const f4 *)((h_in ? h_in : y) + (size_t)t * H + c);
+        sv[q] = *(const f4 *)((has_sh ? ysh : y) + (size_t)t * H + c);
+        wq[q] = *(const f4 *)((nw ? nw : y) + c);
     }
+    const float g = has_sh ? sigmoid_f(sgt) : 0.0f;
 #pragma unroll
     for (int q = 0; q < PW; q++) {
         const int i = wv + CN_W * q, c = 256 * i + 4 * lane;
         if (i < NI) {
-            const f4 o = combine4(y, ysh, pk, v[q], w, g, has_sh, h_in, t, H, K, c);
+            const f4 o = combine4<KM>(v[q], wk, K, h_in ? hb[q] : f4{0, 0, 0, 0}, sv[q], g, has_sh);
             *(f4 *)(h_out + (size_t)t * H + c) = o;
             ro[i][lane] = o;
         }
@@ -196,12 +213,12 @@ __global__ __launch_bounds__(64 * CN_W) void k_combine_norm(const float *y, cons
         const int i = wv + CN_W * q, j = 256 * i + 4 * lane;
         if (i < NI) {
             const f4 o = ro[i][lane];
-            const f4 wq = nw ? *(const f4 *)(nw + j) : f4{1, 1, 1, 1};
+            const f4 wn = nw ? wq[q] : f4{1, 1, 1, 1};
             f4 r;
-            r.x = (o.x * scale) * __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, wq.x) & 0xFFFF0000u);
-            r.y = (o.y * scale) * __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, wq.y) & 0xFFFF0000u);
-            r.z = (o.z * scale) * __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, wq.z) & 0xFFFF0000u);
-            r.w = (o.w * scale) * __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, wq.w) & 0xFFFF0000u);
+            r.x = (o.x * scale) * __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, wn.x) & 0xFFFF0000u);
+            r.y = (o.y * scale) * __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, wn.y) & 0xFFFF0000u);
+            r.z = (o.z * scale) * __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, wn.z) & 0xFFFF0000u);
+            r.w = (o.w * scale) * __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, wn.w) & 0xFFFF0000u);
             *(f4 *)(xnorm + (size_t)t * H + j) = r;
         }
     }
@@ -211,10 +228,16 @@ int launch_combine_norm(const float *y, const float *ysh, const uint32_t *pos, c
                         int has_shared, const float *h_in, float *h_out, int T, int H, int K, const float *nw,
                         float eps, float *xnorm, hipStream_t s) {
     const int NI = H / 256;
-    if (H % 512 || NI > 2 * 8 || NI > CANON_NI) return -2;
-#define CN_LAUNCH(CW)                                                                                           \
-    hipLaunchKernelGGL(k_combine_norm<CW>, dim3((unsigned)T), dim3(64 * CW), 0, s, y, ysh, pos, w, sgl, has_shared, \
-                       h_in, h_out, T, H, K, nw, eps, xnorm)
+    if (H % 512 || NI > 2 * 8 || NI > CANON_NI || K < 1 || K > OROME_MAXK) return -2;
+#define CN_LAUNCH(CW)                                                                                            \
+    do {                                                                                                         \
+        if (K <= 8)                                                                                              \
+            hipLaunchKernelGGL((k_combine_norm<CW, 8>), dim3((unsigned)T), dim3(64 * CW), 0, s, y, ysh, pos, w,   \
+                               sgl, has_shared, h_in, h_out, T, H, K, nw, eps, xnorm);                           \
+        else                                                                                                     \
+            hipLaunchKernelGGL((k_combine_norm<CW, OROME_MAXK>), dim3((unsigned)T), dim3(64 * CW), 0, s, y, ysh, \
+                               pos, w, sgl, has_shared, h_in, h_out, T, H, K, nw, eps, xnorm);                   \
+    } while (0)
     switch (NI / 2) {
         case 1: CN_LAUNCH(1); break;
         case 2: CN_LAUNCH(2); break;
@@ -232,10 +255,13 @@ int launch_combine_norm(const float *y, const float *ysh, const uint32_t *pos, c
 int launch_combine(const float *y, const float *ysh, const uint32_t *pos, const float *w,
                    const float *sgl, int has_shared, const float *h_in, float *h_out, int T, int H,
                    int K, hipStream_t s) {
-    if (H % 4) return -2;
+    if (H % 4 || K < 1 || K > OROME_MAXK) return -2;
     dim3 grid((H / 4 + 255) / 256, T);
-    hipLaunchKernelGGL(k_combine, grid, dim3(256), 0, s, y, ysh, pos, w, sgl, has_shared, h_in,
-                       h_out, T, H, K);
+    if (K <= 8)
+        hipLaunchKernelGGL(k_combine<8>, grid, dim3(256), 0, s, y, ysh, pos, w, sgl, has_shared, h_in, h_out, T, H, K);
+    else
+        hipLaunchKernelGGL(k_combine<OROME_MAXK>, grid, dim3(256), 0, s, y, ysh, pos, w, sgl, has_shared, h_in, h_out,
+                           T, H, K);
     return hipGetLastError() == hipSuccess ? 0 : -3;
 }
 
