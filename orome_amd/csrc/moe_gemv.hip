@@ -53,6 +53,19 @@ DEV float load_x16_f32(const float *p, h2 *o) {
     for (int v = 0; v < 8; v++) s = dot2(o[v], one, s);
     return s;
 }
+/* load_x16_f32 on 16 floats already loaded */
+DEV float cvt_x16_f32(const f4 *a, h2 *o) {
+    float s = 0.0f;
+#pragma unroll
+    for (int v = 0; v < 4; v++) {
+        o[2 * v] = h2{(_Float16)a[v].x, (_Float16)a[v].y};
+        o[2 * v + 1] = h2{(_Float16)a[v].z, (_Float16)a[v].w};
+    }
+    const h2 one = {(_Float16)1.0f, (_Float16)1.0f};
+#pragma unroll
+    for (int v = 0; v < 8; v++) s = dot2(o[v], one, s);
+    return s;
+}
 /* 8 consecutive fp16 (16 bytes) -> 4 pairs; LX: p points into LDS */
 template <bool LX = false>
 DEV void load_h8(const _Float16 *p, h2 *o) {
@@ -336,10 +349,29 @@ DEV void k_gemv_gate_up1_body(GUArgs a, RouteArgs ra) {
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int rows_blk = 4 * GU_RPW, b = blockIdx.x;
     const int E = a.E, K = a.K;
+    /* x, then the logits (and bias), issued in every block and held here:
+     * one round trip for both (the compiler would otherwise load the logits
+     * inside the routed branch, after converting x) */
     int klo;
     q4_pos(lane, klo);
+    f4 xr[8];
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        xr[q] = *(const f4 *)(a.x + klo + 4 * q);
+        xr[4 + q] = *(const f4 *)(a.x + klo + 32 + 4 * q);
+    }
+    const float *l = ra.logits, *bias = ra.bias ? ra.bias : ra.logits;
+    float v[EPL], bv[EPL];
+#pragma unroll
+    for (int j = 0; j < EPL; j++) {
+        v[j] = l[min(lane * EPL + j, E - 1)];
+        bv[j] = bias[min(lane * EPL + j, E - 1)];
+    }
+    const float sg = l[E];
+#pragma unroll
+    for (int j = 0; j < EPL; j++) asm volatile("" : : "v"(v[j]), "v"(bv[j]));
     h2 xl[8], xh[8];
-    const float Xl = load_x16_f32(a.x + klo, xl), Xh = load_x16_f32(a.x + klo + 32, xh);
+    const float Xl = cvt_x16_f32(xr, xl), Xh = cvt_x16_f32(xr + 4, xh);
     if (b >= a.routed_blocks) { /* shared expert (Q4_K): needs no routing */
         const int r0 = (b - a.routed_blocks) * rows_blk + wv * GU_RPW;
         gu_body1<GU_RPW>(a, a.sh_gate, a.sh_up, r0, xl, xh, Xl, Xh, a.act_sh, lane);
@@ -348,14 +380,6 @@ DEV void k_gemv_gate_up1_body(GUArgs a, RouteArgs ra) {
     const int bpe = a.M / rows_blk, u = b / bpe, r0 = (b % bpe) * rows_blk + wv * GU_RPW;
     const size_t rb = row_bytes(FQ4K, a.H);
 
-    const float *l = ra.logits;
-    float v[EPL], bv[EPL];
-#pragma unroll
-    for (int j = 0; j < EPL; j++) v[j] = l[min(lane * EPL + j, E - 1)];
-    const float sg = l[E];
-    if (ra.bias)
-#pragma unroll
-        for (int j = 0; j < EPL; j++) bv[j] = ra.bias[min(lane * EPL + j, E - 1)];
     uint32_t key[EPL];
     int kj[EPL];
 #pragma unroll

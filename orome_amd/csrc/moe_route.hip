@@ -24,81 +24,77 @@ extern "C" __attribute__((visibility("default"))) int orome_trace_fetch_route(un
 }
 #endif
 
-/* canonical dot of one wave over H (H % 256 == 0, H <= 256 CANON_NI), for
- * up to TMAX tokens; all loads of a row are issued before the multiply-adds */
-template <int TMAX>
-DEV void canon_dots(const float *wrow, const float *x, int T, int H, int lane, float *acc) {
-    const int NI = H / 256;
-    f4 wv[CANON_NI];
-#pragma unroll
-    for (int i = 0; i < CANON_NI; i++)
-        if (i < NI) wv[i] = *(const f4 *)(wrow + 256 * i + 4 * lane);
-#pragma unroll
-    for (int t = 0; t < TMAX; t++) {
-        acc[t] = 0.0f;
-        if (t < T) {
-            f4 xv[CANON_NI];
-#pragma unroll
-            for (int i = 0; i < CANON_NI; i++)
-                if (i < NI) xv[i] = *(const f4 *)(x + (size_t)t * H + 256 * i + 4 * lane);
-            float a = 0.0f;
-#pragma unroll
-            for (int i = 0; i < CANON_NI; i++)
-                if (i < NI) {
-                    a = __builtin_fmaf(wv[i].x, xv[i].x, a);
-                    a = __builtin_fmaf(wv[i].y, xv[i].y, a);
-                    a = __builtin_fmaf(wv[i].z, xv[i].z, a);
-                    a = __builtin_fmaf(wv[i].w, xv[i].w, a);
-                }
-            acc[t] = wave_sum_canon(a);
-        }
-    }
-}
-
-/* As canon_dots, with x = RMSNorm(h) computed in place (RMSNorm of
+/* Canonical dots of one wave over H (H % 256 == 0, H <= 256 NIM) for up to
+ * TMAX tokens, with NORM x = RMSNorm(h) computed in place (RMSNorm of
  * inference/src/shaders.metal:128-149, the same arithmetic and canonical sum
- * of squares as k_rmsnorm, so x is bit-identical to that kernel's output);
- * write_x stores x for the later kernels. */
-template <int TMAX>
-DEV void canon_dots_norm(const float *wrow, const RouteArgs &a, int lane, bool write_x, float *acc) {
+ * of squares as k_rmsnorm, so x is bit-identical to that kernel's output;
+ * write_x stores it for the later kernels).  Tokens go in chunks of up to 4
+ * whose row loads are issued together with the router row's; every load is
+ * unconditional (indices clamped, values past T or H unused), since a load
+ * under a branch is waited for alone.  A NULL wrow gives zeros. */
+template <int TMAX, int NIM, bool NORM>
+DEV void canon_dots(const float *wrow, const RouteArgs &a, int lane, bool write_x, float *acc) {
+    constexpr int TC = TMAX < 4 ? TMAX : 4;
     const int NI = a.H / 256, H = a.H, T = a.T;
-    f4 wv[CANON_NI], nw[CANON_NI];
+    const float *xs = NORM ? a.norm_h : a.x;
+    f4 wv[NIM], nw[NIM];
 #pragma unroll
-    for (int i = 0; i < CANON_NI; i++)
-        if (i < NI) {
-            wv[i] = wrow ? *(const f4 *)(wrow + 256 * i + 4 * lane) : f4{0, 0, 0, 0};
-            const f4 w = a.norm_w ? *(const f4 *)(a.norm_w + 256 * i + 4 * lane) : f4{1, 1, 1, 1};
-            nw[i] = f4{__builtin_bit_cast(float, __builtin_bit_cast(uint32_t, w.x) & 0xFFFF0000u),
-                       __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, w.y) & 0xFFFF0000u),
-                       __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, w.z) & 0xFFFF0000u),
-                       __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, w.w) & 0xFFFF0000u)};
+    for (int i = 0; i < NIM; i++) {
+        const int ic = 256 * min(i, NI - 1) + 4 * lane;
+        wv[i] = *(const f4 *)((wrow ? wrow : xs) + ic);
+        if (NORM) nw[i] = *(const f4 *)((a.norm_w ? a.norm_w : xs) + ic);
+    }
+#pragma unroll
+    for (int t0 = 0; t0 < TMAX; t0 += TC) {
+        if (t0 >= T) break;
+        f4 hv[TC][NIM];
+#pragma unroll
+        for (int c = 0; c < TC; c++)
+#pragma unroll
+            for (int i = 0; i < NIM; i++)
+                hv[c][i] = *(const f4 *)(xs + (size_t)min(t0 + c, T - 1) * H + 256 * min(i, NI - 1) + 4 * lane);
+        if (t0 == 0) {
+#pragma unroll
+            for (int i = 0; i < NIM; i++) {
+                if (!wrow) wv[i] = f4{0, 0, 0, 0};
+                if (NORM) {
+                    const f4 w = a.norm_w ? nw[i] : f4{1, 1, 1, 1};
+                    nw[i] = f4{__builtin_bit_cast(float, __builtin_bit_cast(uint32_t, w.x) & 0xFFFF0000u),
+                               __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, w.y) & 0xFFFF0000u),
+                               __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, w.z) & 0xFFFF0000u),
+                               __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, w.w) & 0xFFFF0000u)};
+                }
+            }
         }
 #pragma unroll
-    for (int t = 0; t < TMAX; t++) {
-        acc[t] = 0.0f;
-        if (t < T) {
-            f4 hv[CANON_NI];
+        for (int c = 0; c < TC; c++) {
+            const int t = t0 + c;
+            acc[t] = 0.0f;
+            if (t >= T || (!NORM && !wrow)) continue;
+            float scale = 1.0f;
+            if (NORM) {
+                float ss = 0.0f;
 #pragma unroll
-            for (int i = 0; i < CANON_NI; i++)
-                if (i < NI) hv[i] = *(const f4 *)(a.norm_h + (size_t)t * H + 256 * i + 4 * lane);
-            float ss = 0.0f;
-#pragma unroll
-            for (int i = 0; i < CANON_NI; i++)
-                if (i < NI) {
-                    ss = __builtin_fmaf(hv[i].x, hv[i].x, ss);
-                    ss = __builtin_fmaf(hv[i].y, hv[i].y, ss);
-                    ss = __builtin_fmaf(hv[i].z, hv[i].z, ss);
-                    ss = __builtin_fmaf(hv[i].w, hv[i].w, ss);
-                }
-            ss = wave_sum_canon(ss);
-            const float scale = 1.0f / sqrtf(ss / (float)H + a.norm_eps);
+                for (int i = 0; i < NIM; i++)
+                    if (i < NI) {
+                        ss = __builtin_fmaf(hv[c][i].x, hv[c][i].x, ss);
+                        ss = __builtin_fmaf(hv[c][i].y, hv[c][i].y, ss);
+                        ss = __builtin_fmaf(hv[c][i].z, hv[c][i].z, ss);
+                        ss = __builtin_fmaf(hv[c][i].w, hv[c][i].w, ss);
+                    }
+                ss = wave_sum_canon(ss);
+                scale = 1.0f / sqrtf(ss / (float)H + a.norm_eps);
+            }
             float d = 0.0f;
 #pragma unroll
-            for (int i = 0; i < CANON_NI; i++)
+            for (int i = 0; i < NIM; i++)
                 if (i < NI) {
-                    const f4 x = {(hv[i].x * scale) * nw[i].x, (hv[i].y * scale) * nw[i].y,
-                                  (hv[i].z * scale) * nw[i].z, (hv[i].w * scale) * nw[i].w};
-                    if (write_x) *(f4 *)(a.xnorm + (size_t)t * H + 256 * i + 4 * lane) = x;
+                    f4 x = hv[c][i];
+                    if (NORM) {
+                        x = f4{(x.x * scale) * nw[i].x, (x.y * scale) * nw[i].y, (x.z * scale) * nw[i].z,
+                               (x.w * scale) * nw[i].w};
+                        if (write_x) *(f4 *)(a.xnorm + (size_t)t * H + 256 * i + 4 * lane) = x;
+                    }
                     d = __builtin_fmaf(wv[i].x, x.x, d);
                     d = __builtin_fmaf(wv[i].y, x.y, d);
                     d = __builtin_fmaf(wv[i].z, x.z, d);
@@ -112,25 +108,18 @@ DEV void canon_dots_norm(const float *wrow, const RouteArgs &a, int lane, bool w
 /* Small-batch router logits (T <= 16): every wave computes one router row
  * (or the shared-gate row) for all tokens; with NORM, x is RMSNorm(norm_h)
  * and the row-0 wave also writes it out. */
-template <bool NORM>
+template <bool NORM, int TMAX, int NIM>
 __global__ __launch_bounds__(256) void k_route_small(RouteArgs a) {
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int row = blockIdx.x * 4 + wv;
     const int E = a.E, H = a.H, T = a.T;
     if (row > E) return;
     const float *wr = row < E ? a.W + (size_t)row * H : a.wsg;
-    float acc[16];
-    if (NORM) {
-        canon_dots_norm<16>(wr, a, lane, row == 0, acc);
-    } else if (wr) {
-        canon_dots<16>(wr, a.x, T, H, lane, acc);
-    } else {
-#pragma unroll
-        for (int t = 0; t < 16; t++) acc[t] = 0.0f;
-    }
+    float acc[TMAX];
+    canon_dots<TMAX, NIM, NORM>(wr, a, lane, NORM && row == 0, acc);
     if (lane == 0) {
 #pragma unroll
-        for (int t = 0; t < 16; t++)
+        for (int t = 0; t < TMAX; t++)
             if (t < T) a.logits[(size_t)t * (E + 1) + row] = acc[t];
     }
 }
@@ -736,6 +725,7 @@ __global__ __launch_bounds__(DSP_TOK) void k_dispatch_scatter(RouteArgs a, const
  * earlier sub-chunks + the popcount of its sub-chunk's mask below its token.
  * LDS: masks and word prefixes for DSP1_SUB sub-chunks of up to 256 experts. */
 #define DSP1_SUB (DSP_THREADS / DSP_TOK)
+template <int KM>
 __global__ __launch_bounds__(DSP_THREADS) void k_dispatch_one(RouteArgs a, uint32_t *tiles_s, uint32_t *tiles_b,
                                                               int has_shared) {
     __shared__ uint32_t hist[DSP_THREADS], offs[DSP_THREADS], arank[DSP_THREADS], ts[DSP_THREADS],
@@ -745,13 +735,16 @@ __global__ __launch_bounds__(DSP_THREADS) void k_dispatch_one(RouteArgs a, uint3
     const int sub = tid / DSP_TOK, tl = tid % DSP_TOK;
     for (int i = tid; i < DSP1_SUB * E * DSP_WORDS; i += DSP_THREADS) mask[i] = 0;
     __syncthreads();
-    int ek[OROME_MAXK];
+    /* the token's K expert ids, loaded together (indices clamped; a load
+     * under a branch is waited for alone), then marked */
+    int ek[KM];
 #pragma unroll
-    for (int k = 0; k < OROME_MAXK; k++)
-        if (k < K) {
-            ek[k] = tid < T ? a.idx[tid * K + k] : -1;
-            if (ek[k] >= 0) atomicOr(&mask[(sub * E + ek[k]) * DSP_WORDS + (tl >> 5)], 1u << (tl & 31));
-        }
+    for (int k = 0; k < KM; k++) ek[k] = a.idx[min(tid, T - 1) * K + min(k, K - 1)];
+#pragma unroll
+    for (int k = 0; k < KM; k++) {
+        if (k >= K || tid >= T) ek[k] = -1;
+        if (ek[k] >= 0) atomicOr(&mask[(sub * E + ek[k]) * DSP_WORDS + (tl >> 5)], 1u << (tl & 31));
+    }
     __syncthreads();
     if (tid < E) { /* word prefixes from 0, and the expert's count */
         uint32_t run = 0;
@@ -773,8 +766,8 @@ __global__ __launch_bounds__(DSP_THREADS) void k_dispatch_one(RouteArgs a, uint3
     __syncthreads();
     const uint32_t below = (1u << (tl & 31)) - 1u;
 #pragma unroll
-    for (int k = 0; k < OROME_MAXK; k++)
-        if (k < K && ek[k] >= 0) {
+    for (int k = 0; k < KM; k++)
+        if (ek[k] >= 0) {
             const int e = ek[k], i = (sub * E + e) * DSP_WORDS + (tl >> 5);
             const uint32_t pos = offs[e] - hist[e] + wpre[i] + __popc(mask[i] & below);
             const uint32_t p = (uint32_t)(tid * K + k);
@@ -785,18 +778,23 @@ __global__ __launch_bounds__(DSP_THREADS) void k_dispatch_one(RouteArgs a, uint3
 
 /* RMSNorm (inference/src/shaders.metal:128-149) with the canonical sum of
  * squares: x = (h * (1 / sqrt(ss/H + eps))) * bf16(w); one wave per token. */
+template <int NIM>
 __global__ __launch_bounds__(64) void k_rmsnorm(const float *h, const float *w, int H, float eps,
                                                 float *x) {
     const int lane = threadIdx.x, t = blockIdx.x;
     const float *ht = h + (size_t)t * H;
     const int NI = H / 256;
-    f4 v[CANON_NI];
+    /* every load unconditional (row index clamped) and issued before the
+     * first use: a load under a branch, or one behind a store, is waited
+     * for alone */
+    f4 v[NIM], wv[NIM];
 #pragma unroll
-    for (int i = 0; i < CANON_NI; i++)
-        if (i < NI) v[i] = *(const f4 *)(ht + 256 * i + 4 * lane);
+    for (int i = 0; i < NIM; i++) v[i] = *(const f4 *)(ht + 256 * min(i, NI - 1) + 4 * lane);
+#pragma unroll
+    for (int i = 0; i < NIM; i++) wv[i] = *(const f4 *)((w ? w : ht) + 256 * min(i, NI - 1) + 4 * lane);
     float acc = 0.0f;
 #pragma unroll
-    for (int i = 0; i < CANON_NI; i++)
+    for (int i = 0; i < NIM; i++)
         if (i < NI) {
             acc = __builtin_fmaf(v[i].x, v[i].x, acc);
             acc = __builtin_fmaf(v[i].y, v[i].y, acc);
@@ -807,15 +805,15 @@ __global__ __launch_bounds__(64) void k_rmsnorm(const float *h, const float *w, 
     /* sqrtf and / lower to correctly rounded sequences (__fsqrt_rn does not) */
     float scale = 1.0f / sqrtf(ss / (float)H + eps);
 #pragma unroll
-    for (int i = 0; i < CANON_NI; i++)
+    for (int i = 0; i < NIM; i++)
         if (i < NI) {
             const int j = 256 * i + 4 * lane;
-            f4 wv = w ? *(const f4 *)(w + j) : f4{1, 1, 1, 1};
+            const f4 wq = w ? wv[i] : f4{1, 1, 1, 1};
             f4 o;
-            o.x = (v[i].x * scale) * __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, wv.x) & 0xFFFF0000u);
-            o.y = (v[i].y * scale) * __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, wv.y) & 0xFFFF0000u);
-            o.z = (v[i].z * scale) * __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, wv.z) & 0xFFFF0000u);
-            o.w = (v[i].w * scale) * __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, wv.w) & 0xFFFF0000u);
+            o.x = (v[i].x * scale) * __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, wq.x) & 0xFFFF0000u);
+            o.y = (v[i].y * scale) * __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, wq.y) & 0xFFFF0000u);
+            o.z = (v[i].z * scale) * __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, wq.z) & 0xFFFF0000u);
+            o.w = (v[i].w * scale) * __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, wq.w) & 0xFFFF0000u);
             *(f4 *)(x + (size_t)t * H + j) = o;
         }
 }
@@ -842,8 +840,23 @@ static int epl_for(int E) {
 
 int launch_route_small(const RouteArgs &a, hipStream_t s) {
     if (a.T < 1 || a.T > 16 || a.T * a.K > 256 || a.H % 256 || a.H > 4096) return -2;
-    if (a.norm_h) hipLaunchKernelGGL(k_route_small<true>, dim3((a.E + 1 + 3) / 4), dim3(256), 0, s, a);
-    else hipLaunchKernelGGL(k_route_small<false>, dim3((a.E + 1 + 3) / 4), dim3(256), 0, s, a);
+    const dim3 g((a.E + 1 + 3) / 4);
+#define RS_LAUNCH(TM, NIMV)                                                                        \
+    do {                                                                                           \
+        if (a.norm_h) hipLaunchKernelGGL((k_route_small<true, TM, NIMV>), g, dim3(256), 0, s, a);  \
+        else hipLaunchKernelGGL((k_route_small<false, TM, NIMV>), g, dim3(256), 0, s, a);          \
+    } while (0)
+#define RS_T(NIMV)                          \
+    do {                                    \
+        if (a.T == 1) RS_LAUNCH(1, NIMV);   \
+        else if (a.T <= 4) RS_LAUNCH(4, NIMV); \
+        else if (a.T <= 8) RS_LAUNCH(8, NIMV); \
+        else RS_LAUNCH(16, NIMV);           \
+    } while (0)
+    if (a.H <= 256 * 8) RS_T(8);
+    else RS_T(CANON_NI);
+#undef RS_T
+#undef RS_LAUNCH
     return hipGetLastError() == hipSuccess ? 0 : -3;
 }
 
@@ -932,7 +945,8 @@ int launch_dispatch(const RouteArgs &a, uint32_t *tiles_s, uint32_t *tiles_b, in
 #define DISPATCH_ONE 1
 #endif
     if (DISPATCH_ONE && a.E <= 256 && a.T <= DSP_THREADS) {
-        hipLaunchKernelGGL(k_dispatch_one, dim3(1), dim3(DSP_THREADS), 0, s, a, tiles_s, tiles_b, has_shared);
+        if (a.K <= 8) hipLaunchKernelGGL(k_dispatch_one<8>, dim3(1), dim3(DSP_THREADS), 0, s, a, tiles_s, tiles_b, has_shared);
+        else hipLaunchKernelGGL(k_dispatch_one<OROME_MAXK>, dim3(1), dim3(DSP_THREADS), 0, s, a, tiles_s, tiles_b, has_shared);
         return hipGetLastError() == hipSuccess ? 0 : -3;
     }
     const int G = dispatch_blocks(a.T);
@@ -944,6 +958,7 @@ int launch_dispatch(const RouteArgs &a, uint32_t *tiles_s, uint32_t *tiles_b, in
 
 int launch_rmsnorm(const float *h, const float *w, int T, int H, float eps, float *x, hipStream_t s) {
     if (H % 256 || H > 256 * CANON_NI) return -2;
-    hipLaunchKernelGGL(k_rmsnorm, dim3(T), dim3(64), 0, s, h, w, H, eps, x);
+    if (H <= 256 * 8) hipLaunchKernelGGL(k_rmsnorm<8>, dim3(T), dim3(64), 0, s, h, w, H, eps, x);
+    else hipLaunchKernelGGL(k_rmsnorm<CANON_NI>, dim3(T), dim3(64), 0, s, h, w, H, eps, x);
     return hipGetLastError() == hipSuccess ? 0 : -3;
 }
