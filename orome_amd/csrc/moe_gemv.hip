@@ -858,55 +858,38 @@ struct DnRaw<FQ8> {
     }
 };
 
-template <int EFMT, int SFMT>
-__global__ __launch_bounds__(128) void k_gemv_down_combine1(DownArgs a, RouteArgs ra, const float *h_in,
-                                                            float *h_out) {
-    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-    const int cl = lane & 15, r = blockIdx.x * 8 + wv * 4 + (lane >> 4);
-    const int K = a.K;
-    const size_t rb = row_bytes(EFMT, a.M);
-    DnRaw<EFMT> raw[DC_K];
-    const _Float16 *xr[DC_K];
-#pragma unroll
-    for (int k = 0; k < DC_K; k++) {
-        const int kk = k < K ? k : K - 1;
-        const int e = ra.idx[kk];
-        raw[k].load(a.down + (size_t)e * a.down_stride + (size_t)r * rb, cl);
-        xr[k] = a.act + (size_t)ra.pos[kk] * a.M;
-    }
-    DnRaw<SFMT> rsh;
-    const bool has_sh = a.sh_down != nullptr;
-    if (has_sh) rsh.load(a.sh_down + (size_t)r * row_bytes(SFMT, a.S), cl);
-    float y[DC_K];
-#pragma unroll
-    for (int k = 0; k < DC_K; k++) y[k] = row_sum16(raw[k].dot(cl, xr[k]));
-    const float ysh = has_sh ? row_sum16(rsh.dot(cl, a.act_sh)) : 0.0f;
-    if (cl == 0) {
-        float moe = 0.0f;
-#pragma unroll
-        for (int k = 0; k < DC_K; k++)
-            if (k < K) moe += ra.w[k] * y[k];
-        float o = (h_in ? h_in[r] : 0.0f) + moe;
-        if (has_sh) o = o + sigmoid_f(ra.sgl[0]) * ysh;
-        h_out[r] = o;
-    }
-}
-
 /* Activation values of chunk c of one token, loaded once and used for
- * every weight row of the lane (the DnRaw<FMT> chunk layouts). */
+ * every weight row of the lane (the DnRaw<FMT> chunk layouts).  offs gives
+ * the four 8-value runs a lane reads, set fills the values from those runs
+ * (so a kernel can issue the loads of many chunks before using any). */
 template <int FMT>
 struct DnX;
 template <>
 struct DnX<FQ4K> {
     h2 xl[8], xh[8];
     float Xl, Xh;
-    MDEV void load(int c, const _Float16 *x) {
+    static MDEV void offs(int c, int (&o)[4]) {
         int klo;
         q4_pos(c, klo);
-        load_h8(x + klo, xl);
-        load_h8(x + klo + 8, xl + 4);
-        load_h8(x + klo + 32, xh);
-        load_h8(x + klo + 40, xh + 4);
+        o[0] = klo; o[1] = klo + 8; o[2] = klo + 32; o[3] = klo + 40;
+    }
+    MDEV void set(const u4 (&q)[4]) {
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            xl[4 * j] = as_h2(q[j].x); xl[4 * j + 1] = as_h2(q[j].y); xl[4 * j + 2] = as_h2(q[j].z); xl[4 * j + 3] = as_h2(q[j].w);
+            xh[4 * j] = as_h2(q[2 + j].x); xh[4 * j + 1] = as_h2(q[2 + j].y);
+            xh[4 * j + 2] = as_h2(q[2 + j].z); xh[4 * j + 3] = as_h2(q[2 + j].w);
+        }
+        Xl = hsum(xl, 8);
+        Xh = hsum(xh, 8);
+    }
+    MDEV void load(int c, const _Float16 *x) {
+        int o[4];
+        offs(c, o);
+        load_h8(x + o[0], xl);
+        load_h8(x + o[1], xl + 4);
+        load_h8(x + o[2], xh);
+        load_h8(x + o[3], xh + 4);
         Xl = hsum(xl, 8);
         Xh = hsum(xh, 8);
     }
@@ -915,23 +898,120 @@ struct DnX<FQ4K> {
 template <>
 struct DnX<FQ6K> {
     h2 x[16];
-    MDEV void load(int c, const _Float16 *xr) {
+    static MDEV void offs(int c, int (&o)[4]) {
         int k0;
         q6_pos(c, k0);
 #pragma unroll
-        for (int gq = 0; gq < 4; gq++) load_h8(xr + k0 + 32 * gq, x + 4 * gq);
+        for (int gq = 0; gq < 4; gq++) o[gq] = k0 + 32 * gq;
+    }
+    MDEV void set(const u4 (&q)[4]) {
+#pragma unroll
+        for (int gq = 0; gq < 4; gq++) {
+            x[4 * gq] = as_h2(q[gq].x); x[4 * gq + 1] = as_h2(q[gq].y);
+            x[4 * gq + 2] = as_h2(q[gq].z); x[4 * gq + 3] = as_h2(q[gq].w);
+        }
+    }
+    MDEV void load(int c, const _Float16 *xr) {
+        int o[4];
+        offs(c, o);
+#pragma unroll
+        for (int gq = 0; gq < 4; gq++) load_h8(xr + o[gq], x + 4 * gq);
     }
     MDEV float dot(const DnRaw<FQ6K> &r, int c) const { return q6_dot(r.r, c, x); }
 };
 template <>
 struct DnX<FQ8> {
     h2 x[16];
-    MDEV void load(int c, const _Float16 *xr) {
+    static MDEV void offs(int c, int (&o)[4]) {
 #pragma unroll
-        for (int gq = 0; gq < 4; gq++) load_h8(xr + c * 32 + 8 * gq, x + 4 * gq);
+        for (int gq = 0; gq < 4; gq++) o[gq] = c * 32 + 8 * gq;
+    }
+    MDEV void set(const u4 (&q)[4]) {
+#pragma unroll
+        for (int gq = 0; gq < 4; gq++) {
+            x[4 * gq] = as_h2(q[gq].x); x[4 * gq + 1] = as_h2(q[gq].y);
+            x[4 * gq + 2] = as_h2(q[gq].z); x[4 * gq + 3] = as_h2(q[gq].w);
+        }
+    }
+    MDEV void load(int c, const _Float16 *xr) {
+        int o[4];
+        offs(c, o);
+#pragma unroll
+        for (int gq = 0; gq < 4; gq++) load_h8(xr + o[gq], x + 4 * gq);
     }
     MDEV float dot(const DnRaw<FQ8> &r, int) const { return q8_dot(r.r, x); }
 };
+
+template <int EFMT, int SFMT>
+__global__ __launch_bounds__(128) void k_gemv_down_combine1(DownArgs a, RouteArgs ra, const float *h_in,
+                                                            float *h_out) {
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int cl = lane & 15, r = blockIdx.x * 8 + wv * 4 + (lane >> 4);
+    const int K = a.K;
+    const size_t rb = row_bytes(EFMT, a.M);
+    const bool has_sh = a.sh_down != nullptr;
+    /* every load up front and unconditional, in dependence order: the slots'
+     * experts, positions and weights; then all weight chunks; then all
+     * activation chunks, the residual and the gate (a load under a branch,
+     * or one made inside a slot's dot, is waited for alone) */
+    /* the 8 slots' experts, positions and weights as three 32-byte reads
+     * (the context sizes these buffers for 16 per token); a slot k >= K
+     * takes slot 0's expert and position (a valid address) and is not summed */
+    static_assert(DC_K == 8 && OROME_MAXK >= 8, "slot reads");
+    typedef int i4v __attribute__((ext_vector_type(4)));
+    const i4v e0 = *(const i4v *)ra.idx, e1 = *(const i4v *)(ra.idx + 4);
+    const u4 p0 = *(const u4 *)ra.pos, p1 = *(const u4 *)(ra.pos + 4);
+    const f4 w0 = *(const f4 *)ra.w, w1 = *(const f4 *)(ra.w + 4);
+    const int ev[DC_K] = {e0.x, e0.y, e0.z, e0.w, e1.x, e1.y, e1.z, e1.w};
+    const int pv[DC_K] = {(int)p0.x, (int)p0.y, (int)p0.z, (int)p0.w, (int)p1.x, (int)p1.y, (int)p1.z, (int)p1.w};
+    const float wk[DC_K] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+    int e[DC_K], ps[DC_K];
+#pragma unroll
+    for (int k = 0; k < DC_K; k++) {
+        e[k] = k < K ? ev[k] : ev[0];
+        ps[k] = k < K ? pv[k] : pv[0];
+    }
+    DnRaw<EFMT> raw[DC_K];
+#pragma unroll
+    for (int k = 0; k < DC_K; k++) raw[k].load(a.down + (size_t)e[k] * a.down_stride + (size_t)r * rb, cl);
+    DnRaw<SFMT> rsh;
+    rsh.load(has_sh ? a.sh_down + (size_t)r * row_bytes(SFMT, a.S) : a.down + (size_t)r * rb, cl);
+    int o[4], osh[4];
+    DnX<EFMT>::offs(cl, o);
+    DnX<SFMT>::offs(cl, osh);
+    u4 xq[DC_K][4], sq[4];
+#pragma unroll
+    for (int k = 0; k < DC_K; k++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) xq[k][j] = ld_u4((const uint8_t *)(a.act + (size_t)ps[k] * a.M + o[j]));
+    const _Float16 *xs = has_sh ? a.act_sh : a.act;
+#pragma unroll
+    for (int j = 0; j < 4; j++) sq[j] = ld_u4((const uint8_t *)(xs + osh[j]));
+    const float hb = (h_in ? h_in : h_out)[r];
+    const float sgv = ra.sgl[0];
+    float y[DC_K];
+#pragma unroll
+    for (int k = 0; k < DC_K; k++) {
+        DnX<EFMT> xv;
+        xv.set(xq[k]);
+        y[k] = row_sum16(xv.dot(raw[k], cl));
+    }
+    float ysh = 0.0f;
+    if (has_sh) {
+        DnX<SFMT> xv;
+        xv.set(sq);
+        ysh = row_sum16(xv.dot(rsh, cl));
+    }
+    if (cl == 0) {
+        float moe = 0.0f;
+#pragma unroll
+        for (int k = 0; k < DC_K; k++)
+            if (k < K) moe += wk[k] * y[k];
+        float o = (h_in ? hb : 0.0f) + moe;
+        if (has_sh) o = o + sigmoid_f(sgv) * ysh;
+        h_out[r] = o;
+    }
+}
 
 /* Batched down (T <= 8, in_dim = 512): a block = 4 waves = 64 output rows of
  * one slot (an active routed expert, or the shared expert over all T
