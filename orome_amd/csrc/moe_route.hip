@@ -307,7 +307,13 @@ __global__ __launch_bounds__(64 * NW) void k_route_approx(RouteArgs a) {
     const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int E = a.E, H = a.H, T = a.T;
     RSTAMP(0);
-    const int e0 = blockIdx.x * (16 * TES), t0 = blockIdx.y * (16 * TTS);
+    /* XCD-aware tiles: work-groups are dealt to the 8 XCDs round-robin by
+     * linear id, so the expert tiles of one token tile take ids that share
+     * id % 8 and read the token rows through one L2 (HBM reads x once) */
+    const int nex = (E + 16 * TES - 1) / (16 * TES), q = blockIdx.x >> 3;
+    const int ex = q % nex, ty = (q / nex) * 8 + (blockIdx.x & 7);
+    if (ty * 16 * TTS >= T) return;
+    const int e0 = ex * (16 * TES), t0 = ty * (16 * TTS);
     const int r = lane & 15, kq = (lane >> 4) * 8;
     const float *xr[TTS];
     bool stage[TTS];
@@ -315,7 +321,7 @@ __global__ __launch_bounds__(64 * NW) void k_route_approx(RouteArgs a) {
     for (int ts = 0; ts < TTS; ts++) {
         const int t = t0 + ts * 16 + r;
         xr[ts] = a.x + (size_t)min(t, T - 1) * H + kq;
-        stage[ts] = a.x16 && blockIdx.x == 0 && t < T;
+        stage[ts] = a.x16 && ex == 0 && t < T;
     }
     const _Float16 *wr[TES];
 #pragma unroll
@@ -415,7 +421,7 @@ __global__ __launch_bounds__(64 * NW) void k_route_approx(RouteArgs a) {
     }
     RSTAMP(4);
     RSTAMP(5);
-    if (blockIdx.y == 0 && wv == 0) RSTAMP_FLUSH(60000);
+    if (ty == 0 && wv == 0) RSTAMP_FLUSH(60000);
 }
 
 /* Pass 2: WPT waves per token (the lane layout of wave_topk).  Every wave of
@@ -898,10 +904,12 @@ int launch_pack_router(const float *W, int E, int H, _Float16 *W16, float *wscal
  * fewest bytes moved per logit). */
 int launch_route_approx(const RouteArgs &a, hipStream_t s) {
     if (!a.W16 || !a.wscale || a.H % 256 || a.T < 1) return -2;
+    /* 1-D grid: expert tiles x token tiles rounded up to 8 (see the kernel) */
+    auto grid = [&](int te, int tt) { return dim3((unsigned)((a.E + te - 1) / te * (((a.T + tt - 1) / tt + 7) / 8 * 8))); };
     if (a.T <= 1024)
-        hipLaunchKernelGGL((k_route_approx<1, 2, 8, 8>), dim3((a.E + 31) / 32, (a.T + 15) / 16), dim3(512), 0, s, a);
+        hipLaunchKernelGGL((k_route_approx<1, 2, 8, 8>), grid(32, 16), dim3(512), 0, s, a);
     else
-        hipLaunchKernelGGL((k_route_approx<2, 4, 4, 4>), dim3((a.E + 63) / 64, (a.T + 31) / 32), dim3(256), 0, s, a);
+        hipLaunchKernelGGL((k_route_approx<2, 4, 4, 4>), grid(64, 32), dim3(256), 0, s, a);
     return hipGetLastError() == hipSuccess ? 0 : -3;
 }
 
