@@ -586,23 +586,29 @@ __global__ __launch_bounds__(256) void k_topk_exact(RouteArgs a) {
 #define DSP_WORDS (DSP_TOK / 32)
 #define DSP_THREADS 1024
 
-DEV void dispatch_masks(const RouteArgs &a, uint32_t *mask, int ek[OROME_MAXK]) {
+template <int KM>
+DEV void dispatch_masks(const RouteArgs &a, uint32_t *mask, int (&ek)[KM]) {
     const int E = a.E, K = a.K, tid = threadIdx.x, t = blockIdx.x * DSP_TOK + tid;
+    /* the token's ids loaded together (indices clamped; a load under a
+     * branch is waited for alone); -1 marks no pair */
+#pragma unroll
+    for (int k = 0; k < KM; k++) ek[k] = a.idx[min(t, a.T - 1) * K + min(k, K - 1)];
     for (int i = tid; i < E * DSP_WORDS; i += DSP_TOK) mask[i] = 0;
 #pragma unroll
-    for (int k = 0; k < OROME_MAXK; k++)
-        if (k < K) ek[k] = t < a.T ? a.idx[t * K + k] : -1;
+    for (int k = 0; k < KM; k++)
+        if (k >= K || t >= a.T) ek[k] = -1;
     __syncthreads();
 #pragma unroll
-    for (int k = 0; k < OROME_MAXK; k++)
-        if (k < K && ek[k] >= 0) atomicOr(&mask[ek[k] * DSP_WORDS + (tid >> 5)], 1u << (tid & 31));
+    for (int k = 0; k < KM; k++)
+        if (ek[k] >= 0) atomicOr(&mask[ek[k] * DSP_WORDS + (tid >> 5)], 1u << (tid & 31));
     __syncthreads();
 }
 
+template <int KM>
 __global__ __launch_bounds__(DSP_TOK) void k_dispatch_count(RouteArgs a, uint32_t *cnt) {
     extern __shared__ uint32_t mask[]; /* E * DSP_WORDS */
-    int ek[OROME_MAXK];
-    dispatch_masks(a, mask, ek);
+    int ek[KM];
+    dispatch_masks<KM>(a, mask, ek);
     for (int e = threadIdx.x; e < a.E; e += DSP_TOK) {
         uint32_t c = 0;
 #pragma unroll
@@ -680,11 +686,19 @@ __global__ __launch_bounds__(DSP_THREADS) void k_dispatch_scan(RouteArgs a, uint
         tbg[DSP_THREADS];
     const int E = a.E, T = a.T, tid = threadIdx.x;
     if (tid < E) {
+        /* counts 16 blocks at a time, all loaded before the prefixes are
+         * stored (a load behind a store waits for it) */
         uint32_t run = 0;
-        for (int g = 0; g < G; g++) {
-            const uint32_t c = cnt[(size_t)g * E + tid];
-            cnt[(size_t)g * E + tid] = run;
-            run += c;
+        for (int g0 = 0; g0 < G; g0 += 16) {
+            uint32_t c[16];
+#pragma unroll
+            for (int j = 0; j < 16; j++) c[j] = cnt[(size_t)min(g0 + j, G - 1) * E + tid];
+#pragma unroll
+            for (int j = 0; j < 16; j++)
+                if (g0 + j < G) {
+                    cnt[(size_t)(g0 + j) * E + tid] = run;
+                    run += c[j];
+                }
         }
         hist[tid] = run;
         offs[tid] = run;
@@ -696,11 +710,12 @@ __global__ __launch_bounds__(DSP_THREADS) void k_dispatch_scan(RouteArgs a, uint
     dispatch_lists(a, hist, offs, arank, ts, tbg, tiles_s, tiles_b, has_shared);
 }
 
+template <int KM>
 __global__ __launch_bounds__(DSP_TOK) void k_dispatch_scatter(RouteArgs a, const uint32_t *base) {
     extern __shared__ uint32_t mask[]; /* E * DSP_WORDS, then E * DSP_WORDS word prefixes */
     uint32_t *wpre = mask + a.E * DSP_WORDS;
-    int ek[OROME_MAXK];
-    dispatch_masks(a, mask, ek);
+    int ek[KM];
+    dispatch_masks<KM>(a, mask, ek);
     const int E = a.E, K = a.K, tid = threadIdx.x, t = blockIdx.x * DSP_TOK + tid;
     for (int e = tid; e < E; e += DSP_TOK) {
         uint32_t run = a.offsets[e] + base[(size_t)blockIdx.x * E + e];
@@ -713,8 +728,8 @@ __global__ __launch_bounds__(DSP_TOK) void k_dispatch_scatter(RouteArgs a, const
     __syncthreads();
     const uint32_t below = (1u << (tid & 31)) - 1u;
 #pragma unroll
-    for (int k = 0; k < OROME_MAXK; k++)
-        if (k < K && ek[k] >= 0) {
+    for (int k = 0; k < KM; k++)
+        if (ek[k] >= 0) {
             const int i = ek[k] * DSP_WORDS + (tid >> 5);
             const uint32_t pos = wpre[i] + __popc(mask[i] & below);
             const uint32_t p = (uint32_t)(t * K + k);
@@ -958,9 +973,11 @@ int launch_dispatch(const RouteArgs &a, uint32_t *tiles_s, uint32_t *tiles_b, in
         return hipGetLastError() == hipSuccess ? 0 : -3;
     }
     const int G = dispatch_blocks(a.T);
-    hipLaunchKernelGGL(k_dispatch_count, dim3(G), dim3(DSP_TOK), lds / 2, s, a, cnt);
+    if (a.K <= 8) hipLaunchKernelGGL(k_dispatch_count<8>, dim3(G), dim3(DSP_TOK), lds / 2, s, a, cnt);
+    else hipLaunchKernelGGL(k_dispatch_count<OROME_MAXK>, dim3(G), dim3(DSP_TOK), lds / 2, s, a, cnt);
     hipLaunchKernelGGL(k_dispatch_scan, dim3(1), dim3(DSP_THREADS), 0, s, a, cnt, G, tiles_s, tiles_b, has_shared);
-    hipLaunchKernelGGL(k_dispatch_scatter, dim3(G), dim3(DSP_TOK), lds, s, a, (const uint32_t *)cnt);
+    if (a.K <= 8) hipLaunchKernelGGL(k_dispatch_scatter<8>, dim3(G), dim3(DSP_TOK), lds, s, a, (const uint32_t *)cnt);
+    else hipLaunchKernelGGL(k_dispatch_scatter<OROME_MAXK>, dim3(G), dim3(DSP_TOK), lds, s, a, (const uint32_t *)cnt);
     return hipGetLastError() == hipSuccess ? 0 : -3;
 }
 
