@@ -59,6 +59,8 @@ def main():
     ap.add_argument("--steps", type=int, default=None)
     ap.add_argument("--warmup", type=int, default=None)
     ap.add_argument("--config", default="0", choices=sorted(CONFIGS))
+    ap.add_argument("--path", default="auto", choices=["auto", "gemv", "mfma"],
+                    help="kernel path (auto: GEMV up to 8 tokens, grouped MFMA GEMMs above)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
@@ -95,8 +97,11 @@ def main():
     print("[bench] config %s (%s): %d synthetic layers, T=%d" % (args.config, cf["name"], L, T),
           file=sys.stderr, flush=True)
     img = orome_amd.synth_gguf(spec)
-    gm = orome_amd.MoEModel(image=img, max_tokens=max(T, 16), pack=T > 8)
+    mfma = args.path == "mfma" or (args.path == "auto" and T > 8)
+    gm = orome_amd.MoEModel(image=img, max_tokens=max(T, 16), pack=mfma)
     ctx = gm.ctx
+    if args.path != "auto":
+        ctx.set_path(_lib.OROME_PATH_MFMA if mfma else _lib.OROME_PATH_GEMV)
     stack = cf["mode"] == "stack"
     xs_h = [orome_amd.synth_normal(77, i, T * H).reshape(T, H) for i in range(NX)]
     hs_h = [orome_amd.synth_normal(78, i, T * H).reshape(T, H) for i in range(NX)]
@@ -272,6 +277,7 @@ def main():
         "data": "synthetic seeded GGUF per BASELINE config %s (%d layers, %d input batches)"
                 % (args.config, L, NX),
         "config": {"workload": cf["name"], "baseline_config": args.config, "tokens_per_step": T,
+                   "kernel_path": "mfma" if mfma else "gemv",
                    "layers_per_step": nl, "hidden": H, "experts": E, "top_k": K,
                    "expert_intermediate": M, "shared_intermediate": S, "parallelism": "single GPU"},
         "roofline": roof,
