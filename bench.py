@@ -60,7 +60,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=None)
     ap.add_argument("--config", default="0", choices=sorted(CONFIGS))
     ap.add_argument("--path", default="auto", choices=["auto", "gemv", "mfma"],
-                    help="kernel path (auto: GEMV up to 8 tokens, grouped MFMA GEMMs above)")
+                    help="kernel path (auto: GEMV up to 2 tokens, small-batch routing with the small-tile "
+                         "grouped GEMMs for 3..8, large-batch routing and grouped GEMMs above)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
@@ -97,11 +98,14 @@ def main():
     print("[bench] config %s (%s): %d synthetic layers, T=%d" % (args.config, cf["name"], L, T),
           file=sys.stderr, flush=True)
     img = orome_amd.synth_gguf(spec)
-    mfma = args.path == "mfma" or (args.path == "auto" and T > 8)
-    gm = orome_amd.MoEModel(image=img, max_tokens=max(T, 16), pack=mfma)
+    # the library's choice under "auto": GEMV kernels up to 2 tokens, the
+    # small-batch routing with the small-tile grouped GEMMs for 3..8, the
+    # large-batch routing and grouped GEMMs above
+    kpath = args.path if args.path != "auto" else ("gemv" if T <= 2 else "small_batch_gemm" if T <= 8 else "mfma")
+    gm = orome_amd.MoEModel(image=img, max_tokens=max(T, 16), pack=kpath != "gemv")
     ctx = gm.ctx
     if args.path != "auto":
-        ctx.set_path(_lib.OROME_PATH_MFMA if mfma else _lib.OROME_PATH_GEMV)
+        ctx.set_path(_lib.OROME_PATH_MFMA if kpath == "mfma" else _lib.OROME_PATH_GEMV)
     stack = cf["mode"] == "stack"
     xs_h = [orome_amd.synth_normal(77, i, T * H).reshape(T, H) for i in range(NX)]
     hs_h = [orome_amd.synth_normal(78, i, T * H).reshape(T, H) for i in range(NX)]
@@ -208,7 +212,7 @@ def main():
     n_q6 = sum(1 for l in range(L) if cf["spec"].get("q6k_every") and l % 4 == 3) if stack else 0
     down_e = q6k_bytes(H, M) if cf["spec"].get("down") == Q6K else q4k_bytes(H, M)
     rows = T * K + T  # routed pairs plus shared-expert rows
-    gu_bytes = (u_mean + 1) * 2 * q4k_bytes(M, H) + T * H * (4 if T <= 8 else 2) + rows * M * 2
+    gu_bytes = (u_mean + 1) * 2 * q4k_bytes(M, H) + T * H * (4 if kpath == "gemv" else 2) + rows * M * 2
     gu_flops = 2.0 * 2 * rows * M * H
     layer_bytes = (u_mean * (2 * q4k_bytes(M, H) + down_e) + 3 * q4k_bytes(S, H) + E * H * 4 + H * 4
                    + T * H * 4 * 3)
@@ -224,7 +228,7 @@ def main():
         roof = {"bound": "mfma", "kernel": "gemm_gate_up", "achieved": round(gu_tflops, 2),
                 "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(gu_tflops / MFMA_F16_PEAK_TFLOPS, 4)}
     else:
-        roof = {"bound": "hbm", "kernel": "gemv_gate_up" if T <= 8 else "gemm_gate_up",
+        roof = {"bound": "hbm", "kernel": "gemv_gate_up" if kpath == "gemv" else "gemm_gate_up",
                 "achieved": round(gu_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(gu_gbs / HBM_PEAK_GBS, 4)}
     traffic = None
@@ -277,7 +281,7 @@ def main():
         "data": "synthetic seeded GGUF per BASELINE config %s (%d layers, %d input batches)"
                 % (args.config, L, NX),
         "config": {"workload": cf["name"], "baseline_config": args.config, "tokens_per_step": T,
-                   "kernel_path": "mfma" if mfma else "gemv",
+                   "kernel_path": kpath,
                    "layers_per_step": nl, "hidden": H, "experts": E, "top_k": K,
                    "expert_intermediate": M, "shared_intermediate": S, "parallelism": "single GPU"},
         "roofline": roof,

@@ -259,6 +259,32 @@ static int kfmt(QuantFormat f) {
 
 /* ------------------------------------------------- tile-major repacking */
 
+/* The grouped GEMMs' view of a layer: registered layers read their
+ * tile-major copies. */
+static const Pack *find_pack(const orome_hip_ctx *c, const uint8_t *gate, const uint8_t *sh_gate);
+static void apply_pack(const orome_hip_ctx *c, int S, ExpertSide &exm, SharedSide &shm) {
+    const Pack *pk = find_pack(c, exm.gate, shm.gate);
+    if (!pk) return;
+    exm.gate = pk->gate;
+    exm.up = pk->up;
+    exm.gate_stride = exm.up_stride = pk->gate_stride;
+    exm.gate_fmt = GEMM_FMT_Q4K_TILED;
+    if (S) {
+        shm.gate = pk->sgate;
+        shm.up = pk->sup;
+        shm.gate_fmt = GEMM_FMT_Q4K_TILED;
+    }
+    if (pk->down) {
+        exm.down = pk->down;
+        exm.down_stride = pk->down_stride;
+        exm.down_fmt = pk->down_fmt;
+        if (S) {
+            shm.down = pk->sdown;
+            shm.down_fmt = pk->sdown_fmt;
+        }
+    }
+}
+
 /* OROME_ROUTE_EXACT=1 keeps the one-pass canonical router on registered
  * layers too (the two routers select identically; this is for comparing them). */
 static bool route_exact_only() {
@@ -469,8 +495,16 @@ static int forward_impl(orome_hip_ctx *c, const ModelConfig *cfg, const ExpertLa
     a.norm_h = NULL; a.norm_w = NULL; a.norm_eps = cfg->rms_norm_eps; a.xnorm = c->xnorm;
     a.x16 = NULL;
     a.W16 = NULL; a.wscale = NULL; a.wnorm = NULL; a.eps_c1 = a.eps_c2 = 0.0f;
+    a.tiles_s = NULL; a.has_shared = 0;
 
     int path = c->path;
+    /* AUTO: GEMV kernels up to 2 tokens (routing folded into gate/up), the
+     * small-batch routing with the grouped GEMMs for 3..8, the large-batch
+     * routing and grouped GEMMs above */
+    ExpertSide hx = ex;
+    SharedSide hs = sh;
+    apply_pack(c, S, hx, hs);
+    const bool hybrid = path == OROME_PATH_AUTO && T >= 3 && T <= 8 && gemm_small_tiles_ok(hx, hs, H, M);
     if (path == OROME_PATH_AUTO) path = T <= 8 ? OROME_PATH_GEMV : OROME_PATH_MFMA;
     hipStream_t s = c->stream;
     if (norm_h) {
@@ -485,11 +519,34 @@ static int forward_impl(orome_hip_ctx *c, const ModelConfig *cfg, const ExpertLa
     }
     if (path == OROME_PATH_GEMV) {
         if (T > 8) return orome_fail(OROME_EUNSUPPORTED, "GEMV path handles T <= 8 (T=%d)", T);
+        if (hybrid) { /* the router stages x16 and the dispatch writes the small-tile list */
+            a.x16 = c->x16;
+            a.tiles_s = c->tiles;
+            a.has_shared = S ? 1 : 0;
+        }
         TLAUNCH(c, ST_ROUTE, launch_route_small(a, s), "router logits");
         /* one or two tokens: every gate/up block selects the experts itself
          * (saves a launch); larger batches route once in a separate kernel */
         const int fold = T <= 2;
         if (!fold) TLAUNCH(c, ST_TOPK, launch_topk_dispatch_small(a, s), "top-k + dispatch");
+        if (hybrid) {
+            /* every expert holds at most 8 rows: the small-tile grouped GEMMs
+             * alone, then the combine */
+            const int ns_max = E + (S ? 1 : 0);
+            TLAUNCH(c, ST_GATE_UP,
+                    launch_gemm_gate_up(hx, hs, c->x16, c->tmax, T, H, M, K, E, GEMM_TILE_SMALL, c->tiles, ns_max,
+                                        c->pairs, c->act, c->act_sh, s, c->kt, c->kt_blocks),
+                    "grouped gate/up (small tiles)");
+            TLAUNCH(c, ST_DOWN,
+                    launch_gemm_down(hx, hs, c->act, c->act_sh, c->tmax * c->kmax, c->tmax, T, H, M, K, E,
+                                     GEMM_TILE_SMALL, c->tiles, ns_max, c->y, c->ysh, s),
+                    "grouped down (small tiles)");
+            TLAUNCH(c, ST_COMBINE, launch_combine(c->y, c->ysh, c->pos, c->w, c->sgl, S ? 1 : 0, h_in, h_out, T, H, K, s),
+                    "combine");
+            c->last_T = T;
+            c->last_K = K;
+            return OROME_OK;
+        }
         TLAUNCH(c, ST_GATE_UP, launch_gemv_gate_up(ex, sh, a, fold, x, T, H, M, K, E, c->act, c->act_sh, s, c->kt, c->kt_blocks),
                 "gemv gate/up");
         /* one token: down and combine in one kernel when the shape allows */
@@ -530,26 +587,7 @@ static int forward_impl(orome_hip_ctx *c, const ModelConfig *cfg, const ExpertLa
         /* registered layers: the grouped GEMMs read the tile-major copies */
         ExpertSide exm = ex;
         SharedSide shm = sh;
-        if (const Pack *pk = find_pack(c, ex.gate, sh.gate)) {
-            exm.gate = pk->gate;
-            exm.up = pk->up;
-            exm.gate_stride = exm.up_stride = pk->gate_stride;
-            exm.gate_fmt = GEMM_FMT_Q4K_TILED;
-            if (S) {
-                shm.gate = pk->sgate;
-                shm.up = pk->sup;
-                shm.gate_fmt = GEMM_FMT_Q4K_TILED;
-            }
-            if (pk->down) {
-                exm.down = pk->down;
-                exm.down_stride = pk->down_stride;
-                exm.down_fmt = pk->down_fmt;
-                if (S) {
-                    shm.down = pk->sdown;
-                    shm.down_fmt = pk->sdown_fmt;
-                }
-            }
-        }
+        apply_pack(c, S, exm, shm);
         auto gate_up = [&](int tm, hipStream_t st) {
             return tm == GEMM_TILE_SMALL
                        ? launch_gemm_gate_up(exm, shm, c->x16, c->tmax, T, H, M, K, E, tm, c->tiles, ns_max, c->pairs, c->act,

@@ -42,6 +42,10 @@ struct RouteArgs {
     const _Float16 *W16;
     const float *wscale, *wnorm;
     float eps_c1, eps_c2;
+    /* small-batch dispatch feeding the grouped GEMMs: also write the small
+     * tile list (one tile per active expert, then the shared expert's) */
+    uint32_t *tiles_s;
+    int has_shared;
 };
 
 struct ExpertSide {
@@ -60,6 +64,8 @@ int launch_route_small(const RouteArgs &a, hipStream_t s);
 int launch_route_logits(const RouteArgs &a, hipStream_t s);
 int launch_topk(const RouteArgs &a, hipStream_t s);
 int launch_route_approx(const RouteArgs &a, hipStream_t s);
+/* whether the small-tile grouped GEMMs take these shapes and formats */
+int gemm_small_tiles_ok(const ExpertSide &ex, const SharedSide &sh, int H, int M);
 int launch_topk_exact(const RouteArgs &a, hipStream_t s);
 int launch_pack_router(const float *W, int E, int H, _Float16 *W16, float *wscale, float *wnorm, hipStream_t s);
 void route_eps_coeffs(int H, float *c1, float *c2);

@@ -834,16 +834,41 @@ static unsigned persist_blocks() {
 }
 
 /* ------------------------------------------------------------ launch */
-int launch_gemm_gate_up(const ExpertSide &ex, const SharedSide &sh, const _Float16 *x16, int zrow, int T,
-                        int H, int M, int K, int E, int tile_m, const uint32_t *tiles, int n_tiles_max,
-                        const uint32_t *pairs, _Float16 *act, _Float16 *act_sh, hipStream_t s,
-                        unsigned long long *kt, int kt_cap) {
+/* Shapes and formats the launchers take (0) or decline (-2). */
+static int gate_up_shape(const ExpertSide &ex, const SharedSide &sh, int H, int M, int tile_m) {
     const int W = tile_m == GEMM_TILE_SMALL ? Shape<GEMM_TILE_SMALL / 16>::W : Shape<GEMM_TILE_BIG / 16>::W;
     const int NB = W * 16 * GU_RPW;
     if ((H / KC * GU_RPW) % 4) return -2; /* every ring depth used divides the unit count */
     if (H % KCH || M % NB || (sh.gate && sh.S % NB) || (ex.gate_fmt != FQ4K && ex.gate_fmt != FQ4KT)) return -2;
     const bool tiled = ex.gate_fmt == FQ4KT;
     if (sh.gate && (tiled ? sh.gate_fmt != FQ4KT : sh.gate_fmt != FQ4K && sh.gate_fmt != FQ8)) return -2;
+    return 0;
+}
+static int down_shape(const ExpertSide &ex, const SharedSide &sh, int H, int M, int tile_m) {
+    const int W = tile_m == GEMM_TILE_SMALL ? Shape<GEMM_TILE_SMALL / 16>::W : Shape<GEMM_TILE_BIG / 16>::W;
+    const int NB = W * 16 * DN_RPW;
+    if ((M / KC * DN_RPW) % 4 || (sh.gate && (sh.S / KC * DN_RPW) % 4)) return -2;
+    /* all of a tile's activations stay resident: in_dim <= 2 chunks */
+    if (H % NB || M % KCH || M > 2 * KCH || (sh.gate && (sh.S % KCH || sh.S > 2 * KCH))) return -2;
+    const bool dtiled = ex.down_fmt == FQ4KT || ex.down_fmt == FQ6KT;
+    if (ex.down_fmt != FQ4K && ex.down_fmt != FQ6K && !dtiled) return -2;
+    /* a tile-major routed down needs a tile-major shared down (or none) */
+    const int sf = sh.gate ? sh.down_fmt : dtiled ? ex.down_fmt : FQ4K;
+    if (dtiled ? sf != FQ4KT && sf != FQ6KT : sf != FQ4K && sf != FQ6K && sf != FQ8) return -2;
+    return 0;
+}
+int gemm_small_tiles_ok(const ExpertSide &ex, const SharedSide &sh, int H, int M) {
+    return !gate_up_shape(ex, sh, H, M, GEMM_TILE_SMALL) && !down_shape(ex, sh, H, M, GEMM_TILE_SMALL);
+}
+
+int launch_gemm_gate_up(const ExpertSide &ex, const SharedSide &sh, const _Float16 *x16, int zrow, int T,
+                        int H, int M, int K, int E, int tile_m, const uint32_t *tiles, int n_tiles_max,
+                        const uint32_t *pairs, _Float16 *act, _Float16 *act_sh, hipStream_t s,
+                        unsigned long long *kt, int kt_cap) {
+    if (gate_up_shape(ex, sh, H, M, tile_m)) return -2;
+    const int W = tile_m == GEMM_TILE_SMALL ? Shape<GEMM_TILE_SMALL / 16>::W : Shape<GEMM_TILE_BIG / 16>::W;
+    const int NB = W * 16 * GU_RPW;
+    const bool tiled = ex.gate_fmt == FQ4KT;
     GemmArgs a = {};
     a.wa = ex.gate; a.wb = ex.up; a.stride_a = ex.gate_stride; a.stride_b = ex.up_stride;
     a.sh_a = sh.gate; a.sh_b = sh.up;
@@ -887,16 +912,11 @@ int launch_gemm_gate_up(const ExpertSide &ex, const SharedSide &sh, const _Float
 int launch_gemm_down(const ExpertSide &ex, const SharedSide &sh, const _Float16 *act,
                      const _Float16 *act_sh, int zrow, int zrow_sh, int T, int H, int M, int K, int E, int tile_m,
                      const uint32_t *tiles, int n_tiles_max, float *y, float *ysh, hipStream_t s) {
+    if (down_shape(ex, sh, H, M, tile_m)) return -2;
     const int W = tile_m == GEMM_TILE_SMALL ? Shape<GEMM_TILE_SMALL / 16>::W : Shape<GEMM_TILE_BIG / 16>::W;
     const int NB = W * 16 * DN_RPW;
-    if ((M / KC * DN_RPW) % 4 || (sh.gate && (sh.S / KC * DN_RPW) % 4)) return -2;
-    /* all of a tile's activations stay resident: in_dim <= 2 chunks */
-    if (H % NB || M % KCH || M > 2 * KCH || (sh.gate && (sh.S % KCH || sh.S > 2 * KCH))) return -2;
     const bool dtiled = ex.down_fmt == FQ4KT || ex.down_fmt == FQ6KT;
-    if (ex.down_fmt != FQ4K && ex.down_fmt != FQ6K && !dtiled) return -2;
-    /* a tile-major routed down needs a tile-major shared down (or none) */
     const int sf = sh.gate ? sh.down_fmt : dtiled ? ex.down_fmt : FQ4K;
-    if (dtiled ? sf != FQ4KT && sf != FQ6KT : sf != FQ4K && sf != FQ6K && sf != FQ8) return -2;
     GemmArgs a = {};
     a.wa = ex.down; a.stride_a = ex.down_stride;
     a.sh_a = sh.gate ? sh.down : nullptr;

@@ -34,6 +34,8 @@ extern "C" __attribute__((visibility("default"))) int orome_trace_fetch_route(un
  * under a branch is waited for alone.  A NULL wrow gives zeros. */
 template <int TMAX, int NIM, bool NORM>
 DEV void canon_dots(const float *wrow, const RouteArgs &a, int lane, bool write_x, float *acc) {
+    /* write_x also stages fp16(x) into a.x16 when set (round to nearest
+     * even, each 4-group stored (0,2,1,3), the grouped GEMMs' layout) */
     constexpr int TC = TMAX < 4 ? TMAX : 4;
     const int NI = a.H / 256, H = a.H, T = a.T;
     const float *xs = NORM ? a.norm_h : a.x;
@@ -95,6 +97,9 @@ DEV void canon_dots(const float *wrow, const RouteArgs &a, int lane, bool write_
                                (x.w * scale) * nw[i].w};
                         if (write_x) *(f4 *)(a.xnorm + (size_t)t * H + 256 * i + 4 * lane) = x;
                     }
+                    if (write_x && a.x16)
+                        *(h4 *)(a.x16 + (size_t)t * H + 256 * i + 4 * lane) =
+                            h4{(_Float16)x.x, (_Float16)x.z, (_Float16)x.y, (_Float16)x.w};
                     d = __builtin_fmaf(wv[i].x, x.x, d);
                     d = __builtin_fmaf(wv[i].y, x.y, d);
                     d = __builtin_fmaf(wv[i].z, x.z, d);
@@ -116,7 +121,7 @@ __global__ __launch_bounds__(256) void k_route_small(RouteArgs a) {
     if (row > E) return;
     const float *wr = row < E ? a.W + (size_t)row * H : a.wsg;
     float acc[TMAX];
-    canon_dots<TMAX, NIM, NORM>(wr, a, lane, NORM && row == 0, acc);
+    canon_dots<TMAX, NIM, NORM>(wr, a, lane, (NORM || a.x16) && row == 0, acc);
     if (lane == 0) {
 #pragma unroll
         for (int t = 0; t < TMAX; t++)

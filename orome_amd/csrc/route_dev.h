@@ -192,6 +192,11 @@ DEV void topk_dispatch_block(const RouteArgs &a) {
             if (cnt[j]) {
                 ACT_E(a.list, rank) = (uint32_t)e;
                 ACT_OFF(a.list, E, rank) = off;
+                if (a.tiles_s) { /* T <= 16 rows: one small tile */
+                    a.tiles_s[1 + 3 * rank] = (uint32_t)e;
+                    a.tiles_s[2 + 3 * rank] = off;
+                    a.tiles_s[3 + 3 * rank] = cnt[j];
+                }
                 rank++;
             }
             off += cnt[j];
@@ -202,6 +207,14 @@ DEV void topk_dispatch_block(const RouteArgs &a) {
         a.offsets[E] = (uint32_t)NP;
         ACT_N(a.list) = n;
         ACT_OFF(a.list, E, n) = (uint32_t)NP;
+        if (a.tiles_s) {
+            if (a.has_shared) {
+                a.tiles_s[1 + 3 * n] = (uint32_t)E;
+                a.tiles_s[2 + 3 * n] = 0u;
+                a.tiles_s[3 + 3 * n] = (uint32_t)T;
+            }
+            a.tiles_s[0] = n + (a.has_shared ? 1u : 0u);
+        }
     }
     __syncthreads();
     if (tid < NP) {
