@@ -112,9 +112,9 @@ class MoEModel:
     """A GGUF MoE model resident in HBM (all layers), ready for forward calls."""
 
     def __init__(self, image=None, path=None, max_tokens=16, device=0, pack=None):
-        """pack: register every layer's tile-major Q4_K copies for the MFMA
-        path (orome_hip_pack_layer); default when max_tokens > 8, the sizes
-        that take that path."""
+        """pack: register every layer's tile-major Q4_K copies for the grouped
+        GEMMs (orome_hip_pack_layer); default when max_tokens > 2, the batch
+        sizes that use those GEMMs."""
         if (image is None) == (path is None):
             raise ValueError("give exactly one of image or path")
         self._image = image  # keep the host image alive while parsed
@@ -138,7 +138,7 @@ class MoEModel:
         if not self._cache:
             raise _lib.OromeError("build_tensor_cache_gguf failed")
         self.caches = C.cast(self._cache, C.POINTER(_lib.LayerTensorCache * L)).contents
-        if pack if pack is not None else max_tokens > 8:
+        if pack if pack is not None else max_tokens > 2:
             self.pack_layers()
 
     def pack_layers(self):
