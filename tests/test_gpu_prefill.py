@@ -90,13 +90,19 @@ def test_prefill_variants(kw, T):
 
 def test_prefill_matches_decode_path(base):
     """The GEMV and MFMA paths agree on the same 8 tokens (both within the
-    tolerance of the oracle; fp16 weight tiles vs exact fp32 weights)."""
-    banner("mfma vs gemv, T=8")
+    tolerance of the oracle; fp16 weight tiles vs exact fp32 weights), and
+    the AUTO path at 8 tokens (small-batch routing feeding the small-tile
+    grouped GEMMs) equals the MFMA path bit for bit: same tiles, same fp16
+    activations, same GEMM kernels."""
+    banner("mfma vs gemv vs auto, T=8")
     x, h = base.inputs(8, seed=8)
     a, da = base.run(0, x, h, path=_lib.OROME_PATH_GEMV)
     b, db = base.run(0, x, h, path=_lib.OROME_PATH_MFMA)
+    c, dc = base.run(0, x, h, path=_lib.OROME_PATH_AUTO)
     assert np.array_equal(da["idx"], db["idx"]) and np.array_equal(da["pairs"], db["pairs"])
+    assert np.array_equal(dc["idx"], db["idx"]) and np.array_equal(dc["pairs"], db["pairs"])
     assert rel_l2(b - h, a - h) < TOL
+    assert np.array_equal(c, b), "small-batch grouped GEMMs vs MFMA path"
 
 
 def test_persistent_gemm_bit_identical(base, monkeypatch):
