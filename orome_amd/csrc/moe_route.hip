@@ -33,12 +33,13 @@ extern "C" __attribute__((visibility("default"))) int orome_trace_fetch_route(un
  * unconditional (indices clamped, values past T or H unused), since a load
  * under a branch is waited for alone.  A NULL wrow gives zeros. */
 template <int TMAX, int NIM, bool NORM>
-DEV void canon_dots(const float *wrow, const RouteArgs &a, int lane, bool write_x, float *acc) {
+DEV void canon_dots(const float *wrow, const RouteArgs &a, int lane, bool write_x, float *acc, int tb = 0) {
+    /* tokens tb .. tb + TMAX - 1 (acc[t - tb]) */
     /* write_x also stages fp16(x) into a.x16 when set (round to nearest
      * even, each 4-group stored (0,2,1,3), the grouped GEMMs' layout) */
     constexpr int TC = TMAX < 4 ? TMAX : 4;
-    const int NI = a.H / 256, H = a.H, T = a.T;
-    const float *xs = NORM ? a.norm_h : a.x;
+    const int NI = a.H / 256, H = a.H, T = a.T - tb;
+    const float *xs = (NORM ? a.norm_h : a.x) + (size_t)tb * a.H;
     f4 wv[NIM], nw[NIM];
 #pragma unroll
     for (int i = 0; i < NIM; i++) {
@@ -95,10 +96,10 @@ DEV void canon_dots(const float *wrow, const RouteArgs &a, int lane, bool write_
                     if (NORM) {
                         x = f4{(x.x * scale) * nw[i].x, (x.y * scale) * nw[i].y, (x.z * scale) * nw[i].z,
                                (x.w * scale) * nw[i].w};
-                        if (write_x) *(f4 *)(a.xnorm + (size_t)t * H + 256 * i + 4 * lane) = x;
+                        if (write_x) *(f4 *)(a.xnorm + (size_t)(tb + t) * H + 256 * i + 4 * lane) = x;
                     }
                     if (write_x && a.x16)
-                        *(h4 *)(a.x16 + (size_t)t * H + 256 * i + 4 * lane) =
+                        *(h4 *)(a.x16 + (size_t)(tb + t) * H + 256 * i + 4 * lane) =
                             h4{(_Float16)x.x, (_Float16)x.z, (_Float16)x.y, (_Float16)x.w};
                     d = __builtin_fmaf(wv[i].x, x.x, d);
                     d = __builtin_fmaf(wv[i].y, x.y, d);
@@ -113,19 +114,22 @@ DEV void canon_dots(const float *wrow, const RouteArgs &a, int lane, bool write_
 /* Small-batch router logits (T <= 16): every wave computes one router row
  * (or the shared-gate row) for all tokens; with NORM, x is RMSNorm(norm_h)
  * and the row-0 wave also writes it out. */
-template <bool NORM, int TMAX, int NIM>
+/* RS waves per row: wave h of a row takes tokens h TMAX .. h TMAX + TMAX - 1
+ * (5..8 tokens: two waves of 4 instead of one wave with two dependent
+ * 4-token chunks). */
+template <bool NORM, int TMAX, int NIM, int RS>
 __global__ __launch_bounds__(256) void k_route_small(RouteArgs a) {
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-    const int row = blockIdx.x * 4 + wv;
+    const int row = blockIdx.x * (4 / RS) + wv / RS, tb = (wv % RS) * TMAX;
     const int E = a.E, H = a.H, T = a.T;
-    if (row > E) return;
+    if (row > E || tb >= T) return;
     const float *wr = row < E ? a.W + (size_t)row * H : a.wsg;
     float acc[TMAX];
-    canon_dots<TMAX, NIM, NORM>(wr, a, lane, (NORM || a.x16) && row == 0, acc);
+    canon_dots<TMAX, NIM, NORM>(wr, a, lane, (NORM || a.x16) && row == 0, acc, tb);
     if (lane == 0) {
 #pragma unroll
         for (int t = 0; t < TMAX; t++)
-            if (t < T) a.logits[(size_t)t * (E + 1) + row] = acc[t];
+            if (tb + t < T) a.logits[(size_t)(tb + t) * (E + 1) + row] = acc[t];
     }
 }
 
@@ -866,18 +870,18 @@ static int epl_for(int E) {
 
 int launch_route_small(const RouteArgs &a, hipStream_t s) {
     if (a.T < 1 || a.T > 16 || a.T * a.K > 256 || a.H % 256 || a.H > 4096) return -2;
-    const dim3 g((a.E + 1 + 3) / 4);
-#define RS_LAUNCH(TM, NIMV)                                                                        \
-    do {                                                                                           \
-        if (a.norm_h) hipLaunchKernelGGL((k_route_small<true, TM, NIMV>), g, dim3(256), 0, s, a);  \
-        else hipLaunchKernelGGL((k_route_small<false, TM, NIMV>), g, dim3(256), 0, s, a);          \
+    const dim3 g((a.E + 1 + 3) / 4), g2((a.E + 1 + 1) / 2);
+#define RS_LAUNCH(TM, NIMV, RSV, G)                                                                      \
+    do {                                                                                                 \
+        if (a.norm_h) hipLaunchKernelGGL((k_route_small<true, TM, NIMV, RSV>), G, dim3(256), 0, s, a);  \
+        else hipLaunchKernelGGL((k_route_small<false, TM, NIMV, RSV>), G, dim3(256), 0, s, a);          \
     } while (0)
-#define RS_T(NIMV)                          \
-    do {                                    \
-        if (a.T == 1) RS_LAUNCH(1, NIMV);   \
-        else if (a.T <= 4) RS_LAUNCH(4, NIMV); \
-        else if (a.T <= 8) RS_LAUNCH(8, NIMV); \
-        else RS_LAUNCH(16, NIMV);           \
+#define RS_T(NIMV)                                \
+    do {                                          \
+        if (a.T == 1) RS_LAUNCH(1, NIMV, 1, g);   \
+        else if (a.T <= 4) RS_LAUNCH(4, NIMV, 1, g); \
+        else if (a.T <= 8) RS_LAUNCH(4, NIMV, 2, g2); \
+        else RS_LAUNCH(16, NIMV, 1, g);           \
     } while (0)
     if (a.H <= 256 * 8) RS_T(8);
     else RS_T(CANON_NI);
