@@ -191,10 +191,12 @@ def test_dequant_bit_exact(fmt_name, kw):
     p.gm.close()
 
 
-def test_layer_forward_and_stack():
-    banner("layer/stack forward, 3 layers, mixed Q6_K down, T=2")
+@pytest.mark.parametrize("T", [2, 5])
+def test_layer_forward_and_stack(T):
+    """T=2: GEMV kernels; T=5: small-batch routing (RMSNorm in the router)
+    feeding the small-tile grouped GEMMs."""
+    banner("layer/stack forward, 3 layers, mixed Q6_K down, T=%d" % T)
     p = Pair(layers=3, q6k_every=2, seed=9, centered=True)
-    T = 2
     h0 = (orome_amd.synth_normal(9, 3, T * p.H) * 4).reshape(T, p.H)
     dh = DeviceBuffer.from_array(p.ctx, h0)
     h = h0.copy()
