@@ -61,7 +61,7 @@ def main():
     ap.add_argument("--config", default="0", choices=sorted(CONFIGS))
     ap.add_argument("--path", default="auto", choices=["auto", "gemv", "mfma"],
                     help="kernel path (auto: GEMV up to 2 tokens, small-batch routing with the small-tile "
-                         "grouped GEMMs for 3..8, large-batch routing and grouped GEMMs above)")
+                         "grouped GEMMs for 3..16, large-batch routing and grouped GEMMs above)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
@@ -99,9 +99,9 @@ def main():
           file=sys.stderr, flush=True)
     img = orome_amd.synth_gguf(spec)
     # the library's choice under "auto": GEMV kernels up to 2 tokens, the
-    # small-batch routing with the small-tile grouped GEMMs for 3..8, the
+    # small-batch routing with the small-tile grouped GEMMs for 3..16, the
     # large-batch routing and grouped GEMMs above
-    kpath = args.path if args.path != "auto" else ("gemv" if T <= 2 else "small_batch_gemm" if T <= 8 else "mfma")
+    kpath = args.path if args.path != "auto" else ("gemv" if T <= 2 else "small_batch_gemm" if T <= 16 else "mfma")
     gm = orome_amd.MoEModel(image=img, max_tokens=max(T, 16), pack=kpath != "gemv")
     ctx = gm.ctx
     if args.path != "auto":

@@ -172,8 +172,9 @@ const char *orome_last_error(void);
 
 /* Kernel path for orome_moe_forward.  AUTO: the GEMV kernels for 1-2 tokens
  * (routing folded into gate/up), the small-batch routing with the small-tile
- * grouped MFMA GEMMs for 3..8 tokens (the GEMV kernels where those GEMMs do
- * not take the shapes), the large-batch routing and grouped GEMMs above 8.
+ * grouped MFMA GEMMs for 3..16 tokens (T K <= 256; where those GEMMs do not
+ * take the shapes, the GEMV kernels up to 8 tokens and the MFMA path above),
+ * the large-batch routing and grouped GEMMs above 16.
  * GEMV and MFMA force one kernel family for every T (GEMV: T <= 8). */
 enum { OROME_PATH_AUTO = 0, OROME_PATH_GEMV = 1, OROME_PATH_MFMA = 2 };
 int orome_hip_set_path(orome_hip_ctx *ctx, int path);

@@ -499,13 +499,16 @@ static int forward_impl(orome_hip_ctx *c, const ModelConfig *cfg, const ExpertLa
 
     int path = c->path;
     /* AUTO: GEMV kernels up to 2 tokens (routing folded into gate/up), the
-     * small-batch routing with the grouped GEMMs for 3..8, the large-batch
-     * routing and grouped GEMMs above */
+     * small-batch routing with the small-tile grouped GEMMs for 3..16, the
+     * large-batch routing and grouped GEMMs above */
     ExpertSide hx = ex;
     SharedSide hs = sh;
     apply_pack(c, S, hx, hs);
-    const bool hybrid = path == OROME_PATH_AUTO && T >= 3 && T <= 8 && gemm_small_tiles_ok(hx, hs, H, M);
-    if (path == OROME_PATH_AUTO) path = T <= 8 ? OROME_PATH_GEMV : OROME_PATH_MFMA;
+    /* (up to 16 tokens: one 32-row small tile per expert, T K <= 256 for the
+     * small-batch dispatch) */
+    const bool hybrid = path == OROME_PATH_AUTO && T >= 3 && T <= 16 && T * K <= 256 &&
+                        gemm_small_tiles_ok(hx, hs, H, M);
+    if (path == OROME_PATH_AUTO) path = T <= 8 || hybrid ? OROME_PATH_GEMV : OROME_PATH_MFMA;
     hipStream_t s = c->stream;
     if (norm_h) {
         if (path == OROME_PATH_GEMV) { /* the router kernel normalises and writes xnorm */
@@ -518,7 +521,7 @@ static int forward_impl(orome_hip_ctx *c, const ModelConfig *cfg, const ExpertLa
         a.x = x;
     }
     if (path == OROME_PATH_GEMV) {
-        if (T > 8) return orome_fail(OROME_EUNSUPPORTED, "GEMV path handles T <= 8 (T=%d)", T);
+        if (T > 8 && !hybrid) return orome_fail(OROME_EUNSUPPORTED, "GEMV path handles T <= 8 (T=%d)", T);
         if (hybrid) { /* the router stages x16 and the dispatch writes the small-tile list */
             a.x16 = c->x16;
             a.tiles_s = c->tiles;
@@ -530,8 +533,8 @@ static int forward_impl(orome_hip_ctx *c, const ModelConfig *cfg, const ExpertLa
         const int fold = T <= 2;
         if (!fold) TLAUNCH(c, ST_TOPK, launch_topk_dispatch_small(a, s), "top-k + dispatch");
         if (hybrid) {
-            /* every expert holds at most 8 rows: the small-tile grouped GEMMs
-             * alone, then the combine */
+            /* every expert holds at most 16 rows: the small-tile grouped
+             * GEMMs alone, then the combine */
             const int ns_max = E + (S ? 1 : 0);
             TLAUNCH(c, ST_GATE_UP,
                     launch_gemm_gate_up(hx, hs, c->x16, c->tmax, T, H, M, K, E, GEMM_TILE_SMALL, c->tiles, ns_max,
@@ -659,7 +662,9 @@ extern "C" int orome_moe_stack_forward(orome_hip_ctx *c, const ModelConfig *cfg,
     if (set_dev(c)) return OROME_EHIP;
     /* on the MFMA path each layer's combine also computes the next layer's
      * RMSNorm (same bits as the separate norm kernel), which then is skipped */
-    const int path = c->path == OROME_PATH_AUTO ? (T <= 8 ? OROME_PATH_GEMV : OROME_PATH_MFMA) : c->path;
+    /* (AUTO takes the small-batch routing, with the norm in the router, up
+     * to 16 tokens) */
+    const int path = c->path == OROME_PATH_AUTO ? (T <= 16 ? OROME_PATH_GEMV : OROME_PATH_MFMA) : c->path;
     const bool fuse = path == OROME_PATH_MFMA && cfg->hidden_dim % 512 == 0 && cfg->hidden_dim <= 4096;
     auto norm_w = [&](int l) -> const float * {
         return lts[l].post_norm.buffer && lts[l].post_norm.format == QFMT_F32

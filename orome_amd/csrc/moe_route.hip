@@ -115,8 +115,8 @@ DEV void canon_dots(const float *wrow, const RouteArgs &a, int lane, bool write_
  * (or the shared-gate row) for all tokens; with NORM, x is RMSNorm(norm_h)
  * and the row-0 wave also writes it out. */
 /* RS waves per row: wave h of a row takes tokens h TMAX .. h TMAX + TMAX - 1
- * (5..8 tokens: two waves of 4 instead of one wave with two dependent
- * 4-token chunks). */
+ * (5..8 tokens: two waves of 4, 9..16: four, instead of one wave with
+ * dependent 4-token chunks). */
 template <bool NORM, int TMAX, int NIM, int RS>
 __global__ __launch_bounds__(256) void k_route_small(RouteArgs a) {
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
@@ -870,7 +870,7 @@ static int epl_for(int E) {
 
 int launch_route_small(const RouteArgs &a, hipStream_t s) {
     if (a.T < 1 || a.T > 16 || a.T * a.K > 256 || a.H % 256 || a.H > 4096) return -2;
-    const dim3 g((a.E + 1 + 3) / 4), g2((a.E + 1 + 1) / 2);
+    const dim3 g((a.E + 1 + 3) / 4), g2((a.E + 1 + 1) / 2), g4((unsigned)(a.E + 1));
 #define RS_LAUNCH(TM, NIMV, RSV, G)                                                                      \
     do {                                                                                                 \
         if (a.norm_h) hipLaunchKernelGGL((k_route_small<true, TM, NIMV, RSV>), G, dim3(256), 0, s, a);  \
@@ -881,7 +881,7 @@ int launch_route_small(const RouteArgs &a, hipStream_t s) {
         if (a.T == 1) RS_LAUNCH(1, NIMV, 1, g);   \
         else if (a.T <= 4) RS_LAUNCH(4, NIMV, 1, g); \
         else if (a.T <= 8) RS_LAUNCH(4, NIMV, 2, g2); \
-        else RS_LAUNCH(16, NIMV, 1, g);           \
+        else RS_LAUNCH(4, NIMV, 4, g4);           \
     } while (0)
     if (a.H <= 256 * 8) RS_T(8);
     else RS_T(CANON_NI);

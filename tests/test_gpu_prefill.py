@@ -262,3 +262,16 @@ def test_persistent_down_mixed_formats_2048(monkeypatch):
     ref = p.om.forward(0, x[sel], h[sel])
     assert rel_l2(out[sel] - h[sel], ref - h[sel]) < TOL
     p.gm.close()
+
+
+@pytest.mark.parametrize("T", [12, 16])
+def test_small_batch_path_up_to_16(base, T):
+    """9..16 tokens take the small-batch routing feeding the small-tile
+    grouped GEMMs under AUTO: routing bit-exact and output within tolerance
+    of the oracle, and equal bit for bit to the MFMA path (same tiles, same
+    fp16 activations, same GEMM kernels)."""
+    banner("small-batch path, T=%d" % T)
+    out, dbg = run_and_check(base, T, seed=1200 + T, path=_lib.OROME_PATH_AUTO)
+    x, h = base.inputs(T, seed=1200 + T)
+    ref, _ = base.run(0, x, h, path=_lib.OROME_PATH_MFMA)
+    assert np.array_equal(out, ref)
