@@ -504,8 +504,10 @@ static int forward_impl(orome_hip_ctx *c, const ModelConfig *cfg, const ExpertLa
     ExpertSide hx = ex;
     SharedSide hs = sh;
     apply_pack(c, S, hx, hs);
-    /* (up to 16 tokens: one 32-row small tile per expert, T K <= 256 for the
-     * small-batch dispatch) */
+    /* (from 3 tokens: the separate top-k + dispatch kernel, which writes the
+     * small-tile list, runs only there -- 1..2 tokens fold the routing into
+     * the GEMV gate/up; up to 16: one 32-row small tile per expert, and
+     * T K <= 256 for the small-batch dispatch) */
     const bool hybrid = path == OROME_PATH_AUTO && T >= 3 && T <= 16 && T * K <= 256 &&
                         gemm_small_tiles_ok(hx, hs, H, M);
     if (path == OROME_PATH_AUTO) path = T <= 8 || hybrid ? OROME_PATH_GEMV : OROME_PATH_MFMA;
