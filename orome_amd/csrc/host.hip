@@ -535,11 +535,12 @@ static int forward_impl(orome_hip_ctx *c, const ModelConfig *cfg, const ExpertLa
         const int fold = T <= 2;
         if (!fold) TLAUNCH(c, ST_TOPK, launch_topk_dispatch_small(a, s), "top-k + dispatch");
         if (hybrid) {
-            /* every expert holds at most 16 rows: the small-tile grouped
-             * GEMMs alone, then the combine */
+            /* every expert holds at most 16 rows: the grouped GEMMs alone
+             * (gate/up on 16-row tiles; down keeps the persistent 32-row
+             * kernel, faster here), then the combine */
             const int ns_max = E + (S ? 1 : 0);
             TLAUNCH(c, ST_GATE_UP,
-                    launch_gemm_gate_up(hx, hs, c->x16, c->tmax, T, H, M, K, E, GEMM_TILE_SMALL, c->tiles, ns_max,
+                    launch_gemm_gate_up(hx, hs, c->x16, c->tmax, T, H, M, K, E, GEMM_TILE_MIN, c->tiles, ns_max,
                                         c->pairs, c->act, c->act_sh, s, c->kt, c->kt_blocks),
                     "grouped gate/up (small tiles)");
             TLAUNCH(c, ST_DOWN,

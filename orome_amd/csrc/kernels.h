@@ -129,6 +129,9 @@ int launch_combine(const float *y, const float *ysh, const uint32_t *pos, const 
  * joins the small list when T*K <= GEMM_TILE_SMALL*E.  Capacities: small
  * E + T/SMALL + 1, big T*K/BIG + E + T/BIG + 1. */
 #define GEMM_TILE_SMALL 32
+/* 16-row tiles for lists whose experts hold at most 16 rows (the small-batch
+ * path: T <= 16); per-tile kernels only */
+#define GEMM_TILE_MIN 16
 #ifndef GEMM_TILE_BIG
 #define GEMM_TILE_BIG 80
 #endif

@@ -834,9 +834,14 @@ static unsigned persist_blocks() {
 }
 
 /* ------------------------------------------------------------ launch */
+/* Waves per block of a tile size (16- and 32-row tiles share a shape). */
+static_assert(Shape<GEMM_TILE_MIN / 16>::W == Shape<GEMM_TILE_SMALL / 16>::W, "tile shapes");
+static int tile_waves(int tile_m) {
+    return tile_m == GEMM_TILE_BIG ? Shape<GEMM_TILE_BIG / 16>::W : Shape<GEMM_TILE_SMALL / 16>::W;
+}
 /* Shapes and formats the launchers take (0) or decline (-2). */
 static int gate_up_shape(const ExpertSide &ex, const SharedSide &sh, int H, int M, int tile_m) {
-    const int W = tile_m == GEMM_TILE_SMALL ? Shape<GEMM_TILE_SMALL / 16>::W : Shape<GEMM_TILE_BIG / 16>::W;
+    const int W = tile_waves(tile_m);
     const int NB = W * 16 * GU_RPW;
     if ((H / KC * GU_RPW) % 4) return -2; /* every ring depth used divides the unit count */
     if (H % KCH || M % NB || (sh.gate && sh.S % NB) || (ex.gate_fmt != FQ4K && ex.gate_fmt != FQ4KT)) return -2;
@@ -845,7 +850,7 @@ static int gate_up_shape(const ExpertSide &ex, const SharedSide &sh, int H, int 
     return 0;
 }
 static int down_shape(const ExpertSide &ex, const SharedSide &sh, int H, int M, int tile_m) {
-    const int W = tile_m == GEMM_TILE_SMALL ? Shape<GEMM_TILE_SMALL / 16>::W : Shape<GEMM_TILE_BIG / 16>::W;
+    const int W = tile_waves(tile_m);
     const int NB = W * 16 * DN_RPW;
     if ((M / KC * DN_RPW) % 4 || (sh.gate && (sh.S / KC * DN_RPW) % 4)) return -2;
     /* all of a tile's activations stay resident: in_dim <= 2 chunks */
@@ -866,7 +871,7 @@ int launch_gemm_gate_up(const ExpertSide &ex, const SharedSide &sh, const _Float
                         const uint32_t *pairs, _Float16 *act, _Float16 *act_sh, hipStream_t s,
                         unsigned long long *kt, int kt_cap) {
     if (gate_up_shape(ex, sh, H, M, tile_m)) return -2;
-    const int W = tile_m == GEMM_TILE_SMALL ? Shape<GEMM_TILE_SMALL / 16>::W : Shape<GEMM_TILE_BIG / 16>::W;
+    const int W = tile_waves(tile_m);
     const int NB = W * 16 * GU_RPW;
     const bool tiled = ex.gate_fmt == FQ4KT;
     GemmArgs a = {};
@@ -878,7 +883,8 @@ int launch_gemm_gate_up(const ExpertSide &ex, const SharedSide &sh, const _Float
     a.nyb = (M > a.S ? M : a.S) / NB;
     const dim3 grid((unsigned)((n_tiles_max + 7) / 8 * 8 * a.nyb)), block(W * 64);
     const bool q8 = sh.gate && sh.gate_fmt == FQ8;
-    const unsigned pb = !GEMM_PERSIST ? 0u : tile_m == GEMM_TILE_BIG ? persist_blocks() : GEMM_PERSIST_SMALL * persist_blocks();
+    const unsigned pb = !GEMM_PERSIST || tile_m == GEMM_TILE_MIN ? 0u
+                        : tile_m == GEMM_TILE_BIG ? persist_blocks() : GEMM_PERSIST_SMALL * persist_blocks();
     a.kt = kt && (long)grid.x <= kt_cap ? kt : nullptr;
     if (pb && H == 2048 && (!sh.gate || (sh.gate_fmt == ex.gate_fmt && sh.S == M))) {
         a.kt = kt && (long)pb <= kt_cap ? kt : nullptr;
@@ -891,12 +897,13 @@ int launch_gemm_gate_up(const ExpertSide &ex, const SharedSide &sh, const _Float
         }
         return hipGetLastError() == hipSuccess ? 0 : -3;
     }
-    if (tile_m != GEMM_TILE_SMALL && tile_m != GEMM_TILE_BIG) return -2;
+    if (tile_m != GEMM_TILE_SMALL && tile_m != GEMM_TILE_BIG && tile_m != GEMM_TILE_MIN) return -2;
     /* compile-time stage count for the common hidden size (Q4_K shared
      * expert); other shapes take the generic loop */
 #define GU_LAUNCH(SF, NS)                                                                    \
     do {                                                                                     \
         if (tile_m == GEMM_TILE_SMALL) hipLaunchKernelGGL((k_gemm_gate_up<SF, NS, GEMM_TILE_SMALL / 16>), grid, block, 0, s, a); \
+        else if (tile_m == GEMM_TILE_MIN) hipLaunchKernelGGL((k_gemm_gate_up<SF, NS, GEMM_TILE_MIN / 16>), grid, block, 0, s, a); \
         else hipLaunchKernelGGL((k_gemm_gate_up<SF, NS, GEMM_TILE_BIG / 16>), grid, block, 0, s, a);              \
     } while (0)
     if (tiled) {
@@ -913,7 +920,7 @@ int launch_gemm_down(const ExpertSide &ex, const SharedSide &sh, const _Float16 
                      const _Float16 *act_sh, int zrow, int zrow_sh, int T, int H, int M, int K, int E, int tile_m,
                      const uint32_t *tiles, int n_tiles_max, float *y, float *ysh, hipStream_t s) {
     if (down_shape(ex, sh, H, M, tile_m)) return -2;
-    const int W = tile_m == GEMM_TILE_SMALL ? Shape<GEMM_TILE_SMALL / 16>::W : Shape<GEMM_TILE_BIG / 16>::W;
+    const int W = tile_waves(tile_m);
     const int NB = W * 16 * DN_RPW;
     const bool dtiled = ex.down_fmt == FQ4KT || ex.down_fmt == FQ6KT;
     const int sf = sh.gate ? sh.down_fmt : dtiled ? ex.down_fmt : FQ4K;
@@ -925,8 +932,9 @@ int launch_gemm_down(const ExpertSide &ex, const SharedSide &sh, const _Float16 
     a.tiles = tiles; a.y = y; a.ysh = ysh;
     a.nyb = H / NB;
     const dim3 grid((unsigned)((n_tiles_max + 7) / 8 * 8 * a.nyb)), block(W * 64);
-    if (tile_m != GEMM_TILE_SMALL && tile_m != GEMM_TILE_BIG) return -2;
-    const unsigned pb = !GEMM_PERSIST ? 0u : tile_m == GEMM_TILE_BIG ? persist_blocks() : GEMM_PERSIST_SMALL_DN * persist_blocks();
+    if (tile_m != GEMM_TILE_SMALL && tile_m != GEMM_TILE_BIG && tile_m != GEMM_TILE_MIN) return -2;
+    const unsigned pb = !GEMM_PERSIST || tile_m == GEMM_TILE_MIN ? 0u
+                        : tile_m == GEMM_TILE_BIG ? persist_blocks() : GEMM_PERSIST_SMALL_DN * persist_blocks();
     /* the shared expert's tiles end the list that holds most of the routed
      * work (as the dispatch builds it); nsh of them here */
     const bool sh_small = (size_t)T * K <= (size_t)GEMM_TILE_SMALL * E;
@@ -963,6 +971,7 @@ int launch_gemm_down(const ExpertSide &ex, const SharedSide &sh, const _Float16 
 #define DN_LAUNCH(EF, SF)                                                                    \
     do {                                                                                     \
         if (tile_m == GEMM_TILE_SMALL) hipLaunchKernelGGL((k_gemm_down<EF, SF, 0, GEMM_TILE_SMALL / 16>), grid, block, 0, s, a); \
+        else if (tile_m == GEMM_TILE_MIN) hipLaunchKernelGGL((k_gemm_down<EF, SF, 0, GEMM_TILE_MIN / 16>), grid, block, 0, s, a); \
         else hipLaunchKernelGGL((k_gemm_down<EF, SF, 0, GEMM_TILE_BIG / 16>), grid, block, 0, s, a);              \
     } while (0)
     if (ex.down_fmt == FQ4KT) {
