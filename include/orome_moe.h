@@ -1,12 +1,19 @@
 /*
  * orome_moe.h -- C ABI of the MI355X (gfx950) MoE feed-forward library.
  *
- * Drop-in boundary for Orome's MoE hot path.  The types keep the C subset of
- * the reference's interfaces (inference/include/orome.h) with the Metal
- * handles replaced by HIP device pointers; the functions replace the
+ * Drop-in boundary for Orome's MoE hot path.  The types carry the fields of
+ * the C subset of the reference's interfaces (inference/include/orome.h) with
+ * the Metal handles replaced by HIP device pointers; the functions replace the
  * reference's GGUF loader, weight-format layer, GPU context and the MoE
  * encoder (encode_experts_gguf).  Every declaration names the reference
  * interface it replaces as path:line relative to the reference repository.
+ *
+ * Every exported type, enumerator and function carries an OromeHip / OROME_ /
+ * orome_ prefix, so this header and the reference's orome.h can be included in
+ * one translation unit and both libraries linked into one engine: the
+ * reference's ModelConfig, TensorRef, GGUFFile, gguf_open, ... keep their own
+ * layouts and symbols, and the engine copies the MoE fields across once at
+ * load time.  Enumerator values equal the reference's (QuantFormat, FFNType).
  *
  * Conventions
  *   - Return codes: OROME_OK (0) or a negative OROME_E* code; a message is
@@ -15,8 +22,8 @@
  *     (inference/src/metal.m:44-56, inference/src/gguf.m:274-308).
  *   - All device pointers are HBM addresses from this library's allocator
  *     (or any hipMalloc'd memory on the context's device).
- *   - A context owns one HIP stream; forward calls are asynchronous on it and
- *     orome_hip_sync() waits.  A context is not thread-safe (the reference is
+ *   - A context owns one HIP stream; forward calls are asynchronous on it (or
+ *     on a stream the caller passes) and orome_hip_sync() waits.  A context is not thread-safe (the reference is
  *     single-threaded too: inference/src/metal.m:51).
  */
 #ifndef OROME_MOE_H
@@ -31,8 +38,11 @@ extern "C" {
 #endif
 #pragma GCC visibility push(default)
 
-/* inference/include/orome.h:29 -- upper bound on active experts per token. */
+/* inference/include/orome.h:29 -- upper bound on active experts per token
+ * (the same definition, so both headers may be included together). */
+#ifndef OROME_MAX_ACTIVE
 #define OROME_MAX_ACTIVE 16
+#endif
 
 enum {
     OROME_OK = 0,
@@ -45,32 +55,32 @@ enum {
 };
 
 /* inference/include/orome.h:40-43 */
-typedef enum { FFN_MOE, FFN_DENSE } FFNType;
+typedef enum { OROME_FFN_MOE, OROME_FFN_DENSE } OromeHipFFNType;
 
-/* MoE-path subset of ModelConfig (inference/include/orome.h:49-98); field
- * names and meanings are the reference's. */
+/* MoE-path subset of the reference's ModelConfig (inference/include/orome.h:49-98);
+ * field names and meanings are the reference's. */
 typedef struct {
     char name[64];
     int hidden_dim;           /* H, e.g. 2048 */
     int num_layers;
     float rms_norm_eps;       /* e.g. 1e-6 */
-    FFNType ffn_type;
+    OromeHipFFNType ffn_type;
     int num_experts;          /* E, e.g. 256 */
     int num_experts_per_tok;  /* K, e.g. 8 */
     int moe_intermediate;     /* M, e.g. 512 */
     int shared_intermediate;  /* S, e.g. 512; 0 = no shared expert */
-} ModelConfig;
+} OromeHipModelConfig;
 
 /* inference/include/orome.h:227-235 (same values, same order). */
 typedef enum {
-    QFMT_GGUF_Q4_K,
-    QFMT_GGUF_Q5_K,
-    QFMT_GGUF_Q6_K,
-    QFMT_GGUF_Q8_0,
-    QFMT_F16,
-    QFMT_BF16,
-    QFMT_F32,
-} QuantFormat;
+    OROME_QFMT_GGUF_Q4_K,
+    OROME_QFMT_GGUF_Q5_K,
+    OROME_QFMT_GGUF_Q6_K,
+    OROME_QFMT_GGUF_Q8_0,
+    OROME_QFMT_F16,
+    OROME_QFMT_BF16,
+    OROME_QFMT_F32,
+} OromeHipQuantFormat;
 
 /* inference/include/orome.h:239-246.  `buffer` is the device base of the
  * uploaded GGUF data (it was an id<MTLBuffer>); `offset` is the same GGUF byte
@@ -79,84 +89,84 @@ typedef enum {
 typedef struct {
     void *buffer;
     size_t offset;
-    QuantFormat format;
+    OromeHipQuantFormat format;
     uint32_t out_dim;
     uint32_t in_dim;
-} TensorRef;
+} OromeHipTensorRef;
 
 /* inference/include/orome.h:249-254 */
 typedef struct {
     size_t offset;
     size_t expert_stride;
-    QuantFormat format;
-} ExpertProjRef;
+    OromeHipQuantFormat format;
+} OromeHipExpertProjRef;
 
 /* inference/include/orome.h:256-259 */
 typedef struct {
     void *buffer;
-    ExpertProjRef gate, up, down;
-} ExpertLayerRef;
+    OromeHipExpertProjRef gate, up, down;
+} OromeHipExpertLayerRef;
 
-/* MoE subset of LayerTensorCache (inference/include/orome.h:264-279), plus
+/* MoE subset of the reference's LayerTensorCache (inference/include/orome.h:264-279), plus
  * `routing_bias`: an optional fp32 [E] bias added to the router logits
  * before top-k (synthetic skewed-routing workloads; a zeroed ref = none). */
 typedef struct {
-    TensorRef post_norm;           /* F32 [H]; truncated to bf16 when applied */
-    TensorRef routing_gate;        /* F32 [E x H] */
-    TensorRef shared_gate;         /* Q4_K/Q8_0 [S x H] */
-    TensorRef shared_up;           /* Q4_K/Q8_0 [S x H] */
-    TensorRef shared_down;         /* Q4_K/Q6_K/Q8_0 [H x S] */
-    TensorRef shared_expert_gate;  /* F32 [1 x H] */
-    TensorRef routing_bias;        /* F32 [E] or empty */
-} LayerTensorCache;
+    OromeHipTensorRef post_norm;           /* F32 [H]; truncated to bf16 when applied */
+    OromeHipTensorRef routing_gate;        /* F32 [E x H] */
+    OromeHipTensorRef shared_gate;         /* Q4_K/Q8_0 [S x H] */
+    OromeHipTensorRef shared_up;           /* Q4_K/Q8_0 [S x H] */
+    OromeHipTensorRef shared_down;         /* Q4_K/Q6_K/Q8_0 [H x S] */
+    OromeHipTensorRef shared_expert_gate;  /* F32 [1 x H] */
+    OromeHipTensorRef routing_bias;        /* F32 [E] or empty */
+} OromeHipLayerTensorCache;
 
 /* ------------------------------------------------------------------ GGUF */
 
 /* inference/include/orome.h:415-421 */
-typedef struct GGUFTensorInfo {
+typedef struct OromeHipGGUFTensorInfo {
     char *name;
     uint32_t n_dims;
     uint64_t dims[4];
     uint32_t type;    /* ggml type id */
     uint64_t offset;  /* relative to the data section */
-} GGUFTensorInfo;
+} OromeHipGGUFTensorInfo;
 
-/* MoE subset of GGUFFile (inference/include/orome.h:423-437). */
-typedef struct GGUFFile {
+/* MoE subset of the reference's GGUFFile (inference/include/orome.h:423-437). */
+typedef struct OromeHipGGUFFile {
     int fd;                 /* -1 for an in-memory image */
     void *mmap_base;        /* start of the image */
     size_t file_size;
     size_t data_offset;     /* absolute offset of the tensor data section */
-    GGUFTensorInfo *tensors;
+    OromeHipGGUFTensorInfo *tensors;
     uint64_t num_tensors;
     uint32_t alignment;
     char arch[32];
-    FFNType ffn_type;
+    OromeHipFFNType ffn_type;
     int num_layers, hidden_dim, num_experts, num_experts_per_tok, moe_intermediate;
     float rms_norm_eps;
     void *index;            /* private name index */
     bool owns_map;
-} GGUFFile;
+} OromeHipGGUFFile;
 
 /* inference/src/gguf.m:273-518 (mmap + parse; v2/v3; alignment rule 511-512) */
-GGUFFile *gguf_open(const char *path);
+OromeHipGGUFFile *orome_hip_gguf_open(const char *path);
 /* Same parser over an image already in host memory (not copied; must outlive
- * the GGUFFile).  No counterpart in the reference (it only maps files). */
-GGUFFile *gguf_open_memory(const void *data, size_t size);
+ * the OromeHipGGUFFile).  No counterpart in the reference (it only maps files). */
+OromeHipGGUFFile *orome_hip_gguf_open_memory(const void *data, size_t size);
 /* inference/src/gguf.m:520-531 */
-void gguf_close(GGUFFile *gf);
+void orome_hip_gguf_close(OromeHipGGUFFile *gf);
 /* inference/src/gguf.m:533-537 */
-GGUFTensorInfo *gguf_find_tensor(GGUFFile *gf, const char *name);
+OromeHipGGUFTensorInfo *orome_hip_gguf_find_tensor(OromeHipGGUFFile *gf, const char *name);
 /* inference/src/gguf.m:540-550 */
-size_t gguf_tensor_size(const GGUFTensorInfo *ti);
+size_t orome_hip_gguf_tensor_size(const OromeHipGGUFTensorInfo *ti);
 /* inference/src/gguf.m:552-575 */
-const char *ggml_type_name(uint32_t type);
+const char *orome_hip_ggml_type_name(uint32_t type);
 /* inference/src/format.m:326-337.  Unknown types are an error here
  * (OROME_EUNSUPPORTED) instead of the reference's silent Q4_K fallback. */
-int format_from_ggml_type(uint32_t ggml_type, QuantFormat *out);
-/* ModelConfig fields read from GGUF metadata and tensor shapes
+int orome_hip_format_from_ggml_type(uint32_t ggml_type, OromeHipQuantFormat *out);
+/* The MoE fields of ModelConfig read from GGUF metadata and tensor shapes
  * (inference/src/main.m:443-633, shared_intermediate at 576-588). */
-int model_config_from_gguf(const GGUFFile *gf, ModelConfig *cfg);
+int orome_hip_model_config_from_gguf(const OromeHipGGUFFile *gf, OromeHipModelConfig *cfg);
 
 /* ---------------------------------------------------------- HIP context */
 
@@ -164,7 +174,7 @@ int model_config_from_gguf(const GGUFFile *gf, ModelConfig *cfg);
  * inference/src/metal.m:41-256, 321-328): binds a device, creates the stream,
  * and sizes the scratch arena for up to `max_tokens` tokens per call. */
 typedef struct orome_hip_ctx orome_hip_ctx;
-orome_hip_ctx *orome_hip_create(const ModelConfig *cfg, int max_tokens, int device);
+orome_hip_ctx *orome_hip_create(const OromeHipModelConfig *cfg, int max_tokens, int device);
 void orome_hip_destroy(orome_hip_ctx *ctx);
 int orome_hip_sync(orome_hip_ctx *ctx);
 void *orome_hip_get_stream(orome_hip_ctx *ctx);   /* hipStream_t */
@@ -199,8 +209,8 @@ int orome_hip_set_path(orome_hip_ctx *ctx, int path);
  * proven bound) elsewhere.  OROME_ROUTE_EXACT=1 in the environment keeps the
  * one-pass router.
  * orome_hip_unpack_all frees every copy (orome_hip_destroy calls it). */
-int orome_hip_pack_layer(orome_hip_ctx *ctx, const ModelConfig *cfg, const ExpertLayerRef *layer,
-                         const LayerTensorCache *lt);
+int orome_hip_pack_layer(orome_hip_ctx *ctx, const OromeHipModelConfig *cfg, const OromeHipExpertLayerRef *layer,
+                         const OromeHipLayerTensorCache *lt);
 int orome_hip_unpack_all(orome_hip_ctx *ctx);
 
 /* Launch timing of the gate/up stage for measurement tools (no counterpart in
@@ -224,59 +234,73 @@ int orome_hip_dtoh(orome_hip_ctx *ctx, void *dst, const void *src, size_t bytes)
  * copy of the GGUF image from data_offset on; device addresses are
  * model_buf + (gguf offset - data_offset). */
 typedef struct {
-    GGUFFile *gguf;
+    OromeHipGGUFFile *gguf;
     void *model_buf;      /* device base, already shifted so that
                              model_buf + gguf_offset addresses the tensor */
     void *alloc_base;     /* the allocation itself */
     size_t model_bytes;
     orome_hip_ctx *ctx;
-} FormatProvider;
+} OromeHipFormatProvider;
 
 /* inference/src/format.m:343-363: the reference wraps the mmap without a copy
  * (unified memory); here the data section is copied unchanged into one HBM
  * allocation, so the same GGUF bytes feed the kernels. */
-FormatProvider *format_provider_open_gguf(GGUFFile *gf, orome_hip_ctx *ctx);
+OromeHipFormatProvider *orome_hip_format_provider_open_gguf(OromeHipGGUFFile *gf, orome_hip_ctx *ctx);
 /* inference/src/format.m:365-369 */
-void format_provider_close(FormatProvider *fp);
+void orome_hip_format_provider_close(OromeHipFormatProvider *fp);
 /* inference/src/format.m:374-409.  A missing tensor leaves a zeroed ref. */
-ExpertLayerRef format_resolve_expert_layer(FormatProvider *fp, int layer_idx,
+OromeHipExpertLayerRef orome_hip_format_resolve_expert_layer(OromeHipFormatProvider *fp, int layer_idx,
                                            uint32_t num_experts);
 /* MoE part of build_tensor_cache_gguf (inference/src/format.m:458-590,
  * MoE refs 495-509).  Returns cfg->num_layers entries; free with
- * free_tensor_cache(). */
-LayerTensorCache *build_tensor_cache_gguf(FormatProvider *fp, const ModelConfig *cfg);
-void free_tensor_cache(LayerTensorCache *cache);
+ * orome_hip_free_tensor_cache(). */
+OromeHipLayerTensorCache *orome_hip_build_tensor_cache_gguf(OromeHipFormatProvider *fp, const OromeHipModelConfig *cfg);
+void orome_hip_free_tensor_cache(OromeHipLayerTensorCache *cache);
 
 /* ------------------------------------------------------------ MoE block */
 
-/* One MoE feed-forward block for T tokens, on the context stream.
+/* One MoE feed-forward block for T tokens.
  * Replaces the routing matvec (inference/src/engine.m:656-685) plus
- * encode_experts_gguf (inference/src/engine.m:158-340):
+ * encode_experts_gguf (inference/src/engine.m:158-340) with its final
+ * moe_combine_copy_sq_k8 (inference/src/shaders.metal:1079-1135):
  *   logits = [W_r x ; w_sg x]   (fp32, fixed reduction order)
  *   idx, w = top-K of logits (+routing_bias), renormalised softmax
  *   h_out  = (h_in + sum_k w_k E_idx_k(x)) + sigmoid(w_sg x) * S(x)
  * x_dev: fp32 [T x H] normalised input.  h_in_dev: fp32 [T x H] residual or
- * NULL (zero).  h_out_dev may alias h_in_dev.  K <= OROME_MAX_ACTIVE. */
-int orome_moe_forward(orome_hip_ctx *ctx, const ModelConfig *cfg, const ExpertLayerRef *elr,
-                      const LayerTensorCache *lt, const float *x_dev, const float *h_in_dev,
-                      float *h_out_dev, int T, int K);
+ * NULL (zero).  h_out_dev may alias h_in_dev.  K <= OROME_MAX_ACTIVE.
+ * The combine's other two outputs, as the reference's kernel writes them:
+ *   residual_out_dev  fp32 [T x H] copy of h_out (NULL: not written);
+ *   sumsq_parts_dev   fp32 [T x H/256]: part b of token t is the sum of
+ *                     h_out[t][j]^2 over j in [256 b, 256 b + 256), summed
+ *                     in the canonical order of the router's dots (lane L of
+ *                     a wave64 owns j = 256 b + 4 L + c, fma over c from
+ *                     zero, then the contiguous balanced tree over lanes);
+ *                     the next RMSNorm adds the parts (NULL: not written).
+ * stream: a hipStream_t on the context's device, or NULL for the context's
+ * own stream; the call is asynchronous on it. */
+int orome_moe_forward(orome_hip_ctx *ctx, const OromeHipModelConfig *cfg,
+                      const OromeHipExpertLayerRef *elr, const OromeHipLayerTensorCache *lt,
+                      const float *x_dev, const float *h_in_dev, float *h_out_dev,
+                      float *residual_out_dev, float *sumsq_parts_dev, int T, int K, void *stream);
 
 /* RMSNorm (post_norm, bf16-truncated weights) then the MoE block with the
  * residual add, in place on h_dev [T x H]: h = h + MoE(RMSNorm(h)).
  * The reference fuses the same norm into the previous combine
- * (inference/src/shaders.metal:90-149, 1079-1135; inference/src/engine.m:627-653). */
-int orome_moe_layer_forward(orome_hip_ctx *ctx, const ModelConfig *cfg,
-                            const ExpertLayerRef *elr, const LayerTensorCache *lt, float *h_dev,
-                            int T, int K);
+ * (inference/src/shaders.metal:90-149, 1079-1135; inference/src/engine.m:627-653).
+ * stream as for orome_moe_forward. */
+int orome_moe_layer_forward(orome_hip_ctx *ctx, const OromeHipModelConfig *cfg,
+                            const OromeHipExpertLayerRef *elr, const OromeHipLayerTensorCache *lt,
+                            float *h_dev, int T, int K, void *stream);
 
 /* n_layers consecutive orome_moe_layer_forward calls (the per-layer loop of
- * engine_step restricted to the FFN blocks, inference/src/engine.m:481-694). */
-int orome_moe_stack_forward(orome_hip_ctx *ctx, const ModelConfig *cfg,
-                            const ExpertLayerRef *elrs, const LayerTensorCache *lts, int n_layers,
-                            float *h_dev, int T, int K);
+ * engine_step restricted to the FFN blocks, inference/src/engine.m:481-694).
+ * stream as for orome_moe_forward. */
+int orome_moe_stack_forward(orome_hip_ctx *ctx, const OromeHipModelConfig *cfg,
+                            const OromeHipExpertLayerRef *elrs, const OromeHipLayerTensorCache *lts,
+                            int n_layers, float *h_dev, int T, int K, void *stream);
 
 /* Parity hooks: copy the intermediates of the most recent forward to host
- * memory (synchronises the stream).  Any pointer may be NULL.
+ * memory (synchronises the stream that forward ran on).  Any pointer may be NULL.
  *   logits  [T x (E+1)]  router logits, slot E = shared-gate logit
  *   idx     [T x K]      expert indices, descending logit per token
  *   w       [T x K]      renormalised weights
@@ -293,12 +317,12 @@ int orome_moe_topk(orome_hip_ctx *ctx, const float *logits_dev, const float *bia
 
 /* Scalar dequant of `rows` rows of `in_dim` weights to fp32 on the GPU
  * (format_decode_row_f32, inference/src/format.m:176-218; bit-exact). */
-int orome_dequant_rows(orome_hip_ctx *ctx, QuantFormat fmt, const void *src_dev, uint32_t rows,
+int orome_dequant_rows(orome_hip_ctx *ctx, OromeHipQuantFormat fmt, const void *src_dev, uint32_t rows,
                        uint32_t in_dim, float *out_dev);
 
 /* The fp16 weight tiles that the MFMA path feeds to the matrix cores:
  * fp16(dequant(w)) rounded to nearest even, [rows x in_dim]. */
-int orome_dequant_rows_f16(orome_hip_ctx *ctx, QuantFormat fmt, const void *src_dev,
+int orome_dequant_rows_f16(orome_hip_ctx *ctx, OromeHipQuantFormat fmt, const void *src_dev,
                            uint32_t rows, uint32_t in_dim, uint16_t *out_dev);
 
 /* ------------------------------------------------- graphs and timing */

@@ -213,6 +213,25 @@ class OracleModel:
         return self.forward(l, self.rmsnorm(l, h), h_in=h, K=K, omp=omp)
 
 
+def canon_dot(a, b):
+    a = np.ascontiguousarray(a, np.float32)
+    b = np.ascontiguousarray(b, np.float32)
+    return np.float32(lib().orc_canon_dot(p(a), p(b), a.size))
+
+
+def sumsq_parts(h):
+    """[T][H/256] sums of squares per 256-column block in the canonical order
+    (the Sigma h^2 partials moe_combine_copy_sq_k8 writes,
+    inference/src/shaders.metal:1079-1135, in this build's fixed order)."""
+    T, H = h.shape
+    out = np.empty((T, H // 256), np.float32)
+    for t in range(T):
+        for b in range(H // 256):
+            blk = h[t, 256 * b:256 * (b + 1)]
+            out[t, b] = canon_dot(blk, blk)
+    return out
+
+
 def dispatch(idx, E):
     T, K = idx.shape
     off = np.empty(E + 1, np.uint32)

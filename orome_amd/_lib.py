@@ -11,7 +11,7 @@ import os
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "liborome_moe.so")
 
-# QuantFormat (inference/include/orome.h:227-235)
+# OromeHipQuantFormat: the values of QuantFormat (inference/include/orome.h:227-235)
 QFMT_GGUF_Q4_K, QFMT_GGUF_Q5_K, QFMT_GGUF_Q6_K, QFMT_GGUF_Q8_0, QFMT_F16, QFMT_BF16, QFMT_F32 = range(7)
 FFN_MOE, FFN_DENSE = 0, 1
 OROME_PATH_AUTO, OROME_PATH_GEMV, OROME_PATH_MFMA = 0, 1, 2
@@ -83,14 +83,14 @@ P = C.POINTER
 
 # name -> (restype, argtypes); every symbol declared in include/*.h
 SIGNATURES = {
-    "gguf_open": (P(GGUFFile), [C.c_char_p]),
-    "gguf_open_memory": (P(GGUFFile), [VP, SZ]),
-    "gguf_close": (None, [P(GGUFFile)]),
-    "gguf_find_tensor": (P(GGUFTensorInfo), [P(GGUFFile), C.c_char_p]),
-    "gguf_tensor_size": (SZ, [P(GGUFTensorInfo)]),
-    "ggml_type_name": (C.c_char_p, [U32]),
-    "format_from_ggml_type": (I, [U32, P(C.c_int)]),
-    "model_config_from_gguf": (I, [P(GGUFFile), P(ModelConfig)]),
+    "orome_hip_gguf_open": (P(GGUFFile), [C.c_char_p]),
+    "orome_hip_gguf_open_memory": (P(GGUFFile), [VP, SZ]),
+    "orome_hip_gguf_close": (None, [P(GGUFFile)]),
+    "orome_hip_gguf_find_tensor": (P(GGUFTensorInfo), [P(GGUFFile), C.c_char_p]),
+    "orome_hip_gguf_tensor_size": (SZ, [P(GGUFTensorInfo)]),
+    "orome_hip_ggml_type_name": (C.c_char_p, [U32]),
+    "orome_hip_format_from_ggml_type": (I, [U32, P(C.c_int)]),
+    "orome_hip_model_config_from_gguf": (I, [P(GGUFFile), P(ModelConfig)]),
     "orome_hip_create": (VP, [P(ModelConfig), I, I]),
     "orome_hip_destroy": (None, [VP]),
     "orome_hip_sync": (I, [VP]),
@@ -104,17 +104,17 @@ SIGNATURES = {
     "orome_hip_pack_layer": (I, [VP, P(ModelConfig), P(ExpertLayerRef), P(LayerTensorCache)]),
     "orome_hip_unpack_all": (I, [VP]),
     "orome_hip_kernel_timing": (I, [VP, VP, I]),
-    "format_provider_open_gguf": (P(FormatProvider), [P(GGUFFile), VP]),
-    "format_provider_close": (None, [P(FormatProvider)]),
-    "format_resolve_expert_layer": (ExpertLayerRef, [P(FormatProvider), I, U32]),
-    "build_tensor_cache_gguf": (P(LayerTensorCache), [P(FormatProvider), P(ModelConfig)]),
-    "free_tensor_cache": (None, [P(LayerTensorCache)]),
+    "orome_hip_format_provider_open_gguf": (P(FormatProvider), [P(GGUFFile), VP]),
+    "orome_hip_format_provider_close": (None, [P(FormatProvider)]),
+    "orome_hip_format_resolve_expert_layer": (ExpertLayerRef, [P(FormatProvider), I, U32]),
+    "orome_hip_build_tensor_cache_gguf": (P(LayerTensorCache), [P(FormatProvider), P(ModelConfig)]),
+    "orome_hip_free_tensor_cache": (None, [P(LayerTensorCache)]),
     "orome_moe_forward": (I, [VP, P(ModelConfig), P(ExpertLayerRef), P(LayerTensorCache), VP, VP,
-                              VP, I, I]),
+                              VP, VP, VP, I, I, VP]),
     "orome_moe_layer_forward": (I, [VP, P(ModelConfig), P(ExpertLayerRef), P(LayerTensorCache), VP,
-                                    I, I]),
+                                    I, I, VP]),
     "orome_moe_stack_forward": (I, [VP, P(ModelConfig), P(ExpertLayerRef), P(LayerTensorCache), I,
-                                    VP, I, I]),
+                                    VP, I, I, VP]),
     "orome_moe_debug_outputs": (I, [VP, VP, VP, VP, VP, VP]),
     "orome_moe_topk": (I, [VP, VP, VP, I, I, I, VP, VP]),
     "orome_dequant_rows": (I, [VP, I, VP, U32, U32, VP]),

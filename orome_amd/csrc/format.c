@@ -1,7 +1,7 @@
 /*
  * format.c -- weight-format layer: GGUF tensors -> HBM-resident TensorRefs.
  *
- * Mirrors the reference's FormatProvider / tensor cache
+ * Mirrors the reference's OromeHipFormatProvider / tensor cache
  * (inference/src/format.m:326-409, 458-590) for the MoE block.  The reference
  * wraps the whole GGUF mmap as one Metal buffer without copying (unified
  * memory, format.m:343-363); MI355X memory is discrete, so the data section
@@ -15,8 +15,8 @@
 #include "orome_internal.h"
 #include "orome_moe.h"
 
-FormatProvider *format_provider_open_gguf(GGUFFile *gf, orome_hip_ctx *ctx) {
-    if (!gf || !ctx) { orome_fail(OROME_EINVAL, "format_provider_open_gguf: NULL argument"); return NULL; }
+OromeHipFormatProvider *orome_hip_format_provider_open_gguf(OromeHipGGUFFile *gf, orome_hip_ctx *ctx) {
+    if (!gf || !ctx) { orome_fail(OROME_EINVAL, "orome_hip_format_provider_open_gguf: NULL argument"); return NULL; }
     size_t bytes = gf->file_size - gf->data_offset;
     void *dev = orome_hip_malloc(ctx, bytes ? bytes : 1);
     if (!dev) return NULL;
@@ -24,7 +24,7 @@ FormatProvider *format_provider_open_gguf(GGUFFile *gf, orome_hip_ctx *ctx) {
         orome_hip_free(ctx, dev);
         return NULL;
     }
-    FormatProvider *fp = calloc(1, sizeof *fp);
+    OromeHipFormatProvider *fp = calloc(1, sizeof *fp);
     fp->gguf = gf;
     fp->alloc_base = dev;
     /* model_buf + (data_offset + tensor offset) == device address of the tensor */
@@ -34,26 +34,26 @@ FormatProvider *format_provider_open_gguf(GGUFFile *gf, orome_hip_ctx *ctx) {
     return fp;
 }
 
-void format_provider_close(FormatProvider *fp) {
+void orome_hip_format_provider_close(OromeHipFormatProvider *fp) {
     if (!fp) return;
     if (fp->alloc_base) orome_hip_free(fp->ctx, fp->alloc_base);
     free(fp);
 }
 
-static int proj(FormatProvider *fp, const char *name, uint32_t E, ExpertProjRef *out) {
-    GGUFTensorInfo *ti = gguf_find_tensor(fp->gguf, name);
+static int proj(OromeHipFormatProvider *fp, const char *name, uint32_t E, OromeHipExpertProjRef *out) {
+    OromeHipGGUFTensorInfo *ti = orome_hip_gguf_find_tensor(fp->gguf, name);
     if (!ti) return OROME_ENOTFOUND;
-    QuantFormat f;
-    int rc = format_from_ggml_type(ti->type, &f);
+    OromeHipQuantFormat f;
+    int rc = orome_hip_format_from_ggml_type(ti->type, &f);
     if (rc) return rc;
     out->offset = fp->gguf->data_offset + ti->offset;
     out->format = f;
-    out->expert_stride = gguf_tensor_size(ti) / E;
+    out->expert_stride = orome_hip_gguf_tensor_size(ti) / E;
     return OROME_OK;
 }
 
-ExpertLayerRef format_resolve_expert_layer(FormatProvider *fp, int layer, uint32_t E) {
-    ExpertLayerRef r;
+OromeHipExpertLayerRef orome_hip_format_resolve_expert_layer(OromeHipFormatProvider *fp, int layer, uint32_t E) {
+    OromeHipExpertLayerRef r;
     memset(&r, 0, sizeof r);
     if (!fp || !E) return r;
     r.buffer = fp->model_buf;
@@ -68,13 +68,13 @@ ExpertLayerRef format_resolve_expert_layer(FormatProvider *fp, int layer, uint32
 }
 
 /* gguf_ref (inference/src/format.m:416-427) */
-static TensorRef ref(FormatProvider *fp, const char *name, uint32_t out_dim, uint32_t in_dim) {
-    TensorRef t;
+static OromeHipTensorRef ref(OromeHipFormatProvider *fp, const char *name, uint32_t out_dim, uint32_t in_dim) {
+    OromeHipTensorRef t;
     memset(&t, 0, sizeof t);
-    GGUFTensorInfo *ti = gguf_find_tensor(fp->gguf, name);
+    OromeHipGGUFTensorInfo *ti = orome_hip_gguf_find_tensor(fp->gguf, name);
     if (!ti) return t;
-    QuantFormat f;
-    if (format_from_ggml_type(ti->type, &f)) return t;
+    OromeHipQuantFormat f;
+    if (orome_hip_format_from_ggml_type(ti->type, &f)) return t;
     t.buffer = fp->model_buf;
     t.offset = fp->gguf->data_offset + ti->offset;
     t.format = f;
@@ -83,17 +83,17 @@ static TensorRef ref(FormatProvider *fp, const char *name, uint32_t out_dim, uin
     return t;
 }
 
-LayerTensorCache *build_tensor_cache_gguf(FormatProvider *fp, const ModelConfig *cfg) {
+OromeHipLayerTensorCache *orome_hip_build_tensor_cache_gguf(OromeHipFormatProvider *fp, const OromeHipModelConfig *cfg) {
     if (!fp || !cfg || cfg->num_layers <= 0) {
-        orome_fail(OROME_EINVAL, "build_tensor_cache_gguf: bad arguments");
+        orome_fail(OROME_EINVAL, "orome_hip_build_tensor_cache_gguf: bad arguments");
         return NULL;
     }
-    LayerTensorCache *c = calloc((size_t)cfg->num_layers, sizeof *c);
+    OromeHipLayerTensorCache *c = calloc((size_t)cfg->num_layers, sizeof *c);
     uint32_t H = (uint32_t)cfg->hidden_dim, E = (uint32_t)cfg->num_experts;
     uint32_t S = (uint32_t)(cfg->shared_intermediate > 0 ? cfg->shared_intermediate : 0);
     char nm[128];
     for (int i = 0; i < cfg->num_layers; i++) {
-        LayerTensorCache *l = &c[i];
+        OromeHipLayerTensorCache *l = &c[i];
         snprintf(nm, sizeof nm, "blk.%d.ffn_norm.weight", i);
         l->post_norm = ref(fp, nm, 1, H);
         if (!l->post_norm.buffer) {
@@ -118,4 +118,4 @@ LayerTensorCache *build_tensor_cache_gguf(FormatProvider *fp, const ModelConfig 
     return c;
 }
 
-void free_tensor_cache(LayerTensorCache *c) { free(c); }
+void orome_hip_free_tensor_cache(OromeHipLayerTensorCache *c) { free(c); }

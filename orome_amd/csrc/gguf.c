@@ -123,7 +123,7 @@ static size_t blk_bytes(uint32_t t) {
     return 0;
 }
 
-size_t gguf_tensor_size(const GGUFTensorInfo *ti) {
+size_t orome_hip_gguf_tensor_size(const OromeHipGGUFTensorInfo *ti) {
     if (!ti) return 0;
     size_t be = blk_elems(ti->type), bb = blk_bytes(ti->type);
     if (!be || !bb) return 0;
@@ -132,7 +132,7 @@ size_t gguf_tensor_size(const GGUFTensorInfo *ti) {
     return (size_t)(n / be) * bb;
 }
 
-const char *ggml_type_name(uint32_t t) {
+const char *orome_hip_ggml_type_name(uint32_t t) {
     switch (t) {
         case 0: return "F32"; case 1: return "F16"; case 30: return "BF16";
         case 2: return "Q4_0"; case 3: return "Q4_1"; case 6: return "Q5_0"; case 7: return "Q5_1";
@@ -142,19 +142,19 @@ const char *ggml_type_name(uint32_t t) {
     return "UNKNOWN";
 }
 
-int format_from_ggml_type(uint32_t t, QuantFormat *out) {
-    QuantFormat f;
+int orome_hip_format_from_ggml_type(uint32_t t, OromeHipQuantFormat *out) {
+    OromeHipQuantFormat f;
     switch (t) {
-        case 8: f = QFMT_GGUF_Q8_0; break;
-        case 12: f = QFMT_GGUF_Q4_K; break;
-        case 13: f = QFMT_GGUF_Q5_K; break;
-        case 14: f = QFMT_GGUF_Q6_K; break;
-        case 1: f = QFMT_F16; break;
-        case 30: f = QFMT_BF16; break;
-        case 0: f = QFMT_F32; break;
+        case 8: f = OROME_QFMT_GGUF_Q8_0; break;
+        case 12: f = OROME_QFMT_GGUF_Q4_K; break;
+        case 13: f = OROME_QFMT_GGUF_Q5_K; break;
+        case 14: f = OROME_QFMT_GGUF_Q6_K; break;
+        case 1: f = OROME_QFMT_F16; break;
+        case 30: f = OROME_QFMT_BF16; break;
+        case 0: f = OROME_QFMT_F32; break;
         default:
             return orome_fail(OROME_EUNSUPPORTED, "ggml type %u (%s) has no kernel", t,
-                              ggml_type_name(t));
+                              orome_hip_ggml_type_name(t));
     }
     if (out) *out = f;
     return OROME_OK;
@@ -164,15 +164,15 @@ int format_from_ggml_type(uint32_t t, QuantFormat *out) {
 typedef struct {
     uint64_t n;
     uint64_t *ids;
-    const GGUFTensorInfo *tensors;
+    const OromeHipGGUFTensorInfo *tensors;
 } name_index;
 
-static const GGUFTensorInfo *g_sort_base;
+static const OromeHipGGUFTensorInfo *g_sort_base;
 static int cmp_ids(const void *a, const void *b) {
     return strcmp(g_sort_base[*(const uint64_t *)a].name, g_sort_base[*(const uint64_t *)b].name);
 }
 
-GGUFTensorInfo *gguf_find_tensor(GGUFFile *gf, const char *name) {
+OromeHipGGUFTensorInfo *orome_hip_gguf_find_tensor(OromeHipGGUFFile *gf, const char *name) {
     if (!gf || !name || !gf->index) return NULL;
     name_index *ix = (name_index *)gf->index;
     uint64_t lo = 0, hi = ix->n;
@@ -185,7 +185,7 @@ GGUFTensorInfo *gguf_find_tensor(GGUFFile *gf, const char *name) {
     return NULL;
 }
 
-void gguf_close(GGUFFile *gf) {
+void orome_hip_gguf_close(OromeHipGGUFFile *gf) {
     if (!gf) return;
     if (gf->tensors) {
         for (uint64_t i = 0; i < gf->num_tensors; i++) free(gf->tensors[i].name);
@@ -200,7 +200,7 @@ void gguf_close(GGUFFile *gf) {
     free(gf);
 }
 
-static GGUFFile *parse(const uint8_t *img, size_t size, GGUFFile *gf) {
+static OromeHipGGUFFile *parse(const uint8_t *img, size_t size, OromeHipGGUFFile *gf) {
     rd_t r = {img, size, 0, 0};
     uint32_t magic = (uint32_t)rd_uint(&r, 4);
     if (r.bad || magic != GGUF_MAGIC) {
@@ -277,10 +277,10 @@ static GGUFFile *parse(const uint8_t *img, size_t size, GGUFFile *gf) {
         goto fail;
     }
     gf->num_tensors = n_tensors;
-    gf->tensors = calloc(n_tensors ? n_tensors : 1, sizeof(GGUFTensorInfo));
+    gf->tensors = calloc(n_tensors ? n_tensors : 1, sizeof(OromeHipGGUFTensorInfo));
     if (!gf->tensors) { orome_fail(OROME_ENOMEM, "gguf: out of host memory"); goto fail; }
     for (uint64_t i = 0; i < n_tensors; i++) {
-        GGUFTensorInfo *ti = &gf->tensors[i];
+        OromeHipGGUFTensorInfo *ti = &gf->tensors[i];
         uint64_t nl;
         const char *nm = rd_str(&r, &nl);
         ti->n_dims = (uint32_t)rd_uint(&r, 4);
@@ -300,8 +300,8 @@ static GGUFFile *parse(const uint8_t *img, size_t size, GGUFFile *gf) {
     size_t a = gf->alignment;
     gf->data_offset = (r.pos + a - 1) & ~(a - 1);
     for (uint64_t i = 0; i < n_tensors; i++) {
-        GGUFTensorInfo *ti = &gf->tensors[i];
-        size_t sz = gguf_tensor_size(ti);
+        OromeHipGGUFTensorInfo *ti = &gf->tensors[i];
+        size_t sz = orome_hip_gguf_tensor_size(ti);
         if (gf->data_offset + ti->offset + sz > size) {
             orome_fail(OROME_EFORMAT, "gguf: tensor %s extends past the end of the image", ti->name);
             goto fail;
@@ -318,21 +318,21 @@ static GGUFFile *parse(const uint8_t *img, size_t size, GGUFFile *gf) {
     int moe = 0;
     for (uint64_t i = 0; i < n_tensors; i++)
         if (strstr(gf->tensors[i].name, "_exps")) { moe = 1; break; }
-    gf->ffn_type = (moe || gf->num_experts > 0) ? FFN_MOE : FFN_DENSE;
+    gf->ffn_type = (moe || gf->num_experts > 0) ? OROME_FFN_MOE : OROME_FFN_DENSE;
     if (!gf->moe_intermediate && moe) {
         /* gguf.m:476-488: the gate_exps dimension that is neither H nor E */
-        GGUFTensorInfo *g = gguf_find_tensor(gf, "blk.0.ffn_gate_exps.weight");
+        OromeHipGGUFTensorInfo *g = orome_hip_gguf_find_tensor(gf, "blk.0.ffn_gate_exps.weight");
         if (g && g->n_dims >= 2) gf->moe_intermediate = (int)g->dims[1];
     }
     return gf;
 fail:
-    gguf_close(gf);
+    orome_hip_gguf_close(gf);
     return NULL;
 }
 
-GGUFFile *gguf_open_memory(const void *data, size_t size) {
+OromeHipGGUFFile *orome_hip_gguf_open_memory(const void *data, size_t size) {
     if (!data) { orome_fail(OROME_EINVAL, "gguf: NULL image"); return NULL; }
-    GGUFFile *gf = calloc(1, sizeof *gf);
+    OromeHipGGUFFile *gf = calloc(1, sizeof *gf);
     gf->fd = -1;
     gf->mmap_base = (void *)data;
     gf->file_size = size;
@@ -340,7 +340,7 @@ GGUFFile *gguf_open_memory(const void *data, size_t size) {
     return parse((const uint8_t *)data, size, gf);
 }
 
-GGUFFile *gguf_open(const char *path) {
+OromeHipGGUFFile *orome_hip_gguf_open(const char *path) {
     int fd = open(path, O_RDONLY);
     if (fd < 0) { orome_fail(OROME_ENOTFOUND, "gguf: cannot open %s", path); return NULL; }
     struct stat st;
@@ -355,7 +355,7 @@ GGUFFile *gguf_open(const char *path) {
         orome_fail(OROME_EHIP, "gguf: mmap of %s failed", path);
         return NULL;
     }
-    GGUFFile *gf = calloc(1, sizeof *gf);
+    OromeHipGGUFFile *gf = calloc(1, sizeof *gf);
     gf->fd = fd;
     gf->mmap_base = m;
     gf->file_size = (size_t)st.st_size;
@@ -363,8 +363,8 @@ GGUFFile *gguf_open(const char *path) {
     return parse((const uint8_t *)m, (size_t)st.st_size, gf);
 }
 
-int model_config_from_gguf(const GGUFFile *gf, ModelConfig *cfg) {
-    if (!gf || !cfg) return orome_fail(OROME_EINVAL, "model_config_from_gguf: NULL argument");
+int orome_hip_model_config_from_gguf(const OromeHipGGUFFile *gf, OromeHipModelConfig *cfg) {
+    if (!gf || !cfg) return orome_fail(OROME_EINVAL, "orome_hip_model_config_from_gguf: NULL argument");
     memset(cfg, 0, sizeof *cfg);
     snprintf(cfg->name, sizeof cfg->name, "%s", gf->arch);
     cfg->hidden_dim = gf->hidden_dim;
@@ -375,7 +375,7 @@ int model_config_from_gguf(const GGUFFile *gf, ModelConfig *cfg) {
     cfg->num_experts_per_tok = gf->num_experts_per_tok;
     cfg->moe_intermediate = gf->moe_intermediate;
     /* inference/src/main.m:576-588: S from the shared gate's second dim */
-    GGUFTensorInfo *sg = gguf_find_tensor((GGUFFile *)gf, "blk.0.ffn_gate_shexp.weight");
+    OromeHipGGUFTensorInfo *sg = orome_hip_gguf_find_tensor((OromeHipGGUFFile *)gf, "blk.0.ffn_gate_shexp.weight");
     cfg->shared_intermediate = (sg && sg->n_dims >= 2) ? (int)sg->dims[1] : 0;
     if (cfg->hidden_dim <= 0 || cfg->num_layers <= 0)
         return orome_fail(OROME_EFORMAT, "gguf: missing block_count/embedding_length");

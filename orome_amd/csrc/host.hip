@@ -44,7 +44,7 @@ struct orome_hip_ctx {
     hipStream_t stream;
     hipStream_t side;        /* second stream: the big-tile GEMM list runs beside the small one */
     hipEvent_t fork, join;
-    ModelConfig cfg;
+    OromeHipModelConfig cfg;
     int tmax, kmax, path;
     /* scratch */
     float *logits, *w, *sgl, *y, *ysh, *xnorm;
@@ -54,6 +54,7 @@ struct orome_hip_ctx {
     void *arena;
     size_t arena_bytes;
     int last_T, last_K;
+    hipStream_t last_stream; /* stream of the most recent forward (debug outputs wait for it) */
     /* per-stage kernel timing (eager launches only) */
     int timing, tcap;
     hipEvent_t *ev;          /* [N_STAGES][tcap][2] */
@@ -85,7 +86,7 @@ static int set_dev(orome_hip_ctx *c) {
     return OROME_OK;
 }
 
-extern "C" orome_hip_ctx *orome_hip_create(const ModelConfig *cfg, int max_tokens, int device) {
+extern "C" orome_hip_ctx *orome_hip_create(const OromeHipModelConfig *cfg, int max_tokens, int device) {
     if (!cfg || max_tokens < 1 || cfg->hidden_dim <= 0 || cfg->num_experts <= 0 ||
         cfg->moe_intermediate <= 0) {
         orome_fail(OROME_EINVAL, "orome_hip_create: invalid config or max_tokens");
@@ -248,11 +249,11 @@ static const uint8_t *dev_addr(const void *buffer, size_t offset) {
     return buffer ? (const uint8_t *)buffer + offset : NULL;
 }
 
-static int kfmt(QuantFormat f) {
+static int kfmt(OromeHipQuantFormat f) {
     switch (f) {
-        case QFMT_GGUF_Q4_K: return 0;
-        case QFMT_GGUF_Q6_K: return 2;
-        case QFMT_GGUF_Q8_0: return 3;
+        case OROME_QFMT_GGUF_Q4_K: return 0;
+        case OROME_QFMT_GGUF_Q6_K: return 2;
+        case OROME_QFMT_GGUF_Q8_0: return 3;
         default: return -1;
     }
 }
@@ -260,7 +261,8 @@ static int kfmt(QuantFormat f) {
 /* ------------------------------------------------- tile-major repacking */
 
 /* The grouped GEMMs' view of a layer: registered layers read their
- * tile-major copies. */
+ * tile-major copies (each matrix that was repacked; a Q8_0 shared expert
+ * stays row-major). */
 static const Pack *find_pack(const orome_hip_ctx *c, const uint8_t *gate, const uint8_t *sh_gate);
 static void apply_pack(const orome_hip_ctx *c, int S, ExpertSide &exm, SharedSide &shm) {
     const Pack *pk = find_pack(c, exm.gate, shm.gate);
@@ -269,7 +271,7 @@ static void apply_pack(const orome_hip_ctx *c, int S, ExpertSide &exm, SharedSid
     exm.up = pk->up;
     exm.gate_stride = exm.up_stride = pk->gate_stride;
     exm.gate_fmt = GEMM_FMT_Q4K_TILED;
-    if (S) {
+    if (S && pk->sgate) {
         shm.gate = pk->sgate;
         shm.up = pk->sup;
         shm.gate_fmt = GEMM_FMT_Q4K_TILED;
@@ -278,10 +280,10 @@ static void apply_pack(const orome_hip_ctx *c, int S, ExpertSide &exm, SharedSid
         exm.down = pk->down;
         exm.down_stride = pk->down_stride;
         exm.down_fmt = pk->down_fmt;
-        if (S) {
-            shm.down = pk->sdown;
-            shm.down_fmt = pk->sdown_fmt;
-        }
+    }
+    if (S && pk->sdown) {
+        shm.down = pk->sdown;
+        shm.down_fmt = pk->sdown_fmt;
     }
 }
 
@@ -298,28 +300,28 @@ static const Pack *find_pack(const orome_hip_ctx *c, const uint8_t *gate, const 
     return NULL;
 }
 
-extern "C" int orome_hip_pack_layer(orome_hip_ctx *c, const ModelConfig *cfg, const ExpertLayerRef *elr,
-                                    const LayerTensorCache *lt) {
+extern "C" int orome_hip_pack_layer(orome_hip_ctx *c, const OromeHipModelConfig *cfg, const OromeHipExpertLayerRef *elr,
+                                    const OromeHipLayerTensorCache *lt) {
     if (!c || !cfg || !elr || !lt || !elr->buffer) return orome_fail(OROME_EINVAL, "orome_hip_pack_layer: NULL argument");
     const int H = cfg->hidden_dim, E = cfg->num_experts, M = cfg->moe_intermediate;
     if (H != c->cfg.hidden_dim || E != c->cfg.num_experts || M != c->cfg.moe_intermediate)
         return orome_fail(OROME_EINVAL, "orome_hip_pack_layer: config differs from the context's");
-    if (elr->gate.format != QFMT_GGUF_Q4_K || elr->up.format != QFMT_GGUF_Q4_K || H % 256 || M % 256)
+    if (elr->gate.format != OROME_QFMT_GGUF_Q4_K || elr->up.format != OROME_QFMT_GGUF_Q4_K || H % 256 || M % 256)
         return orome_fail(OROME_EUNSUPPORTED, "orome_hip_pack_layer: routed gate/up must be Q4_K, H and M multiples of 256");
     const int S = lt->shared_gate.buffer ? (int)lt->shared_gate.out_dim : 0;
-    /* gate/up are repacked with the shared expert's (Q4_K or absent); down
-     * likewise; anything else keeps the row-major path */
-    const bool sh_gu = S && lt->shared_gate.format == QFMT_GGUF_Q4_K && lt->shared_up.format == QFMT_GGUF_Q4_K;
-    if (S && !sh_gu) return OROME_OK;
-    if (S % 16 || (S && S % 256)) return OROME_OK;
-    /* down projections: Q4_K or Q6_K on both sides (or no shared expert) */
-    auto tileable = [](QuantFormat f) { return f == QFMT_GGUF_Q4_K || f == QFMT_GGUF_Q6_K; };
-    const bool dn = tileable(elr->down.format) && (!S || tileable(lt->shared_down.format));
-    const bool rq6 = elr->down.format == QFMT_GGUF_Q6_K, sq6 = S && lt->shared_down.format == QFMT_GGUF_Q6_K;
+    if (S % 256) return orome_fail(OROME_EUNSUPPORTED, "orome_hip_pack_layer: shared intermediate %d not a multiple of 256", S);
+    /* Every matrix the tile-major spans can hold is repacked: routed gate/up
+     * (Q4_K), the shared gate/up when Q4_K, each down projection when Q4_K or
+     * Q6_K.  A Q8_0 shared expert (the reference's 35B layout) stays
+     * row-major; the grouped GEMMs read it in place beside the copies. */
+    auto tileable = [](OromeHipQuantFormat f) { return f == OROME_QFMT_GGUF_Q4_K || f == OROME_QFMT_GGUF_Q6_K; };
+    const bool sh_gu = S && lt->shared_gate.format == OROME_QFMT_GGUF_Q4_K && lt->shared_up.format == OROME_QFMT_GGUF_Q4_K;
+    const bool dn = tileable(elr->down.format), sdn_t = S && dn && tileable(lt->shared_down.format);
+    const bool rq6 = elr->down.format == OROME_QFMT_GGUF_Q6_K, sq6 = S && lt->shared_down.format == OROME_QFMT_GGUF_Q6_K;
     const size_t gu = packed_q4k_bytes(M, H, E),
                  dnb = !dn ? 0 : rq6 ? packed_q6k_bytes(H, M, E) : packed_q4k_bytes(H, M, E),
-                 sgu = S ? packed_q4k_bytes(S, H, 1) : 0,
-                 sdn = !(S && dn) ? 0 : sq6 ? packed_q6k_bytes(H, S, 1) : packed_q4k_bytes(H, S, 1);
+                 sgu = sh_gu ? packed_q4k_bytes(S, H, 1) : 0,
+                 sdn = !sdn_t ? 0 : sq6 ? packed_q6k_bytes(H, S, 1) : packed_q4k_bytes(H, S, 1);
     if (set_dev(c)) return OROME_EHIP;
     const uint8_t *gate = dev_addr(elr->buffer, elr->gate.offset), *sh_gate = S ? dev_addr(lt->shared_gate.buffer, lt->shared_gate.offset) : NULL;
     if (c->npacks == c->pcap) {
@@ -332,8 +334,9 @@ extern "C" int orome_hip_pack_layer(orome_hip_ctx *c, const ModelConfig *cfg, co
     Pack pk = {};
     pk.key = gate;
     pk.sh_key = sh_gate;
-    /* router copy (fp32 router only): fp16 rows, scales, norms */
-    const bool rt = lt->routing_gate.buffer && lt->routing_gate.format == QFMT_F32 && H % 128 == 0;
+    /* router copy (fp32 router, whatever the shared expert's format): fp16
+     * rows, scales, norms */
+    const bool rt = lt->routing_gate.buffer && lt->routing_gate.format == OROME_QFMT_F32 && H % 128 == 0;
     const size_t rb16 = rt ? ((size_t)E * H * 2 + 255) / 256 * 256 : 0, rbf = rt ? ((size_t)E * 4 + 255) / 256 * 256 : 0;
     const size_t body = (2 * gu + dnb + 2 * sgu + sdn + 255) / 256 * 256;
     HIP_OK(hipMalloc(&pk.mem, body + rb16 + 2 * rbf), OROME_ENOMEM);
@@ -361,19 +364,19 @@ extern "C" int orome_hip_pack_layer(orome_hip_ctx *c, const ModelConfig *cfg, co
         m += dnb;
         pk.down_stride = dnb / E;
     }
-    if (S) {
+    if (sh_gu) {
         pk.sgate = m;
         rc |= launch_pack_q4k(sh_gate, m, S, H, 1, 0, c->stream);
         m += sgu;
         pk.sup = m;
         rc |= launch_pack_q4k(dev_addr(lt->shared_up.buffer, lt->shared_up.offset), m, S, H, 1, 0, c->stream);
         m += sgu;
-        if (dn) {
-            pk.sdown = m;
-            pk.sdown_fmt = sq6 ? GEMM_FMT_Q6K_TILED : GEMM_FMT_Q4K_TILED;
-            rc |= (sq6 ? launch_pack_q6k : launch_pack_q4k)(dev_addr(lt->shared_down.buffer, lt->shared_down.offset), m,
-                                                             H, S, 1, 0, c->stream);
-        }
+    }
+    if (sdn_t) {
+        pk.sdown = m;
+        pk.sdown_fmt = sq6 ? GEMM_FMT_Q6K_TILED : GEMM_FMT_Q4K_TILED;
+        rc |= (sq6 ? launch_pack_q6k : launch_pack_q4k)(dev_addr(lt->shared_down.buffer, lt->shared_down.offset), m,
+                                                         H, S, 1, 0, c->stream);
     }
     if (rc || hipStreamSynchronize(c->stream) != hipSuccess) {
         (void)hipFree(pk.mem);
@@ -416,17 +419,17 @@ static int launch_rc(int rc, const char *what) {
         if (rc_) return rc_;                \
     } while (0)
 
-/* launch with optional per-stage event bracketing */
+/* launch with optional per-stage event bracketing (on the call's stream s) */
 #define TLAUNCH(c, st, call, what)                                                         \
     do {                                                                                   \
         hipEvent_t *ev_ = NULL;                                                            \
         if ((c)->timing) {                                                                 \
             ev_ = &(c)->ev[((st) * (c)->tcap + (c)->tcount[st] % (c)->tcap) * 2];          \
-            (void)hipEventRecord(ev_[0], (c)->stream);                                     \
+            (void)hipEventRecord(ev_[0], s);                                     \
         }                                                                                  \
         LAUNCH(call, what);                                                                \
         if (ev_) {                                                                         \
-            (void)hipEventRecord(ev_[1], (c)->stream);                                     \
+            (void)hipEventRecord(ev_[1], s);                                     \
             (c)->tcount[st]++;                                                             \
         }                                                                                  \
     } while (0)
@@ -434,9 +437,15 @@ static int launch_rc(int rc, const char *what) {
 /* The MoE block on x (or, with norm_h, on RMSNorm(norm_h) * bf16(norm_w),
  * which the small-batch router computes itself and the large-batch path
  * computes in a separate kernel first). */
-static int forward_impl(orome_hip_ctx *c, const ModelConfig *cfg, const ExpertLayerRef *elr,
-                        const LayerTensorCache *lt, const float *x, const float *h_in, float *h_out, int T,
-                        int K, const float *norm_h, const float *norm_w,
+/* Outputs beside h_out: the residual copy and the Sigma h^2 parts (either
+ * may be NULL). */
+struct FwdOut {
+    float *res, *ssq;
+};
+
+static int forward_impl(orome_hip_ctx *c, const OromeHipModelConfig *cfg, const OromeHipExpertLayerRef *elr,
+                        const OromeHipLayerTensorCache *lt, const float *x, const float *h_in, float *h_out, int T,
+                        int K, const float *norm_h, const float *norm_w, hipStream_t s, FwdOut fo,
                         const float *next_norm_w = NULL, int fuse_next_norm = 0, int pre_normed = 0) {
     if (!c || !cfg || !elr || !lt || !(x || norm_h) || !h_out)
         return orome_fail(OROME_EINVAL, "orome_moe_forward: NULL argument");
@@ -448,11 +457,11 @@ static int forward_impl(orome_hip_ctx *c, const ModelConfig *cfg, const ExpertLa
     if (K < 1 || K > OROME_MAX_ACTIVE || K > E)
         return orome_fail(OROME_EINVAL, "orome_moe_forward: K=%d outside 1..min(%d, E)", K, OROME_MAX_ACTIVE);
     if (H % 256 || M % 256) return orome_fail(OROME_EUNSUPPORTED, "orome_moe_forward: H and M must be multiples of 256");
-    if (!elr->buffer || elr->gate.format != QFMT_GGUF_Q4_K || elr->up.format != QFMT_GGUF_Q4_K)
+    if (!elr->buffer || elr->gate.format != OROME_QFMT_GGUF_Q4_K || elr->up.format != OROME_QFMT_GGUF_Q4_K)
         return orome_fail(OROME_EUNSUPPORTED, "orome_moe_forward: routed gate/up must be Q4_K");
     if (kfmt(elr->down.format) != 0 && kfmt(elr->down.format) != 2)
         return orome_fail(OROME_EUNSUPPORTED, "orome_moe_forward: routed down must be Q4_K or Q6_K");
-    if (!lt->routing_gate.buffer || lt->routing_gate.format != QFMT_F32)
+    if (!lt->routing_gate.buffer || lt->routing_gate.format != OROME_QFMT_F32)
         return orome_fail(OROME_EUNSUPPORTED, "orome_moe_forward: router must be F32");
     const int S = lt->shared_gate.buffer ? (int)lt->shared_gate.out_dim : 0;
     SharedSide sh = {NULL, NULL, NULL, 0, 0, 0};
@@ -483,7 +492,7 @@ static int forward_impl(orome_hip_ctx *c, const ModelConfig *cfg, const ExpertLa
 
     RouteArgs a;
     a.W = (const float *)dev_addr(lt->routing_gate.buffer, lt->routing_gate.offset);
-    a.wsg = lt->shared_expert_gate.buffer && lt->shared_expert_gate.format == QFMT_F32
+    a.wsg = lt->shared_expert_gate.buffer && lt->shared_expert_gate.format == OROME_QFMT_F32
                 ? (const float *)dev_addr(lt->shared_expert_gate.buffer, lt->shared_expert_gate.offset)
                 : NULL;
     a.bias = lt->routing_bias.buffer ? (const float *)dev_addr(lt->routing_bias.buffer, lt->routing_bias.offset) : NULL;
@@ -511,7 +520,7 @@ static int forward_impl(orome_hip_ctx *c, const ModelConfig *cfg, const ExpertLa
     const bool hybrid = path == OROME_PATH_AUTO && T >= 3 && T <= 16 && T * K <= 256 &&
                         gemm_small_tiles_ok(hx, hs, H, M);
     if (path == OROME_PATH_AUTO) path = T <= 8 || hybrid ? OROME_PATH_GEMV : OROME_PATH_MFMA;
-    hipStream_t s = c->stream;
+    c->last_stream = s;
     if (norm_h) {
         if (path == OROME_PATH_GEMV) { /* the router kernel normalises and writes xnorm */
             a.norm_h = norm_h;
@@ -547,7 +556,7 @@ static int forward_impl(orome_hip_ctx *c, const ModelConfig *cfg, const ExpertLa
                     launch_gemm_down(hx, hs, c->act, c->act_sh, c->tmax * c->kmax, c->tmax, T, H, M, K, E,
                                      GEMM_TILE_SMALL, c->tiles, ns_max, c->y, c->ysh, s),
                     "grouped down (small tiles)");
-            TLAUNCH(c, ST_COMBINE, launch_combine(c->y, c->ysh, c->pos, c->w, c->sgl, S ? 1 : 0, h_in, h_out, T, H, K, s),
+            TLAUNCH(c, ST_COMBINE, launch_combine(c->y, c->ysh, c->pos, c->w, c->sgl, S ? 1 : 0, h_in, h_out, fo.res, fo.ssq, T, H, K, s),
                     "combine");
             c->last_T = T;
             c->last_K = K;
@@ -558,13 +567,14 @@ static int forward_impl(orome_hip_ctx *c, const ModelConfig *cfg, const ExpertLa
         /* one token: down and combine in one kernel when the shape allows */
         const bool dc1 = T == 1 && K <= 8 && M == 512 && (!S || S == 512);
         if (dc1) {
-            TLAUNCH(c, ST_DOWN, launch_gemv_down_combine1(ex, sh, a, c->act, c->act_sh, H, M, K, h_in, h_out, s),
+            TLAUNCH(c, ST_DOWN, launch_gemv_down_combine1(ex, sh, a, c->act, c->act_sh, H, M, K, h_in, h_out, fo.res, s),
                     "gemv down + combine");
+            if (fo.ssq) TLAUNCH(c, ST_COMBINE, launch_sumsq_parts(h_out, T, H, fo.ssq, s), "sum-of-squares parts");
         } else {
             TLAUNCH(c, ST_DOWN, launch_gemv_down(ex, sh, c->act, c->act_sh, T, H, M, K, E, c->list, c->y, c->ysh, s),
                     "gemv down");
             TLAUNCH(c, ST_COMBINE,
-                    launch_combine(c->y, c->ysh, c->pos, c->w, c->sgl, S ? 1 : 0, h_in, h_out, T, H, K, s),
+                    launch_combine(c->y, c->ysh, c->pos, c->w, c->sgl, S ? 1 : 0, h_in, h_out, fo.res, fo.ssq, T, H, K, s),
                     "combine");
         }
     } else {
@@ -625,11 +635,11 @@ static int forward_impl(orome_hip_ctx *c, const ModelConfig *cfg, const ExpertLa
         }
         if (fuse_next_norm) /* also the next layer's RMSNorm of h_out into xnorm */
             TLAUNCH(c, ST_COMBINE,
-                    launch_combine_norm(c->y, c->ysh, c->pos, c->w, c->sgl, S ? 1 : 0, h_in, h_out, T, H, K, next_norm_w,
+                    launch_combine_norm(c->y, c->ysh, c->pos, c->w, c->sgl, S ? 1 : 0, h_in, h_out, fo.res, fo.ssq, T, H, K, next_norm_w,
                                         cfg->rms_norm_eps, c->xnorm, s),
                     "combine + next RMSNorm");
         else
-            TLAUNCH(c, ST_COMBINE, launch_combine(c->y, c->ysh, c->pos, c->w, c->sgl, S ? 1 : 0, h_in, h_out, T, H, K, s),
+            TLAUNCH(c, ST_COMBINE, launch_combine(c->y, c->ysh, c->pos, c->w, c->sgl, S ? 1 : 0, h_in, h_out, fo.res, fo.ssq, T, H, K, s),
                     "combine");
     }
     c->last_T = T;
@@ -637,28 +647,33 @@ static int forward_impl(orome_hip_ctx *c, const ModelConfig *cfg, const ExpertLa
     return OROME_OK;
 }
 
-extern "C" int orome_moe_forward(orome_hip_ctx *c, const ModelConfig *cfg, const ExpertLayerRef *elr,
-                                 const LayerTensorCache *lt, const float *x, const float *h_in,
-                                 float *h_out, int T, int K) {
-    if (!x) return orome_fail(OROME_EINVAL, "orome_moe_forward: NULL argument");
-    return forward_impl(c, cfg, elr, lt, x, h_in, h_out, T, K, NULL, NULL);
+static hipStream_t call_stream(const orome_hip_ctx *c, void *stream) {
+    return stream ? (hipStream_t)stream : c->stream;
 }
 
-extern "C" int orome_moe_layer_forward(orome_hip_ctx *c, const ModelConfig *cfg,
-                                       const ExpertLayerRef *elr, const LayerTensorCache *lt,
-                                       float *h, int T, int K) {
+extern "C" int orome_moe_forward(orome_hip_ctx *c, const OromeHipModelConfig *cfg, const OromeHipExpertLayerRef *elr,
+                                 const OromeHipLayerTensorCache *lt, const float *x, const float *h_in, float *h_out,
+                                 float *residual_out, float *sumsq_parts, int T, int K, void *stream) {
+    if (!c || !x) return orome_fail(OROME_EINVAL, "orome_moe_forward: NULL argument");
+    return forward_impl(c, cfg, elr, lt, x, h_in, h_out, T, K, NULL, NULL, call_stream(c, stream),
+                        FwdOut{residual_out, sumsq_parts});
+}
+
+extern "C" int orome_moe_layer_forward(orome_hip_ctx *c, const OromeHipModelConfig *cfg,
+                                       const OromeHipExpertLayerRef *elr, const OromeHipLayerTensorCache *lt,
+                                       float *h, int T, int K, void *stream) {
     if (!c || !cfg || !lt || !h) return orome_fail(OROME_EINVAL, "orome_moe_layer_forward: NULL argument");
     if (T < 1 || T > c->tmax) return orome_fail(OROME_EINVAL, "orome_moe_layer_forward: T=%d", T);
     if (set_dev(c)) return OROME_EHIP;
-    const float *nw = lt->post_norm.buffer && lt->post_norm.format == QFMT_F32
+    const float *nw = lt->post_norm.buffer && lt->post_norm.format == OROME_QFMT_F32
                           ? (const float *)dev_addr(lt->post_norm.buffer, lt->post_norm.offset)
                           : NULL;
-    return forward_impl(c, cfg, elr, lt, NULL, h, h, T, K, h, nw);
+    return forward_impl(c, cfg, elr, lt, NULL, h, h, T, K, h, nw, call_stream(c, stream), FwdOut{NULL, NULL});
 }
 
-extern "C" int orome_moe_stack_forward(orome_hip_ctx *c, const ModelConfig *cfg,
-                                       const ExpertLayerRef *elrs, const LayerTensorCache *lts,
-                                       int n_layers, float *h, int T, int K) {
+extern "C" int orome_moe_stack_forward(orome_hip_ctx *c, const OromeHipModelConfig *cfg,
+                                       const OromeHipExpertLayerRef *elrs, const OromeHipLayerTensorCache *lts,
+                                       int n_layers, float *h, int T, int K, void *stream) {
     if (!elrs || !lts || n_layers < 0) return orome_fail(OROME_EINVAL, "orome_moe_stack_forward: bad arguments");
     if (!c || !cfg || !h) return orome_fail(OROME_EINVAL, "orome_moe_stack_forward: NULL argument");
     if (T < 1 || T > c->tmax) return orome_fail(OROME_EINVAL, "orome_moe_stack_forward: T=%d", T);
@@ -670,15 +685,16 @@ extern "C" int orome_moe_stack_forward(orome_hip_ctx *c, const ModelConfig *cfg,
     const int path = c->path == OROME_PATH_AUTO ? (T <= 16 ? OROME_PATH_GEMV : OROME_PATH_MFMA) : c->path;
     const bool fuse = path == OROME_PATH_MFMA && cfg->hidden_dim % 512 == 0 && cfg->hidden_dim <= 4096;
     auto norm_w = [&](int l) -> const float * {
-        return lts[l].post_norm.buffer && lts[l].post_norm.format == QFMT_F32
+        return lts[l].post_norm.buffer && lts[l].post_norm.format == OROME_QFMT_F32
                    ? (const float *)dev_addr(lts[l].post_norm.buffer, lts[l].post_norm.offset)
                    : NULL;
     };
+    const hipStream_t s = call_stream(c, stream);
     for (int l = 0; l < n_layers; l++) {
         if (!lts[l].routing_gate.buffer) return orome_fail(OROME_EINVAL, "orome_moe_stack_forward: layer %d", l);
         const bool next = fuse && l + 1 < n_layers;
-        int rc = forward_impl(c, cfg, &elrs[l], &lts[l], NULL, h, h, T, K, h, norm_w(l), next ? norm_w(l + 1) : NULL,
-                              next ? 1 : 0, fuse && l > 0 ? 1 : 0);
+        int rc = forward_impl(c, cfg, &elrs[l], &lts[l], NULL, h, h, T, K, h, norm_w(l), s, FwdOut{NULL, NULL},
+                              next ? norm_w(l + 1) : NULL, next ? 1 : 0, fuse && l > 0 ? 1 : 0);
         if (rc) return rc;
     }
     return OROME_OK;
@@ -689,6 +705,8 @@ extern "C" int orome_moe_debug_outputs(orome_hip_ctx *c, float *logits, int32_t 
     if (!c) return orome_fail(OROME_EINVAL, "orome_moe_debug_outputs: NULL ctx");
     if (!c->last_T) return orome_fail(OROME_EINVAL, "orome_moe_debug_outputs: no forward yet");
     const size_t T = (size_t)c->last_T, K = (size_t)c->last_K, E = (size_t)c->cfg.num_experts;
+    if (set_dev(c)) return OROME_EHIP;
+    if (c->last_stream) HIP_OK(hipStreamSynchronize(c->last_stream), OROME_EHIP);
     int rc = 0;
     if (!rc && logits) rc = orome_hip_dtoh(c, logits, c->logits, T * (E + 1) * 4);
     if (!rc && idx) rc = orome_hip_dtoh(c, idx, c->idx, T * K * 4);
@@ -713,7 +731,7 @@ extern "C" int orome_moe_topk(orome_hip_ctx *c, const float *logits, const float
     return OROME_OK;
 }
 
-extern "C" int orome_dequant_rows(orome_hip_ctx *c, QuantFormat fmt, const void *src, uint32_t rows,
+extern "C" int orome_dequant_rows(orome_hip_ctx *c, OromeHipQuantFormat fmt, const void *src, uint32_t rows,
                                   uint32_t in_dim, float *out) {
     if (!c || !src || !out) return orome_fail(OROME_EINVAL, "orome_dequant_rows: NULL argument");
     if (set_dev(c)) return OROME_EHIP;
@@ -721,7 +739,7 @@ extern "C" int orome_dequant_rows(orome_hip_ctx *c, QuantFormat fmt, const void 
     return OROME_OK;
 }
 
-extern "C" int orome_dequant_rows_f16(orome_hip_ctx *c, QuantFormat fmt, const void *src,
+extern "C" int orome_dequant_rows_f16(orome_hip_ctx *c, OromeHipQuantFormat fmt, const void *src,
                                       uint32_t rows, uint32_t in_dim, uint16_t *out) {
     if (!c || !src || !out) return orome_fail(OROME_EINVAL, "orome_dequant_rows_f16: NULL argument");
     if (set_dev(c)) return OROME_EHIP;

@@ -89,7 +89,7 @@ int launch_gemv_down(const ExpertSide &ex, const SharedSide &sh, const _Float16 
  * (K <= 8, M = S = 512); returns -2 when the shape is not covered */
 int launch_gemv_down_combine1(const ExpertSide &ex, const SharedSide &sh, const RouteArgs &ra,
                               const _Float16 *act, const _Float16 *act_sh, int H, int M, int K,
-                              const float *h_in, float *h_out, hipStream_t s);
+                              const float *h_in, float *h_out, float *res, hipStream_t s);
 int launch_delay(uint32_t usec, hipStream_t s);
 int launch_rmsnorm(const float *h, const float *w, int T, int H, float eps, float *x, hipStream_t s);
 int launch_dequant(int fmt, const uint8_t *src, uint32_t rows, uint32_t n, float *out32,
@@ -116,11 +116,15 @@ int launch_pack_q6k(const uint8_t *src, uint8_t *dst, int R, int K, int E, size_
 /* prefill combine of one token per wave that also writes the next layer's
  * RMSNorm of h_out into xnorm (nw: its weight, or NULL for ones) */
 int launch_combine_norm(const float *y, const float *ysh, const uint32_t *pos, const float *w, const float *sgl,
-                        int has_shared, const float *h_in, float *h_out, int T, int H, int K, const float *nw,
-                        float eps, float *xnorm, hipStream_t s);
+                        int has_shared, const float *h_in, float *h_out, float *res, float *ssq, int T, int H, int K,
+                        const float *nw, float eps, float *xnorm, hipStream_t s);
+/* combine; res (a copy of h_out) and ssq (the [T][H/256] canonical Sigma h^2
+ * parts) may be NULL */
 int launch_combine(const float *y, const float *ysh, const uint32_t *pos, const float *w,
-                   const float *sgl, int has_shared, const float *h_in, float *h_out, int T,
-                   int H, int K, hipStream_t s);
+                   const float *sgl, int has_shared, const float *h_in, float *h_out, float *res, float *ssq,
+                   int T, int H, int K, hipStream_t s);
+/* ssq[t][b] = canonical sum of h[t][256 b .. 256 b + 255]^2 */
+int launch_sumsq_parts(const float *h, int T, int H, float *ssq, hipStream_t s);
 
 /* tile list for the grouped GEMM: tiles[0] = count, then (expert, first, rows)
  * triples; expert == E denotes the shared expert over all T tokens */

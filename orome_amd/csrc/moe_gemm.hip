@@ -721,7 +721,9 @@ struct DnPol {
 };
 
 
-template <int SFMT, int NST, int TBM>
+/* RF: routed gate/up format (Q4_K, row-major or tile-major); SF: the shared
+ * expert's (the same, or Q8_0 row-major) */
+template <int RF, int SF, int NST, int TBM>
 DEV void k_gemm_gate_up_body(GemmArgs a) {
     __shared__ __attribute__((aligned(16))) _Float16 xs[2 * TBM * 16 * BLD];
     __shared__ int rowoff[TBM * 16];
@@ -740,20 +742,19 @@ DEV void k_gemm_gate_up_body(GemmArgs a) {
     __syncthreads();
     if (sh) {
         const GuEpi epi{a.act_sh, a.S, (int)first, (int)rows};
-        tile_run<SFMT, 2, GU_RPW, (SFMT == FQ8 ? 2 : Shape<TBM>::DEPTH), NST, TBM>(a.sh_a, a.sh_b, a.H, a.src, a.H, rowoff, (int)rows, yb, xs, epi);
+        tile_run<SF, 2, GU_RPW, (SF == FQ8 ? 2 : Shape<TBM>::DEPTH), NST, TBM>(a.sh_a, a.sh_b, a.H, a.src, a.H, rowoff, (int)rows, yb, xs, epi);
     } else {
         const GuEpi epi{a.act, a.M, (int)first, (int)rows};
-        /* routed gate/up: Q4_K, tile-major exactly when the shared expert's is */
-        tile_run<(SFMT == FQ4KT ? FQ4KT : FQ4K), 2, GU_RPW, Shape<TBM>::DEPTH, NST, TBM>(a.wa + (size_t)e * a.stride_a, a.wb + (size_t)e * a.stride_b, a.H, a.src,
-                                  a.H, rowoff, (int)rows, yb, xs, epi);
+        tile_run<RF, 2, GU_RPW, Shape<TBM>::DEPTH, NST, TBM>(a.wa + (size_t)e * a.stride_a, a.wb + (size_t)e * a.stride_b, a.H, a.src,
+                                                          a.H, rowoff, (int)rows, yb, xs, epi);
     }
     if (threadIdx.x == 0) TSTAMP(6);
 }
 
-template <int SFMT, int NST, int TBM>
+template <int RF, int SF, int NST, int TBM>
 __global__ __launch_bounds__(Shape<TBM>::W * 64) void k_gemm_gate_up(GemmArgs a) {
     KT_BEGIN(a.kt);
-    k_gemm_gate_up_body<SFMT, NST, TBM>(a);
+    k_gemm_gate_up_body<RF, SF, NST, TBM>(a);
     KT_END(a.kt);
 }
 
@@ -796,7 +797,7 @@ template <int TBM, int GF>
 DEV void k_gemm_gate_up_p_body(GemmArgs a) {
     __shared__ __attribute__((aligned(16))) _Float16 xs[3 * TBM * 16 * BLD];
     __shared__ int rowoff[3 * TBM * 16];
-    tile_stream<GF, 2, GU_RPW, Shape<TBM>::DEPTH, 16, TBM>(GuPol{a}, xs, rowoff);
+    tile_stream<GF, 2, GU_RPW, (GF == FQ8 ? 2 : Shape<TBM>::DEPTH), 16, TBM>(GuPol{a}, xs, rowoff);
 }
 
 template <int TBM, int GF>
@@ -845,8 +846,8 @@ static int gate_up_shape(const ExpertSide &ex, const SharedSide &sh, int H, int 
     const int NB = W * 16 * GU_RPW;
     if ((H / KC * GU_RPW) % 4) return -2; /* every ring depth used divides the unit count */
     if (H % KCH || M % NB || (sh.gate && sh.S % NB) || (ex.gate_fmt != FQ4K && ex.gate_fmt != FQ4KT)) return -2;
-    const bool tiled = ex.gate_fmt == FQ4KT;
-    if (sh.gate && (tiled ? sh.gate_fmt != FQ4KT : sh.gate_fmt != FQ4K && sh.gate_fmt != FQ8)) return -2;
+    /* shared expert: the routed format, or Q8_0 (row-major) */
+    if (sh.gate && sh.gate_fmt != ex.gate_fmt && sh.gate_fmt != FQ8) return -2;
     return 0;
 }
 static int down_shape(const ExpertSide &ex, const SharedSide &sh, int H, int M, int tile_m) {
@@ -857,13 +858,23 @@ static int down_shape(const ExpertSide &ex, const SharedSide &sh, int H, int M, 
     if (H % NB || M % KCH || M > 2 * KCH || (sh.gate && (sh.S % KCH || sh.S > 2 * KCH))) return -2;
     const bool dtiled = ex.down_fmt == FQ4KT || ex.down_fmt == FQ6KT;
     if (ex.down_fmt != FQ4K && ex.down_fmt != FQ6K && !dtiled) return -2;
-    /* a tile-major routed down needs a tile-major shared down (or none) */
-    const int sf = sh.gate ? sh.down_fmt : dtiled ? ex.down_fmt : FQ4K;
-    if (dtiled ? sf != FQ4KT && sf != FQ6KT : sf != FQ4K && sf != FQ6K && sf != FQ8) return -2;
+    /* shared down: any supported format; with a tile-major routed down a
+     * Q4_K/Q6_K shared down must be tile-major too (the packer makes both) */
+    const int sf = sh.gate ? sh.down_fmt : ex.down_fmt;
+    if (dtiled ? sf != FQ4KT && sf != FQ6KT && sf != FQ8 : sf != FQ4K && sf != FQ6K && sf != FQ8) return -2;
     return 0;
 }
 int gemm_small_tiles_ok(const ExpertSide &ex, const SharedSide &sh, int H, int M) {
     return !gate_up_shape(ex, sh, H, M, GEMM_TILE_SMALL) && !down_shape(ex, sh, H, M, GEMM_TILE_SMALL);
+}
+
+/* The shared expert's tiles end the list that holds most of the routed work
+ * (the dispatch puts them there); how many of them this list has. */
+static int shared_tiles_in(const SharedSide &sh, int T, int K, int E, int tile_m) {
+    if (!sh.gate) return 0;
+    if (tile_m == GEMM_TILE_MIN) return 1; /* small-batch list: T <= 16, one shared tile */
+    const bool sh_small = (size_t)T * K <= (size_t)GEMM_TILE_SMALL * E;
+    return (tile_m == GEMM_TILE_SMALL) == sh_small ? (T + tile_m - 1) / tile_m : 0;
 }
 
 int launch_gemm_gate_up(const ExpertSide &ex, const SharedSide &sh, const _Float16 *x16, int zrow, int T,
@@ -871,6 +882,7 @@ int launch_gemm_gate_up(const ExpertSide &ex, const SharedSide &sh, const _Float
                         const uint32_t *pairs, _Float16 *act, _Float16 *act_sh, hipStream_t s,
                         unsigned long long *kt, int kt_cap) {
     if (gate_up_shape(ex, sh, H, M, tile_m)) return -2;
+    if (tile_m != GEMM_TILE_SMALL && tile_m != GEMM_TILE_BIG && tile_m != GEMM_TILE_MIN) return -2;
     const int W = tile_waves(tile_m);
     const int NB = W * 16 * GU_RPW;
     const bool tiled = ex.gate_fmt == FQ4KT;
@@ -886,32 +898,45 @@ int launch_gemm_gate_up(const ExpertSide &ex, const SharedSide &sh, const _Float
     const unsigned pb = !GEMM_PERSIST || tile_m == GEMM_TILE_MIN ? 0u
                         : tile_m == GEMM_TILE_BIG ? persist_blocks() : GEMM_PERSIST_SMALL * persist_blocks();
     a.kt = kt && (long)grid.x <= kt_cap ? kt : nullptr;
-    if (pb && H == 2048 && (!sh.gate || (sh.gate_fmt == ex.gate_fmt && sh.S == M))) {
+    if (pb && H == 2048 && (!sh.gate || sh.S == M)) {
         a.kt = kt && (long)pb <= kt_cap ? kt : nullptr;
-        if (tile_m == GEMM_TILE_BIG) {
-            if (tiled) hipLaunchKernelGGL((k_gemm_gate_up_p<GEMM_TILE_BIG / 16, FQ4KT>), dim3(pb), block, 0, s, a);
-            else hipLaunchKernelGGL((k_gemm_gate_up_p<GEMM_TILE_BIG / 16, FQ4K>), dim3(pb), block, 0, s, a);
+#define GP_LAUNCH(GF, ARGS)                                                                                      \
+    do {                                                                                                         \
+        if (tile_m == GEMM_TILE_BIG) hipLaunchKernelGGL((k_gemm_gate_up_p<GEMM_TILE_BIG / 16, GF>), dim3(pb), block, 0, s, ARGS); \
+        else hipLaunchKernelGGL((k_gemm_gate_up_p<GEMM_TILE_SMALL / 16, GF>), dim3(pb), block, 0, s, ARGS);          \
+    } while (0)
+        const int nsh = shared_tiles_in(sh, T, K, E, tile_m);
+        if (nsh && q8) { /* Q8_0 shared expert: one walk over the routed tiles, one over the shared */
+            GemmArgs ar = a, as = a;
+            ar.uwin = -nsh;
+            as.uwin = nsh;
+            as.kt = nullptr;
+            if (tiled) GP_LAUNCH(FQ4KT, ar);
+            else GP_LAUNCH(FQ4K, ar);
+            GP_LAUNCH(FQ8, as);
+        } else if (tiled) {
+            GP_LAUNCH(FQ4KT, a);
         } else {
-            if (tiled) hipLaunchKernelGGL((k_gemm_gate_up_p<GEMM_TILE_SMALL / 16, FQ4KT>), dim3(pb), block, 0, s, a);
-            else hipLaunchKernelGGL((k_gemm_gate_up_p<GEMM_TILE_SMALL / 16, FQ4K>), dim3(pb), block, 0, s, a);
+            GP_LAUNCH(FQ4K, a);
         }
+#undef GP_LAUNCH
         return hipGetLastError() == hipSuccess ? 0 : -3;
     }
-    if (tile_m != GEMM_TILE_SMALL && tile_m != GEMM_TILE_BIG && tile_m != GEMM_TILE_MIN) return -2;
-    /* compile-time stage count for the common hidden size (Q4_K shared
-     * expert); other shapes take the generic loop */
-#define GU_LAUNCH(SF, NS)                                                                    \
+    /* compile-time stage count for the common hidden size; other shapes
+     * take the generic loop */
+#define GU_LAUNCH(RF, SF, NS)                                                                    \
     do {                                                                                     \
-        if (tile_m == GEMM_TILE_SMALL) hipLaunchKernelGGL((k_gemm_gate_up<SF, NS, GEMM_TILE_SMALL / 16>), grid, block, 0, s, a); \
-        else if (tile_m == GEMM_TILE_MIN) hipLaunchKernelGGL((k_gemm_gate_up<SF, NS, GEMM_TILE_MIN / 16>), grid, block, 0, s, a); \
-        else hipLaunchKernelGGL((k_gemm_gate_up<SF, NS, GEMM_TILE_BIG / 16>), grid, block, 0, s, a);              \
+        if (tile_m == GEMM_TILE_SMALL) hipLaunchKernelGGL((k_gemm_gate_up<RF, SF, NS, GEMM_TILE_SMALL / 16>), grid, block, 0, s, a); \
+        else if (tile_m == GEMM_TILE_MIN) hipLaunchKernelGGL((k_gemm_gate_up<RF, SF, NS, GEMM_TILE_MIN / 16>), grid, block, 0, s, a); \
+        else hipLaunchKernelGGL((k_gemm_gate_up<RF, SF, NS, GEMM_TILE_BIG / 16>), grid, block, 0, s, a);              \
     } while (0)
     if (tiled) {
-        if (H == 2048) GU_LAUNCH(FQ4KT, 16);
-        else GU_LAUNCH(FQ4KT, 0);
-    } else if (q8) GU_LAUNCH(FQ8, 0);
-    else if (H == 2048) GU_LAUNCH(FQ4K, 16);
-    else GU_LAUNCH(FQ4K, 0);
+        if (q8) GU_LAUNCH(FQ4KT, FQ8, 0);
+        else if (H == 2048) GU_LAUNCH(FQ4KT, FQ4KT, 16);
+        else GU_LAUNCH(FQ4KT, FQ4KT, 0);
+    } else if (q8) GU_LAUNCH(FQ4K, FQ8, 0);
+    else if (H == 2048) GU_LAUNCH(FQ4K, FQ4K, 16);
+    else GU_LAUNCH(FQ4K, FQ4K, 0);
 #undef GU_LAUNCH
     return hipGetLastError() == hipSuccess ? 0 : -3;
 }
@@ -922,8 +947,7 @@ int launch_gemm_down(const ExpertSide &ex, const SharedSide &sh, const _Float16 
     if (down_shape(ex, sh, H, M, tile_m)) return -2;
     const int W = tile_waves(tile_m);
     const int NB = W * 16 * DN_RPW;
-    const bool dtiled = ex.down_fmt == FQ4KT || ex.down_fmt == FQ6KT;
-    const int sf = sh.gate ? sh.down_fmt : dtiled ? ex.down_fmt : FQ4K;
+    const int sf = sh.gate ? sh.down_fmt : ex.down_fmt;
     GemmArgs a = {};
     a.wa = ex.down; a.stride_a = ex.down_stride;
     a.sh_a = sh.gate ? sh.down : nullptr;
@@ -935,18 +959,15 @@ int launch_gemm_down(const ExpertSide &ex, const SharedSide &sh, const _Float16 
     if (tile_m != GEMM_TILE_SMALL && tile_m != GEMM_TILE_BIG && tile_m != GEMM_TILE_MIN) return -2;
     const unsigned pb = !GEMM_PERSIST || tile_m == GEMM_TILE_MIN ? 0u
                         : tile_m == GEMM_TILE_BIG ? persist_blocks() : GEMM_PERSIST_SMALL_DN * persist_blocks();
-    /* the shared expert's tiles end the list that holds most of the routed
-     * work (as the dispatch builds it); nsh of them here */
-    const bool sh_small = (size_t)T * K <= (size_t)GEMM_TILE_SMALL * E;
-    const int nsh = sh.gate && (tile_m == GEMM_TILE_SMALL) == sh_small ? (T + tile_m - 1) / tile_m : 0;
+    const int nsh = shared_tiles_in(sh, T, K, E, tile_m);
     const bool mixed = nsh && sf != ex.down_fmt;
-    const bool two_tiled = (ex.down_fmt == FQ4KT || ex.down_fmt == FQ6KT) && (sf == FQ4KT || sf == FQ6KT);
-    if (pb && M == 512 && (!nsh || sh.S == M) && (!mixed || two_tiled)) {
+    if (pb && M == 512 && (!nsh || sh.S == M)) {
 #define DP_LAUNCH(F, TB, ARGS)                                                                                        \
     do {                                                                                                              \
         if ((F) == FQ4K) hipLaunchKernelGGL((k_gemm_down_p<FQ4K, TB>), dim3(pb), block, 0, s, ARGS);                    \
         else if ((F) == FQ4KT) hipLaunchKernelGGL((k_gemm_down_p<FQ4KT, TB>), dim3(pb), block, 0, s, ARGS);             \
         else if ((F) == FQ6KT) hipLaunchKernelGGL((k_gemm_down_p<FQ6KT, TB>), dim3(pb), block, 0, s, ARGS);             \
+        else if ((F) == FQ8) hipLaunchKernelGGL((k_gemm_down_p<FQ8, TB>), dim3(pb), block, 0, s, ARGS);                 \
         else hipLaunchKernelGGL((k_gemm_down_p<FQ6K, TB>), dim3(pb), block, 0, s, ARGS);                                \
     } while (0)
 #define DP_TILE(F, ARGS)                                                        \
@@ -976,10 +997,12 @@ int launch_gemm_down(const ExpertSide &ex, const SharedSide &sh, const _Float16 
     } while (0)
     if (ex.down_fmt == FQ4KT) {
         if (sf == FQ4KT) DN_LAUNCH(FQ4KT, FQ4KT);
-        else DN_LAUNCH(FQ4KT, FQ6KT);
+        else if (sf == FQ6KT) DN_LAUNCH(FQ4KT, FQ6KT);
+        else DN_LAUNCH(FQ4KT, FQ8);
     } else if (ex.down_fmt == FQ6KT) {
         if (sf == FQ4KT) DN_LAUNCH(FQ6KT, FQ4KT);
-        else DN_LAUNCH(FQ6KT, FQ6KT);
+        else if (sf == FQ6KT) DN_LAUNCH(FQ6KT, FQ6KT);
+        else DN_LAUNCH(FQ6KT, FQ8);
     } else if (ex.down_fmt == FQ4K) {
         if (sf == FQ4K) DN_LAUNCH(FQ4K, FQ4K);
         else if (sf == FQ6K) DN_LAUNCH(FQ4K, FQ6K);

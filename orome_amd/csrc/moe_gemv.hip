@@ -944,7 +944,7 @@ struct DnX<FQ8> {
 
 template <int EFMT, int SFMT>
 __global__ __launch_bounds__(128) void k_gemv_down_combine1(DownArgs a, RouteArgs ra, const float *h_in,
-                                                            float *h_out) {
+                                                            float *h_out, float *res) {
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int cl = lane & 15, r = blockIdx.x * 8 + wv * 4 + (lane >> 4);
     const int K = a.K;
@@ -1010,6 +1010,7 @@ __global__ __launch_bounds__(128) void k_gemv_down_combine1(DownArgs a, RouteArg
         float o = (h_in ? hb : 0.0f) + moe;
         if (has_sh) o = o + sigmoid_f(sgv) * ysh;
         h_out[r] = o;
+        if (res) res[r] = o;
     }
 }
 
@@ -1173,7 +1174,7 @@ int launch_gemv_down(const ExpertSide &ex, const SharedSide &sh, const _Float16 
 
 int launch_gemv_down_combine1(const ExpertSide &ex, const SharedSide &sh, const RouteArgs &ra,
                               const _Float16 *act, const _Float16 *act_sh, int H, int M, int K,
-                              const float *h_in, float *h_out, hipStream_t s) {
+                              const float *h_in, float *h_out, float *res, hipStream_t s) {
     if (K < 1 || K > DC_K || H % 8 || M != 512 || (sh.gate && sh.S != 512)) return -2;
     if (ex.down_fmt != FQ4K && ex.down_fmt != FQ6K) return -2;
     const int sf = sh.gate ? sh.down_fmt : FQ4K;
@@ -1182,7 +1183,7 @@ int launch_gemv_down_combine1(const ExpertSide &ex, const SharedSide &sh, const 
     a.down = ex.down; a.down_stride = ex.down_stride; a.fmt = ex.down_fmt;
     a.sh_down = sh.gate ? sh.down : nullptr; a.sh_fmt = sf; a.S = sh.gate ? sh.S : 0;
     a.act = act; a.act_sh = act_sh; a.T = 1; a.H = H; a.M = M; a.K = K;
-#define DC_LAUNCH(EF, SF) hipLaunchKernelGGL((k_gemv_down_combine1<EF, SF>), dim3(H / 8), dim3(128), 0, s, a, ra, h_in, h_out)
+#define DC_LAUNCH(EF, SF) hipLaunchKernelGGL((k_gemv_down_combine1<EF, SF>), dim3(H / 8), dim3(128), 0, s, a, ra, h_in, h_out, res)
     if (ex.down_fmt == FQ4K) {
         if (sf == FQ4K) DC_LAUNCH(FQ4K, FQ4K);
         else if (sf == FQ6K) DC_LAUNCH(FQ4K, FQ6K);

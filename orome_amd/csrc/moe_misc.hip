@@ -128,10 +128,26 @@ DEV void combine_pairs(const uint32_t *pos, const float *w, int t, int K, uint32
     for (int k = 0; k < KM; k++) asm volatile("" : : "s"(wk[k]));
 }
 
+/* Canonical sum of squares of the 256 columns a wave holds as one f4 per
+ * lane (columns 4 L .. 4 L + 3 at lane L): fma over the four from zero, then
+ * the canonical wave sum.  Part b of a row is this over columns 256 b ..
+ * 256 b + 255, the Sigma h^2 partial of moe_combine_copy_sq_k8
+ * (inference/src/shaders.metal:1079-1135) in this library's fixed order. */
+DEV float sumsq_part(f4 o) {
+    float acc = 0.0f;
+    acc = __builtin_fmaf(o.x, o.x, acc);
+    acc = __builtin_fmaf(o.y, o.y, acc);
+    acc = __builtin_fmaf(o.z, o.z, acc);
+    acc = __builtin_fmaf(o.w, o.w, acc);
+    return wave_sum_canon(acc);
+}
+
+/* res: copy of h_out (or NULL); ssq: [T][H/256] parts (or NULL; the
+ * launcher passes it only when every wave holds whole 256-column blocks) */
 template <int KM>
 __global__ void k_combine(const float *y, const float *ysh, const uint32_t *pos, const float *w,
-                          const float *sgl, int has_sh, const float *h_in, float *h_out, int T,
-                          int H, int K) {
+                          const float *sgl, int has_sh, const float *h_in, float *h_out, float *res, float *ssq,
+                          int T, int H, int K) {
     const int t = blockIdx.y;
     const int c = min((int)(blockIdx.x * blockDim.x + threadIdx.x) * 4, H - 4);
     const bool live = (int)(blockIdx.x * blockDim.x + threadIdx.x) * 4 < H;
@@ -147,7 +163,29 @@ __global__ void k_combine(const float *y, const float *ysh, const uint32_t *pos,
     const f4 sv = *(const f4 *)((has_sh ? ysh : y) + (size_t)t * H + c);
     const float g = has_sh ? sigmoid_f(sgt) : 0.0f;
     const f4 o = combine4<KM>(v, wk, K, h_in ? hb : f4{0, 0, 0, 0}, sv, g, has_sh);
-    if (live) *(f4 *)(h_out + (size_t)t * H + c) = o;
+    if (live) {
+        *(f4 *)(h_out + (size_t)t * H + c) = o;
+        if (res) *(f4 *)(res + (size_t)t * H + c) = o;
+    }
+    if (ssq) { /* whole waves of 256 live columns (H % 1024 == 0) */
+        const float part = sumsq_part(o);
+        if ((threadIdx.x & 63) == 0) ssq[(size_t)t * (H / 256) + c / 256] = part;
+    }
+}
+
+/* Sigma h^2 parts of rows already written (sumsq_part per 256 columns): one
+ * wave per (block b, token t). */
+__global__ __launch_bounds__(64) void k_sumsq_parts(const float *h, int H, float *ssq) {
+    const int b = blockIdx.x, t = blockIdx.y, lane = threadIdx.x;
+    const f4 o = *(const f4 *)(h + (size_t)t * H + 256 * b + 4 * lane);
+    const float part = sumsq_part(o);
+    if (lane == 0) ssq[(size_t)t * (H / 256) + b] = part;
+}
+
+int launch_sumsq_parts(const float *h, int T, int H, float *ssq, hipStream_t s) {
+    if (H % 256) return -2;
+    hipLaunchKernelGGL(k_sumsq_parts, dim3((unsigned)(H / 256), (unsigned)T), dim3(64), 0, s, h, H, ssq);
+    return hipGetLastError() == hipSuccess ? 0 : -3;
 }
 
 /* Prefill combine with the next layer's RMSNorm (k_rmsnorm's arithmetic)
@@ -160,8 +198,9 @@ __global__ void k_combine(const float *y, const float *ysh, const uint32_t *pos,
 template <int CN_W, int KM>
 __global__ __launch_bounds__(64 * CN_W) void k_combine_norm(const float *y, const float *ysh, const uint32_t *pos,
                                                              const float *w, const float *sgl, int has_sh,
-                                                             const float *h_in, float *h_out, int T, int H, int K,
-                                                             const float *nw, float eps, float *xnorm) {
+                                                             const float *h_in, float *h_out, float *res, float *ssq,
+                                                             int T, int H, int K, const float *nw, float eps,
+                                                             float *xnorm) {
     __shared__ f4 ro[CANON_NI][64];
     __shared__ float sc;
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, t = blockIdx.x;
@@ -188,7 +227,12 @@ __global__ __launch_bounds__(64 * CN_W) void k_combine_norm(const float *y, cons
         if (i < NI) {
             const f4 o = combine4<KM>(v[q], wk, K, h_in ? hb[q] : f4{0, 0, 0, 0}, sv[q], g, has_sh);
             *(f4 *)(h_out + (size_t)t * H + c) = o;
+            if (res) *(f4 *)(res + (size_t)t * H + c) = o;
             ro[i][lane] = o;
+            if (ssq) {
+                const float part = sumsq_part(o);
+                if (lane == 0) ssq[(size_t)t * NI + i] = part;
+            }
         }
     }
     __syncthreads();
@@ -225,18 +269,18 @@ __global__ __launch_bounds__(64 * CN_W) void k_combine_norm(const float *y, cons
 }
 
 int launch_combine_norm(const float *y, const float *ysh, const uint32_t *pos, const float *w, const float *sgl,
-                        int has_shared, const float *h_in, float *h_out, int T, int H, int K, const float *nw,
-                        float eps, float *xnorm, hipStream_t s) {
+                        int has_shared, const float *h_in, float *h_out, float *res, float *ssq, int T, int H, int K,
+                        const float *nw, float eps, float *xnorm, hipStream_t s) {
     const int NI = H / 256;
     if (H % 512 || NI > 2 * 8 || NI > CANON_NI || K < 1 || K > OROME_MAXK) return -2;
 #define CN_LAUNCH(CW)                                                                                            \
     do {                                                                                                         \
         if (K <= 8)                                                                                              \
             hipLaunchKernelGGL((k_combine_norm<CW, 8>), dim3((unsigned)T), dim3(64 * CW), 0, s, y, ysh, pos, w,   \
-                               sgl, has_shared, h_in, h_out, T, H, K, nw, eps, xnorm);                           \
+                               sgl, has_shared, h_in, h_out, res, ssq, T, H, K, nw, eps, xnorm);               \
         else                                                                                                     \
             hipLaunchKernelGGL((k_combine_norm<CW, OROME_MAXK>), dim3((unsigned)T), dim3(64 * CW), 0, s, y, ysh, \
-                               pos, w, sgl, has_shared, h_in, h_out, T, H, K, nw, eps, xnorm);                   \
+                               pos, w, sgl, has_shared, h_in, h_out, res, ssq, T, H, K, nw, eps, xnorm);         \
     } while (0)
     switch (NI / 2) {
         case 1: CN_LAUNCH(1); break;
@@ -253,16 +297,22 @@ int launch_combine_norm(const float *y, const float *ysh, const uint32_t *pos, c
 }
 
 int launch_combine(const float *y, const float *ysh, const uint32_t *pos, const float *w,
-                   const float *sgl, int has_shared, const float *h_in, float *h_out, int T, int H,
-                   int K, hipStream_t s) {
+                   const float *sgl, int has_shared, const float *h_in, float *h_out, float *res, float *ssq,
+                   int T, int H, int K, hipStream_t s) {
     if (H % 4 || K < 1 || K > OROME_MAXK) return -2;
     dim3 grid((H / 4 + 255) / 256, T);
+    /* the parts come out of the combine when its waves hold whole 256-column
+     * blocks; otherwise from a pass over h_out */
+    float *fused = H % 1024 == 0 ? ssq : nullptr;
     if (K <= 8)
-        hipLaunchKernelGGL(k_combine<8>, grid, dim3(256), 0, s, y, ysh, pos, w, sgl, has_shared, h_in, h_out, T, H, K);
+        hipLaunchKernelGGL(k_combine<8>, grid, dim3(256), 0, s, y, ysh, pos, w, sgl, has_shared, h_in, h_out, res,
+                           fused, T, H, K);
     else
         hipLaunchKernelGGL(k_combine<OROME_MAXK>, grid, dim3(256), 0, s, y, ysh, pos, w, sgl, has_shared, h_in, h_out,
-                           T, H, K);
-    return hipGetLastError() == hipSuccess ? 0 : -3;
+                           res, fused, T, H, K);
+    if (hipGetLastError() != hipSuccess) return -3;
+    if (ssq && !fused) return launch_sumsq_parts(h_out, T, H, ssq, s);
+    return 0;
 }
 
 /* Bounded busy-wait on the GPU (one lane): holds the stream for `ticks` of the

@@ -7,6 +7,7 @@ per-layer MoE step of engine_step (inference/src/engine.m:656-694).
 Every compute call goes through liborome_moe.so; nothing here computes.
 """
 import ctypes as C
+import weakref
 
 import numpy as np
 
@@ -15,7 +16,8 @@ from ._lib import check, lib
 
 
 class DeviceBuffer:
-    """A device allocation on a context's GPU."""
+    """A device allocation on a context's GPU.  The context frees every buffer
+    still alive when it closes, so a buffer never outlives its context."""
 
     def __init__(self, ctx, nbytes):
         self.ctx = ctx
@@ -23,6 +25,7 @@ class DeviceBuffer:
         self.ptr = lib.orome_hip_malloc(ctx.handle, max(self.nbytes, 1))
         if not self.ptr:
             raise _lib.OromeError("orome_hip_malloc(%d): %s" % (nbytes, lib.orome_last_error()))
+        ctx._buffers.add(self)
 
     @classmethod
     def from_array(cls, ctx, arr):
@@ -43,9 +46,10 @@ class DeviceBuffer:
         return out
 
     def free(self):
-        if self.ptr:
+        if self.ptr and self.ctx.handle:
             lib.orome_hip_free(self.ctx.handle, self.ptr)
-            self.ptr = None
+        self.ptr = None
+        self.ctx._buffers.discard(self)
 
     def __del__(self):
         try:
@@ -59,6 +63,7 @@ class Context:
 
     def __init__(self, cfg, max_tokens, device=0):
         self.cfg = cfg
+        self._buffers = weakref.WeakSet()
         self.handle = lib.orome_hip_create(C.byref(cfg), int(max_tokens), int(device))
         if not self.handle:
             raise _lib.OromeError("orome_hip_create: %s" % lib.orome_last_error().decode())
@@ -72,6 +77,8 @@ class Context:
 
     def close(self):
         if self.handle:
+            for b in list(self._buffers):
+                b.free()
             lib.orome_hip_destroy(self.handle)
             self.handle = None
 
@@ -119,22 +126,22 @@ class MoEModel:
             raise ValueError("give exactly one of image or path")
         self._image = image  # keep the host image alive while parsed
         if path is not None:
-            self.gf = lib.gguf_open(path.encode())
+            self.gf = lib.orome_hip_gguf_open(path.encode())
         else:
-            self.gf = lib.gguf_open_memory(image.ctypes.data, image.nbytes)
+            self.gf = lib.orome_hip_gguf_open_memory(image.ctypes.data, image.nbytes)
         if not self.gf:
             raise _lib.OromeError("gguf_open: %s" % lib.orome_last_error().decode())
         self.cfg = _lib.ModelConfig()
-        check(lib.model_config_from_gguf(self.gf, C.byref(self.cfg)), "model_config_from_gguf")
+        check(lib.orome_hip_model_config_from_gguf(self.gf, C.byref(self.cfg)), "orome_hip_model_config_from_gguf")
         self.ctx = Context(self.cfg, max_tokens, device)
-        self.fp = lib.format_provider_open_gguf(self.gf, self.ctx.handle)
+        self.fp = lib.orome_hip_format_provider_open_gguf(self.gf, self.ctx.handle)
         if not self.fp:
             raise _lib.OromeError("format_provider_open_gguf: %s" % lib.orome_last_error().decode())
         L = self.cfg.num_layers
         self.elrs = (_lib.ExpertLayerRef * L)()
         for l in range(L):
-            self.elrs[l] = lib.format_resolve_expert_layer(self.fp, l, self.cfg.num_experts)
-        self._cache = lib.build_tensor_cache_gguf(self.fp, C.byref(self.cfg))
+            self.elrs[l] = lib.orome_hip_format_resolve_expert_layer(self.fp, l, self.cfg.num_experts)
+        self._cache = lib.orome_hip_build_tensor_cache_gguf(self.fp, C.byref(self.cfg))
         if not self._cache:
             raise _lib.OromeError("build_tensor_cache_gguf failed")
         self.caches = C.cast(self._cache, C.POINTER(_lib.LayerTensorCache * L)).contents
@@ -153,23 +160,25 @@ class MoEModel:
     def H(self):
         return self.cfg.hidden_dim
 
-    def forward(self, layer, x, h_in, h_out, T, K=None):
+    def forward(self, layer, x, h_in, h_out, T, K=None, residual_out=None, sumsq_parts=None, stream=None):
         K = self.cfg.num_experts_per_tok if K is None else K
         check(lib.orome_moe_forward(self.ctx.handle, C.byref(self.cfg), C.byref(self.elrs[layer]),
                                     C.byref(self.caches[layer]), _ptr(x), _ptr(h_in), _ptr(h_out),
-                                    T, K), "orome_moe_forward")
+                                    _ptr(residual_out), _ptr(sumsq_parts), T, K, stream),
+              "orome_moe_forward")
 
-    def layer_forward(self, layer, h, T, K=None):
+    def layer_forward(self, layer, h, T, K=None, stream=None):
         K = self.cfg.num_experts_per_tok if K is None else K
         check(lib.orome_moe_layer_forward(self.ctx.handle, C.byref(self.cfg),
                                           C.byref(self.elrs[layer]), C.byref(self.caches[layer]),
-                                          _ptr(h), T, K), "orome_moe_layer_forward")
+                                          _ptr(h), T, K, stream), "orome_moe_layer_forward")
 
-    def stack_forward(self, h, T, K=None, n_layers=None):
+    def stack_forward(self, h, T, K=None, n_layers=None, stream=None):
         K = self.cfg.num_experts_per_tok if K is None else K
         n = self.cfg.num_layers if n_layers is None else n_layers
         check(lib.orome_moe_stack_forward(self.ctx.handle, C.byref(self.cfg), self.elrs,
-                                          self._cache, n, _ptr(h), T, K), "orome_moe_stack_forward")
+                                          self._cache, n, _ptr(h), T, K, stream),
+              "orome_moe_stack_forward")
 
     def debug_outputs(self, T, K=None):
         K = self.cfg.num_experts_per_tok if K is None else K
@@ -185,22 +194,22 @@ class MoEModel:
         return dict(logits=logits, idx=idx, w=w, offsets=offsets, pairs=pairs)
 
     def tensor_device_ptr(self, name):
-        ti = lib.gguf_find_tensor(self.gf, name.encode())
+        ti = lib.orome_hip_gguf_find_tensor(self.gf, name.encode())
         if not ti:
             raise KeyError(name)
         return self.fp.contents.model_buf + self.gf.contents.data_offset + ti.contents.offset
 
     def close(self):
         if getattr(self, "_cache", None):
-            lib.free_tensor_cache(self._cache)
+            lib.orome_hip_free_tensor_cache(self._cache)
             self._cache = None
         if getattr(self, "fp", None):
-            lib.format_provider_close(self.fp)
+            lib.orome_hip_format_provider_close(self.fp)
             self.fp = None
         if getattr(self, "ctx", None):
             self.ctx.close()
         if getattr(self, "gf", None):
-            lib.gguf_close(self.gf)
+            lib.orome_hip_gguf_close(self.gf)
             self.gf = None
 
 

@@ -101,6 +101,36 @@ def test_decode_forward_parity(base, T):
     assert err < TOL
 
 
+@pytest.mark.parametrize("T,path", [(1, _lib.OROME_PATH_AUTO), (4, _lib.OROME_PATH_AUTO),
+                                    (3, _lib.OROME_PATH_GEMV), (40, _lib.OROME_PATH_AUTO)])
+def test_combine_residual_copy_and_sumsq_parts(base, T, path):
+    """The combine's engine-level outputs (moe_combine_copy_sq_k8,
+    inference/src/shaders.metal:1079-1135): residual_out is h_out bit for bit
+    and each 256-column Sigma h^2 part equals the oracle's canonical dot of
+    that block of the GPU's own h_out, bit for bit; h_out itself is unchanged
+    by asking for them.  T=1 takes the fused down+combine and a separate parts
+    kernel, T=4 the small-batch combine, T=3 on the GEMV path the GEMV down
+    with the combine, T=40 the MFMA path."""
+    banner("combine outputs T=%d path=%d" % (T, path))
+    base.ctx.set_path(path)
+    x, h = base.inputs(T, seed=900 + T)
+    dx = DeviceBuffer.from_array(base.ctx, x)
+    dh = DeviceBuffer.from_array(base.ctx, h)
+    d1, d2, dr = (DeviceBuffer(base.ctx, h.nbytes) for _ in range(3))
+    dp = DeviceBuffer(base.ctx, T * (base.H // 256) * 4)
+    base.gm.forward(0, dx, dh, d1, T)
+    base.gm.forward(0, dx, dh, d2, T, residual_out=dr, sumsq_parts=dp)
+    base.ctx.sync()
+    o1, o2, res = (d.download(np.float32, h.shape) for d in (d1, d2, dr))
+    parts = dp.download(np.float32, (T, base.H // 256))
+    base.ctx.set_path(_lib.OROME_PATH_AUTO)
+    assert np.array_equal(o1.view(np.uint32), o2.view(np.uint32))
+    assert np.array_equal(res.view(np.uint32), o2.view(np.uint32))
+    ref = O.sumsq_parts(o2)
+    assert np.array_equal(parts.view(np.uint32), ref.view(np.uint32))
+    assert np.allclose(parts.astype(np.float64).sum(1), (o2.astype(np.float64) ** 2).sum(1), rtol=1e-5)
+
+
 def test_decode_repeat_is_deterministic(base):
     banner("decode determinism")
     x, h = base.inputs(4, seed=7)
