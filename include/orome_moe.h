@@ -299,6 +299,26 @@ int orome_moe_stack_forward(orome_hip_ctx *ctx, const OromeHipModelConfig *cfg,
                             const OromeHipExpertLayerRef *elrs, const OromeHipLayerTensorCache *lts,
                             int n_layers, float *h_dev, int T, int K, void *stream);
 
+/* No counterpart in the reference: orome_moe_forward for callers that cannot
+ * allocate device memory (code under HIP graph capture, serving loops and
+ * harnesses that forbid hipMalloc).  It needs no context and calls no
+ * hipMalloc/hipFree or other allocating routine: its scratch is one static
+ * device array of OROME_NOALLOC_SCRATCH_BYTES per GPU, held until the process
+ * ends.  The device is the calling thread's current one; `stream` (NULL: the
+ * null stream) must belong to it.  Same arguments, semantics and results as
+ * orome_moe_forward with the default (AUTO) kernel path and unregistered
+ * layers, for T <= OROME_NOALLOC_MAX_TOKENS; shapes whose scratch layout
+ * exceeds the array, and larger T, are rejected with OROME_EINVAL.  All calls
+ * on one GPU share that GPU's array and it keeps the last call's contents:
+ * calls that overlap on one GPU (two streams, two threads) race and must be
+ * serialised by the caller. */
+#define OROME_NOALLOC_MAX_TOKENS 16
+#define OROME_NOALLOC_SCRATCH_BYTES (8u << 20)
+int orome_moe_forward_noalloc(const OromeHipModelConfig *cfg, const OromeHipExpertLayerRef *elr,
+                              const OromeHipLayerTensorCache *lt, const float *x_dev,
+                              const float *h_in_dev, float *h_out_dev, float *residual_out_dev,
+                              float *sumsq_parts_dev, int T, int K, void *stream);
+
 /* Parity hooks: copy the intermediates of the most recent forward to host
  * memory (synchronises the stream that forward ran on).  Any pointer may be NULL.
  *   logits  [T x (E+1)]  router logits, slot E = shared-gate logit

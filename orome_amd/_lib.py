@@ -115,6 +115,8 @@ SIGNATURES = {
                                     I, I, VP]),
     "orome_moe_stack_forward": (I, [VP, P(ModelConfig), P(ExpertLayerRef), P(LayerTensorCache), I,
                                     VP, I, I, VP]),
+    "orome_moe_forward_noalloc": (I, [P(ModelConfig), P(ExpertLayerRef), P(LayerTensorCache), VP, VP, VP,
+                                      VP, VP, I, I, VP]),
     "orome_moe_debug_outputs": (I, [VP, VP, VP, VP, VP, VP]),
     "orome_moe_topk": (I, [VP, VP, VP, I, I, I, VP, VP]),
     "orome_dequant_rows": (I, [VP, I, VP, U32, U32, VP]),

@@ -12,6 +12,8 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <mutex>
+
 #include "kernels.h"
 #include "orome_internal.h"
 #include "orome_moe.h"
@@ -81,6 +83,36 @@ struct Pack {
     float *rscale, *rnorm;
 };
 
+/* Carves the scratch buffers of a context sized for c->tmax tokens, K up to
+ * c->kmax and c->cfg's shapes out of `base` (NULL: only sizes); returns the
+ * bytes needed.  Each part starts on a 256-byte boundary. */
+static size_t scratch_layout(orome_hip_ctx *c, uint8_t *base) {
+    const OromeHipModelConfig *cfg = &c->cfg;
+    const size_t T = (size_t)c->tmax, E = (size_t)cfg->num_experts, K = (size_t)c->kmax,
+                 H = (size_t)cfg->hidden_dim, M = (size_t)cfg->moe_intermediate,
+                 S = (size_t)(cfg->shared_intermediate > 0 ? cfg->shared_intermediate : 0);
+    const size_t ntile_s = E + T / GEMM_TILE_SMALL + 2, ntile_b = (T * K) / GEMM_TILE_BIG + E + T / GEMM_TILE_BIG + 2;
+    struct { void **p; size_t bytes; } parts[] = {
+        {(void **)&c->logits, T * (E + 1) * 4}, {(void **)&c->idx, T * K * 4},
+        {(void **)&c->w, T * K * 4},           {(void **)&c->sgl, T * 4},
+        {(void **)&c->offsets, (E + 1) * 4},    {(void **)&c->pairs, T * K * 4},
+        {(void **)&c->pos, T * K * 4},          {(void **)&c->list, (2 * E + 2) * 4},
+        {(void **)&c->counter, 256},            {(void **)&c->tiles, (1 + 3 * ntile_s) * 4},
+        {(void **)&c->tiles_b, (1 + 3 * ntile_b) * 4},
+        {(void **)&c->dcount, (size_t)dispatch_blocks((int)T) * E * 4},
+        /* one extra all-zero row each (index tmax, tmax*kmax, tmax) */
+        {(void **)&c->x16, (T + 1) * H * 2},    {(void **)&c->act, (T * K + 1) * M * 2},
+        {(void **)&c->act_sh, (T + 1) * (S ? S : 1) * 2}, {(void **)&c->y, T * K * H * 4},
+        {(void **)&c->ysh, T * H * 4},          {(void **)&c->xnorm, T * H * 4},
+    };
+    size_t off = 0;
+    for (auto &p : parts) {
+        if (base) *p.p = base + off;
+        off += (p.bytes + 255) / 256 * 256;
+    }
+    return off;
+}
+
 static int set_dev(orome_hip_ctx *c) {
     HIP_OK(hipSetDevice(c->device), OROME_EHIP);
     return OROME_OK;
@@ -115,25 +147,7 @@ extern "C" orome_hip_ctx *orome_hip_create(const OromeHipModelConfig *cfg, int m
         free(c);
         return NULL;
     }
-    const size_t T = (size_t)max_tokens, E = (size_t)cfg->num_experts, K = (size_t)c->kmax,
-                 H = (size_t)cfg->hidden_dim, M = (size_t)cfg->moe_intermediate,
-                 S = (size_t)(cfg->shared_intermediate > 0 ? cfg->shared_intermediate : 0);
-    const size_t ntile_s = E + T / GEMM_TILE_SMALL + 2, ntile_b = (T * K) / GEMM_TILE_BIG + E + T / GEMM_TILE_BIG + 2;
-    struct { void **p; size_t bytes; } parts[] = {
-        {(void **)&c->logits, T * (E + 1) * 4}, {(void **)&c->idx, T * K * 4},
-        {(void **)&c->w, T * K * 4},           {(void **)&c->sgl, T * 4},
-        {(void **)&c->offsets, (E + 1) * 4},    {(void **)&c->pairs, T * K * 4},
-        {(void **)&c->pos, T * K * 4},          {(void **)&c->list, (2 * E + 2) * 4},
-        {(void **)&c->counter, 256},            {(void **)&c->tiles, (1 + 3 * ntile_s) * 4},
-        {(void **)&c->tiles_b, (1 + 3 * ntile_b) * 4},
-        {(void **)&c->dcount, (size_t)dispatch_blocks((int)T) * E * 4},
-        /* one extra all-zero row each (index tmax, tmax*kmax, tmax) */
-        {(void **)&c->x16, (T + 1) * H * 2},    {(void **)&c->act, (T * K + 1) * M * 2},
-        {(void **)&c->act_sh, (T + 1) * (S ? S : 1) * 2}, {(void **)&c->y, T * K * H * 4},
-        {(void **)&c->ysh, T * H * 4},          {(void **)&c->xnorm, T * H * 4},
-    };
-    size_t total = 0;
-    for (auto &p : parts) total += (p.bytes + 255) / 256 * 256;
+    const size_t total = scratch_layout(c, NULL);
     if (hipMalloc(&c->arena, total) != hipSuccess) {
         orome_fail(OROME_ENOMEM, "orome_hip_create: scratch arena of %zu bytes", total);
         (void)hipStreamDestroy(c->side);
@@ -142,13 +156,9 @@ extern "C" orome_hip_ctx *orome_hip_create(const OromeHipModelConfig *cfg, int m
         return NULL;
     }
     c->arena_bytes = total;
-    size_t off = 0;
-    for (auto &p : parts) {
-        *p.p = (uint8_t *)c->arena + off;
-        off += (p.bytes + 255) / 256 * 256;
-    }
-    /* the routing kernel's completion counter must start at zero; the kernel
-     * returns it to zero itself, so this is the only clear ever needed */
+    scratch_layout(c, (uint8_t *)c->arena);
+    /* the zero rows past x16, act and act_sh must read as zeros; nothing
+     * writes them, so this is the only clear needed */
     if (hipMemset(c->arena, 0, total) != hipSuccess || hipDeviceSynchronize() != hipSuccess) {
         orome_fail(OROME_EHIP, "orome_hip_create: scratch clear failed");
         (void)hipFree(c->arena);
@@ -618,7 +628,7 @@ static int forward_impl(orome_hip_ctx *c, const OromeHipModelConfig *cfg, const 
                        : launch_gemm_down(exm, shm, c->act, c->act_sh, c->tmax * c->kmax, c->tmax, T, H, M, K, E, tm, c->tiles_b, nb_max, c->y,
                                           c->ysh, st);
         };
-        if (c->timing) { /* per-stage timing: both lists in order on one stream */
+        if (c->timing || !c->side) { /* per-stage timing (or no side stream): both lists in order on one stream */
             TLAUNCH(c, ST_GATE_UP, (gate_up(GEMM_TILE_SMALL, s) ? -3 : gate_up(GEMM_TILE_BIG, s)), "grouped gate/up");
             TLAUNCH(c, ST_DOWN, (down(GEMM_TILE_SMALL, s) ? -3 : down(GEMM_TILE_BIG, s)), "grouped down");
         } else {
@@ -820,4 +830,65 @@ extern "C" int orome_hip_stream_delay(orome_hip_ctx *c, uint32_t usec) {
     if (set_dev(c)) return OROME_EHIP;
     LAUNCH(launch_delay(usec, c->stream), "delay");
     return OROME_OK;
+}
+
+/* ------------------------------------------- forward without allocation */
+
+/* The scratch of orome_moe_forward_noalloc: one copy per GPU, held until the
+ * process ends.  Host code must not use this name as a device address (it is
+ * the host-side stand-in of the symbol); each device's address comes from
+ * hipGetSymbolAddress on that device, kept in g_na_ptr. */
+static __device__ __align__(256) uint8_t scratch[OROME_NOALLOC_SCRATCH_BYTES];
+
+#define NA_MAX_DEVICES 64
+static std::mutex g_na_lock;
+static uint8_t *g_na_ptr[NA_MAX_DEVICES];
+/* shapes of the layout the device's scratch was last cleared for */
+static int g_na_key[NA_MAX_DEVICES][4];
+
+extern "C" int orome_moe_forward_noalloc(const OromeHipModelConfig *cfg, const OromeHipExpertLayerRef *elr,
+                                         const OromeHipLayerTensorCache *lt, const float *x, const float *h_in,
+                                         float *h_out, float *residual_out, float *sumsq_parts, int T, int K,
+                                         void *stream) {
+    if (!cfg || !elr || !lt || !x || !h_out) return orome_fail(OROME_EINVAL, "orome_moe_forward_noalloc: NULL argument");
+    if (T < 1 || T > OROME_NOALLOC_MAX_TOKENS)
+        return orome_fail(OROME_EINVAL, "orome_moe_forward_noalloc: T=%d outside 1..%d", T, OROME_NOALLOC_MAX_TOKENS);
+    if (cfg->hidden_dim <= 0 || cfg->num_experts <= 0 || cfg->moe_intermediate <= 0 || cfg->shared_intermediate < 0)
+        return orome_fail(OROME_EINVAL, "orome_moe_forward_noalloc: invalid config");
+    int dev = 0;
+    HIP_OK(hipGetDevice(&dev), OROME_EHIP);
+    if (dev < 0 || dev >= NA_MAX_DEVICES) return orome_fail(OROME_EINVAL, "orome_moe_forward_noalloc: device %d", dev);
+    /* a context on the stack: no streams, events or packs of its own */
+    orome_hip_ctx c = {};
+    c.device = dev;
+    c.stream = stream ? (hipStream_t)stream : 0;
+    c.cfg = *cfg;
+    c.tmax = OROME_NOALLOC_MAX_TOKENS;
+    c.kmax = OROME_MAX_ACTIVE;
+    c.path = OROME_PATH_AUTO;
+    const size_t need = scratch_layout(&c, NULL);
+    if (need > sizeof(scratch))
+        return orome_fail(OROME_EINVAL, "orome_moe_forward_noalloc: shapes need %zu bytes of scratch, the maximum is %zu",
+                          need, sizeof(scratch));
+    const int key[4] = {cfg->hidden_dim, cfg->num_experts, cfg->moe_intermediate, cfg->shared_intermediate};
+    uint8_t *base;
+    bool clear = false;
+    {
+        std::lock_guard<std::mutex> g(g_na_lock);
+        if (!g_na_ptr[dev]) {
+            void *p = NULL;
+            HIP_OK(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), OROME_EHIP);
+            g_na_ptr[dev] = (uint8_t *)p;
+        }
+        base = g_na_ptr[dev];
+        /* the zero rows of the layout sit at shape-dependent offsets: clear
+         * the scratch whenever the shapes change (and on the first call) */
+        if (memcmp(g_na_key[dev], key, sizeof key)) {
+            memcpy(g_na_key[dev], key, sizeof key);
+            clear = true;
+        }
+    }
+    if (clear) LAUNCH(launch_zero(base, need, c.stream), "orome_moe_forward_noalloc: scratch clear");
+    scratch_layout(&c, base);
+    return forward_impl(&c, cfg, elr, lt, x, h_in, h_out, T, K, NULL, NULL, c.stream, FwdOut{residual_out, sumsq_parts});
 }

@@ -331,3 +331,19 @@ int launch_delay(uint32_t usec, hipStream_t s) {
     hipLaunchKernelGGL(k_delay, dim3(1), dim3(64), 0, s, (uint64_t)usec * 100u);
     return hipGetLastError() == hipSuccess ? 0 : -3;
 }
+
+/* Zero fill of `words` 32-bit words (a kernel, not a memset node, so that
+ * callers may capture it in a graph). */
+__global__ void k_zero(uint32_t *p, size_t words) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < words; i += (size_t)gridDim.x * blockDim.x)
+        p[i] = 0u;
+}
+
+int launch_zero(void *p, size_t bytes, hipStream_t s) {
+    if (bytes % 4) return -1;
+    const size_t words = bytes / 4;
+    const unsigned blocks = (unsigned)((words + 255) / 256 < 1024 ? (words + 255) / 256 : 1024);
+    if (!blocks) return 0;
+    hipLaunchKernelGGL(k_zero, dim3(blocks), dim3(256), 0, s, (uint32_t *)p, words);
+    return hipGetLastError() == hipSuccess ? 0 : -3;
+}
