@@ -9,7 +9,8 @@ import ctypes as C
 import os
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "liborome_moe.so")
+# OROME_LIB names another build of the same library (e.g. an instrumented one)
+LIB_PATH = os.environ.get("OROME_LIB") or os.path.join(HERE, "liborome_moe.so")
 
 # OromeHipQuantFormat: the values of QuantFormat (inference/include/orome.h:227-235)
 QFMT_GGUF_Q4_K, QFMT_GGUF_Q5_K, QFMT_GGUF_Q6_K, QFMT_GGUF_Q8_0, QFMT_F16, QFMT_BF16, QFMT_F32 = range(7)

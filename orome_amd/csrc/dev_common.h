@@ -120,6 +120,15 @@ DEV float group_sum(float v) {
  * gives -0 (rcp(inf) = 0) */
 DEV float silu_f(float g) { return g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)); }
 DEV float sigmoid_f(float s) { return 1.0f / (1.0f + expf(-s)); }
+/* act = half(silu(g) * u) as the reference stages it: the product rounded to
+ * fp32, then to fp16 (the empty asm keeps the compiler from folding the
+ * product into a mixed-precision FMA that rounds once, straight to fp16,
+ * which differs in rare cases and would differ between kernels) */
+DEV _Float16 glu_f16(float g, float u) {
+    float v = silu_f(g) * u;
+    asm volatile("" : "+v"(v));
+    return (_Float16)v;
+}
 
 /* --------------------------------------------------------------- Q4_K */
 

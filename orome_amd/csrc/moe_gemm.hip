@@ -443,7 +443,7 @@ struct GuEpi {
             if (t >= tb || tok >= rows) continue;
             h4 v; /* act rows are stored (0,2,1,3) within each 4-group */
 #pragma unroll
-            for (int q = 0; q < 4; q++) v[(q & 1) * 2 + (q >> 1)] = (_Float16)(silu_f(c[0][t][q]) * c[1][t][q]);
+            for (int q = 0; q < 4; q++) v[(q & 1) * 2 + (q >> 1)] = glu_f16(c[0][t][q], c[1][t][q]);
             *(h4 *)(out + (size_t)(first + tok) * out_ld + r) = v;
         }
     }

@@ -256,7 +256,7 @@ DEV void gu_body(const GUArgs &a, const uint8_t *gbase, const uint8_t *ubase, in
 #pragma unroll
             for (int i = 0; i < RPW; i++)
                 out[(size_t)j * out_ld + r0 + i] =
-                    (_Float16)(silu_f(red[(i * 2) * 16 + j]) * red[(i * 2 + 1) * 16 + j]);
+                    glu_f16(red[(i * 2) * 16 + j], red[(i * 2 + 1) * 16 + j]);
 }
 
 /* One token, H = 2048 (one 32-weight chunk per lane): x arrives already
@@ -276,7 +276,7 @@ DEV void gu_body1(const GUArgs &a, const uint8_t *gbase, const uint8_t *ubase, i
     for (int i = 0; i < RPW; i++) {
         const float pg = wave_sum_fast(q4_dot(g[i], lane, xl, xh, Xl, Xh));
         const float pu = wave_sum_fast(q4_dot(u[i], lane, xl, xh, Xl, Xh));
-        if (lane == 0) out[r0 + i] = (_Float16)(silu_f(pg) * pu);
+        if (lane == 0) out[r0 + i] = glu_f16(pg, pu);
     }
 }
 
@@ -459,7 +459,7 @@ DEV void k_gemv_gate_up1_body(GUArgs a, RouteArgs ra) {
     for (int i = 0; i < GU_RPW; i++) {
         const float pg = wave_sum_fast(q4_dot(g[i], lane, xl, xh, Xl, Xh));
         const float pu = wave_sum_fast(q4_dot(w2[i], lane, xl, xh, Xl, Xh));
-        if (lane == 0) out[r0 + i] = (_Float16)(silu_f(pg) * pu);
+        if (lane == 0) out[r0 + i] = glu_f16(pg, pu);
     }
 }
 
@@ -561,7 +561,7 @@ DEV void gb_tile(const GbTile &tl, int it, int cl, int q, int wv, int n, const _
             cu += (A[g][2] * ul + A[g][3] * uh) - (B[g][2] * Xl + B[g][3] * Xh);
         }
         const float tg = row_sum16(cg), tu = row_sum16(cu);
-        if (cl == 0) obuf[j * (GB_ROWS * GB_ITER) + rr] = (_Float16)(silu_f(tg) * tu);
+        if (cl == 0) obuf[j * (GB_ROWS * GB_ITER) + rr] = glu_f16(tg, tu);
     }
 }
 

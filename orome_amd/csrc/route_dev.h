@@ -295,3 +295,90 @@ DEV void route_block_lds(const RouteArgs &a, RouteLds &r, bool publish) {
         a.offsets[ee] = (uint32_t)c;
     }
 }
+
+/* Canonical dots of one wave over H (H % 256 == 0, H <= 256 NIM) for up to
+ * TMAX tokens, with NORM x = RMSNorm(h) computed in place (RMSNorm of
+ * inference/src/shaders.metal:128-149, the same arithmetic and canonical sum
+ * of squares as k_rmsnorm, so x is bit-identical to that kernel's output;
+ * write_x stores it for the later kernels).  Tokens go in chunks of up to 4
+ * whose row loads are issued together with the router row's; every load is
+ * unconditional (indices clamped, values past T or H unused), since a load
+ * under a branch is waited for alone.  A NULL wrow gives zeros. */
+template <int TMAX, int NIM, bool NORM>
+DEV void canon_dots(const float *wrow, const RouteArgs &a, int lane, bool write_x, float *acc, int tb = 0) {
+    /* tokens tb .. tb + TMAX - 1 (acc[t - tb]) */
+    /* write_x also stages fp16(x) into a.x16 when set (round to nearest
+     * even, each 4-group stored (0,2,1,3), the grouped GEMMs' layout) */
+    constexpr int TC = TMAX < 4 ? TMAX : 4;
+    const int NI = a.H / 256, H = a.H, T = a.T - tb;
+    const float *xs = (NORM ? a.norm_h : a.x) + (size_t)tb * a.H;
+    f4 wv[NIM], nw[NIM];
+#pragma unroll
+    for (int i = 0; i < NIM; i++) {
+        const int ic = 256 * min(i, NI - 1) + 4 * lane;
+        wv[i] = *(const f4 *)((wrow ? wrow : xs) + ic);
+        if (NORM) nw[i] = *(const f4 *)((a.norm_w ? a.norm_w : xs) + ic);
+    }
+#pragma unroll
+    for (int t0 = 0; t0 < TMAX; t0 += TC) {
+        if (t0 >= T) break;
+        f4 hv[TC][NIM];
+#pragma unroll
+        for (int c = 0; c < TC; c++)
+#pragma unroll
+            for (int i = 0; i < NIM; i++)
+                hv[c][i] = *(const f4 *)(xs + (size_t)min(t0 + c, T - 1) * H + 256 * min(i, NI - 1) + 4 * lane);
+        if (t0 == 0) {
+#pragma unroll
+            for (int i = 0; i < NIM; i++) {
+                if (!wrow) wv[i] = f4{0, 0, 0, 0};
+                if (NORM) {
+                    const f4 w = a.norm_w ? nw[i] : f4{1, 1, 1, 1};
+                    nw[i] = f4{__builtin_bit_cast(float, __builtin_bit_cast(uint32_t, w.x) & 0xFFFF0000u),
+                               __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, w.y) & 0xFFFF0000u),
+                               __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, w.z) & 0xFFFF0000u),
+                               __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, w.w) & 0xFFFF0000u)};
+                }
+            }
+        }
+#pragma unroll
+        for (int c = 0; c < TC; c++) {
+            const int t = t0 + c;
+            acc[t] = 0.0f;
+            if (t >= T || (!NORM && !wrow)) continue;
+            float scale = 1.0f;
+            if (NORM) {
+                float ss = 0.0f;
+#pragma unroll
+                for (int i = 0; i < NIM; i++)
+                    if (i < NI) {
+                        ss = __builtin_fmaf(hv[c][i].x, hv[c][i].x, ss);
+                        ss = __builtin_fmaf(hv[c][i].y, hv[c][i].y, ss);
+                        ss = __builtin_fmaf(hv[c][i].z, hv[c][i].z, ss);
+                        ss = __builtin_fmaf(hv[c][i].w, hv[c][i].w, ss);
+                    }
+                ss = wave_sum_canon(ss);
+                scale = 1.0f / sqrtf(ss / (float)H + a.norm_eps);
+            }
+            float d = 0.0f;
+#pragma unroll
+            for (int i = 0; i < NIM; i++)
+                if (i < NI) {
+                    f4 x = hv[c][i];
+                    if (NORM) {
+                        x = f4{(x.x * scale) * nw[i].x, (x.y * scale) * nw[i].y, (x.z * scale) * nw[i].z,
+                               (x.w * scale) * nw[i].w};
+                        if (write_x) *(f4 *)(a.xnorm + (size_t)(tb + t) * H + 256 * i + 4 * lane) = x;
+                    }
+                    if (write_x && a.x16)
+                        *(h4 *)(a.x16 + (size_t)(tb + t) * H + 256 * i + 4 * lane) =
+                            h4{(_Float16)x.x, (_Float16)x.z, (_Float16)x.y, (_Float16)x.w};
+                    d = __builtin_fmaf(wv[i].x, x.x, d);
+                    d = __builtin_fmaf(wv[i].y, x.y, d);
+                    d = __builtin_fmaf(wv[i].z, x.z, d);
+                    d = __builtin_fmaf(wv[i].w, x.w, d);
+                }
+            acc[t] = wave_sum_canon(d);
+        }
+    }
+}

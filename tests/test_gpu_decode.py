@@ -221,7 +221,7 @@ def test_dequant_bit_exact(fmt_name, kw):
     p.gm.close()
 
 
-@pytest.mark.parametrize("T", [2, 5])
+@pytest.mark.parametrize("T", [1, 2, 5])
 def test_layer_forward_and_stack(T):
     """T=2: GEMV kernels; T=5: small-batch routing (RMSNorm in the router)
     feeding the small-tile grouped GEMMs."""
