@@ -189,25 +189,28 @@ const char *orome_last_error(void);
 enum { OROME_PATH_AUTO = 0, OROME_PATH_GEMV = 1, OROME_PATH_MFMA = 2 };
 int orome_hip_set_path(orome_hip_ctx *ctx, int path);
 
-/* Tile-major copies of a layer's Q4_K expert matrices for the MFMA path.  No
+/* Tile-major copies of a layer's expert matrices for the MFMA path.  No
  * counterpart in the reference (its kernels read the GGUF blocks in place):
  * registering a layer declares its weights immutable while registered and
- * repacks the routed gate/up (Q4_K) and down (Q4_K or Q6_K) and the shared
- * expert's matrices into one allocation on the context's device (the same bytes
- * as the originals); orome_moe_forward then feeds the grouped GEMMs from the
- * copies, so each wave's weight load is one contiguous 1 KB.  Outputs are
- * bit-identical with and without.  Layers are keyed by the routed gate and
- * shared gate addresses; registering again replaces the copy; layers whose
- * shared gate/up is not Q4_K are left as they are (OROME_OK), and a down
- * projection stays row-major when either side is Q8_0.  With an F32 router the
- * copy also holds the router as fp16 rows (one power-of-two scale each) and
- * row-norm bounds: above 8 tokens a registered layer is routed in two passes
- * (approximate logits on the matrix cores, then the canonical fp32 logits of
- * the experts that can win), which selects exactly the experts, order and
- * weights of the one-pass router; the debug logits output then holds the
- * canonical values for those candidates and the approximation (within its
- * proven bound) elsewhere.  OROME_ROUTE_EXACT=1 in the environment keeps the
- * one-pass router.
+ * repacks, into one allocation on the context's device (the same bytes as the
+ * originals), the routed gate/up (Q4_K), each down projection that is Q4_K or
+ * Q6_K, and the shared gate/up when Q4_K; a Q8_0 shared expert (the
+ * reference's 35B layout) stays row-major and the grouped GEMMs read it in
+ * place beside the copies.  orome_moe_forward then feeds the grouped GEMMs
+ * from the copies, so each wave's weight load is one contiguous 1 KB.
+ * Outputs are bit-identical with and without.  Layers are keyed by the routed
+ * gate and shared gate addresses; registering again replaces the copy.  With
+ * an F32 router (any shared-expert format) the copy also holds the router as
+ * fp16 rows (one power-of-two scale each) and row-norm bounds: above 16
+ * tokens under AUTO (at any T on the forced MFMA path) a registered layer is
+ * routed in two passes (approximate logits on the matrix cores, then the
+ * canonical fp32 logits of the experts that can win), which selects exactly
+ * the experts, order and weights of the one-pass router; the debug logits
+ * output then holds the canonical values for those candidates and the
+ * approximation (within its proven bound) elsewhere.  OROME_ROUTE_EXACT=1 in
+ * the environment keeps the one-pass router.  Fails with OROME_EUNSUPPORTED
+ * (nothing registered) when the routed gate/up is not Q4_K or a dimension is
+ * not a multiple of 256.
  * orome_hip_unpack_all frees every copy (orome_hip_destroy calls it). */
 int orome_hip_pack_layer(orome_hip_ctx *ctx, const OromeHipModelConfig *cfg, const OromeHipExpertLayerRef *layer,
                          const OromeHipLayerTensorCache *lt);

@@ -135,6 +135,16 @@ ORC_API void orc_unpack_q4k_pair(const uint8_t *s, uint32_t g, float *sc_lo, flo
     *mn_hi = (float)((mnp >> 4) | ((s[b + 5] >> 6) << 4));
 }
 
+/* orc_unpack_q4k_pair over n 12-byte scale regions: out[16 r + 2 g + h] =
+ * scale of sub-block 2 g + h, out[16 r + 8 + 2 g + h] = its min (lets a test
+ * sweep every byte value of a field in one call). */
+ORC_API void orc_unpack_q4k_batch(const uint8_t *s12, size_t n, float *out) {
+    for (size_t r = 0; r < n; r++)
+        for (uint32_t g = 0; g < 4; g++)
+            orc_unpack_q4k_pair(s12 + 12 * r, g, out + 16 * r + 2 * g, out + 16 * r + 2 * g + 1,
+                                out + 16 * r + 8 + 2 * g, out + 16 * r + 8 + 2 * g + 1);
+}
+
 /* ------------------------------------------------------------- A3-A5 --- */
 /* inference/src/format.m:66-79 */
 static void dec_q8_0(const uint8_t *row, uint32_t n, float *out) {
@@ -297,8 +307,12 @@ ORC_API void orc_router_logits(const float *W, const float *wsg, const float *x,
 /* ---------------------------------------------------------------- A7 --- */
 /* inference/src/shaders.metal:1141-1234 (softmax_topk_route):
  *  - K rounds of argmax over the raw logits (plus the optional per-expert bias
- *    of the skewed-routing config); strict '>' so ties go to the lower index
- *    (1173, 1194); slot order = descending logit;
+ *    of the skewed-routing config); slot order = descending logit;
+ *  - exact ties go to the lower expert index.  That is the rule BASELINE's
+ *    contract states; the reference's own kernel resolves an exact tie by the
+ *    position in its shuffle-down tree (1166-1200: lane L keeps its value
+ *    against L + offset on a tie, so a tie between experts 1 and 2 selects 2,
+ *    one between 8 and 16 selects 16).  Distinct values select identically;
  *  - w_k = exp(l_k - l_0) / sum_k exp(l_j - l_0), summed k = 0..K-1 and
  *    multiplied by the reciprocal of the sum (1212-1226);
  *  - the shared-gate logit is passed through (1232).

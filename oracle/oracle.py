@@ -33,6 +33,7 @@ def _load(name):
         "orc_round_half": (F, [F]),
         "orc_bf16_trunc": (F, [F]),
         "orc_unpack_q4k_pair": (None, [VP, U32, VP, VP, VP, VP]),
+        "orc_unpack_q4k_batch": (None, [VP, C.c_size_t, VP]),
         "orc_row_bytes": (C.c_size_t, [I, U32]),
         "orc_decode_row": (I, [I, VP, U32, VP]),
         "orc_decode_rows": (I, [I, VP, U32, U32, VP]),

@@ -25,14 +25,6 @@ typedef uint32_t u2 __attribute__((ext_vector_type(2)));
 
 #define DEV static __device__ __forceinline__
 #define MDEV __device__ __forceinline__ /* member functions */
-#ifdef OROME_TRACE
-/* per-block phase timestamps (100 MHz clock) of one kernel, for profiling
- * builds only; wave w of the block writes bits 60+ */
-static __device__ unsigned long long g_trace[65536 * 8];
-#define TSTAMP(i) do { if ((threadIdx.x & 63) == 0 && blockIdx.x < 65536) g_trace[blockIdx.x * 8 + (i)] = __builtin_amdgcn_s_memrealtime() | ((unsigned long long)(threadIdx.x >> 6) << 60); } while (0)
-#else
-#define TSTAMP(i) do {} while (0)
-#endif
 /* Optional per-block start/end stamps of a kernel launch (s_memrealtime,
  * 100 MHz) into kt[2 b], kt[2 b + 1] for block b: the launch's duration is
  * max(end) - min(start), the quantity a kernel trace reports.  kt NULL:

@@ -527,9 +527,12 @@ static int forward_impl(orome_hip_ctx *c, const OromeHipModelConfig *cfg, const 
      * small-tile list, runs only there -- 1..2 tokens fold the routing into
      * the GEMV gate/up; up to 16: one 32-row small tile per expert, and
      * T K <= 256 for the small-batch dispatch) */
-    const bool hybrid = path == OROME_PATH_AUTO && T >= 3 && T <= 16 && T * K <= 256 &&
+    /* (the small-batch router takes H <= 4096; wider layers take the MFMA
+     * path under AUTO) */
+    const bool small_router = H <= 4096;
+    const bool hybrid = path == OROME_PATH_AUTO && T >= 3 && T <= 16 && T * K <= 256 && small_router &&
                         gemm_small_tiles_ok(hx, hs, H, M);
-    if (path == OROME_PATH_AUTO) path = T <= 8 || hybrid ? OROME_PATH_GEMV : OROME_PATH_MFMA;
+    if (path == OROME_PATH_AUTO) path = (T <= 8 && small_router) || hybrid ? OROME_PATH_GEMV : OROME_PATH_MFMA;
     c->last_stream = s;
     if (norm_h) {
         if (path == OROME_PATH_GEMV) { /* the router kernel normalises and writes xnorm */

@@ -32,11 +32,6 @@
 #include <cstdlib>
 #include "dev_common.h"
 #include "kernels.h"
-#ifdef OROME_TRACE
-extern "C" __attribute__((visibility("default"))) int orome_trace_fetch_gemm(unsigned long long *h) {
-    return (int)hipMemcpyFromSymbol(h, HIP_SYMBOL(g_trace), sizeof(g_trace));
-}
-#endif
 
 /* FQ4KT, FQ6KT: Q4_K / Q6_K repacked tile-major (launch_pack_q4k,
  * launch_pack_q6k), same values */
@@ -331,7 +326,6 @@ DEV void tile_run(const uint8_t *w0, const uint8_t *w1, int in_dim, const _Float
     }
     if (nch > 2) ch.fetch(src, rowoff, ld, 2 * KCH);
     __syncthreads();
-    if (threadIdx.x == 0) TSTAMP(1);
 
     f4v c[NMAT][TBM];
 #pragma unroll
@@ -386,7 +380,6 @@ DEV void tile_run(const uint8_t *w0, const uint8_t *w1, int in_dim, const _Float
                         c[m][t] = mfma(a[m], b[t], c[m][t]);
                     }
             }
-            if (threadIdx.x == 0 && (j & 3) == 3 && j < 16) TSTAMP(2 + (j >> 2));
             if (j == nst - 1) {
                 epi.template operator()<TBM>(c, rbase + rb * 16 + 4 * kg, tb);
 #pragma unroll
@@ -530,9 +523,6 @@ DEV void tile_stream(const P &pol, _Float16 *xs, int *rowoff) {
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int kg = lane >> 4, i = lane & 15;
     const size_t rbytes = gemm_row_bytes(FMT, pol.in_dim());
-#ifdef OROME_TRACE
-    if (threadIdx.x == 0 && NMAT == 2) g_trace[blockIdx.x * 8] = __builtin_amdgcn_s_memrealtime();
-#endif
     UnitDesc cu = pol.desc(0), nu = pol.desc(1);
     if (!cu.valid) return;
     /* this lane's weight row in matrix m of unit u (row block 0, stage 0);
@@ -665,10 +655,6 @@ DEV void tile_stream(const P &pol, _Float16 *xs, int *rowoff) {
                 }
             }
         }
-#ifdef OROME_TRACE
-        /* unit end times of the gate/up stream, per block (slot 0: start) */
-        if (threadIdx.x == 0 && n < 7 && NMAT == 2) g_trace[blockIdx.x * 8 + 1 + n] = __builtin_amdgcn_s_memrealtime();
-#endif
         if (!nu.valid) break;
         cu = nu;
         nu = fu;
@@ -731,7 +717,6 @@ DEV void k_gemm_gate_up_body(GemmArgs a) {
     block_tile(a.nyb, ti, yb);
     const uint32_t nt = a.tiles[0];
     if ((uint32_t)ti >= nt) return;
-    if (threadIdx.x == 0) TSTAMP(0);
     const uint32_t e = a.tiles[1 + 3 * ti], first = a.tiles[2 + 3 * ti], rows = a.tiles[3 + 3 * ti];
     const bool sh = e == (uint32_t)a.E;
     if (yb * (Shape<TBM>::W * 16 * GU_RPW) >= (sh ? a.S : a.M)) return;
@@ -748,7 +733,6 @@ DEV void k_gemm_gate_up_body(GemmArgs a) {
         tile_run<RF, 2, GU_RPW, Shape<TBM>::DEPTH, NST, TBM>(a.wa + (size_t)e * a.stride_a, a.wb + (size_t)e * a.stride_b, a.H, a.src,
                                                           a.H, rowoff, (int)rows, yb, xs, epi);
     }
-    if (threadIdx.x == 0) TSTAMP(6);
 }
 
 template <int RF, int SF, int NST, int TBM>

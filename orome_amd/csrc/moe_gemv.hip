@@ -26,11 +26,6 @@
 #include "dev_common.h"
 #include "kernels.h"
 #include "route_dev.h"
-#ifdef OROME_TRACE
-extern "C" __attribute__((visibility("default"))) int orome_trace_fetch(unsigned long long *h) {
-    return (int)hipMemcpyFromSymbol(h, HIP_SYMBOL(g_trace), sizeof(g_trace));
-}
-#endif
 
 
 enum { FQ4K = 0, FQ5K = 1, FQ6K = 2, FQ8 = 3 };
@@ -587,7 +582,6 @@ DEV void k_gemv_gu_b_body(GUArgs a, RouteArgs ra) {
     __shared__ RouteLds r;
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, tid = threadIdx.x;
     const int cl = lane & 15, q = lane >> 4;
-    TSTAMP(0);
     const int T = a.T, K = a.K, H = 2048;
     _Float16 *xs = (_Float16 *)gb_dyn;
     float *xsum = (float *)(gb_dyn + (size_t)T * 16 * GB_SEG * 2);
@@ -638,7 +632,6 @@ DEV void k_gemv_gu_b_body(GUArgs a, RouteArgs ra) {
     wu += wave_row;
     const size_t tile_step = (size_t)GB_ROWS * rb;
     GbTile t0, t1;
-    TSTAMP(1);
     t0.load(wg, wu, cl); /* weight bytes first */
     /* stage the tokens: thread t converts x[tok][8t .. 8t+8), four tokens
      * per pass; loads are unconditional (clamped token) so they stay in
@@ -673,7 +666,6 @@ DEV void k_gemv_gu_b_body(GUArgs a, RouteArgs ra) {
         }
     }
     __syncthreads();
-    TSTAMP(2);
     /* outputs wait in LDS (no global stores between the ring's loads) */
     _Float16 *obuf = xs + (size_t)T * 16 * GB_SEG + (size_t)T * 16 * GB_SUM * 2;
     const int ntile = sh ? 1 : GB_ITER;
@@ -687,7 +679,6 @@ DEV void k_gemv_gu_b_body(GUArgs a, RouteArgs ra) {
         const int j = i / (GB_ROWS * GB_ITER), rr = i % (GB_ROWS * GB_ITER);
         out[(size_t)j * ld + base + rr] = obuf[i];
     }
-    TSTAMP(7);
 }
 
 template <int EPL, bool ROUTE>

@@ -9,7 +9,9 @@
  *   DPP within rows of 16 and readlanes across rows.  Identical logits make
  *   the selected experts identical.
  * Selection restates softmax_topk_route (shaders.metal:1141-1234): K rounds
- * of argmax, ties to the lower expert index, softmax over the K winners.
+ * of argmax, exact ties to the lower expert index (the contract's rule; the
+ * reference's tree settles exact ties by tree position), softmax over the K
+ * winners.
  * A round is a wave64 max over order-preserving 32-bit images of the values;
  * the lowest lane holding the maximum settles ties.
  * Dispatch is a stable counting sort of pairs p = t*K + k by expert.
@@ -18,11 +20,6 @@
 #include "kernels.h"
 
 #include "route_dev.h"
-#ifdef OROME_TRACE
-extern "C" __attribute__((visibility("default"))) int orome_trace_fetch_route(unsigned long long *h) {
-    return (int)hipMemcpyFromSymbol(h, HIP_SYMBOL(g_trace), sizeof(g_trace));
-}
-#endif
 
 /* Small-batch router logits (T <= 16): every wave computes one router row
  * (or the shared-gate row) for all tokens; with NORM, x is RMSNorm(norm_h)
@@ -200,21 +197,6 @@ __global__ __launch_bounds__(256) void k_pack_router(const float *W, int H, _Flo
     }
 }
 
-#ifdef OROME_TRACE
-/* phase stamps kept in registers and written once at the end (a store in
- * flight would delay the loads' waits that follow it) */
-#define RSTAMP(i) unsigned long long rst_##i = __builtin_amdgcn_s_memrealtime()
-#define RSTAMP_FLUSH(n)                                                                             \
-    do {                                                                                           \
-        if (lane == 0) {                                                                           \
-            unsigned long long *g = g_trace + ((n) + blockIdx.x) * 8;                              \
-            g[0] = rst_0; g[1] = rst_1; g[2] = rst_2; g[3] = rst_3; g[4] = rst_4; g[5] = rst_5;    \
-        }                                                                                          \
-    } while (0)
-#else
-#define RSTAMP(i) do {} while (0)
-#define RSTAMP_FLUSH(n) do {} while (0)
-#endif
 
 /* Pass 1: a block of NW waves computes 16*TTS tokens x 16*TES experts
  * (v_mfma_f32_16x16x32_f16, tokens as A rows, experts as B columns).  Wave w
@@ -228,7 +210,6 @@ __global__ __launch_bounds__(64 * NW) void k_route_approx(RouteArgs a) {
     /* the wave index is uniform: say so, or the k loop is compiled divergent */
     const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int E = a.E, H = a.H, T = a.T;
-    RSTAMP(0);
     /* XCD-aware tiles: work-groups are dealt to the 8 XCDs round-robin by
      * linear id, so the expert tiles of one token tile take ids that share
      * id % 8 and read the token rows through one L2 (HBM reads x once) */
@@ -313,13 +294,11 @@ __global__ __launch_bounds__(64 * NW) void k_route_approx(RouteArgs a) {
         const int o = threadIdx.x + 64 * NW * j, slot = o >> 6;
         osc[j] = a.wscale[min(e0 + ((slot >> 2) % TES) * 16 + (o & 15), E - 1)];
     }
-    RSTAMP(1);
     compute(kb);
     for (int k0 = kb + 32 * S; k0 < ke; k0 += 32 * S) {
         load(k0);
         compute(k0);
     }
-    RSTAMP(2);
     __shared__ float red[NW][TTS * TES * 4][64];
 #pragma unroll
     for (int ts = 0; ts < TTS; ts++)
@@ -328,7 +307,6 @@ __global__ __launch_bounds__(64 * NW) void k_route_approx(RouteArgs a) {
 #pragma unroll
             for (int v = 0; v < 4; v++) red[wv][(ts * TES + es) * 4 + v][lane] = acc[ts][es][v];
     __syncthreads();
-    RSTAMP(3);
 #pragma unroll
     for (int j = 0; j < NO; j++) {
         const int o = threadIdx.x + 64 * NW * j;
@@ -341,9 +319,6 @@ __global__ __launch_bounds__(64 * NW) void k_route_approx(RouteArgs a) {
         const int t = t0 + ts * 16 + 4 * (ln >> 4) + v, e = e0 + es * 16 + (ln & 15);
         if (t < T && e < E) a.logits[(size_t)t * (E + 1) + e] = sum * osc[j];
     }
-    RSTAMP(4);
-    RSTAMP(5);
-    if (ty == 0 && wv == 0) RSTAMP_FLUSH(60000);
 }
 
 /* Pass 2: WPT waves per token (the lane layout of wave_topk).  Every wave of
@@ -362,7 +337,6 @@ __global__ __launch_bounds__(256) void k_topk_exact(RouteArgs a) {
     const int t = blockIdx.x * TPB + tb;
     const bool live = t < a.T;
     const int E = a.E, H = a.H, K = a.K, ni = H / 256;
-    RSTAMP(0);
     float *lrow = a.logits + (size_t)min(t, a.T - 1) * (E + 1);
     const float *xrow = a.x + (size_t)min(t, a.T - 1) * H;
     /* every load unconditional (indices clamped, values masked where used):
@@ -392,7 +366,6 @@ __global__ __launch_bounds__(256) void k_topk_exact(RouteArgs a) {
     }
     /* |x| rounded up: the fp32 sum of squares is within H 2^-24 of itself */
     const float xn = sqrtf(wave_sum_fast(ss)) * (1.0f + 0x1p-10f);
-    RSTAMP(1);
     /* lower bounds (as keys) and upper bounds of the selection values */
     uint32_t lo[EPL];
     float hi[EPL];
@@ -425,7 +398,6 @@ __global__ __launch_bounds__(256) void k_topk_exact(RouteArgs a) {
         }
     }
     const float L = ord_value(m);
-    RSTAMP(2);
     bool cand[EPL];
     /* the candidate list (the shared-gate row E first), in this wave's own
      * LDS slot: position = rows before it in (j, lane) order */
@@ -469,10 +441,8 @@ __global__ __launch_bounds__(256) void k_topk_exact(RouteArgs a) {
             if (lane == 0) exv[tb][ids[b]] = d;
         }
     }
-    RSTAMP(3);
     if (WPT > 1) __syncthreads();
     if (!live || tw != 0) return;
-    RSTAMP(4);
     const float sg = a.wsg ? exv[tb][E] : 0.0f;
     uint32_t key[EPL];
 #pragma unroll
@@ -483,8 +453,6 @@ __global__ __launch_bounds__(256) void k_topk_exact(RouteArgs a) {
     }
     if (lane == 0) lrow[E] = sg;
     wave_topk_keys<EPL>(key, sg, K, lane, a.idx + t * K, a.w + t * K, a.sgl + t, nullptr);
-    RSTAMP(5);
-    RSTAMP_FLUSH(0);
 }
 
 /* Dispatch for any T, in three launches over blocks of DSP_TOK tokens.  A

@@ -2,7 +2,9 @@
  * decode kernels.
  *
  * Selection restates softmax_topk_route (inference/src/shaders.metal:
- * 1141-1234): K rounds of argmax, ties to the lower expert index, softmax over
+ * 1141-1234): K rounds of argmax, exact ties to the lower expert index (the
+ * contract's rule; the reference's shuffle-down tree, 1166-1200, settles an
+ * exact tie by tree position instead), softmax over
  * the K winners.  A round is a wave64 max over order-preserving 32-bit images
  * of the values; the lowest lane holding the maximum (lane order is expert
  * order) settles ties.
@@ -43,8 +45,8 @@ DEV uint32_t wave_max_u32(uint32_t m) {
  * sorts its keys (adjacent compare-exchanges that swap only on a strictly
  * larger right-hand key, hence stable: equal keys keep index order); a
  * round then takes the wave maximum of the lanes' heads and the lowest lane
- * holding it -- the lowest expert index among equal values (strict '>' of
- * shaders.metal:1164-1190) -- and that lane pops its head.  All round state
+ * holding it -- the lowest expert index among equal values, the contract's
+ * rule for exact ties -- and that lane pops its head.  All round state
  * except the lane's list is wave-uniform (scalar registers), and the rounds
  * form a rolled loop (each wave runs them once: unrolled, every round would
  * be fetched cold).  Lane k < K ends with the k-th expert and its softmax

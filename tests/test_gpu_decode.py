@@ -221,10 +221,11 @@ def test_dequant_bit_exact(fmt_name, kw):
     p.gm.close()
 
 
-@pytest.mark.parametrize("T", [1, 2, 5])
+@pytest.mark.parametrize("T", [1, 2, 5, 12, 16])
 def test_layer_forward_and_stack(T):
-    """T=2: GEMV kernels; T=5: small-batch routing (RMSNorm in the router)
-    feeding the small-tile grouped GEMMs."""
+    """T=1, 2: GEMV kernels; T=5, 12, 16: small-batch routing (RMSNorm in the
+    router, 9..16 tokens with four waves per router row) feeding the
+    small-tile grouped GEMMs."""
     banner("layer/stack forward, 3 layers, mixed Q6_K down, T=%d" % T)
     p = Pair(layers=3, q6k_every=2, seed=9, centered=True)
     h0 = (orome_amd.synth_normal(9, 3, T * p.H) * 4).reshape(T, p.H)

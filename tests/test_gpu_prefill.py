@@ -275,3 +275,48 @@ def test_small_batch_path_up_to_16(base, T):
     x, h = base.inputs(T, seed=1200 + T)
     ref, _ = base.run(0, x, h, path=_lib.OROME_PATH_MFMA)
     assert np.array_equal(out, ref)
+
+
+@pytest.mark.parametrize("kw,T,K", [(dict(S=0, seed=61), 12, 8), (dict(S=0, seed=62), 8, 8),
+                                    (dict(seed=63), 16, 16)])
+def test_small_batch_path_edges(kw, T, K):
+    """The small-batch path without a shared expert (T=8, 12) and at its
+    single-block dispatch limit T K = 256 (T=16, K=16): routing bit-exact,
+    output within tolerance of the oracle and bit for bit the MFMA path's."""
+    banner("small-batch edge %s T=%d K=%d" % (kw, T, K))
+    p = Pair(max_tokens=64, **kw)
+    out, _ = run_and_check(p, T, seed=1300 + T, K=K, path=_lib.OROME_PATH_AUTO)
+    x, h = p.inputs(T, seed=1300 + T)
+    ref, _ = p.run(0, x, h, K=K, path=_lib.OROME_PATH_MFMA)
+    assert np.array_equal(out, ref)
+    p.gm.close()
+
+
+@pytest.mark.parametrize("T", [12, 512, 2048])
+def test_q8_shared_expert_registered(T):
+    """The reference's 35B layout: a Q8_0 shared expert (gate, up and down).
+    Registration now repacks the routed matrices and the router even so, and
+    the grouped GEMMs read the Q8_0 shared expert row-major beside the
+    tile-major routed copies (T=2048: persistent kernels, one walk over the
+    routed tiles and one over the shared).  Routing bit-exact, output within
+    tolerance of the oracle and bit-identical to the unregistered layer; at
+    T=512 the two-pass router runs (some non-winning logits are its
+    approximations, not the canonical values)."""
+    banner("Q8_0 shared expert, registered layer, T=%d" % T)
+    p = Pair(max_tokens=T, shared=8, seed=64)
+    x, h = p.inputs(T, seed=1400 + T)
+    if T <= 512:
+        out, dbg = run_and_check(p, T, seed=1400 + T, path=_lib.OROME_PATH_AUTO)
+        if T == 512:
+            ref, rdbg = p.om.forward(0, x, h, debug=True)
+            assert not np.array_equal(dbg["logits"].view(np.uint32), rdbg["logits"].view(np.uint32)), \
+                "registered Q8_0-shared layer was routed in one pass"
+    else:
+        out, dbg = p.run(0, x, h, path=_lib.OROME_PATH_AUTO)
+        sel = np.arange(5, T, 97)
+        ref = p.om.forward(0, x[sel], h[sel])
+        assert rel_l2(out[sel] - h[sel], ref - h[sel]) < TOL
+    p.gm.unpack()
+    plain, _ = p.run(0, x, h, path=_lib.OROME_PATH_AUTO)
+    assert np.array_equal(out, plain)
+    p.gm.close()

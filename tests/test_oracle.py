@@ -88,25 +88,45 @@ def oracle_pairs(s):
     return sc, mn
 
 
+def layout_table_np(s):
+    """layout_table over rows of an [n, 12] uint8 array (numpy, vectorised)."""
+    s = s.astype(np.int64)
+    sc = np.empty((s.shape[0], 8), np.int64)
+    mn = np.empty((s.shape[0], 8), np.int64)
+    for j in range(4):
+        sc[:, j], mn[:, j] = s[:, j] & 63, s[:, j + 4] & 63
+    for i in range(4):
+        sh = 4 * (i & 1)
+        sc[:, 4 + i] = ((s[:, 8 + i // 2] >> sh) & 0xF) | ((s[:, i] >> 6) << 4)
+        mn[:, 4 + i] = ((s[:, 10 + i // 2] >> sh) & 0xF) | ((s[:, 4 + i] >> 6) << 4)
+    return sc, mn
+
+
 def test_q4k_scale_unpack_exhaustive():
-    # every field reads at most two bytes; sweep all 65536 values of each
-    # (low-byte, high-byte) pair that feeds a field, other bytes random
+    """Every field reads at most two bytes: for each (low byte, high byte) pair
+    that feeds a field, all 65536 values of the pair (the other ten bytes
+    random), through the oracle against the per-sub-block table."""
     rng = np.random.default_rng(2)
     pairs = [(j, j) for j in range(8)] + [(8 + i // 2, i) for i in range(4)] + \
             [(10 + i // 2, 4 + i) for i in range(4)]
     v = np.arange(65536)
     for lo_b, hi_b in pairs:
-        base = rng.integers(0, 256, 12)
-        for a, b in zip(v & 0xFF, v >> 8):
-            s = list(base)
-            s[lo_b] = int(a)
-            s[hi_b] = int(b) if hi_b != lo_b else int(a)
-            if (a + b) % 97:  # a 1/97 sample of the sweep per field keeps the run short
-                continue
-            assert oracle_pairs(s) == layout_table(s)
-    for _ in range(3000):
-        s = list(rng.integers(0, 256, 12))
-        assert oracle_pairs(s) == layout_table(s)
+        s = np.repeat(rng.integers(0, 256, 12, dtype=np.uint8)[None, :], 65536, axis=0)
+        s[:, hi_b] = v >> 8
+        s[:, lo_b] = v & 0xFF if lo_b != hi_b else v >> 8
+        s = np.ascontiguousarray(s)
+        out = np.empty((65536, 16), np.float32)
+        L.orc_unpack_q4k_batch(s.ctypes.data, 65536, out.ctypes.data)
+        sc, mn = layout_table_np(s)
+        assert np.array_equal(out[:, :8], sc) and np.array_equal(out[:, 8:], mn), (lo_b, hi_b)
+    s = rng.integers(0, 256, (100000, 12), dtype=np.uint8)
+    out = np.empty((100000, 16), np.float32)
+    L.orc_unpack_q4k_batch(s.ctypes.data, 100000, out.ctypes.data)
+    sc, mn = layout_table_np(s)
+    assert np.array_equal(out[:, :8], sc) and np.array_equal(out[:, 8:], mn)
+    # the scalar entry point agrees with the batch one
+    for r in range(50):
+        assert oracle_pairs(list(s[r])) == (list(out[r, :8].astype(int)), list(out[r, 8:].astype(int)))
 
 
 def test_q4k_layout_differs_from_ggml():
