@@ -146,7 +146,22 @@ typedef struct OromeHipGGUFFile {
     float rms_norm_eps;
     void *index;            /* private name index */
     bool owns_map;
+    int q4k_layout;         /* OROME_Q4K_LAYOUT_* the file declares (REFERENCE if silent) */
 } OromeHipGGUFFile;
+
+/* Q4_K scale/min packing of a file's Q4_K tensors.  The reference decodes
+ * sub-blocks 4..7 from scale bytes 8..11 as: scales 4,5 = the low/high
+ * nibbles of byte 8, scales 6,7 of byte 9, mins 4,5 of byte 10, mins 6,7 of
+ * byte 11 (inference/src/format.m:41-64).  ggml/llama.cpp files pack byte
+ * 8 + j as scale 4+j (low nibble) | min 4+j (high nibble)
+ * (get_scale_min_k4; the reference's own llama-style kernel,
+ * inference/src/shaders.metal:1575-1578).  The high 2-bit parts agree.  A
+ * file declares ggml packing with the string metadata key
+ * OROME_Q4K_LAYOUT_KEY = "ggml" (or "reference"); the kernels decode the
+ * reference packing only, and a ggml-packed file has bytes 8..11 of every
+ * Q4_K block permuted into it once, on the device, at upload. */
+#define OROME_Q4K_LAYOUT_KEY "orome.q4_k.scale_layout"
+enum { OROME_Q4K_LAYOUT_FILE = 0, OROME_Q4K_LAYOUT_REFERENCE = 1, OROME_Q4K_LAYOUT_GGML = 2 };
 
 /* inference/src/gguf.m:273-518 (mmap + parse; v2/v3; alignment rule 511-512) */
 OromeHipGGUFFile *orome_hip_gguf_open(const char *path);
@@ -249,6 +264,11 @@ typedef struct {
  * (unified memory); here the data section is copied unchanged into one HBM
  * allocation, so the same GGUF bytes feed the kernels. */
 OromeHipFormatProvider *orome_hip_format_provider_open_gguf(OromeHipGGUFFile *gf, orome_hip_ctx *ctx);
+/* The same with the Q4_K packing given by the caller (OROME_Q4K_LAYOUT_*;
+ * FILE = what the file declares, as orome_hip_format_provider_open_gguf
+ * does).  No counterpart in the reference, which has one packing. */
+OromeHipFormatProvider *orome_hip_format_provider_open_gguf_layout(OromeHipGGUFFile *gf, orome_hip_ctx *ctx,
+                                                                   int q4k_layout);
 /* inference/src/format.m:365-369 */
 void orome_hip_format_provider_close(OromeHipFormatProvider *fp);
 /* inference/src/format.m:374-409.  A missing tensor leaves a zeroed ref. */

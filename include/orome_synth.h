@@ -53,6 +53,9 @@ typedef struct {
     float rms_norm_eps;
     uint64_t seed;
     int centered;                 /* nonzero: zero-mean Q4_K rows (see above) */
+    int q4k_ggml_layout;          /* nonzero: the same Q4_K values, written in the ggml scale
+                                     packing, and the file declares it (orome_moe.h,
+                                     OROME_Q4K_LAYOUT_KEY) */
 } orome_synth_spec;
 
 /* Size in bytes of the GGUF image for `spec` (0 if the spec is invalid). */

@@ -16,6 +16,7 @@ LIB_PATH = os.environ.get("OROME_LIB") or os.path.join(HERE, "liborome_moe.so")
 QFMT_GGUF_Q4_K, QFMT_GGUF_Q5_K, QFMT_GGUF_Q6_K, QFMT_GGUF_Q8_0, QFMT_F16, QFMT_BF16, QFMT_F32 = range(7)
 FFN_MOE, FFN_DENSE = 0, 1
 OROME_PATH_AUTO, OROME_PATH_GEMV, OROME_PATH_MFMA = 0, 1, 2
+OROME_Q4K_LAYOUT_FILE, OROME_Q4K_LAYOUT_REFERENCE, OROME_Q4K_LAYOUT_GGML = 0, 1, 2
 OROME_MAX_ACTIVE = 16
 STAGES = ["norm", "router", "topk", "dispatch", "stage_f16", "gate_up", "down", "combine"]
 ERRORS = {0: "OK", -1: "EINVAL", -2: "EUNSUPPORTED", -3: "EHIP", -4: "ENOMEM", -5: "ENOTFOUND",
@@ -61,7 +62,7 @@ class GGUFFile(C.Structure):
                 ("ffn_type", C.c_int), ("num_layers", C.c_int), ("hidden_dim", C.c_int),
                 ("num_experts", C.c_int), ("num_experts_per_tok", C.c_int),
                 ("moe_intermediate", C.c_int), ("rms_norm_eps", C.c_float), ("index", C.c_void_p),
-                ("owns_map", C.c_bool)]
+                ("owns_map", C.c_bool), ("q4k_layout", C.c_int)]
 
 
 class FormatProvider(C.Structure):
@@ -76,7 +77,8 @@ class SynthSpec(C.Structure):
                 ("up_type", C.c_uint32), ("down_type", C.c_uint32),
                 ("shared_gate_type", C.c_uint32), ("shared_down_type", C.c_uint32),
                 ("q6k_down_every", C.c_int), ("zipf_bias", C.c_int), ("zipf_s", C.c_float),
-                ("rms_norm_eps", C.c_float), ("seed", C.c_uint64), ("centered", C.c_int)]
+                ("rms_norm_eps", C.c_float), ("seed", C.c_uint64), ("centered", C.c_int),
+                ("q4k_ggml_layout", C.c_int)]
 
 
 VP, I, U32, SZ, F32P = C.c_void_p, C.c_int, C.c_uint32, C.c_size_t, C.POINTER(C.c_float)
@@ -106,6 +108,7 @@ SIGNATURES = {
     "orome_hip_unpack_all": (I, [VP]),
     "orome_hip_kernel_timing": (I, [VP, VP, I]),
     "orome_hip_format_provider_open_gguf": (P(FormatProvider), [P(GGUFFile), VP]),
+    "orome_hip_format_provider_open_gguf_layout": (P(FormatProvider), [P(GGUFFile), VP, I]),
     "orome_hip_format_provider_close": (None, [P(FormatProvider)]),
     "orome_hip_format_resolve_expert_layer": (ExpertLayerRef, [P(FormatProvider), I, U32]),
     "orome_hip_build_tensor_cache_gguf": (P(LayerTensorCache), [P(FormatProvider), P(ModelConfig)]),

@@ -15,14 +15,30 @@
 #include "orome_internal.h"
 #include "orome_moe.h"
 
-OromeHipFormatProvider *orome_hip_format_provider_open_gguf(OromeHipGGUFFile *gf, orome_hip_ctx *ctx) {
-    if (!gf || !ctx) { orome_fail(OROME_EINVAL, "orome_hip_format_provider_open_gguf: NULL argument"); return NULL; }
+OromeHipFormatProvider *orome_hip_format_provider_open_gguf_layout(OromeHipGGUFFile *gf, orome_hip_ctx *ctx,
+                                                                   int q4k_layout) {
+    if (!gf || !ctx || q4k_layout < OROME_Q4K_LAYOUT_FILE || q4k_layout > OROME_Q4K_LAYOUT_GGML) {
+        orome_fail(OROME_EINVAL, "orome_hip_format_provider_open_gguf: bad argument");
+        return NULL;
+    }
+    const int layout = q4k_layout == OROME_Q4K_LAYOUT_FILE ? gf->q4k_layout : q4k_layout;
     size_t bytes = gf->file_size - gf->data_offset;
     void *dev = orome_hip_malloc(ctx, bytes ? bytes : 1);
     if (!dev) return NULL;
     if (bytes && orome_hip_htod(ctx, dev, (const uint8_t *)gf->mmap_base + gf->data_offset, bytes)) {
         orome_hip_free(ctx, dev);
         return NULL;
+    }
+    /* ggml-packed Q4_K tensors: bytes 8..11 of each block's scales into the
+     * reference packing the kernels decode (a byte permutation, once) */
+    for (uint64_t i = 0; layout == OROME_Q4K_LAYOUT_GGML && i < gf->num_tensors; i++) {
+        const OromeHipGGUFTensorInfo *ti = &gf->tensors[i];
+        if (ti->type != 12) continue; /* ggml type id of Q4_K */
+        const size_t nb = orome_hip_gguf_tensor_size(ti) / 144;
+        if (nb && orome_hip_q4k_ggml_to_reference(ctx, (uint8_t *)dev + ti->offset, nb)) {
+            orome_hip_free(ctx, dev);
+            return NULL;
+        }
     }
     OromeHipFormatProvider *fp = calloc(1, sizeof *fp);
     fp->gguf = gf;
@@ -32,6 +48,10 @@ OromeHipFormatProvider *orome_hip_format_provider_open_gguf(OromeHipGGUFFile *gf
     fp->model_bytes = bytes;
     fp->ctx = ctx;
     return fp;
+}
+
+OromeHipFormatProvider *orome_hip_format_provider_open_gguf(OromeHipGGUFFile *gf, orome_hip_ctx *ctx) {
+    return orome_hip_format_provider_open_gguf_layout(gf, ctx, OROME_Q4K_LAYOUT_FILE);
 }
 
 void orome_hip_format_provider_close(OromeHipFormatProvider *fp) {

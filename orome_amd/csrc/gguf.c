@@ -220,6 +220,7 @@ static OromeHipGGUFFile *parse(const uint8_t *img, size_t size, OromeHipGGUFFile
     }
     gf->alignment = 32;
     gf->rms_norm_eps = 1e-6f;
+    gf->q4k_layout = OROME_Q4K_LAYOUT_REFERENCE;
     /* pass 1 over the metadata: the architecture prefix may come after the
      * keys that use it, so remember key positions and resolve afterwards */
     size_t kv_start = r.pos;
@@ -246,6 +247,17 @@ static OromeHipGGUFFile *parse(const uint8_t *img, size_t size, OromeHipGGUFFile
                 }
                 if (key_is(k, kl, "general.alignment") && t != GT_STR && t != GT_ARR) {
                     gf->alignment = (uint32_t)rd_num(&r, t);
+                    continue;
+                }
+                if (key_is(k, kl, OROME_Q4K_LAYOUT_KEY) && t == GT_STR) {
+                    uint64_t vl;
+                    const char *v = rd_str(&r, &vl);
+                    if (v && key_is(v, vl, "ggml")) gf->q4k_layout = OROME_Q4K_LAYOUT_GGML;
+                    else if (v && key_is(v, vl, "reference")) gf->q4k_layout = OROME_Q4K_LAYOUT_REFERENCE;
+                    else {
+                        orome_fail(OROME_EFORMAT, "gguf: unknown %s value", OROME_Q4K_LAYOUT_KEY);
+                        goto fail;
+                    }
                     continue;
                 }
                 rd_skip(&r, t, 0);

@@ -253,6 +253,15 @@ extern "C" int orome_hip_dtoh(orome_hip_ctx *c, void *dst, const void *src, size
     return OROME_OK;
 }
 
+extern "C" int orome_hip_q4k_ggml_to_reference(orome_hip_ctx *c, void *blocks, size_t nblocks) {
+    if (!c || !blocks) return orome_fail(OROME_EINVAL, "q4k relayout: NULL argument");
+    if (set_dev(c)) return OROME_EHIP;
+    const int rc = launch_q4k_ggml_to_ref((uint8_t *)blocks, nblocks, c->stream);
+    if (rc) return orome_fail(rc == -1 ? OROME_EINVAL : OROME_EHIP, "q4k relayout: launch failed (%d)", rc);
+    HIP_OK(hipStreamSynchronize(c->stream), OROME_EHIP);
+    return OROME_OK;
+}
+
 /* --------------------------------------------------------------- forward */
 
 static const uint8_t *dev_addr(const void *buffer, size_t offset) {

@@ -125,6 +125,8 @@ int launch_combine(const float *y, const float *ysh, const uint32_t *pos, const 
                    int T, int H, int K, hipStream_t s);
 /* ssq[t][b] = canonical sum of h[t][256 b .. 256 b + 255]^2 */
 int launch_sumsq_parts(const float *h, int T, int H, float *ssq, hipStream_t s);
+/* ggml -> reference Q4_K scale packing of n blocks in place */
+int launch_q4k_ggml_to_ref(uint8_t *blocks, size_t n, hipStream_t s);
 /* zero fill by a kernel (bytes a multiple of 4) */
 int launch_zero(void *p, size_t bytes, hipStream_t s);
 

@@ -332,6 +332,28 @@ int launch_delay(uint32_t usec, hipStream_t s) {
     return hipGetLastError() == hipSuccess ? 0 : -3;
 }
 
+/* Q4_K scale bytes 8..11 (block bytes 12..15) from the ggml packing
+ * (byte 8 + j = scale 4+j low nibble | min 4+j high nibble) to the
+ * reference's (byte 8 = scales 4|5, 9 = scales 6|7, 10 = mins 4|5,
+ * 11 = mins 6|7, inference/src/format.m:41-64); one thread per 144-byte
+ * block. */
+__global__ void k_q4k_ggml_to_ref(uint8_t *blocks, size_t n) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    uint32_t *w = (uint32_t *)(blocks + i * 144 + 12);
+    const uint32_t g = *w;
+    const uint32_t g8 = g & 0xFFu, g9 = (g >> 8) & 0xFFu, g10 = (g >> 16) & 0xFFu, g11 = g >> 24;
+    const uint32_t r8 = (g8 & 0xFu) | ((g9 & 0xFu) << 4), r9 = (g10 & 0xFu) | ((g11 & 0xFu) << 4);
+    const uint32_t r10 = (g8 >> 4) | (g9 & 0xF0u), r11 = (g10 >> 4) | (g11 & 0xF0u);
+    *w = r8 | (r9 << 8) | (r10 << 16) | (r11 << 24);
+}
+
+int launch_q4k_ggml_to_ref(uint8_t *blocks, size_t n, hipStream_t s) {
+    if (((uintptr_t)blocks & 3) || !n) return -1;
+    hipLaunchKernelGGL(k_q4k_ggml_to_ref, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, blocks, n);
+    return hipGetLastError() == hipSuccess ? 0 : -3;
+}
+
 /* Zero fill of `words` 32-bit words (a kernel, not a memset node, so that
  * callers may capture it in a graph). */
 __global__ void k_zero(uint32_t *p, size_t words) {

@@ -69,7 +69,19 @@ static uint16_t to_f16(float f) {
 static void put16(uint8_t *p, uint16_t v) { p[0] = (uint8_t)v; p[1] = (uint8_t)(v >> 8); }
 
 /* one row-block range of a quantized tensor: `n` weights */
-static void fill_quant(xo_t *r, uint32_t type, uint8_t *dst, size_t nweights, int centered) {
+/* Scale bytes 8..11 of a Q4_K block from the reference packing (8 = scales
+ * 4|5, 9 = scales 6|7, 10 = mins 4|5, 11 = mins 6|7) to ggml's (8 + j =
+ * scale 4+j | min 4+j << 4); the values the block decodes to are unchanged. */
+static void q4k_to_ggml(uint8_t *blk) {
+    uint8_t *b = blk + 12;
+    const uint8_t r8 = b[0], r9 = b[1], r10 = b[2], r11 = b[3];
+    b[0] = (uint8_t)((r8 & 0xF) | ((r10 & 0xF) << 4));
+    b[1] = (uint8_t)((r8 >> 4) | (r10 & 0xF0));
+    b[2] = (uint8_t)((r9 & 0xF) | ((r11 & 0xF) << 4));
+    b[3] = (uint8_t)((r9 >> 4) | (r11 & 0xF0));
+}
+
+static void fill_quant(xo_t *r, uint32_t type, uint8_t *dst, size_t nweights, int centered, int ggml) {
     if (type == 12) {  /* Q4_K */
         for (size_t b = 0; b < nweights / 256; b++) {
             uint8_t *p = dst + b * 144;
@@ -88,6 +100,7 @@ static void fill_quant(xo_t *r, uint32_t type, uint8_t *dst, size_t nweights, in
                 memcpy(p + 8, p + 4, 4);
                 memcpy(p + 14, p + 12, 2);
             }
+            if (ggml) q4k_to_ggml(p);
         }
     } else if (type == 14) {  /* Q6_K */
         for (size_t b = 0; b < nweights / 256; b++) {
@@ -218,6 +231,7 @@ static int make_kvs(const orome_synth_spec *s, kv_t *kv, char keys[][64]) {
     }
     snprintf(keys[6], 64, "qwen35moe.attention.layer_norm_rms_epsilon");
     kv[n++] = (kv_t){keys[6], 0, 0, s->rms_norm_eps, 1, NULL};
+    if (s->q4k_ggml_layout) kv[n++] = (kv_t){OROME_Q4K_LAYOUT_KEY, 1, 0, 0, 0, "ggml"};
     return n;
 }
 
@@ -306,7 +320,7 @@ int orome_synth_gguf_write(const orome_synth_spec *s, void *dst, size_t size) {
         if (t->type != 0) {
             size_t per = t->bytes / ((t->n_dims == 3) ? t->dims[2] : 1);
             size_t nw = (size_t)t->dims[0] * t->dims[1];
-            fill_quant(&r, t->type, out + e * per, nw, s->centered);
+            fill_quant(&r, t->type, out + e * per, nw, s->centered, s->q4k_ggml_layout);
             continue;
         }
         float *f = (float *)out;

@@ -101,7 +101,7 @@ def synth_normal(seed, stream, n, std=1.0):
 
 def make_spec(layers=1, H=2048, E=256, K=8, M=512, S=512, down=_lib.GGML_Q4_K,
               shared=_lib.GGML_Q4_K, shared_down=None, q6k_every=0, zipf=False, zipf_s=1.1,
-              eps=1e-6, seed=0, centered=False):
+              eps=1e-6, seed=0, centered=False, q4k_ggml=False):
     s = _lib.SynthSpec()
     s.num_layers, s.hidden_dim, s.num_experts, s.num_experts_per_tok = layers, H, E, K
     s.moe_intermediate, s.shared_intermediate = M, S
@@ -112,16 +112,19 @@ def make_spec(layers=1, H=2048, E=256, K=8, M=512, S=512, down=_lib.GGML_Q4_K,
     s.q6k_down_every, s.zipf_bias, s.zipf_s = q6k_every, int(bool(zipf)), zipf_s
     s.rms_norm_eps, s.seed = eps, seed
     s.centered = int(bool(centered))
+    s.q4k_ggml_layout = int(bool(q4k_ggml))
     return s
 
 
 class MoEModel:
     """A GGUF MoE model resident in HBM (all layers), ready for forward calls."""
 
-    def __init__(self, image=None, path=None, max_tokens=16, device=0, pack=None):
+    def __init__(self, image=None, path=None, max_tokens=16, device=0, pack=None,
+                 q4k_layout=_lib.OROME_Q4K_LAYOUT_FILE):
         """pack: register every layer's tile-major Q4_K copies for the grouped
         GEMMs (orome_hip_pack_layer); default when max_tokens > 2, the batch
-        sizes that use those GEMMs."""
+        sizes that use those GEMMs.  q4k_layout: the Q4_K scale packing
+        (OROME_Q4K_LAYOUT_*; FILE = what the file declares)."""
         if (image is None) == (path is None):
             raise ValueError("give exactly one of image or path")
         self._image = image  # keep the host image alive while parsed
@@ -134,7 +137,7 @@ class MoEModel:
         self.cfg = _lib.ModelConfig()
         check(lib.orome_hip_model_config_from_gguf(self.gf, C.byref(self.cfg)), "orome_hip_model_config_from_gguf")
         self.ctx = Context(self.cfg, max_tokens, device)
-        self.fp = lib.orome_hip_format_provider_open_gguf(self.gf, self.ctx.handle)
+        self.fp = lib.orome_hip_format_provider_open_gguf_layout(self.gf, self.ctx.handle, int(q4k_layout))
         if not self.fp:
             raise _lib.OromeError("format_provider_open_gguf: %s" % lib.orome_last_error().decode())
         L = self.cfg.num_layers

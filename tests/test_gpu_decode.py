@@ -343,3 +343,32 @@ def test_kernel_timing_stamps(T):
     assert 0.5 < span_us < 5000
     assert np.array_equal(out, ref)
     p.gm.close()
+
+
+@pytest.mark.parametrize("T", [1, 8, 512])
+def test_ggml_q4k_packing_file(T):
+    """A file whose Q4_K tensors use the ggml scale packing (and declare it)
+    gives bit for bit the outputs of the same weights in the reference
+    packing: the upload permutes the scale bytes once and the kernels keep
+    one decoder.  Read as the reference packing instead, it gives different
+    outputs (the option is not a no-op)."""
+    banner("ggml Q4_K packing, T=%d" % T)
+    kw = dict(layers=1, H=2048, E=256, K=8, M=512, S=512, seed=66)
+    outs = []
+    for ggml, layout in ((False, _lib.OROME_Q4K_LAYOUT_FILE), (True, _lib.OROME_Q4K_LAYOUT_FILE),
+                         (True, _lib.OROME_Q4K_LAYOUT_REFERENCE)):
+        img = orome_amd.synth_gguf(orome_amd.make_spec(q4k_ggml=ggml, **kw))
+        gm = orome_amd.MoEModel(image=img, max_tokens=T, q4k_layout=layout)
+        x = orome_amd.synth_normal(80 + T, 1, T * 2048).reshape(T, 2048)
+        h = orome_amd.synth_normal(80 + T, 2, T * 2048).reshape(T, 2048)
+        dx, dh, do = (DeviceBuffer.from_array(gm.ctx, x), DeviceBuffer.from_array(gm.ctx, h),
+                      DeviceBuffer(gm.ctx, h.nbytes))
+        gm.forward(0, dx, dh, do, T)
+        gm.ctx.sync()
+        outs.append(do.download(np.float32, h.shape))
+        if len(outs) == 1:
+            ref = O.OracleModel(img).forward(0, x, h)
+            assert rel_l2(outs[0] - h, ref - h) < TOL
+        gm.close()
+    assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
+    assert not np.array_equal(outs[0], outs[2])
