@@ -17,6 +17,8 @@
  *         centered: mins equal the scales and dmin = fp16(7.5*d), so a
  *         weight is d*sc*q - fp16(7.5 d)*sc, about zero-mean (stacked layers
  *         with residuals stay finite under fp16 activation staging)
+ *   Q5_K  d = fp16(|N|*1e-3), dmin = fp16(|N|*1e-3), 12 scale bytes, 32 qh
+ *         and 128 ql bytes uniform
  *   Q6_K  ql/qh bytes uniform, 16 int8 scales uniform in [-64, 63],
  *         d = fp16(|N|*2e-3)
  *   Q8_0  d = fp16(|N|*4e-3), 32 int8 quants uniform in [-127, 127]
@@ -42,7 +44,7 @@ typedef struct {
     int num_experts_per_tok;
     int moe_intermediate;
     int shared_intermediate;      /* 0: no shared expert tensors */
-    uint32_t gate_type;           /* ggml type ids: 12 Q4_K, 14 Q6_K, 8 Q8_0 */
+    uint32_t gate_type;           /* ggml type ids: 12 Q4_K, 13 Q5_K, 14 Q6_K, 8 Q8_0 */
     uint32_t up_type;
     uint32_t down_type;
     uint32_t shared_gate_type;    /* gate and up of the shared expert */

@@ -193,6 +193,22 @@ DEV void q4_bias_h2(uint32_t w, h2 &l02, h2 &l13, h2 &h02, h2 &h13) {
     h13 = as_h2(p13 & 0xFFF0FFF0u);
 }
 
+/* --------------------------------------------------------------- Q5_K */
+
+/* Five-bit quants of a Q5_K dword as biased exact fp16 pairs: w = 4 ql bytes
+ * (positions l..l+3 of group g), h = the 4 qh bytes of the same positions;
+ * low value = (w & 15) | bit 2g of h << 4, high value = (w >> 4) | bit 2g+1
+ * of h << 4 (inference/src/format.m:110-141).  lo01 = (lo[l], lo[l+1]) + 1024
+ * etc.: the values OR-ed under the 0x64 exponent byte. */
+DEV void q5_bias_h2(uint32_t w, uint32_t h, int g, h2 &lo01, h2 &lo23, h2 &hi01, h2 &hi23) {
+    const uint32_t lo = (w & 0x0F0F0F0Fu) | (((h >> (2 * g)) & 0x01010101u) << 4);
+    const uint32_t hi = ((w >> 4) & 0x0F0F0F0Fu) | (((h >> (2 * g + 1)) & 0x01010101u) << 4);
+    lo01 = as_h2(__builtin_amdgcn_perm(0x64646464u, lo, 0x05010400u));
+    lo23 = as_h2(__builtin_amdgcn_perm(0x64646464u, lo, 0x05030402u));
+    hi01 = as_h2(__builtin_amdgcn_perm(0x64646464u, hi, 0x05010400u));
+    hi23 = as_h2(__builtin_amdgcn_perm(0x64646464u, hi, 0x05030402u));
+}
+
 /* --------------------------------------------------------------- Q6_K */
 
 /* Six-bit quants minus 32 as exact fp16 pairs: inputs are 4 ql bytes

@@ -271,6 +271,7 @@ static const uint8_t *dev_addr(const void *buffer, size_t offset) {
 static int kfmt(OromeHipQuantFormat f) {
     switch (f) {
         case OROME_QFMT_GGUF_Q4_K: return 0;
+        case OROME_QFMT_GGUF_Q5_K: return 1;
         case OROME_QFMT_GGUF_Q6_K: return 2;
         case OROME_QFMT_GGUF_Q8_0: return 3;
         default: return -1;
@@ -478,8 +479,8 @@ static int forward_impl(orome_hip_ctx *c, const OromeHipModelConfig *cfg, const 
     if (H % 256 || M % 256) return orome_fail(OROME_EUNSUPPORTED, "orome_moe_forward: H and M must be multiples of 256");
     if (!elr->buffer || elr->gate.format != OROME_QFMT_GGUF_Q4_K || elr->up.format != OROME_QFMT_GGUF_Q4_K)
         return orome_fail(OROME_EUNSUPPORTED, "orome_moe_forward: routed gate/up must be Q4_K");
-    if (kfmt(elr->down.format) != 0 && kfmt(elr->down.format) != 2)
-        return orome_fail(OROME_EUNSUPPORTED, "orome_moe_forward: routed down must be Q4_K or Q6_K");
+    if (kfmt(elr->down.format) < 0 || kfmt(elr->down.format) > 2)
+        return orome_fail(OROME_EUNSUPPORTED, "orome_moe_forward: routed down must be Q4_K, Q5_K or Q6_K");
     if (!lt->routing_gate.buffer || lt->routing_gate.format != OROME_QFMT_F32)
         return orome_fail(OROME_EUNSUPPORTED, "orome_moe_forward: router must be F32");
     const int S = lt->shared_gate.buffer ? (int)lt->shared_gate.out_dim : 0;
@@ -488,8 +489,8 @@ static int forward_impl(orome_hip_ctx *c, const OromeHipModelConfig *cfg, const 
         if (S > c->cfg.shared_intermediate)
             return orome_fail(OROME_EINVAL, "orome_moe_forward: shared expert larger than the context's");
         if (!lt->shared_up.buffer || !lt->shared_down.buffer ||
-            lt->shared_gate.format != lt->shared_up.format || kfmt(lt->shared_gate.format) == 2 ||
-            kfmt(lt->shared_gate.format) < 0 || kfmt(lt->shared_down.format) < 0)
+            lt->shared_gate.format != lt->shared_up.format || kfmt(lt->shared_gate.format) == 1 ||
+            kfmt(lt->shared_gate.format) == 2 || kfmt(lt->shared_gate.format) < 0 || kfmt(lt->shared_down.format) < 0)
             return orome_fail(OROME_EUNSUPPORTED, "orome_moe_forward: shared expert formats");
         sh.gate = dev_addr(lt->shared_gate.buffer, lt->shared_gate.offset);
         sh.up = dev_addr(lt->shared_up.buffer, lt->shared_up.offset);

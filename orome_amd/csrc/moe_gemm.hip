@@ -35,7 +35,7 @@
 
 /* FQ4KT, FQ6KT: Q4_K / Q6_K repacked tile-major (launch_pack_q4k,
  * launch_pack_q6k), same values */
-enum { FQ4K = 0, FQ6K = 2, FQ8 = 3, FQ4KT = GEMM_FMT_Q4K_TILED, FQ6KT = GEMM_FMT_Q6K_TILED };
+enum { FQ4K = 0, FQ5K = 1, FQ6K = 2, FQ8 = 3, FQ4KT = GEMM_FMT_Q4K_TILED, FQ6KT = GEMM_FMT_Q6K_TILED };
 
 typedef float f4v __attribute__((ext_vector_type(4)));
 
@@ -54,7 +54,10 @@ struct Shape {
 #define BLD (KCH + 16)                  /* chunk row pitch (halves): 544 bytes, B-fragment reads conflict-free */
 
 DEV size_t gemm_row_bytes(int fmt, int n) {
-    return fmt == FQ4K || fmt == FQ4KT ? (size_t)(n / 256) * 144 : fmt == FQ6K || fmt == FQ6KT ? (size_t)(n / 256) * 210 : (size_t)(n / 32) * 34;
+    return fmt == FQ4K || fmt == FQ4KT ? (size_t)(n / 256) * 144
+           : fmt == FQ5K               ? (size_t)(n / 256) * 176
+           : fmt == FQ6K || fmt == FQ6KT ? (size_t)(n / 256) * 210
+                                         : (size_t)(n / 32) * 34;
 }
 /* offset of lane row i of the 16-row block starting at row0: a row of its
  * own, or (tile-major Q4_K) the block base plus the lane's 16-byte column */
@@ -91,7 +94,7 @@ DEV void q8_h2_0213(uint32_t w, h2 &p02, h2 &p13) {
  * copied into LDS unchanged. */
 template <int FMT>
 DEV int frag_pos(int c) {
-    if (FMT == FQ4K || FMT == FQ4KT) { /* lane kg, step s: k = 64(kg>>1) + 16(kg&1) + 4s (+32 high nibbles) */
+    if (FMT == FQ4K || FMT == FQ4KT || FMT == FQ5K) { /* lane kg, step s: k = 64(kg>>1) + 16(kg&1) + 4s (+32 high nibbles) */
         const int g = c >> 4, r = c & 15, hi = r >> 3, rr = r & 7;
         return (((rr & 3) * 4 + 2 * g + (rr >> 2)) * 8) + 4 * hi;
     } else if (FMT == FQ6K || FMT == FQ6KT) { /* k = 32(kg&1) + 16(kg>>1) + 4s (+64 high nibbles) */
@@ -172,6 +175,58 @@ struct Span<FQ4KT> : Span<FQ4K> {
         const uint8_t *b = p + (size_t)(j >> 1) * 2304;
         hdr = ld_u4(b);
         q = ld_u4(b + 256 + (j & 1) * 1024 + kg * 256);
+    }
+};
+
+/* Q5_K (176-byte super-blocks: header as Q4_K, qh[32] @16, ql[128] @48):
+ * the lane mapping of Q4_K, with bit 2g (low values) or 2g+1 (high) of
+ * qh[l] as the fifth bit (inference/src/format.m:110-141).  The values are
+ * moved to the low bits, so the exact q*sc (<= 31*63 < 2048) takes the
+ * scales unscaled. */
+template <>
+struct Span<FQ5K> {
+    u4 hdr, q, qh;
+    MDEV void init(int) {}
+    MDEV void load(const uint8_t *row, int j, int kg) {
+        const uint8_t *p = row + (size_t)(j >> 1) * 176;
+        hdr = ld_u4(p);
+        q = ld_u4(p + 48 + 16 * (kg + 4 * (j & 1)));
+        qh = ld_u4(p + 16 + 16 * (kg & 1));
+    }
+    h2 d, sc, nc, mb;
+    int sh_lo; /* qh bit of the low values: 2g, g = 2(j&1) + kg/2 */
+    MDEV void prepare(int j, int kg) {
+        asm volatile("" ::"v"(hdr.w));
+        const uint32_t hb = (uint32_t)kg >> 1, sel = 0x0C010C00u + hb * 0x00020002u;
+        uint32_t s2, m2;
+        if ((j & 1) == 0) {
+            s2 = __builtin_amdgcn_perm(0u, hdr.y, sel) & 0x003F003Fu;
+            m2 = __builtin_amdgcn_perm(0u, hdr.z, sel) & 0x003F003Fu;
+        } else {
+            const uint32_t sp = (hdr.w >> (8 * hb)) & 0xFFu, mp = (hdr.w >> (8 * hb + 16)) & 0xFFu;
+            s2 = ((sp | (sp << 12)) & 0x000F000Fu) | ((__builtin_amdgcn_perm(0u, hdr.y, sel) >> 2) & 0x00300030u);
+            m2 = ((mp | (mp << 12)) & 0x000F000Fu) | ((__builtin_amdgcn_perm(0u, hdr.z, sel) >> 2) & 0x00300030u);
+        }
+        const h2 bias = {(_Float16)1024.0f, (_Float16)1024.0f};
+        const h2 S = or_bias(s2) - bias, M = or_bias(m2) - bias;
+        sc = S;
+        nc = S * h2{(_Float16)-1024.0f, (_Float16)-1024.0f};
+        const _Float16 dmin = __builtin_bit_cast(_Float16, (uint16_t)(hdr.x >> 16));
+        mb = M * h2{-dmin, -dmin};
+        d = splat(__builtin_bit_cast(_Float16, (uint16_t)(hdr.x & 0xFFFFu)));
+        sh_lo = 2 * (2 * (j & 1) + (kg >> 1));
+    }
+    /* k order of the result: l, l+2, l+1, l+3, l+32, l+34, l+33, l+35 */
+    MDEV h8 frag(int s) const {
+        const uint32_t w = u4_at(q, s), h = u4_at(qh, s);
+        const uint32_t lo = (w & 0x0F0F0F0Fu) | (((h >> sh_lo) & 0x01010101u) << 4);
+        const uint32_t hi = ((w >> 4) & 0x0F0F0F0Fu) | (((h >> (sh_lo + 1)) & 0x01010101u) << 4);
+        const h2 t0 = hfma(as_h2(__builtin_amdgcn_perm(0x64646464u, lo, 0x04020400u)), splat(sc.x), splat(nc.x));
+        const h2 t1 = hfma(as_h2(__builtin_amdgcn_perm(0x64646464u, lo, 0x04030401u)), splat(sc.x), splat(nc.x));
+        const h2 t2 = hfma(as_h2(__builtin_amdgcn_perm(0x64646464u, hi, 0x04020400u)), splat(sc.y), splat(nc.y));
+        const h2 t3 = hfma(as_h2(__builtin_amdgcn_perm(0x64646464u, hi, 0x04030401u)), splat(sc.y), splat(nc.y));
+        return cat4(hfma(t0, d, splat(mb.x)), hfma(t1, d, splat(mb.x)), hfma(t2, d, splat(mb.y)),
+                    hfma(t3, d, splat(mb.y)));
     }
 };
 
@@ -841,11 +896,13 @@ static int down_shape(const ExpertSide &ex, const SharedSide &sh, int H, int M, 
     /* all of a tile's activations stay resident: in_dim <= 2 chunks */
     if (H % NB || M % KCH || M > 2 * KCH || (sh.gate && (sh.S % KCH || sh.S > 2 * KCH))) return -2;
     const bool dtiled = ex.down_fmt == FQ4KT || ex.down_fmt == FQ6KT;
-    if (ex.down_fmt != FQ4K && ex.down_fmt != FQ6K && !dtiled) return -2;
+    if (ex.down_fmt != FQ4K && ex.down_fmt != FQ5K && ex.down_fmt != FQ6K && !dtiled) return -2;
     /* shared down: any supported format; with a tile-major routed down a
      * Q4_K/Q6_K shared down must be tile-major too (the packer makes both) */
     const int sf = sh.gate ? sh.down_fmt : ex.down_fmt;
-    if (dtiled ? sf != FQ4KT && sf != FQ6KT && sf != FQ8 : sf != FQ4K && sf != FQ6K && sf != FQ8) return -2;
+    if (dtiled ? sf != FQ4KT && sf != FQ6KT && sf != FQ5K && sf != FQ8
+               : sf != FQ4K && sf != FQ5K && sf != FQ6K && sf != FQ8)
+        return -2;
     return 0;
 }
 int gemm_small_tiles_ok(const ExpertSide &ex, const SharedSide &sh, int H, int M) {
@@ -952,6 +1009,7 @@ int launch_gemm_down(const ExpertSide &ex, const SharedSide &sh, const _Float16 
         else if ((F) == FQ4KT) hipLaunchKernelGGL((k_gemm_down_p<FQ4KT, TB>), dim3(pb), block, 0, s, ARGS);             \
         else if ((F) == FQ6KT) hipLaunchKernelGGL((k_gemm_down_p<FQ6KT, TB>), dim3(pb), block, 0, s, ARGS);             \
         else if ((F) == FQ8) hipLaunchKernelGGL((k_gemm_down_p<FQ8, TB>), dim3(pb), block, 0, s, ARGS);                 \
+        else if ((F) == FQ5K) hipLaunchKernelGGL((k_gemm_down_p<FQ5K, TB>), dim3(pb), block, 0, s, ARGS);               \
         else hipLaunchKernelGGL((k_gemm_down_p<FQ6K, TB>), dim3(pb), block, 0, s, ARGS);                                \
     } while (0)
 #define DP_TILE(F, ARGS)                                                        \
@@ -982,17 +1040,26 @@ int launch_gemm_down(const ExpertSide &ex, const SharedSide &sh, const _Float16 
     if (ex.down_fmt == FQ4KT) {
         if (sf == FQ4KT) DN_LAUNCH(FQ4KT, FQ4KT);
         else if (sf == FQ6KT) DN_LAUNCH(FQ4KT, FQ6KT);
+        else if (sf == FQ5K) DN_LAUNCH(FQ4KT, FQ5K);
         else DN_LAUNCH(FQ4KT, FQ8);
     } else if (ex.down_fmt == FQ6KT) {
         if (sf == FQ4KT) DN_LAUNCH(FQ6KT, FQ4KT);
         else if (sf == FQ6KT) DN_LAUNCH(FQ6KT, FQ6KT);
+        else if (sf == FQ5K) DN_LAUNCH(FQ6KT, FQ5K);
         else DN_LAUNCH(FQ6KT, FQ8);
     } else if (ex.down_fmt == FQ4K) {
         if (sf == FQ4K) DN_LAUNCH(FQ4K, FQ4K);
+        else if (sf == FQ5K) DN_LAUNCH(FQ4K, FQ5K);
         else if (sf == FQ6K) DN_LAUNCH(FQ4K, FQ6K);
         else DN_LAUNCH(FQ4K, FQ8);
+    } else if (ex.down_fmt == FQ5K) {
+        if (sf == FQ4K) DN_LAUNCH(FQ5K, FQ4K);
+        else if (sf == FQ5K) DN_LAUNCH(FQ5K, FQ5K);
+        else if (sf == FQ6K) DN_LAUNCH(FQ5K, FQ6K);
+        else DN_LAUNCH(FQ5K, FQ8);
     } else {
         if (sf == FQ4K) DN_LAUNCH(FQ6K, FQ4K);
+        else if (sf == FQ5K) DN_LAUNCH(FQ6K, FQ5K);
         else if (sf == FQ6K) DN_LAUNCH(FQ6K, FQ6K);
         else DN_LAUNCH(FQ6K, FQ8);
     }

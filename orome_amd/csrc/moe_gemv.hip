@@ -31,7 +31,8 @@
 enum { FQ4K = 0, FQ5K = 1, FQ6K = 2, FQ8 = 3 };
 
 DEV size_t row_bytes(int fmt, int n) {
-    return fmt == FQ4K ? (size_t)(n / 256) * 144 : fmt == FQ6K ? (size_t)(n / 256) * 210 : (size_t)(n / 32) * 34;
+    return fmt == FQ4K ? (size_t)(n / 256) * 144 : fmt == FQ5K ? (size_t)(n / 256) * 176
+           : fmt == FQ6K ? (size_t)(n / 256) * 210 : (size_t)(n / 32) * 34;
 }
 
 /* 16 consecutive fp32 -> 8 fp16 pairs (RNE) and the sum of the rounded values */
@@ -97,6 +98,33 @@ DEV float q4_dot(const Q4Raw &r, int c, const h2 *xl, const h2 *xh, float Xl, fl
         sl = dot2(l23, xl[2 * d + 1], sl);
         sh = dot2(h01, xh[2 * d], sh);
         sh = dot2(h23, xh[2 * d + 1], sh);
+    }
+    return (af.a_lo * sl + af.a_hi * sh) - (af.b_lo * Xl + af.b_hi * Xh);
+}
+
+/* Q5_K chunk: the same positions as a Q4_K chunk (16 ql bytes, the 16 qh
+ * bytes of those positions, the header) */
+struct Q5Raw {
+    u4 q, qh, hdr;
+};
+DEV Q5Raw q5_load(const uint8_t *row, int c) {
+    const uint8_t *sb = row + (c >> 3) * 176;
+    return Q5Raw{ld_u4(sb + 48 + (c & 7) * 16), ld_u4(sb + 16 + (c & 1) * 16), ld_u4(sb)};
+}
+DEV float q5_dot(const Q5Raw &r, int c, const h2 *xl, const h2 *xh, float Xl, float Xh) {
+    const int g = (c & 7) >> 1;
+    Q4Affine af = q4k_affine(r.hdr, g);
+    float sl = 0.0f, sh = 0.0f;
+    const uint32_t w[4] = {r.q.x, r.q.y, r.q.z, r.q.w}, hb[4] = {r.qh.x, r.qh.y, r.qh.z, r.qh.w};
+    const h2 bias = {(_Float16)1024.0f, (_Float16)1024.0f};
+#pragma unroll
+    for (int d = 0; d < 4; d++) {
+        h2 l01, l23, h01, h23;
+        q5_bias_h2(w[d], hb[d], g, l01, l23, h01, h23);
+        sl = dot2(l01 - bias, xl[2 * d], sl);
+        sl = dot2(l23 - bias, xl[2 * d + 1], sl);
+        sh = dot2(h01 - bias, xh[2 * d], sh);
+        sh = dot2(h23 - bias, xh[2 * d + 1], sh);
     }
     return (af.a_lo * sl + af.a_hi * sh) - (af.b_lo * Xl + af.b_hi * Xh);
 }
@@ -724,6 +752,20 @@ DEV void down_slot(const uint8_t *row, int in_dim, int cl, int n, const _Float16
                 load_h8(xrow[j] + klo + 40, xh + 4);
                 acc[j] += q4_dot(r, c, xl, xh, hsum(xl, 8), hsum(xh, 8));
             }
+        } else if (FMT == FQ5K) {
+            Q5Raw r = q5_load(row, c);
+            int klo;
+            q4_pos(c, klo);
+#pragma unroll
+            for (int j = 0; j < NT; j++) {
+                if (j >= n) break;
+                h2 xl[8], xh[8];
+                load_h8(xrow[j] + klo, xl);
+                load_h8(xrow[j] + klo + 8, xl + 4);
+                load_h8(xrow[j] + klo + 32, xh);
+                load_h8(xrow[j] + klo + 40, xh + 4);
+                acc[j] += q5_dot(r, c, xl, xh, hsum(xl, 8), hsum(xh, 8));
+            }
         } else if (FMT == FQ6K) {
             Q6Raw r = q6_load(row, c);
             int k0;
@@ -786,6 +828,7 @@ __global__ __launch_bounds__(128) void k_gemv_down(DownArgs a) {
 #pragma unroll
     for (int j = 0; j < NT; j++) acc[j] = 0.0f;
     if (fmt == FQ4K) down_slot<NT, FQ4K>(row, in_dim, cl, n, xrow, acc);
+    else if (fmt == FQ5K) down_slot<NT, FQ5K>(row, in_dim, cl, n, xrow, acc);
     else if (fmt == FQ6K) down_slot<NT, FQ6K>(row, in_dim, cl, n, xrow, acc);
     else down_slot<NT, FQ8>(row, in_dim, cl, n, xrow, acc);
 #pragma unroll
@@ -823,6 +866,11 @@ struct DnRaw<FQ4K> {
         load_h8(x + klo + 40, xh + 4);
         return q4_dot(r, c, xl, xh, hsum(xl, 8), hsum(xh, 8));
     }
+};
+template <>
+struct DnRaw<FQ5K> {
+    Q5Raw r;
+    MDEV void load(const uint8_t *row, int c) { r = q5_load(row, c); }
 };
 template <>
 struct DnRaw<FQ6K> {
@@ -885,6 +933,12 @@ struct DnX<FQ4K> {
         Xh = hsum(xh, 8);
     }
     MDEV float dot(const DnRaw<FQ4K> &r, int c) const { return q4_dot(r.r, c, xl, xh, Xl, Xh); }
+};
+/* Q5_K chunks cover the positions of Q4_K chunks: the same activation runs
+ * and sums, a five-bit dot */
+template <>
+struct DnX<FQ5K> : DnX<FQ4K> {
+    MDEV float dot(const DnRaw<FQ5K> &r, int c) const { return q5_dot(r.r, c, xl, xh, Xl, Xh); }
 };
 template <>
 struct DnX<FQ6K> {
@@ -1122,6 +1176,22 @@ int launch_gemv_gate_up(const ExpertSide &ex, const SharedSide &sh, const RouteA
 }
 
 
+/* MACRO(EF, SF) for the runtime pair (routed down format in {Q4_K, Q5_K,
+ * Q6_K}, shared down format in {Q4_K, Q5_K, Q6_K, Q8_0}) */
+#define DOWN_SF_SWITCH(EF, SF, MACRO)       \
+    do {                                    \
+        if ((SF) == FQ4K) MACRO(EF, FQ4K);  \
+        else if ((SF) == FQ5K) MACRO(EF, FQ5K); \
+        else if ((SF) == FQ6K) MACRO(EF, FQ6K); \
+        else MACRO(EF, FQ8);                \
+    } while (0)
+#define DOWN_FMT_SWITCH(EFR, SFR, MACRO)                    \
+    do {                                                    \
+        if ((EFR) == FQ4K) DOWN_SF_SWITCH(FQ4K, SFR, MACRO); \
+        else if ((EFR) == FQ5K) DOWN_SF_SWITCH(FQ5K, SFR, MACRO); \
+        else DOWN_SF_SWITCH(FQ6K, SFR, MACRO);              \
+    } while (0)
+
 static int nt_for(int T) { return T <= 1 ? 1 : T <= 2 ? 2 : T <= 4 ? 4 : T <= 8 ? 8 : 0; }
 
 int launch_gemv_down(const ExpertSide &ex, const SharedSide &sh, const _Float16 *act,
@@ -1129,8 +1199,8 @@ int launch_gemv_down(const ExpertSide &ex, const SharedSide &sh, const _Float16 
                      float *y, float *ysh, hipStream_t s) {
     const int NT = nt_for(T);
     if (!NT || H % 8 || M % 512 || (sh.gate && sh.S % 512)) return -2;
-    if (ex.down_fmt != FQ4K && ex.down_fmt != FQ6K) return -2;
-    if (sh.gate && sh.down_fmt != FQ4K && sh.down_fmt != FQ6K && sh.down_fmt != FQ8) return -2;
+    if (ex.down_fmt != FQ4K && ex.down_fmt != FQ5K && ex.down_fmt != FQ6K) return -2;
+    if (sh.gate && sh.down_fmt != FQ4K && sh.down_fmt != FQ5K && sh.down_fmt != FQ6K && sh.down_fmt != FQ8) return -2;
     DownArgs a;
     a.down = ex.down; a.down_stride = ex.down_stride; a.fmt = ex.down_fmt;
     a.sh_down = sh.gate ? sh.down : nullptr; a.sh_fmt = sh.down_fmt; a.S = sh.S;
@@ -1141,15 +1211,7 @@ int launch_gemv_down(const ExpertSide &ex, const SharedSide &sh, const _Float16 
         const dim3 g((unsigned)((umax + (sh.gate ? 1 : 0)) * (H / DB_ROWS)));
         const int sf = sh.gate ? sh.down_fmt : FQ4K;
 #define DB_LAUNCH(EF, SF) hipLaunchKernelGGL((k_gemv_down_b<EF, SF>), g, dim3(256), 0, s, a)
-        if (ex.down_fmt == FQ4K) {
-            if (sf == FQ4K) DB_LAUNCH(FQ4K, FQ4K);
-            else if (sf == FQ6K) DB_LAUNCH(FQ4K, FQ6K);
-            else DB_LAUNCH(FQ4K, FQ8);
-        } else {
-            if (sf == FQ4K) DB_LAUNCH(FQ6K, FQ4K);
-            else if (sf == FQ6K) DB_LAUNCH(FQ6K, FQ6K);
-            else DB_LAUNCH(FQ6K, FQ8);
-        }
+        DOWN_FMT_SWITCH(ex.down_fmt, sf, DB_LAUNCH);
 #undef DB_LAUNCH
         return hipGetLastError() == hipSuccess ? 0 : -3;
     }
@@ -1167,23 +1229,15 @@ int launch_gemv_down_combine1(const ExpertSide &ex, const SharedSide &sh, const 
                               const _Float16 *act, const _Float16 *act_sh, int H, int M, int K,
                               const float *h_in, float *h_out, float *res, hipStream_t s) {
     if (K < 1 || K > DC_K || H % 8 || M != 512 || (sh.gate && sh.S != 512)) return -2;
-    if (ex.down_fmt != FQ4K && ex.down_fmt != FQ6K) return -2;
+    if (ex.down_fmt != FQ4K && ex.down_fmt != FQ5K && ex.down_fmt != FQ6K) return -2;
     const int sf = sh.gate ? sh.down_fmt : FQ4K;
-    if (sf != FQ4K && sf != FQ6K && sf != FQ8) return -2;
+    if (sf != FQ4K && sf != FQ5K && sf != FQ6K && sf != FQ8) return -2;
     DownArgs a = {};
     a.down = ex.down; a.down_stride = ex.down_stride; a.fmt = ex.down_fmt;
     a.sh_down = sh.gate ? sh.down : nullptr; a.sh_fmt = sf; a.S = sh.gate ? sh.S : 0;
     a.act = act; a.act_sh = act_sh; a.T = 1; a.H = H; a.M = M; a.K = K;
 #define DC_LAUNCH(EF, SF) hipLaunchKernelGGL((k_gemv_down_combine1<EF, SF>), dim3(H / 8), dim3(128), 0, s, a, ra, h_in, h_out, res)
-    if (ex.down_fmt == FQ4K) {
-        if (sf == FQ4K) DC_LAUNCH(FQ4K, FQ4K);
-        else if (sf == FQ6K) DC_LAUNCH(FQ4K, FQ6K);
-        else DC_LAUNCH(FQ4K, FQ8);
-    } else {
-        if (sf == FQ4K) DC_LAUNCH(FQ6K, FQ4K);
-        else if (sf == FQ6K) DC_LAUNCH(FQ6K, FQ6K);
-        else DC_LAUNCH(FQ6K, FQ8);
-    }
+    DOWN_FMT_SWITCH(ex.down_fmt, sf, DC_LAUNCH);
 #undef DC_LAUNCH
     return hipGetLastError() == hipSuccess ? 0 : -3;
 }

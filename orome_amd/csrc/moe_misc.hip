@@ -6,7 +6,7 @@
 
 /* Row dequant to fp32 (and optionally fp16 RNE), one thread per 32-weight
  * chunk.  Arithmetic restates format_decode_row_f32
- * (inference/src/format.m:66-174): Q4_K (d*sc)*q - dmin*m, Q6_K (d*sc)*q,
+ * (inference/src/format.m:66-174): Q4_K and Q5_K (d*sc)*q - dmin*m, Q6_K (d*sc)*q,
  * Q8_0 d*q; every product is exact in fp32, so fused or not the result is
  * the same. */
 __global__ void k_dequant(int fmt, const uint8_t *src, uint32_t rows, uint32_t n, float *o32,
@@ -28,6 +28,19 @@ __global__ void k_dequant(int fmt, const uint8_t *src, uint32_t rows, uint32_t n
             v[i] = af.a_lo * (float)(byte & 0xF) - af.b_lo;
             pos[i] = k;
             v[16 + i] = af.a_hi * (float)(byte >> 4) - af.b_hi;
+            pos[16 + i] = k + 32;
+        }
+    } else if (fmt == 1) { /* Q5_K: the Q4_K chunks plus bit 2g / 2g+1 of qh[l] */
+        const uint8_t *sb = src + (size_t)r * (n / 256) * 176 + (c >> 3) * 176;
+        u4 hdr = ld_u4(sb);
+        const int g = (c & 7) >> 1, lh = (c & 1) * 16;
+        Q4Affine af = q4k_affine(hdr, g);
+        for (int i = 0; i < 16; i++) {
+            const uint32_t byte = sb[48 + g * 32 + lh + i], qh = sb[16 + lh + i];
+            const int k = (c >> 3) * 256 + g * 64 + lh + i;
+            v[i] = af.a_lo * (float)((byte & 0xF) | ((qh >> (2 * g)) & 1u) << 4) - af.b_lo;
+            pos[i] = k;
+            v[16 + i] = af.a_hi * (float)((byte >> 4) | ((qh >> (2 * g + 1)) & 1u) << 4) - af.b_hi;
             pos[16 + i] = k + 32;
         }
     } else if (fmt == 2) { /* Q6_K: chunk = (super-block, half, 8 positions) */
@@ -63,7 +76,7 @@ __global__ void k_dequant(int fmt, const uint8_t *src, uint32_t rows, uint32_t n
 
 int launch_dequant(int fmt, const uint8_t *src, uint32_t rows, uint32_t n, float *o32,
                    _Float16 *o16, hipStream_t s) {
-    if (fmt != 0 && fmt != 2 && fmt != 3) return -2;
+    if (fmt < 0 || fmt > 3) return -2;
     if ((fmt == 3 && n % 32) || (fmt != 3 && n % 256)) return -1;
     size_t work = (size_t)rows * (n / 32);
     if (!work) return 0;

@@ -102,6 +102,13 @@ static void fill_quant(xo_t *r, uint32_t type, uint8_t *dst, size_t nweights, in
             }
             if (ggml) q4k_to_ggml(p);
         }
+    } else if (type == 13) {  /* Q5_K: Q4_K's header, qh[32] and ql[128] uniform */
+        for (size_t b = 0; b < nweights / 256; b++) {
+            uint8_t *p = dst + b * 176;
+            put16(p, to_f16((float)(fabs(xo_normal(r)) * 1e-3)));
+            put16(p + 2, to_f16((float)(fabs(xo_normal(r)) * 1e-3)));
+            xo_bytes(r, p + 4, 172);
+        }
     } else if (type == 14) {  /* Q6_K */
         for (size_t b = 0; b < nweights / 256; b++) {
             uint8_t *p = dst + b * 210;
@@ -122,6 +129,7 @@ static size_t type_bytes(uint32_t type, size_t n) {
     switch (type) {
         case 0: return n * 4;
         case 12: return n / 256 * 144;
+        case 13: return n / 256 * 176;
         case 14: return n / 256 * 210;
         case 8: return n / 32 * 34;
     }
@@ -148,12 +156,12 @@ static int spec_ok(const orome_synth_spec *s) {
         s->num_experts <= 0 || s->moe_intermediate <= 0 || s->moe_intermediate % 256 ||
         s->shared_intermediate < 0 || s->shared_intermediate % 256)
         return 0;
-    uint32_t ok[] = {12, 14, 8};
+    uint32_t ok[] = {12, 13, 14, 8};
     uint32_t ts[] = {s->gate_type, s->up_type, s->down_type, s->shared_gate_type, s->shared_down_type};
     for (int i = 0; i < 5; i++) {
         if (i >= 3 && !s->shared_intermediate) continue;
         int f = 0;
-        for (int j = 0; j < 3; j++) f |= ts[i] == ok[j];
+        for (int j = 0; j < 4; j++) f |= ts[i] == ok[j];
         if (!f) return 0;
     }
     return 1;

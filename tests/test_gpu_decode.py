@@ -153,7 +153,9 @@ def test_decode_other_k(base, K):
                                    (dict(down=14, zipf=True, seed=1), 8),
                                    (dict(shared=8, seed=2), 4),
                                    (dict(shared=8, shared_down=14, seed=3), 3),
-                                   (dict(S=0, seed=4), 2)])
+                                   (dict(S=0, seed=4), 2),
+                                   (dict(down=13, seed=15), 1), (dict(down=13, shared_down=13, seed=16), 2),
+                                   (dict(down=13, shared=8, seed=17), 1)])
 def test_decode_variants(kw, T):
     banner("decode variant %s T=%d" % (kw, T))
     p = Pair(**kw)
@@ -196,12 +198,14 @@ def test_topk_teacher_forced(base):
             assert np.allclose(w[ok], rw[ok], rtol=2e-6, atol=1e-7)
 
 
-@pytest.mark.parametrize("fmt_name,kw", [("Q4_K", {}), ("Q6_K", dict(down=14)), ("Q8_0", dict(shared=8))])
+@pytest.mark.parametrize("fmt_name,kw", [("Q4_K", {}), ("Q5_K", dict(down=13)), ("Q6_K", dict(down=14)),
+                                         ("Q8_0", dict(shared=8))])
 def test_dequant_bit_exact(fmt_name, kw):
     banner("dequant %s" % fmt_name)
     p = Pair(E=8, **kw)
     om = p.om
     name, rows, n = {"Q4_K": ("blk.0.ffn_gate_exps.weight", 8 * 512, 2048),
+                     "Q5_K": ("blk.0.ffn_down_exps.weight", 8 * 2048, 512),
                      "Q6_K": ("blk.0.ffn_down_exps.weight", 8 * 2048, 512),
                      "Q8_0": ("blk.0.ffn_gate_shexp.weight", 512, 2048)}[fmt_name]
     dims, typ, off, nb = om.tensors[name]

@@ -77,7 +77,9 @@ def test_prefill_2048_properties(base):
     assert rel_l2(out[sel] - h[sel], ref - h[sel]) < TOL
 
 
-@pytest.mark.parametrize("kw,T", [(dict(down=14, zipf=True, seed=31), 512),
+@pytest.mark.parametrize("kw,T", [(dict(down=13, seed=32), 512), (dict(down=13, shared=8, seed=33), 2048),
+                                   (dict(down=13, shared_down=13, seed=34), 12),
+                                   (dict(down=14, zipf=True, seed=31), 512),
                                    (dict(shared=8, seed=32), 64),
                                    (dict(shared=8, shared_down=14, seed=33), 48),
                                    (dict(S=0, seed=34), 40)])

@@ -279,6 +279,53 @@ def test_q6k_matches_ggml_layout_and_one_hot():
     assert np.nonzero(w != base)[0].tolist() == [37] and w[37] == -16
 
 
+def q5k_independent(blocks):
+    """Q5_K blocks [n, 176] -> [n, 256]: the published ggml q5_K formula (per
+    64-value group j, the low nibble of ql[32 j + l] plus 16 if bit 2 j of
+    qh[l] is set, the high nibble plus 16 if bit 2 j + 1 is set; y = d sc q
+    - dmin m), with the scales and mins of the reference packing
+    (layout_table_np, format.m:41-64)."""
+    b = blocks.astype(np.uint32)
+    d = blocks[:, 0:2].copy().view(np.float16).astype(np.float32)[:, 0]
+    dmin = blocks[:, 2:4].copy().view(np.float16).astype(np.float32)[:, 0]
+    sc, mn = layout_table_np(blocks[:, 4:16])
+    qh, ql = b[:, 16:48], b[:, 48:176]
+    y = np.empty((len(b), 256), np.float32)
+    for j in range(4):
+        for h in range(2):
+            s = 2 * j + h
+            q = ((ql[:, 32 * j:32 * j + 32] >> (4 * h)) & 0xF) + 16 * ((qh >> (2 * j + h)) & 1)
+            y[:, 64 * j + 32 * h:64 * j + 32 * h + 32] = (d * sc[:, s].astype(np.float32))[:, None] * \
+                q.astype(np.float32) - (dmin * mn[:, s].astype(np.float32))[:, None]
+    return y
+
+
+def test_q5k_matches_independent_decoder_and_one_hot():
+    """Q5_K (inference/src/format.m:110-141): random blocks against the
+    independent decoder bit for bit; a single qh bit moves exactly one weight
+    by 16 d sc."""
+    rng = np.random.default_rng(14)
+    blk = rng.integers(0, 256, (2000, 176)).astype(np.uint8)
+    blk[:, 0:2] = np.frombuffer((np.abs(rng.standard_normal(2000)) * 1e-2).astype(np.float16).tobytes(),
+                                np.uint8).reshape(-1, 2)
+    blk[:, 2:4] = np.frombuffer((np.abs(rng.standard_normal(2000)) * 1e-2).astype(np.float16).tobytes(),
+                                np.uint8).reshape(-1, 2)
+    got = O.decode_rows(O.Q5_K, blk, 2000, 256)
+    assert np.array_equal(got.view(np.uint32), q5k_independent(blk).view(np.uint32))
+    one = np.zeros(176, np.uint8)
+    one[0:2] = np.frombuffer(np.float16(1.0).tobytes(), np.uint8)
+    one[4:16] = 1  # every scale 1 (and the packed high parts 0), every min 1
+    base = O.decode_rows(O.Q5_K, one, 1, 256)[0]
+    one[16 + 7] = 1 << 4  # qh[7] bit 4: group 2, low half -> weight 2*64 + 7 (sub-block 4, scale 1)
+    w = O.decode_rows(O.Q5_K, one, 1, 256)[0]
+    assert sc_of(one, 4) == 1
+    assert np.nonzero(w != base)[0].tolist() == [135] and w[135] - base[135] == 16.0
+
+
+def sc_of(blk, s):
+    return layout_table(list(blk[4:16]))[0][s]
+
+
 # ------------------------------------------------------------------ A6
 def test_canonical_dot_exact_on_integers_and_bounded():
     rng = np.random.default_rng(5)
