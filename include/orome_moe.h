@@ -363,10 +363,26 @@ int orome_moe_topk(orome_hip_ctx *ctx, const float *logits_dev, const float *bia
 int orome_dequant_rows(orome_hip_ctx *ctx, OromeHipQuantFormat fmt, const void *src_dev, uint32_t rows,
                        uint32_t in_dim, float *out_dev);
 
-/* The fp16 weight tiles that the MFMA path feeds to the matrix cores:
- * fp16(dequant(w)) rounded to nearest even, [rows x in_dim]. */
+/* fp16(dequant(w)) rounded to nearest even, [rows x in_dim] (the scalar
+ * dequant above, then one rounding).  For Q8_0 and for Q6_K with
+ * |q sc| <= 2048 these are the MFMA path's weights; Q4_K and Q5_K there
+ * round d sc q - fp16(dmin m) once, which can differ by one ulp
+ * (orome_debug_mfma_weights returns the MFMA path's own values). */
 int orome_dequant_rows_f16(orome_hip_ctx *ctx, OromeHipQuantFormat fmt, const void *src_dev,
                            uint32_t rows, uint32_t in_dim, uint16_t *out_dev);
+
+/* The fp16 weights the grouped GEMMs feed to the matrix cores, read back
+ * through the real down-projection GEMM: one matrix [rows x in_dim]
+ * (rows = the context's hidden size, in_dim = its expert intermediate size)
+ * of `fmt` (Q4_K, Q5_K, Q6_K, Q8_0) is multiplied by in_dim one-hot fp16
+ * activation rows, so out_dev[j][r] = the fp16 weight (r, j) the matrix cores
+ * used, exactly (products with 1, sums of zeros).  tiled: repack it first
+ * (Q4_K, Q6_K) as orome_hip_pack_layer does and read the tile-major copy.
+ * out_dev: fp32 [in_dim x rows].  For tests; not thread-safe with forward
+ * calls on the context (it uses the context's scratch).  No counterpart in
+ * the reference. */
+int orome_debug_mfma_weights(orome_hip_ctx *ctx, OromeHipQuantFormat fmt, int tiled, const void *w_dev,
+                             uint32_t rows, uint32_t in_dim, float *out_dev);
 
 /* ------------------------------------------------- graphs and timing */
 

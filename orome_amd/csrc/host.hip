@@ -771,6 +771,72 @@ extern "C" int orome_dequant_rows_f16(orome_hip_ctx *c, OromeHipQuantFormat fmt,
     return OROME_OK;
 }
 
+/* one-hot activation rows for orome_debug_mfma_weights: row j is e_j in the
+ * (0,2,1,3)-per-4-group storage order of the GEMM sources */
+__global__ void k_one_hot_f16(_Float16 *act, int n, int ld) {
+    const int j = blockIdx.x;
+    for (int i = threadIdx.x; i < ld; i += blockDim.x) act[(size_t)j * ld + i] = (_Float16)0.0f;
+    __syncthreads();
+    if (threadIdx.x == 0 && j < n) {
+        const int perm[4] = {0, 2, 1, 3};
+        act[(size_t)j * ld + (j & ~3) + perm[j & 3]] = (_Float16)1.0f;
+    }
+}
+
+extern "C" int orome_debug_mfma_weights(orome_hip_ctx *c, OromeHipQuantFormat fmt, int tiled, const void *w,
+                                        uint32_t rows, uint32_t in_dim, float *out) {
+    if (!c || !w || !out) return orome_fail(OROME_EINVAL, "orome_debug_mfma_weights: NULL argument");
+    const int H = c->cfg.hidden_dim, M = c->cfg.moe_intermediate;
+    const int f = kfmt(fmt);
+    if ((int)rows != H || (int)in_dim != M || f < 0 || (tiled && f != 0 && f != 2))
+        return orome_fail(OROME_EINVAL, "orome_debug_mfma_weights: a %ux%u %s matrix does not fit", rows, in_dim,
+                          tiled ? "tile-major" : "row-major");
+    if ((size_t)M > (size_t)c->tmax * c->kmax)
+        return orome_fail(OROME_EINVAL, "orome_debug_mfma_weights: context too small for %d one-hot rows", M);
+    if (set_dev(c)) return OROME_EHIP;
+    hipStream_t s = c->stream;
+    void *packed = NULL;
+    ExpertSide ex = {};
+    ex.down = (const uint8_t *)w;
+    ex.down_fmt = f;
+    ex.gate_fmt = 0;
+    if (tiled) {
+        const size_t nb = f == 0 ? packed_q4k_bytes(H, M, 1) : packed_q6k_bytes(H, M, 1);
+        HIP_OK(hipMalloc(&packed, nb), OROME_ENOMEM);
+        const int rc = (f == 0 ? launch_pack_q4k : launch_pack_q6k)((const uint8_t *)w, (uint8_t *)packed, H, M, 1, 0, s);
+        if (rc) {
+            (void)hipFree(packed);
+            return launch_rc(rc, "orome_debug_mfma_weights: repack");
+        }
+        ex.down = (const uint8_t *)packed;
+        ex.down_fmt = f == 0 ? GEMM_FMT_Q4K_TILED : GEMM_FMT_Q6K_TILED;
+    }
+    SharedSide sh = {NULL, NULL, NULL, 0, 0, 0};
+    /* M one-hot rows as the pairs of expert 0, in 32-row tiles */
+    hipLaunchKernelGGL(k_one_hot_f16, dim3((unsigned)M), dim3(256), 0, s, c->act, M, M);
+    const int ntile = (M + GEMM_TILE_SMALL - 1) / GEMM_TILE_SMALL;
+    uint32_t *hl = (uint32_t *)calloc(1 + 3 * (size_t)ntile, 4);
+    hl[0] = (uint32_t)ntile;
+    for (int t = 0; t < ntile; t++) {
+        hl[1 + 3 * t] = 0;
+        hl[2 + 3 * t] = (uint32_t)(t * GEMM_TILE_SMALL);
+        hl[3 + 3 * t] = (uint32_t)(M - t * GEMM_TILE_SMALL < GEMM_TILE_SMALL ? M - t * GEMM_TILE_SMALL : GEMM_TILE_SMALL);
+    }
+    hipError_t e = hipMemcpyAsync(c->tiles, hl, (1 + 3 * (size_t)ntile) * 4, hipMemcpyHostToDevice, s);
+    int rc = e == hipSuccess ? 0 : -3;
+    if (!rc) e = hipStreamSynchronize(s);
+    free(hl);
+    if (!rc && e == hipSuccess)
+        rc = launch_gemm_down(ex, sh, c->act, c->act_sh, c->tmax * c->kmax, c->tmax, M, H, M, 1, 1, GEMM_TILE_SMALL,
+                              c->tiles, ntile, c->y, c->ysh, s);
+    if (!rc) e = hipMemcpyAsync(out, c->y, (size_t)M * H * 4, hipMemcpyDeviceToDevice, s);
+    if (!rc && e == hipSuccess) e = hipStreamSynchronize(s);
+    if (packed) (void)hipFree(packed);
+    if (rc) return launch_rc(rc, "orome_debug_mfma_weights: grouped down GEMM");
+    if (e != hipSuccess) return orome_fail(OROME_EHIP, "orome_debug_mfma_weights: %s", hipGetErrorString(e));
+    return OROME_OK;
+}
+
 /* ------------------------------------------------------- graphs, timing */
 
 extern "C" int orome_hip_capture_begin(orome_hip_ctx *c) {

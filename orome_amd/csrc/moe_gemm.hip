@@ -896,7 +896,9 @@ static int down_shape(const ExpertSide &ex, const SharedSide &sh, int H, int M, 
     /* all of a tile's activations stay resident: in_dim <= 2 chunks */
     if (H % NB || M % KCH || M > 2 * KCH || (sh.gate && (sh.S % KCH || sh.S > 2 * KCH))) return -2;
     const bool dtiled = ex.down_fmt == FQ4KT || ex.down_fmt == FQ6KT;
-    if (ex.down_fmt != FQ4K && ex.down_fmt != FQ5K && ex.down_fmt != FQ6K && !dtiled) return -2;
+    /* (a Q8_0 routed down only reaches here from the weight read-back debug
+     * entry; the forward rejects it) */
+    if (ex.down_fmt != FQ4K && ex.down_fmt != FQ5K && ex.down_fmt != FQ6K && ex.down_fmt != FQ8 && !dtiled) return -2;
     /* shared down: any supported format; with a tile-major routed down a
      * Q4_K/Q6_K shared down must be tile-major too (the packer makes both) */
     const int sf = sh.gate ? sh.down_fmt : ex.down_fmt;
@@ -1030,6 +1032,7 @@ int launch_gemm_down(const ExpertSide &ex, const SharedSide &sh, const _Float16 
 #undef DP_LAUNCH
         return hipGetLastError() == hipSuccess ? 0 : -3;
     }
+    if (ex.down_fmt == FQ8) return -2; /* persistent kernels only */
     /* generic unit loop (a compile-time stage count spills here) */
 #define DN_LAUNCH(EF, SF)                                                                    \
     do {                                                                                     \

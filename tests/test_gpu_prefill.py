@@ -9,6 +9,8 @@ import orome_amd
 import oracle as O
 from conftest import banner
 from orome_amd import _lib
+from orome_amd._lib import lib
+from orome_amd.moe import DeviceBuffer
 from test_gpu_decode import Pair, assert_logits, rel_l2
 
 pytestmark = pytest.mark.gpu
@@ -321,4 +323,91 @@ def test_q8_shared_expert_registered(T):
     p.gm.unpack()
     plain, _ = p.run(0, x, h, path=_lib.OROME_PATH_AUTO)
     assert np.array_equal(out, plain)
+    p.gm.close()
+
+
+def f16(x):
+    return np.asarray(x, np.float64).astype(np.float16)
+
+
+def mfma_weights_model(fmt_blocks):
+    """The documented in-register fp16 dequant of the grouped GEMMs, emulated
+    in numpy (every step's rounding explicit) for whole matrices:
+      Q4_K, Q5_K  t = q sc (exact in fp16), w = fp16(t d - fp16(dmin m))
+      Q6_K        w = fp16(fp16(q sc) d)
+      Q8_0        w = fp16(q d)
+    blocks -> [rows, cols] float16."""
+    fmt, blocks, rows, cols = fmt_blocks
+    if fmt in ("Q4_K", "Q5_K"):
+        bb = 144 if fmt == "Q4_K" else 176
+        b = blocks.reshape(-1, bb)
+        d = b[:, 0:2].copy().view(np.float16).astype(np.float64)[:, 0]
+        dmin = b[:, 2:4].copy().view(np.float16).astype(np.float64)[:, 0]
+        from test_oracle import layout_table_np
+        sc, mn = layout_table_np(b[:, 4:16])
+        out = np.empty((len(b), 256), np.float16)
+        for j in range(4):
+            for h in range(2):
+                s = 2 * j + h
+                if fmt == "Q4_K":
+                    q = (b[:, 16 + 32 * j:16 + 32 * j + 32].astype(np.int64) >> (4 * h)) & 0xF
+                else:
+                    qh = b[:, 16:48].astype(np.int64)
+                    q = ((b[:, 48 + 32 * j:48 + 32 * j + 32].astype(np.int64) >> (4 * h)) & 0xF) + \
+                        16 * ((qh >> (2 * j + h)) & 1)
+                t = q * sc[:, s][:, None]                      # exact (< 2048)
+                mb = f16(dmin * mn[:, s]).astype(np.float64)   # fp16(dmin m)
+                out[:, 64 * j + 32 * h:64 * j + 32 * h + 32] = f16(t * d[:, None] - mb[:, None])
+        return out.reshape(rows, cols)
+    if fmt == "Q6_K":
+        b = blocks.reshape(-1, 210).astype(np.int64)
+        d = blocks.reshape(-1, 210)[:, 208:210].copy().view(np.float16).astype(np.float64)[:, 0]
+        sc = blocks.reshape(-1, 210)[:, 192:208].view(np.int8).astype(np.int64)
+        out = np.empty((len(b), 256), np.float16)
+        for h in range(2):
+            ql, qh = b[:, 64 * h:64 * h + 64], b[:, 128 + 32 * h:128 + 32 * h + 32]
+            for l in range(32):
+                q = [(ql[:, l] & 15) | ((qh[:, l] & 3) << 4), (ql[:, 32 + l] & 15) | (((qh[:, l] >> 2) & 3) << 4),
+                     (ql[:, l] >> 4) | (((qh[:, l] >> 4) & 3) << 4), (ql[:, 32 + l] >> 4) | (((qh[:, l] >> 6) & 3) << 4)]
+                for g in range(4):
+                    a = f16((q[g] - 32) * sc[:, 8 * h + l // 16 + 2 * g]).astype(np.float64)
+                    out[:, 128 * h + 32 * g + l] = f16(a * d)
+        return out.reshape(rows, cols)
+    b = blocks.reshape(-1, 34)
+    d = b[:, 0:2].copy().view(np.float16).astype(np.float64)[:, 0]
+    q = b[:, 2:34].view(np.int8).astype(np.float64)
+    return f16(q * d[:, None]).reshape(rows, cols)
+
+
+@pytest.mark.parametrize("fmt,tiled", [("Q4_K", 0), ("Q4_K", 1), ("Q5_K", 0), ("Q6_K", 0), ("Q6_K", 1),
+                                       ("Q8_0", 0)])
+def test_mfma_fp16_weights_bit_exact(fmt, tiled):
+    """The fp16 weights the matrix cores multiply (read back through the real
+    grouped down GEMM with one-hot activations, orome_debug_mfma_weights)
+    equal, bit for bit, the numpy emulation of the documented factored fp16
+    dequant, for row-major and tile-major copies; and each is within the
+    stated rounding of the oracle's exact fp32 value."""
+    banner("MFMA fp16 weights %s tiled=%d" % (fmt, tiled))
+    ggml = {"Q4_K": 12, "Q5_K": 13, "Q6_K": 14, "Q8_0": 8}[fmt]
+    kw = dict(down=ggml) if fmt != "Q8_0" else dict(shared=8)
+    p = Pair(max_tokens=32, E=8, seed=71, **kw)
+    name = "blk.0.ffn_down_exps.weight" if fmt != "Q8_0" else "blk.0.ffn_down_shexp.weight"
+    dims, typ, off, nb = p.om.tensors[name]
+    H, M = 2048, 512
+    one = nb // 8 if fmt != "Q8_0" else nb          # expert 0's matrix
+    blocks = p.img[off:off + one]
+    out = DeviceBuffer(p.ctx, M * H * 4)
+    fmt_id = O.GGML_TO_FMT[typ]
+    _lib.check(lib.orome_debug_mfma_weights(p.ctx.handle, fmt_id, tiled, p.gm.tensor_device_ptr(name), H, M,
+                                            out.ptr), "orome_debug_mfma_weights")
+    got = out.download(np.float32, (M, H)).T              # [H rows, M cols]
+    model = mfma_weights_model((fmt, blocks, H, M))
+    assert np.array_equal(got.astype(np.float16).view(np.uint16), model.view(np.uint16))
+    assert np.array_equal(got, model.astype(np.float32))  # the GEMM's fp32 outputs are those fp16 values
+    exact = O.decode_rows(fmt_id, blocks, H, M)
+    if fmt in ("Q6_K", "Q8_0"):  # one or two roundings of the exact value
+        ulp = np.abs(exact) * 2.0 ** -10 + 2.0 ** -24
+        assert np.all(np.abs(got.astype(np.float64) - exact) <= 2 * ulp)
+    else:  # fp16(dmin m) can carry an error larger than w itself where they cancel
+        assert rel_l2(got, exact) < 1e-3
     p.gm.close()
