@@ -20,9 +20,11 @@ pytestmark = pytest.mark.gpu
 
 
 def _noalloc(gm, layer, dx, dh, dout, dres, dparts, T, K=8):
+    """On the context's stream, so that the context's copies and syncs are
+    ordered after it."""
     return lib.orome_moe_forward_noalloc(C.byref(gm.cfg), C.byref(gm.elrs[layer]), C.byref(gm.caches[layer]),
                                          dx.ptr, dh.ptr, dout.ptr, dres.ptr if dres else None,
-                                         dparts.ptr if dparts else None, T, K, None)
+                                         dparts.ptr if dparts else None, T, K, lib.orome_hip_get_stream(gm.ctx.handle))
 
 
 def test_noalloc_matches_context_forward():
