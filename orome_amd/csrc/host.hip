@@ -542,7 +542,10 @@ static int forward_impl(orome_hip_ctx *c, const OromeHipModelConfig *cfg, const 
     const bool small_router = H <= 4096;
     const bool hybrid = path == OROME_PATH_AUTO && T >= 3 && T <= 16 && T * K <= 256 && small_router &&
                         gemm_small_tiles_ok(hx, hs, H, M);
-    if (path == OROME_PATH_AUTO) path = (T <= 8 && small_router) || hybrid ? OROME_PATH_GEMV : OROME_PATH_MFMA;
+    /* (the GEMV down kernels take in_dim multiples of 512) */
+    const bool gemv_shapes = M % 512 == 0 && (!S || S % 512 == 0);
+    if (path == OROME_PATH_AUTO)
+        path = (T <= 8 && small_router && gemv_shapes) || hybrid ? OROME_PATH_GEMV : OROME_PATH_MFMA;
     c->last_stream = s;
     if (norm_h) {
         if (path == OROME_PATH_GEMV) { /* the router kernel normalises and writes xnorm */
