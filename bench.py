@@ -6,12 +6,22 @@ tokens, or for config 4 the whole 40-layer stack (RMSNorm + MoE + residual per
 layer).  Inputs and all weights are resident in HBM before timing; the timed
 steps replay a HIP graph.  Layer-mode configs rotate over several
 independently seeded layers and a bank of seeded inputs, so the routed
-experts of a step are mostly cold in the 256 MB last-level cache.
+experts of a step are cold in the 256 MB last-level cache; the warm-up runs on
+layers and inputs of its own, disjoint from the timed ones, whatever --steps
+is.
 
-Default (no flags): config 0, B=1 decode, the headline of BASELINE.json.
-Prints one JSON line; extra fields hold the roofline of the dominant kernel
-(per-launch HIP event timing inside a replay of the same graph), the C
-oracle on this host as CPU baseline, and per-stage kernel times.
+Default (no --config): BASELINE's metric is quoted on two workloads, B=1
+decode and B=512 prefill; the line is config 0 (B=1 decode) and carries
+config 2 (T=512 prefill, balanced) as "secondary", each with its own roofline
+and CPU baseline, both timed for --steps steps.  --config C runs one config.
+
+Per config the line holds the roofline of the dominant kernel: algorithmic
+bytes (or flops) per launch over that kernel's average duration, measured with
+HIP events that its launches record themselves (start when the kernel begins,
+stop when it ends) while the timed steps run again back to back on the
+context stream (profiles/ holds the rocprofv3 kernel-trace figures of the
+same command); the C oracle on this host's cores as the CPU baseline (one thread,
+and all cores with OpenMP); and per-stage kernel times.
 """
 import argparse
 import ctypes as C
@@ -30,7 +40,8 @@ HBM_PEAK_GBS = 8000.0
 MFMA_F16_PEAK_TFLOPS = 2500.0
 Q4K, Q6K = 12, 14
 
-# name, tokens/step, mode, rotating layers (layer mode) or stack depth, spec
+# name, tokens/step, mode, timed layers (layer mode) or stack depth, spec,
+# input bank, default steps
 CONFIGS = {
     "0": dict(T=1, name="moe_decode_b1", mode="layer", layers=8, spec={}, xbank=64, steps=2000),
     "1": dict(T=8, name="moe_decode_b8", mode="layer", layers=8, spec={}, xbank=64, steps=2000),
@@ -43,6 +54,7 @@ CONFIGS = {
     "4p": dict(T=2048, name="moe_stack40_prefill_2048", mode="stack", layers=40,
                spec=dict(q6k_every=4, centered=True), xbank=2, steps=4),
 }
+WARM_LAYERS = 2  # layer mode: extra layers used only by the warm-up
 
 
 def q4k_bytes(rows, cols):
@@ -53,12 +65,266 @@ def q6k_bytes(rows, cols):
     return rows * (cols // 256) * 210
 
 
+def log(msg):
+    print("[bench] " + msg, file=sys.stderr, flush=True)
+
+
+def cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def run_config(key, steps, warmup, path, cpu_seconds, no_cpu):
+    import orome_amd
+    from orome_amd import _lib
+    from orome_amd._lib import check, lib
+    from orome_amd.moe import DeviceBuffer
+
+    cf = CONFIGS[key]
+    T, L, NX = cf["T"], cf["layers"], cf["xbank"]
+    steps = steps or cf["steps"]
+    warmup = warmup if warmup is not None else max(1, steps // 10)
+    stack = cf["mode"] == "stack"
+    H, E, K, M, S = 2048, 256, 8, 512, 512
+    LW = 0 if stack else WARM_LAYERS
+    spec = orome_amd.make_spec(layers=L + LW, H=H, E=E, K=K, M=M, S=S, seed=1234, **cf["spec"])
+    log("config %s (%s): %d timed + %d warm-up synthetic layers, T=%d" % (key, cf["name"], L, LW, T))
+    img = orome_amd.synth_gguf(spec)
+    # the library's choice under "auto": GEMV kernels up to 2 tokens, the
+    # small-batch routing with the small-tile grouped GEMMs for 3..16, the
+    # large-batch routing and grouped GEMMs above
+    kpath = path if path != "auto" else ("gemv" if T <= 2 else "small_batch_gemm" if T <= 16 else "mfma")
+    gm = orome_amd.MoEModel(image=img, max_tokens=max(T, 16), pack=kpath != "gemv")
+    ctx = gm.ctx
+    if path != "auto":
+        ctx.set_path(_lib.OROME_PATH_MFMA if kpath == "mfma" else _lib.OROME_PATH_GEMV)
+    # timed inputs: bank 0..NX-1; warm-up inputs: a bank of their own
+    xs_h = [orome_amd.synth_normal(77, i, T * H).reshape(T, H) for i in range(NX)]
+    hs_h = [orome_amd.synth_normal(78, i, T * H).reshape(T, H) for i in range(NX)]
+    wx_h = [orome_amd.synth_normal(79, i, T * H).reshape(T, H) for i in range(2)]
+    xs = [DeviceBuffer.from_array(ctx, v) for v in xs_h]
+    hs = [DeviceBuffer.from_array(ctx, v) for v in hs_h]
+    wx = [DeviceBuffer.from_array(ctx, v) for v in wx_h]
+    outs = [DeviceBuffer(ctx, T * H * 4) for _ in range(2)]
+
+    def step(i):
+        if stack:  # h = x_i, then 40 x (h += MoE_l(RMSNorm(h))) in place
+            gm.stack_forward(xs[i % NX], T)
+        else:
+            gm.forward(i % L, xs[i % NX], hs[i % NX], outs[i % 2], T)
+
+    def warm_step(i):
+        if stack:
+            gm.stack_forward(wx[i % 2], T)
+        else:  # warm-up layers L .. L+LW-1 with the warm-up inputs
+            gm.forward(L + i % LW, wx[i % 2], wx[(i + 1) % 2], outs[i % 2], T)
+
+    def restore():
+        if stack:  # the stack works in place: pristine inputs between runs
+            for b, v in zip(xs, xs_h):
+                b.upload(v)
+            for b, v in zip(wx, wx_h):
+                b.upload(v)
+
+    # touched experts per step (weights are counted once per touched expert)
+    G = min(steps, 200 if not stack else max(1, min(steps, 10)))
+    touched = []
+    for i in range(min(G, 64)):
+        if stack:
+            gm.layer_forward(L - 1, xs[i % NX], T)
+        else:
+            gm.forward(i % L, xs[i % NX], hs[i % NX], outs[0], T)
+        off = gm.debug_outputs(T)["offsets"].astype(np.int64)
+        touched.append(int(np.count_nonzero(np.diff(off))))
+    restore()
+    u_mean = float(np.mean(touched))
+
+    def capture(fn, n):
+        check(lib.orome_hip_capture_begin(ctx.handle), "capture")
+        for i in range(n):
+            fn(i)
+        ex = C.c_void_p()
+        check(lib.orome_hip_capture_end(ctx.handle, C.byref(ex)), "capture_end")
+        return ex
+
+    g_main = capture(step, G)
+    rem = steps % G
+    g_rem = capture(step, rem) if rem else None
+    g_warm = capture(warm_step, max(1, min(warmup, G)))
+    reps = steps // G
+    for _ in range(max(1, math.ceil(warmup / G))):
+        check(lib.orome_hip_graph_launch(ctx.handle, g_warm))
+    ctx.sync()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        check(lib.orome_hip_graph_launch(ctx.handle, g_main))
+    if g_rem:
+        check(lib.orome_hip_graph_launch(ctx.handle, g_rem))
+    ctx.sync()
+    elapsed = time.perf_counter() - t0
+    restore()
+
+    # per-kernel durations: the timed steps launched again, eagerly, on the
+    # context stream, each stage's kernels recording its event pair
+    # (orome_hip_stage_timing), all queued behind a GPU-side delay so that
+    # they run back to back as in the graph; after a warm-up replay
+    n_prof = min(steps, G)
+    check(lib.orome_hip_graph_launch(ctx.handle, g_warm))
+    check(lib.orome_hip_stage_timing(ctx.handle, n_prof * (L if stack else 1)))
+    check(lib.orome_hip_stream_delay(ctx.handle, 200000))
+    for i in range(n_prof):
+        step(i)
+    tot = (C.c_float * 8)()
+    cnt = (C.c_int * 8)()
+    check(lib.orome_hip_stage_times(ctx.handle, tot, cnt, 8))
+    check(lib.orome_hip_stage_timing(ctx.handle, 0))
+    stage_us = {_lib.STAGES[i]: (round(tot[i] / cnt[i] * 1000.0, 3) if cnt[i] else None) for i in range(8)}
+    restore()
+
+    # in-kernel view of the same launches: every block of the gate/up kernels
+    # stamps its start and end (s_memrealtime); first start to last end
+    KTB = 16384
+    ktbuf = DeviceBuffer(ctx, KTB * 2 * 8)
+    zeros = np.zeros(KTB * 2, np.uint64)
+    check(lib.orome_hip_kernel_timing(ctx.handle, ktbuf.ptr, KTB), "kernel_timing")
+    spans = []
+    for i in range(40):
+        ktbuf.upload(zeros)
+        if stack:
+            gm.layer_forward(i % L, xs[i % NX], T)
+        else:
+            gm.forward(i % L, xs[i % NX], hs[i % NX], outs[i % 2], T)
+        ctx.sync()
+        v = ktbuf.download(np.uint64, (KTB, 2)).astype(np.int64)
+        ok = (v[:, 0] > 0) & (v[:, 1] > 0)
+        spans.append((v[ok, 1].max() - v[ok, 0].min()) * 0.01)  # 100 MHz ticks -> us
+    check(lib.orome_hip_kernel_timing(ctx.handle, None, 0), "kernel_timing")
+    ktbuf.free()
+    restore()
+
+    # algorithmic work per gate/up launch and per MoE layer
+    nl = L if stack else 1
+    n_q6 = sum(1 for l in range(L) if cf["spec"].get("q6k_every") and l % 4 == 3) if stack else 0
+    down_e = q6k_bytes(H, M) if cf["spec"].get("down") == Q6K else q4k_bytes(H, M)
+    rows = T * K + T  # routed pairs plus shared-expert rows
+    gu_bytes = (u_mean + 1) * 2 * q4k_bytes(M, H) + T * H * (4 if kpath == "gemv" else 2) + rows * M * 2
+    gu_flops = 2.0 * 2 * rows * M * H
+    layer_bytes = (u_mean * (2 * q4k_bytes(M, H) + down_e) + 3 * q4k_bytes(S, H) + E * H * 4 + H * 4
+                   + T * H * 4 * 3)
+    if stack:
+        layer_bytes += (q6k_bytes(H, M) - q4k_bytes(H, M)) * u_mean * n_q6 / L
+    step_bytes = layer_bytes * nl
+    step_flops = 2.0 * (rows * M * H * 3 + T * (E + 1) * H) * nl
+    gu_us = stage_us["gate_up"]
+    gu_gbs = gu_bytes / (gu_us * 1e-6) / 1e9
+    gu_tflops = gu_flops / (gu_us * 1e-6) / 1e12
+    kname = {"gemv": "gemv_gate_up", "small_batch_gemm": "gemm_gate_up (16-row tiles)",
+             "mfma": "gemm_gate_up (small + big tile lists)"}[kpath]
+    if T >= 2048:
+        roof = {"bound": "mfma", "kernel": kname, "achieved": round(gu_tflops, 2),
+                "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(gu_tflops / MFMA_F16_PEAK_TFLOPS, 4)}
+    else:
+        roof = {"bound": "hbm", "kernel": kname, "achieved": round(gu_gbs, 1), "peak": HBM_PEAK_GBS,
+                "unit": "GB/s", "frac": round(gu_gbs / HBM_PEAK_GBS, 4)}
+    traffic = None
+    tf = os.path.join(ROOT, "profiles", "traffic_%s.json" % cf["name"])
+    if os.path.exists(tf):
+        traffic = json.load(open(tf)).get("gate_up_hbm_bytes_per_launch")
+    roof.update({"traffic": traffic, "algorithmic_bytes_per_launch": int(gu_bytes),
+                 "algorithmic_flops_per_launch": gu_flops, "avg_launch_us": gu_us,
+                 "timing": "HIP events recorded by the gate/up launches themselves (hipExtLaunchKernel "
+                           "start/stop, on the launch's stream), the timed steps relaunched back to back "
+                           "(%d launches)" % (n_prof * nl),
+                 "in_kernel_us": round(float(np.mean(spans)), 3),
+                 "gbs": round(gu_gbs, 1), "tflops": round(gu_tflops, 2)})
+
+    cpu = None if no_cpu else cpu_baseline(img, xs_h, hs_h, T, L, NX, nl, stack, cpu_seconds)
+
+    value = T * steps / elapsed
+    out = {
+        "metric": "MoE-layer tokens/s" if not stack else "MoE 40-layer stack tokens/s",
+        "value": round(value, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": warmup,
+        "ms_per_step": round(elapsed / steps * 1000, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "q4_k/q6_k weights, fp16 activations, fp32 accumulate",
+        "data": "synthetic seeded GGUF per BASELINE config %s (%d timed layers, %d input batches; warm-up on "
+                "%d layers and inputs of its own)" % (key, L, NX, LW),
+        "config": {"workload": cf["name"], "baseline_config": key, "tokens_per_step": T,
+                   "kernel_path": kpath,
+                   "layers_per_step": nl, "hidden": H, "experts": E, "top_k": K,
+                   "expert_intermediate": M, "shared_intermediate": S, "parallelism": "single GPU"},
+        "roofline": roof,
+        "step": {"algorithmic_bytes": int(step_bytes), "touched_experts_per_layer": u_mean,
+                 "gbs": round(step_bytes * steps / elapsed / 1e9, 1),
+                 "hbm_frac": round(step_bytes * steps / elapsed / 1e9 / HBM_PEAK_GBS, 4),
+                 "tflops": round(step_flops * steps / elapsed / 1e12, 2),
+                 "mfma_frac": round(step_flops * steps / elapsed / 1e12 / MFMA_F16_PEAK_TFLOPS, 4),
+                 "us_per_layer": round(elapsed / steps / nl * 1e6, 3)},
+        "stage_us": stage_us,
+        "cpu_baseline": cpu,
+    }
+    for g in (g_main, g_rem, g_warm):
+        if g:
+            lib.orome_hip_graph_destroy(g)
+    gm.close()
+    return out
+
+
+def cpu_baseline(img, xs_h, hs_h, T, L, NX, nl, stack, seconds):
+    """The C oracle (scalar, -O2) on this host: one thread for `seconds`, then
+    OpenMP over all the threads OMP_NUM_THREADS allows for half as long, on
+    the first (up to) 64 tokens of each input batch.  Rates are tokens/s of a
+    full step (nl layers)."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+    om = O.OracleModel(img)
+    tsub = min(T, 64)
+
+    def timed(omp, secs):
+        n = 0
+        c0 = time.perf_counter()
+        while time.perf_counter() - c0 < secs:
+            xi = xs_h[n % NX][:tsub]
+            if stack:
+                om.layer_forward(n % L, xi.copy(), omp=omp)
+            else:
+                om.forward(n % L, xi, hs_h[n % NX][:tsub], omp=omp)
+            n += 1
+        ct = time.perf_counter() - c0
+        return n, ct, n * tsub / ct / nl
+
+    n1, t1, r1 = timed(False, seconds)
+    threads = int(O.lib(True).orc_num_threads())
+    nm, tm, rm = timed(True, seconds / 2)
+    sample = "first %d token(s) of each batch" % tsub if tsub < T else "full batch"
+    scaled = "; scaled to the %d-layer step" % nl if nl > 1 else ""
+    return {"value": round(r1, 4), "unit": "tokens/s", "cores": 1, "kind": "port",
+            "sample": "%d single-layer passes of %d token(s) (%s), scalar C oracle (-O2), 1 thread, %.1f s%s"
+                      % (n1, tsub, sample, t1, scaled),
+            "all_cores": {"value": round(rm, 4), "unit": "tokens/s", "cores": threads,
+                          "sample": "%d passes as above, OpenMP over output rows and tokens, %d threads, %.1f s"
+                                    % (nm, threads, tm)},
+            "host": {"nproc": os.cpu_count(), "cpu_model": cpu_model()}}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=None)
     ap.add_argument("--warmup", type=int, default=None)
-    ap.add_argument("--config", default="0", choices=sorted(CONFIGS))
+    ap.add_argument("--config", default=None, choices=sorted(CONFIGS),
+                    help="one config; default: config 0 with config 2 as the secondary workload")
     ap.add_argument("--path", default="auto", choices=["auto", "gemv", "mfma"],
                     help="kernel path (auto: GEMV up to 2 tokens, small-batch routing with the small-tile "
                          "grouped GEMMs for 3..16, large-batch routing and grouped GEMMs above)")
@@ -84,220 +350,15 @@ def main():
         print(json.dumps({"copy_bytes_per_launch": n, "launches": 5}))
         return
 
-    import orome_amd
-    from orome_amd import _lib
-    from orome_amd._lib import check, lib
-    from orome_amd.moe import DeviceBuffer
-
-    cf = CONFIGS[args.config]
-    T, L, NX = cf["T"], cf["layers"], cf["xbank"]
-    steps = args.steps or cf["steps"]
-    warmup = args.warmup if args.warmup is not None else max(1, steps // 10)
-    H, E, K, M, S = 2048, 256, 8, 512, 512
-    spec = orome_amd.make_spec(layers=L, H=H, E=E, K=K, M=M, S=S, seed=1234, **cf["spec"])
-    print("[bench] config %s (%s): %d synthetic layers, T=%d" % (args.config, cf["name"], L, T),
-          file=sys.stderr, flush=True)
-    img = orome_amd.synth_gguf(spec)
-    # the library's choice under "auto": GEMV kernels up to 2 tokens, the
-    # small-batch routing with the small-tile grouped GEMMs for 3..16, the
-    # large-batch routing and grouped GEMMs above
-    kpath = args.path if args.path != "auto" else ("gemv" if T <= 2 else "small_batch_gemm" if T <= 16 else "mfma")
-    gm = orome_amd.MoEModel(image=img, max_tokens=max(T, 16), pack=kpath != "gemv")
-    ctx = gm.ctx
-    if args.path != "auto":
-        ctx.set_path(_lib.OROME_PATH_MFMA if kpath == "mfma" else _lib.OROME_PATH_GEMV)
-    stack = cf["mode"] == "stack"
-    xs_h = [orome_amd.synth_normal(77, i, T * H).reshape(T, H) for i in range(NX)]
-    hs_h = [orome_amd.synth_normal(78, i, T * H).reshape(T, H) for i in range(NX)]
-    xs = [DeviceBuffer.from_array(ctx, v) for v in xs_h]
-    hs = [DeviceBuffer.from_array(ctx, v) for v in hs_h]
-    outs = [DeviceBuffer(ctx, T * H * 4) for _ in range(2)]
-
-    def step(i):
-        if stack:  # h = x_i, then 40 x (h += MoE_l(RMSNorm(h))) in place
-            gm.stack_forward(xs[i % NX], T)
-        else:
-            gm.forward(i % L, xs[i % NX], hs[i % NX], outs[i % 2], T)
-
-    if stack:
-        # the stack works in place: keep pristine copies to restore between runs
-        def restore():
-            for b, v in zip(xs, xs_h):
-                b.upload(v)
+    if args.config is not None:
+        out = run_config(args.config, args.steps, args.warmup, args.path, args.cpu_seconds, args.no_cpu)
     else:
-        def restore():
-            pass
-
-    # touched experts per step (weights are counted once per touched expert)
-    G = min(steps, 200 if not stack else max(1, min(steps, 10)))
-    touched = []
-    for i in range(min(G, 64)):
-        if stack:
-            gm.layer_forward(L - 1, xs[i % NX], T)
-        else:
-            gm.forward(i % L, xs[i % NX], hs[i % NX], outs[0], T)
-        off = gm.debug_outputs(T)["offsets"].astype(np.int64)
-        touched.append(int(np.count_nonzero(np.diff(off))))
-    restore()
-    u_mean = float(np.mean(touched))
-
-    def capture(n):
-        check(lib.orome_hip_capture_begin(ctx.handle), "capture")
-        for i in range(n):
-            step(i)
-        ex = C.c_void_p()
-        check(lib.orome_hip_capture_end(ctx.handle, C.byref(ex)), "capture_end")
-        return ex
-
-    g_main = capture(G)
-    rem = steps % G
-    g_rem = capture(rem) if rem else None
-    reps = steps // G
-    for _ in range(max(1, math.ceil(warmup / G))):
-        check(lib.orome_hip_graph_launch(ctx.handle, g_main))
-    ctx.sync()
-    t0 = time.perf_counter()
-    for _ in range(reps):
-        check(lib.orome_hip_graph_launch(ctx.handle, g_main))
-    if g_rem:
-        check(lib.orome_hip_graph_launch(ctx.handle, g_rem))
-    ctx.sync()
-    elapsed = time.perf_counter() - t0
-
-    # per-kernel durations: the same steps launched eagerly with HIP event
-    # pairs around every launch, queued behind a GPU delay so the kernels run
-    # back to back (no host launch gaps inside the brackets)
-    n_prof = min(steps, 400 if not stack else 8)
-    check(lib.orome_hip_stage_timing(ctx.handle, n_prof * (L if stack else 1)))
-    check(lib.orome_hip_stream_delay(ctx.handle, 400000))
-    for i in range(n_prof):
-        step(i)
-    tot = (C.c_float * 8)()
-    cnt = (C.c_int * 8)()
-    check(lib.orome_hip_stage_times(ctx.handle, tot, cnt, 8))
-    check(lib.orome_hip_stage_timing(ctx.handle, 0))
-    stage_us = {_lib.STAGES[i]: (round(tot[i] / cnt[i] * 1000.0, 3) if cnt[i] else None)
-                for i in range(8)}
-    restore()
-
-    # gate/up launch durations as a kernel trace reports them: every block of
-    # the gate/up kernels stamps its start and end (orome_hip_kernel_timing);
-    # a launch lasts from its first block's start to its last block's end
-    # (the big- and small-tile launches of the MFMA path together)
-    KTB = 16384
-    ktbuf = DeviceBuffer(ctx, KTB * 2 * 8)
-    zeros = np.zeros(KTB * 2, np.uint64)
-    check(lib.orome_hip_kernel_timing(ctx.handle, ktbuf.ptr, KTB), "kernel_timing")
-    spans, spans_big, spans_small = [], [], []
-    for i in range(40):
-        ktbuf.upload(zeros)
-        if stack:
-            gm.layer_forward(i % L, xs[i % NX], T)
-        else:
-            gm.forward(i % L, xs[i % NX], hs[i % NX], outs[i % 2], T)
-        ctx.sync()
-        v = ktbuf.download(np.uint64, (KTB, 2)).astype(np.int64)
-        ok = (v[:, 0] > 0) & (v[:, 1] > 0)
-        spans.append((v[ok, 1].max() - v[ok, 0].min()) * 0.01)  # 100 MHz ticks -> us
-        for part, lst in ((v[:KTB // 2], spans_big), (v[KTB // 2:], spans_small)):
-            okp = (part[:, 0] > 0) & (part[:, 1] > 0)
-            if okp.any():
-                lst.append((part[okp, 1].max() - part[okp, 0].min()) * 0.01)
-    check(lib.orome_hip_kernel_timing(ctx.handle, None, 0), "kernel_timing")
-    ktbuf.free()
-    restore()
-
-    # algorithmic work per gate/up launch and per MoE layer
-    nl = L if stack else 1
-    n_q6 = sum(1 for l in range(L) if cf["spec"].get("q6k_every") and l % 4 == 3) if stack else 0
-    down_e = q6k_bytes(H, M) if cf["spec"].get("down") == Q6K else q4k_bytes(H, M)
-    rows = T * K + T  # routed pairs plus shared-expert rows
-    gu_bytes = (u_mean + 1) * 2 * q4k_bytes(M, H) + T * H * (4 if kpath == "gemv" else 2) + rows * M * 2
-    gu_flops = 2.0 * 2 * rows * M * H
-    layer_bytes = (u_mean * (2 * q4k_bytes(M, H) + down_e) + 3 * q4k_bytes(S, H) + E * H * 4 + H * 4
-                   + T * H * 4 * 3)
-    if stack:
-        layer_bytes += (q6k_bytes(H, M) - q4k_bytes(H, M)) * u_mean * n_q6 / L
-    step_bytes = layer_bytes * nl
-    step_flops = 2.0 * (rows * M * H * 3 + T * (E + 1) * H) * nl
-    gu_us = float(np.mean(spans))
-    gu_gbs = gu_bytes / (gu_us * 1e-6) / 1e9
-    gu_tflops = gu_flops / (gu_us * 1e-6) / 1e12
-    mfma_bound = T >= 2048
-    if mfma_bound:
-        roof = {"bound": "mfma", "kernel": "gemm_gate_up", "achieved": round(gu_tflops, 2),
-                "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(gu_tflops / MFMA_F16_PEAK_TFLOPS, 4)}
-    else:
-        roof = {"bound": "hbm", "kernel": "gemv_gate_up" if kpath == "gemv" else "gemm_gate_up",
-                "achieved": round(gu_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(gu_gbs / HBM_PEAK_GBS, 4)}
-    traffic = None
-    tf = os.path.join(ROOT, "profiles", "traffic_%s.json" % cf["name"])
-    if os.path.exists(tf):
-        traffic = json.load(open(tf)).get("gate_up_hbm_bytes_per_launch")
-    roof.update({"traffic": traffic, "algorithmic_bytes_per_launch": int(gu_bytes),
-                 "algorithmic_flops_per_launch": gu_flops, "avg_launch_us": round(gu_us, 3),
-                 "timing": "per-block s_memrealtime stamps of 40 launches (first start to last end)",
-                 "event_us": stage_us["gate_up"],
-                 "big_tile_us": round(float(np.mean(spans_big)), 3) if spans_big else None,
-                 "small_tile_us": round(float(np.mean(spans_small)), 3) if spans_small and T > 8 else None,
-                 "gbs": round(gu_gbs, 1), "tflops": round(gu_tflops, 2)})
-
-    cpu = None
-    if not args.no_cpu:
-        sys.path.insert(0, os.path.join(ROOT, "oracle"))
-        import oracle as O
-        om = O.OracleModel(img)
-        tsub = min(T, 64)
-        n = 0
-        c0 = time.perf_counter()
-        while time.perf_counter() - c0 < args.cpu_seconds:
-            xi = xs_h[n % NX][:tsub]
-            if stack:
-                om.layer_forward(n % L, xi.copy(), omp=False)
-            else:
-                om.forward(n % L, xi, hs_h[n % NX][:tsub], omp=False)
-            n += 1
-        ct = time.perf_counter() - c0
-        rate = n * tsub / ct / nl  # tokens/s for a full step (nl layers)
-        cpu = {"value": round(rate, 4), "unit": "tokens/s", "cores": 1, "kind": "port",
-               "sample": "%d single-layer passes of %d token(s) (%s), scalar C oracle, 1 thread, %.1f s%s"
-                         % (n, tsub, "first %d of each batch" % tsub if tsub < T else "full batch",
-                            ct, "; scaled to the %d-layer step" % nl if nl > 1 else "")}
-
-    value = T * steps / elapsed
-    out = {
-        "metric": "MoE-layer tokens/s" if not stack else "MoE 40-layer stack tokens/s",
-        "value": round(value, 1),
-        "unit": "tokens/s",
-        "n_gpus": 1,
-        "steps": steps,
-        "warmup": warmup,
-        "ms_per_step": round(elapsed / steps * 1000, 5),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "q4_k/q6_k weights, fp16 activations, fp32 accumulate",
-        "data": "synthetic seeded GGUF per BASELINE config %s (%d layers, %d input batches)"
-                % (args.config, L, NX),
-        "config": {"workload": cf["name"], "baseline_config": args.config, "tokens_per_step": T,
-                   "kernel_path": kpath,
-                   "layers_per_step": nl, "hidden": H, "experts": E, "top_k": K,
-                   "expert_intermediate": M, "shared_intermediate": S, "parallelism": "single GPU"},
-        "roofline": roof,
-        "step": {"algorithmic_bytes": int(step_bytes), "touched_experts_per_layer": u_mean,
-                 "gbs": round(step_bytes * steps / elapsed / 1e9, 1),
-                 "hbm_frac": round(step_bytes * steps / elapsed / 1e9 / HBM_PEAK_GBS, 4),
-                 "tflops": round(step_flops * steps / elapsed / 1e12, 2),
-                 "mfma_frac": round(step_flops * steps / elapsed / 1e12 / MFMA_F16_PEAK_TFLOPS, 4),
-                 "us_per_layer": round(elapsed / steps / nl * 1e6, 3)},
-        "stage_us": stage_us,
-        "cpu_baseline": cpu,
-    }
+        out = run_config("0", args.steps, args.warmup, args.path, args.cpu_seconds, args.no_cpu)
+        sec = run_config("2", args.steps, args.warmup, args.path, args.cpu_seconds / 2, args.no_cpu)
+        out["secondary"] = {k: sec[k] for k in ("metric", "value", "unit", "steps", "warmup", "ms_per_step",
+                                                 "config", "roofline", "step", "stage_us", "cpu_baseline",
+                                                 "data")}
     print(json.dumps(out), flush=True)
-    for g in (g_main, g_rem):
-        if g:
-            lib.orome_hip_graph_destroy(g)
 
 
 if __name__ == "__main__":

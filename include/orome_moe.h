@@ -397,9 +397,13 @@ int orome_hip_capture_end(orome_hip_ctx *ctx, void **graph_exec);
 int orome_hip_graph_launch(orome_hip_ctx *ctx, void *graph_exec);
 int orome_hip_graph_destroy(void *graph_exec);
 
-/* Per-stage kernel timing with HIP events around each launch of eager
- * (non-captured) forward calls; `capacity` samples are kept per stage
- * (0 turns timing off).  Replaces the reference's CPU-side [profile]
+/* Per-stage kernel timing of eager (not captured) forward calls with HIP
+ * events on the launches themselves (hipExtLaunchKernel: the first kernel of
+ * a stage records the start event when it begins, each records the stop
+ * event when it ends, so a pair spans the stage's kernels as a kernel trace
+ * does); `capacity` samples are kept per stage (0 turns timing off).  While
+ * timing is on, the two tile lists of the MFMA path run one after the other
+ * on the context stream.  Replaces the reference's CPU-side [profile]
  * timers (inference/src/engine.m:687-693, 1063-1068), which measured
  * encode time rather than GPU time.  Stages: 0 norm, 1 router, 2 top-k,
  * 3 dispatch, 4 fp16 staging, 5 gate/up, 6 down, 7 combine. */

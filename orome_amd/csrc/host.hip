@@ -439,19 +439,20 @@ static int launch_rc(int rc, const char *what) {
         if (rc_) return rc_;                \
     } while (0)
 
-/* launch with optional per-stage event bracketing (on the call's stream s) */
+/* launch with optional per-stage timing: the stage's kernels carry the
+ * stage's event pair (KLAUNCH) */
+thread_local LaunchEvents g_launch_ev = {nullptr, nullptr};
 #define TLAUNCH(c, st, call, what)                                                         \
     do {                                                                                   \
         hipEvent_t *ev_ = NULL;                                                            \
         if ((c)->timing) {                                                                 \
             ev_ = &(c)->ev[((st) * (c)->tcap + (c)->tcount[st] % (c)->tcap) * 2];          \
-            (void)hipEventRecord(ev_[0], s);                                     \
+            g_launch_ev = LaunchEvents{ev_[0], ev_[1]};                                    \
         }                                                                                  \
-        LAUNCH(call, what);                                                                \
-        if (ev_) {                                                                         \
-            (void)hipEventRecord(ev_[1], s);                                     \
-            (c)->tcount[st]++;                                                             \
-        }                                                                                  \
+        const int trc_ = launch_rc((call), (what));                                        \
+        g_launch_ev = LaunchEvents{nullptr, nullptr};                                      \
+        if (trc_) return trc_;                                                             \
+        if (ev_) (c)->tcount[st]++;                                                        \
     } while (0)
 
 /* The MoE block on x (or, with norm_h, on RMSNorm(norm_h) * bf16(norm_w),
@@ -816,7 +817,7 @@ extern "C" int orome_debug_mfma_weights(orome_hip_ctx *c, OromeHipQuantFormat fm
     }
     SharedSide sh = {NULL, NULL, NULL, 0, 0, 0};
     /* M one-hot rows as the pairs of expert 0, in 32-row tiles */
-    hipLaunchKernelGGL(k_one_hot_f16, dim3((unsigned)M), dim3(256), 0, s, c->act, M, M);
+    KLAUNCH(k_one_hot_f16, dim3((unsigned)M), dim3(256), 0, s, c->act, M, M);
     const int ntile = (M + GEMM_TILE_SMALL - 1) / GEMM_TILE_SMALL;
     uint32_t *hl = (uint32_t *)calloc(1 + 3 * (size_t)ntile, 4);
     hl[0] = (uint32_t)ntile;

@@ -1,8 +1,29 @@
 /* kernels.h -- launch interface between the C-ABI host code and the kernels. */
 #pragma once
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stddef.h>
 #include <stdint.h>
+
+/* Kernel launches of the library.  While the host's stage timing brackets a
+ * stage, g_launch_ev holds that stage's event pair: the stage's kernels are
+ * launched with hipExtLaunchKernel, the first one recording `start` when it
+ * begins and each one recording `stop` when it ends, so the pair spans
+ * exactly the stage's kernels (the dispatches' own begin/end times, not
+ * separate marker packets).  Otherwise a plain launch. */
+struct LaunchEvents {
+    hipEvent_t start, stop;
+};
+extern thread_local LaunchEvents g_launch_ev;
+#define KLAUNCH(K, G, B, SH, S, ...)                                                                     \
+    do {                                                                                                 \
+        if (g_launch_ev.stop) {                                                                          \
+            hipExtLaunchKernelGGL(K, G, B, SH, S, g_launch_ev.start, g_launch_ev.stop, 0, __VA_ARGS__);  \
+            g_launch_ev.start = nullptr;                                                                 \
+        } else {                                                                                         \
+            hipLaunchKernelGGL(K, G, B, SH, S, __VA_ARGS__);                                             \
+        }                                                                                                \
+    } while (0)
 
 /* Compact list of the experts a call touches, written by the routing kernels:
  *   list[0]            n_active

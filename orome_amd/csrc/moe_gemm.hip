@@ -945,8 +945,8 @@ int launch_gemm_gate_up(const ExpertSide &ex, const SharedSide &sh, const _Float
         a.kt = kt && (long)pb <= kt_cap ? kt : nullptr;
 #define GP_LAUNCH(GF, ARGS)                                                                                      \
     do {                                                                                                         \
-        if (tile_m == GEMM_TILE_BIG) hipLaunchKernelGGL((k_gemm_gate_up_p<GEMM_TILE_BIG / 16, GF>), dim3(pb), block, 0, s, ARGS); \
-        else hipLaunchKernelGGL((k_gemm_gate_up_p<GEMM_TILE_SMALL / 16, GF>), dim3(pb), block, 0, s, ARGS);          \
+        if (tile_m == GEMM_TILE_BIG) KLAUNCH((k_gemm_gate_up_p<GEMM_TILE_BIG / 16, GF>), dim3(pb), block, 0, s, ARGS); \
+        else KLAUNCH((k_gemm_gate_up_p<GEMM_TILE_SMALL / 16, GF>), dim3(pb), block, 0, s, ARGS);          \
     } while (0)
         const int nsh = shared_tiles_in(sh, T, K, E, tile_m);
         if (nsh && q8) { /* Q8_0 shared expert: one walk over the routed tiles, one over the shared */
@@ -969,9 +969,9 @@ int launch_gemm_gate_up(const ExpertSide &ex, const SharedSide &sh, const _Float
      * take the generic loop */
 #define GU_LAUNCH(RF, SF, NS)                                                                    \
     do {                                                                                     \
-        if (tile_m == GEMM_TILE_SMALL) hipLaunchKernelGGL((k_gemm_gate_up<RF, SF, NS, GEMM_TILE_SMALL / 16>), grid, block, 0, s, a); \
-        else if (tile_m == GEMM_TILE_MIN) hipLaunchKernelGGL((k_gemm_gate_up<RF, SF, NS, GEMM_TILE_MIN / 16>), grid, block, 0, s, a); \
-        else hipLaunchKernelGGL((k_gemm_gate_up<RF, SF, NS, GEMM_TILE_BIG / 16>), grid, block, 0, s, a);              \
+        if (tile_m == GEMM_TILE_SMALL) KLAUNCH((k_gemm_gate_up<RF, SF, NS, GEMM_TILE_SMALL / 16>), grid, block, 0, s, a); \
+        else if (tile_m == GEMM_TILE_MIN) KLAUNCH((k_gemm_gate_up<RF, SF, NS, GEMM_TILE_MIN / 16>), grid, block, 0, s, a); \
+        else KLAUNCH((k_gemm_gate_up<RF, SF, NS, GEMM_TILE_BIG / 16>), grid, block, 0, s, a);              \
     } while (0)
     if (tiled) {
         if (q8) GU_LAUNCH(FQ4KT, FQ8, 0);
@@ -1007,12 +1007,12 @@ int launch_gemm_down(const ExpertSide &ex, const SharedSide &sh, const _Float16 
     if (pb && M == 512 && (!nsh || sh.S == M)) {
 #define DP_LAUNCH(F, TB, ARGS)                                                                                        \
     do {                                                                                                              \
-        if ((F) == FQ4K) hipLaunchKernelGGL((k_gemm_down_p<FQ4K, TB>), dim3(pb), block, 0, s, ARGS);                    \
-        else if ((F) == FQ4KT) hipLaunchKernelGGL((k_gemm_down_p<FQ4KT, TB>), dim3(pb), block, 0, s, ARGS);             \
-        else if ((F) == FQ6KT) hipLaunchKernelGGL((k_gemm_down_p<FQ6KT, TB>), dim3(pb), block, 0, s, ARGS);             \
-        else if ((F) == FQ8) hipLaunchKernelGGL((k_gemm_down_p<FQ8, TB>), dim3(pb), block, 0, s, ARGS);                 \
-        else if ((F) == FQ5K) hipLaunchKernelGGL((k_gemm_down_p<FQ5K, TB>), dim3(pb), block, 0, s, ARGS);               \
-        else hipLaunchKernelGGL((k_gemm_down_p<FQ6K, TB>), dim3(pb), block, 0, s, ARGS);                                \
+        if ((F) == FQ4K) KLAUNCH((k_gemm_down_p<FQ4K, TB>), dim3(pb), block, 0, s, ARGS);                    \
+        else if ((F) == FQ4KT) KLAUNCH((k_gemm_down_p<FQ4KT, TB>), dim3(pb), block, 0, s, ARGS);             \
+        else if ((F) == FQ6KT) KLAUNCH((k_gemm_down_p<FQ6KT, TB>), dim3(pb), block, 0, s, ARGS);             \
+        else if ((F) == FQ8) KLAUNCH((k_gemm_down_p<FQ8, TB>), dim3(pb), block, 0, s, ARGS);                 \
+        else if ((F) == FQ5K) KLAUNCH((k_gemm_down_p<FQ5K, TB>), dim3(pb), block, 0, s, ARGS);               \
+        else KLAUNCH((k_gemm_down_p<FQ6K, TB>), dim3(pb), block, 0, s, ARGS);                                \
     } while (0)
 #define DP_TILE(F, ARGS)                                                        \
     do {                                                                        \
@@ -1036,9 +1036,9 @@ int launch_gemm_down(const ExpertSide &ex, const SharedSide &sh, const _Float16 
     /* generic unit loop (a compile-time stage count spills here) */
 #define DN_LAUNCH(EF, SF)                                                                    \
     do {                                                                                     \
-        if (tile_m == GEMM_TILE_SMALL) hipLaunchKernelGGL((k_gemm_down<EF, SF, 0, GEMM_TILE_SMALL / 16>), grid, block, 0, s, a); \
-        else if (tile_m == GEMM_TILE_MIN) hipLaunchKernelGGL((k_gemm_down<EF, SF, 0, GEMM_TILE_MIN / 16>), grid, block, 0, s, a); \
-        else hipLaunchKernelGGL((k_gemm_down<EF, SF, 0, GEMM_TILE_BIG / 16>), grid, block, 0, s, a);              \
+        if (tile_m == GEMM_TILE_SMALL) KLAUNCH((k_gemm_down<EF, SF, 0, GEMM_TILE_SMALL / 16>), grid, block, 0, s, a); \
+        else if (tile_m == GEMM_TILE_MIN) KLAUNCH((k_gemm_down<EF, SF, 0, GEMM_TILE_MIN / 16>), grid, block, 0, s, a); \
+        else KLAUNCH((k_gemm_down<EF, SF, 0, GEMM_TILE_BIG / 16>), grid, block, 0, s, a);              \
     } while (0)
     if (ex.down_fmt == FQ4KT) {
         if (sf == FQ4KT) DN_LAUNCH(FQ4KT, FQ4KT);
@@ -1100,7 +1100,7 @@ size_t packed_q4k_bytes(int R, int K, int E) { return (size_t)E * R * (K / 256) 
 int launch_pack_q4k(const uint8_t *src, uint8_t *dst, int R, int K, int E, size_t src_stride, hipStream_t s) {
     if (R % 16 || K % 256 || E < 1 || ((uintptr_t)src & 15) || ((uintptr_t)dst & 15) || (src_stride & 15)) return -2;
     const int nsb = K / 256;
-    hipLaunchKernelGGL(k_pack_q4k, dim3((unsigned)(R / 16 * nsb), (unsigned)E), dim3(144), 0, s, src, dst, R, nsb, src_stride);
+    KLAUNCH(k_pack_q4k, dim3((unsigned)(R / 16 * nsb), (unsigned)E), dim3(144), 0, s, src, dst, R, nsb, src_stride);
     return hipGetLastError() == hipSuccess ? 0 : -3;
 }
 
@@ -1145,6 +1145,6 @@ size_t packed_q6k_bytes(int R, int K, int E) { return (size_t)E * R * (K / 256) 
 int launch_pack_q6k(const uint8_t *src, uint8_t *dst, int R, int K, int E, size_t src_stride, hipStream_t s) {
     if (R % 16 || K % 256 || E < 1 || ((uintptr_t)src & 1) || ((uintptr_t)dst & 15) || (src_stride & 1)) return -2;
     const int nsb = K / 256;
-    hipLaunchKernelGGL(k_pack_q6k, dim3((unsigned)(R / 16 * nsb), (unsigned)E), dim3(256), 0, s, src, dst, R, nsb, src_stride);
+    KLAUNCH(k_pack_q6k, dim3((unsigned)(R / 16 * nsb), (unsigned)E), dim3(256), 0, s, src, dst, R, nsb, src_stride);
     return hipGetLastError() == hipSuccess ? 0 : -3;
 }

@@ -1132,9 +1132,9 @@ int launch_gemv_gate_up(const ExpertSide &ex, const SharedSide &sh, const RouteA
 #define GB_LAUNCH(EPLV)                                                                                       \
     do {                                                                                                      \
         if (route_in_block)                                                                                   \
-            hipLaunchKernelGGL((k_gemv_gu_b<EPLV, true>), dim3(gblocks), dim3(256), lds, s, a, ra);           \
+            KLAUNCH((k_gemv_gu_b<EPLV, true>), dim3(gblocks), dim3(256), lds, s, a, ra);           \
         else                                                                                                  \
-            hipLaunchKernelGGL((k_gemv_gu_b<EPLV, false>), dim3(gblocks), dim3(256), lds, s, a, ra);          \
+            KLAUNCH((k_gemv_gu_b<EPLV, false>), dim3(gblocks), dim3(256), lds, s, a, ra);          \
     } while (0)
         switch (epl_of(E)) {
             case 1: GB_LAUNCH(1); break;
@@ -1147,7 +1147,7 @@ int launch_gemv_gate_up(const ExpertSide &ex, const SharedSide &sh, const RouteA
         return hipGetLastError() == hipSuccess ? 0 : -3;
     }
     if (route_in_block && T == 1 && H == 2048 && (!sh.gate || sh.gate_fmt == FQ4K)) {
-#define GU1_LAUNCH(EPLV) hipLaunchKernelGGL((k_gemv_gate_up1<EPLV>), dim3(blocks), dim3(256), 0, s, a, ra)
+#define GU1_LAUNCH(EPLV) KLAUNCH((k_gemv_gate_up1<EPLV>), dim3(blocks), dim3(256), 0, s, a, ra)
         switch (epl_of(E)) {
             case 1: GU1_LAUNCH(1); break;
             case 2: GU1_LAUNCH(2); break;
@@ -1161,9 +1161,9 @@ int launch_gemv_gate_up(const ExpertSide &ex, const SharedSide &sh, const RouteA
 #define GU_LAUNCH(EPLV)                                                                          \
     do {                                                                                          \
         if (route_in_block)                                                                       \
-            hipLaunchKernelGGL((k_gemv_gate_up<EPLV, true>), dim3(blocks), dim3(256), 0, s, a, ra);  \
+            KLAUNCH((k_gemv_gate_up<EPLV, true>), dim3(blocks), dim3(256), 0, s, a, ra);  \
         else                                                                                      \
-            hipLaunchKernelGGL((k_gemv_gate_up<EPLV, false>), dim3(blocks), dim3(256), 0, s, a, ra); \
+            KLAUNCH((k_gemv_gate_up<EPLV, false>), dim3(blocks), dim3(256), 0, s, a, ra); \
     } while (0)
     switch (epl_of(E)) {
         case 1: GU_LAUNCH(1); break;
@@ -1210,17 +1210,17 @@ int launch_gemv_down(const ExpertSide &ex, const SharedSide &sh, const _Float16 
     if (M == 512 && (!sh.gate || sh.S == 512) && H % DB_ROWS == 0) {
         const dim3 g((unsigned)((umax + (sh.gate ? 1 : 0)) * (H / DB_ROWS)));
         const int sf = sh.gate ? sh.down_fmt : FQ4K;
-#define DB_LAUNCH(EF, SF) hipLaunchKernelGGL((k_gemv_down_b<EF, SF>), g, dim3(256), 0, s, a)
+#define DB_LAUNCH(EF, SF) KLAUNCH((k_gemv_down_b<EF, SF>), g, dim3(256), 0, s, a)
         DOWN_FMT_SWITCH(ex.down_fmt, sf, DB_LAUNCH);
 #undef DB_LAUNCH
         return hipGetLastError() == hipSuccess ? 0 : -3;
     }
     dim3 grid((umax + (sh.gate ? 1 : 0)) * (H / 8));
     switch (NT) {
-        case 1: hipLaunchKernelGGL(k_gemv_down<1>, grid, dim3(128), 0, s, a); break;
-        case 2: hipLaunchKernelGGL(k_gemv_down<2>, grid, dim3(128), 0, s, a); break;
-        case 4: hipLaunchKernelGGL(k_gemv_down<4>, grid, dim3(128), 0, s, a); break;
-        default: hipLaunchKernelGGL(k_gemv_down<8>, grid, dim3(128), 0, s, a); break;
+        case 1: KLAUNCH(k_gemv_down<1>, grid, dim3(128), 0, s, a); break;
+        case 2: KLAUNCH(k_gemv_down<2>, grid, dim3(128), 0, s, a); break;
+        case 4: KLAUNCH(k_gemv_down<4>, grid, dim3(128), 0, s, a); break;
+        default: KLAUNCH(k_gemv_down<8>, grid, dim3(128), 0, s, a); break;
     }
     return hipGetLastError() == hipSuccess ? 0 : -3;
 }
@@ -1236,7 +1236,7 @@ int launch_gemv_down_combine1(const ExpertSide &ex, const SharedSide &sh, const 
     a.down = ex.down; a.down_stride = ex.down_stride; a.fmt = ex.down_fmt;
     a.sh_down = sh.gate ? sh.down : nullptr; a.sh_fmt = sf; a.S = sh.gate ? sh.S : 0;
     a.act = act; a.act_sh = act_sh; a.T = 1; a.H = H; a.M = M; a.K = K;
-#define DC_LAUNCH(EF, SF) hipLaunchKernelGGL((k_gemv_down_combine1<EF, SF>), dim3(H / 8), dim3(128), 0, s, a, ra, h_in, h_out, res)
+#define DC_LAUNCH(EF, SF) KLAUNCH((k_gemv_down_combine1<EF, SF>), dim3(H / 8), dim3(128), 0, s, a, ra, h_in, h_out, res)
     DOWN_FMT_SWITCH(ex.down_fmt, sf, DC_LAUNCH);
 #undef DC_LAUNCH
     return hipGetLastError() == hipSuccess ? 0 : -3;

@@ -80,7 +80,7 @@ int launch_dequant(int fmt, const uint8_t *src, uint32_t rows, uint32_t n, float
     if ((fmt == 3 && n % 32) || (fmt != 3 && n % 256)) return -1;
     size_t work = (size_t)rows * (n / 32);
     if (!work) return 0;
-    hipLaunchKernelGGL(k_dequant, dim3((unsigned)((work + 255) / 256)), dim3(256), 0, s, fmt, src,
+    KLAUNCH(k_dequant, dim3((unsigned)((work + 255) / 256)), dim3(256), 0, s, fmt, src,
                        rows, n, o32, o16);
     return hipGetLastError() == hipSuccess ? 0 : -3;
 }
@@ -100,7 +100,7 @@ __global__ void k_to_f16(const float *x, size_t n, _Float16 *o) {
 
 int launch_to_f16(const float *x, int T, int H, _Float16 *x16, hipStream_t s) {
     size_t n = (size_t)T * H;
-    hipLaunchKernelGGL(k_to_f16, dim3((unsigned)((n / 4 + 255) / 256 + 1)), dim3(256), 0, s, x, n, x16);
+    KLAUNCH(k_to_f16, dim3((unsigned)((n / 4 + 255) / 256 + 1)), dim3(256), 0, s, x, n, x16);
     return hipGetLastError() == hipSuccess ? 0 : -3;
 }
 
@@ -197,7 +197,7 @@ __global__ __launch_bounds__(64) void k_sumsq_parts(const float *h, int H, float
 
 int launch_sumsq_parts(const float *h, int T, int H, float *ssq, hipStream_t s) {
     if (H % 256) return -2;
-    hipLaunchKernelGGL(k_sumsq_parts, dim3((unsigned)(H / 256), (unsigned)T), dim3(64), 0, s, h, H, ssq);
+    KLAUNCH(k_sumsq_parts, dim3((unsigned)(H / 256), (unsigned)T), dim3(64), 0, s, h, H, ssq);
     return hipGetLastError() == hipSuccess ? 0 : -3;
 }
 
@@ -289,10 +289,10 @@ int launch_combine_norm(const float *y, const float *ysh, const uint32_t *pos, c
 #define CN_LAUNCH(CW)                                                                                            \
     do {                                                                                                         \
         if (K <= 8)                                                                                              \
-            hipLaunchKernelGGL((k_combine_norm<CW, 8>), dim3((unsigned)T), dim3(64 * CW), 0, s, y, ysh, pos, w,   \
+            KLAUNCH((k_combine_norm<CW, 8>), dim3((unsigned)T), dim3(64 * CW), 0, s, y, ysh, pos, w,   \
                                sgl, has_shared, h_in, h_out, res, ssq, T, H, K, nw, eps, xnorm);               \
         else                                                                                                     \
-            hipLaunchKernelGGL((k_combine_norm<CW, OROME_MAXK>), dim3((unsigned)T), dim3(64 * CW), 0, s, y, ysh, \
+            KLAUNCH((k_combine_norm<CW, OROME_MAXK>), dim3((unsigned)T), dim3(64 * CW), 0, s, y, ysh, \
                                pos, w, sgl, has_shared, h_in, h_out, res, ssq, T, H, K, nw, eps, xnorm);         \
     } while (0)
     switch (NI / 2) {
@@ -318,10 +318,10 @@ int launch_combine(const float *y, const float *ysh, const uint32_t *pos, const 
      * blocks; otherwise from a pass over h_out */
     float *fused = H % 1024 == 0 ? ssq : nullptr;
     if (K <= 8)
-        hipLaunchKernelGGL(k_combine<8>, grid, dim3(256), 0, s, y, ysh, pos, w, sgl, has_shared, h_in, h_out, res,
+        KLAUNCH(k_combine<8>, grid, dim3(256), 0, s, y, ysh, pos, w, sgl, has_shared, h_in, h_out, res,
                            fused, T, H, K);
     else
-        hipLaunchKernelGGL(k_combine<OROME_MAXK>, grid, dim3(256), 0, s, y, ysh, pos, w, sgl, has_shared, h_in, h_out,
+        KLAUNCH(k_combine<OROME_MAXK>, grid, dim3(256), 0, s, y, ysh, pos, w, sgl, has_shared, h_in, h_out,
                            res, fused, T, H, K);
     if (hipGetLastError() != hipSuccess) return -3;
     if (ssq && !fused) return launch_sumsq_parts(h_out, T, H, ssq, s);
@@ -341,7 +341,7 @@ __global__ void k_delay(uint64_t ticks) {
 }
 
 int launch_delay(uint32_t usec, hipStream_t s) {
-    hipLaunchKernelGGL(k_delay, dim3(1), dim3(64), 0, s, (uint64_t)usec * 100u);
+    KLAUNCH(k_delay, dim3(1), dim3(64), 0, s, (uint64_t)usec * 100u);
     return hipGetLastError() == hipSuccess ? 0 : -3;
 }
 
@@ -363,7 +363,7 @@ __global__ void k_q4k_ggml_to_ref(uint8_t *blocks, size_t n) {
 
 int launch_q4k_ggml_to_ref(uint8_t *blocks, size_t n, hipStream_t s) {
     if (((uintptr_t)blocks & 3) || !n) return -1;
-    hipLaunchKernelGGL(k_q4k_ggml_to_ref, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, blocks, n);
+    KLAUNCH(k_q4k_ggml_to_ref, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, blocks, n);
     return hipGetLastError() == hipSuccess ? 0 : -3;
 }
 
@@ -379,6 +379,6 @@ int launch_zero(void *p, size_t bytes, hipStream_t s) {
     const size_t words = bytes / 4;
     const unsigned blocks = (unsigned)((words + 255) / 256 < 1024 ? (words + 255) / 256 : 1024);
     if (!blocks) return 0;
-    hipLaunchKernelGGL(k_zero, dim3(blocks), dim3(256), 0, s, (uint32_t *)p, words);
+    KLAUNCH(k_zero, dim3(blocks), dim3(256), 0, s, (uint32_t *)p, words);
     return hipGetLastError() == hipSuccess ? 0 : -3;
 }

@@ -741,11 +741,11 @@ static int epl_for(int E) {
 
 #define EPL_SWITCH(E, KERNEL, ...)                                        \
     switch (epl_for(E)) {                                                 \
-        case 1: hipLaunchKernelGGL(KERNEL<1>, __VA_ARGS__); break;        \
-        case 2: hipLaunchKernelGGL(KERNEL<2>, __VA_ARGS__); break;        \
-        case 4: hipLaunchKernelGGL(KERNEL<4>, __VA_ARGS__); break;        \
-        case 8: hipLaunchKernelGGL(KERNEL<8>, __VA_ARGS__); break;        \
-        case 16: hipLaunchKernelGGL(KERNEL<16>, __VA_ARGS__); break;      \
+        case 1: KLAUNCH(KERNEL<1>, __VA_ARGS__); break;        \
+        case 2: KLAUNCH(KERNEL<2>, __VA_ARGS__); break;        \
+        case 4: KLAUNCH(KERNEL<4>, __VA_ARGS__); break;        \
+        case 8: KLAUNCH(KERNEL<8>, __VA_ARGS__); break;        \
+        case 16: KLAUNCH(KERNEL<16>, __VA_ARGS__); break;      \
         default: return -2;                                               \
     }
 
@@ -754,8 +754,8 @@ int launch_route_small(const RouteArgs &a, hipStream_t s) {
     const dim3 g((a.E + 1 + 3) / 4), g2((a.E + 1 + 1) / 2), g4((unsigned)(a.E + 1));
 #define RS_LAUNCH(TM, NIMV, RSV, G)                                                                      \
     do {                                                                                                 \
-        if (a.norm_h) hipLaunchKernelGGL((k_route_small<true, TM, NIMV, RSV>), G, dim3(256), 0, s, a);  \
-        else hipLaunchKernelGGL((k_route_small<false, TM, NIMV, RSV>), G, dim3(256), 0, s, a);          \
+        if (a.norm_h) KLAUNCH((k_route_small<true, TM, NIMV, RSV>), G, dim3(256), 0, s, a);  \
+        else KLAUNCH((k_route_small<false, TM, NIMV, RSV>), G, dim3(256), 0, s, a);          \
     } while (0)
 #define RS_T(NIMV)                                \
     do {                                          \
@@ -780,7 +780,7 @@ int launch_topk_dispatch_small(const RouteArgs &a, hipStream_t s) {
 int launch_route_logits(const RouteArgs &a, hipStream_t s) {
     if (a.H % 256) return -2;
     dim3 grid((a.E + 1 + 31) / 32, (a.T + 7) / 8);
-    hipLaunchKernelGGL(k_route_logits, grid, dim3(256), 0, s, a);
+    KLAUNCH(k_route_logits, grid, dim3(256), 0, s, a);
     return hipGetLastError() == hipSuccess ? 0 : -3;
 }
 
@@ -800,7 +800,7 @@ void route_eps_coeffs(int H, float *c1, float *c2) {
 
 int launch_pack_router(const float *W, int E, int H, _Float16 *W16, float *wscale, float *wnorm, hipStream_t s) {
     if (E < 1 || H < 1) return -2;
-    hipLaunchKernelGGL(k_pack_router, dim3(E), dim3(256), 0, s, W, H, W16, wscale, wnorm);
+    KLAUNCH(k_pack_router, dim3(E), dim3(256), 0, s, W, H, W16, wscale, wnorm);
     return hipGetLastError() == hipSuccess ? 0 : -3;
 }
 
@@ -812,9 +812,9 @@ int launch_route_approx(const RouteArgs &a, hipStream_t s) {
     /* 1-D grid: expert tiles x token tiles rounded up to 8 (see the kernel) */
     auto grid = [&](int te, int tt) { return dim3((unsigned)((a.E + te - 1) / te * (((a.T + tt - 1) / tt + 7) / 8 * 8))); };
     if (a.T <= 1024)
-        hipLaunchKernelGGL((k_route_approx<1, 2, 8, 8>), grid(32, 16), dim3(512), 0, s, a);
+        KLAUNCH((k_route_approx<1, 2, 8, 8>), grid(32, 16), dim3(512), 0, s, a);
     else
-        hipLaunchKernelGGL((k_route_approx<2, 4, 4, 4>), grid(64, 32), dim3(256), 0, s, a);
+        KLAUNCH((k_route_approx<2, 4, 4, 4>), grid(64, 32), dim3(256), 0, s, a);
     return hipGetLastError() == hipSuccess ? 0 : -3;
 }
 
@@ -827,11 +827,11 @@ int launch_topk_exact(const RouteArgs &a, hipStream_t s) {
     const dim3 grid((a.T * wpt + 3) / 4);
 #define TKX(NIV, WPTV)                                                                                   \
     switch (epl_for(a.E)) {                                                                              \
-        case 1: hipLaunchKernelGGL((k_topk_exact<1, NIV, WPTV>), grid, dim3(256), 0, s, a); break;   \
-        case 2: hipLaunchKernelGGL((k_topk_exact<2, NIV, WPTV>), grid, dim3(256), 0, s, a); break;   \
-        case 4: hipLaunchKernelGGL((k_topk_exact<4, NIV, WPTV>), grid, dim3(256), 0, s, a); break;   \
-        case 8: hipLaunchKernelGGL((k_topk_exact<8, NIV, WPTV>), grid, dim3(256), 0, s, a); break;   \
-        case 16: hipLaunchKernelGGL((k_topk_exact<16, NIV, WPTV>), grid, dim3(256), 0, s, a); break; \
+        case 1: KLAUNCH((k_topk_exact<1, NIV, WPTV>), grid, dim3(256), 0, s, a); break;   \
+        case 2: KLAUNCH((k_topk_exact<2, NIV, WPTV>), grid, dim3(256), 0, s, a); break;   \
+        case 4: KLAUNCH((k_topk_exact<4, NIV, WPTV>), grid, dim3(256), 0, s, a); break;   \
+        case 8: KLAUNCH((k_topk_exact<8, NIV, WPTV>), grid, dim3(256), 0, s, a); break;   \
+        case 16: KLAUNCH((k_topk_exact<16, NIV, WPTV>), grid, dim3(256), 0, s, a); break; \
         default: return -2;                                                                              \
     }
 #define TKW(NIV)                      \
@@ -858,22 +858,22 @@ int launch_dispatch(const RouteArgs &a, uint32_t *tiles_s, uint32_t *tiles_b, in
 #define DISPATCH_ONE 1
 #endif
     if (DISPATCH_ONE && a.E <= 256 && a.T <= DSP_THREADS) {
-        if (a.K <= 8) hipLaunchKernelGGL(k_dispatch_one<8>, dim3(1), dim3(DSP_THREADS), 0, s, a, tiles_s, tiles_b, has_shared);
-        else hipLaunchKernelGGL(k_dispatch_one<OROME_MAXK>, dim3(1), dim3(DSP_THREADS), 0, s, a, tiles_s, tiles_b, has_shared);
+        if (a.K <= 8) KLAUNCH(k_dispatch_one<8>, dim3(1), dim3(DSP_THREADS), 0, s, a, tiles_s, tiles_b, has_shared);
+        else KLAUNCH(k_dispatch_one<OROME_MAXK>, dim3(1), dim3(DSP_THREADS), 0, s, a, tiles_s, tiles_b, has_shared);
         return hipGetLastError() == hipSuccess ? 0 : -3;
     }
     const int G = dispatch_blocks(a.T);
-    if (a.K <= 8) hipLaunchKernelGGL(k_dispatch_count<8>, dim3(G), dim3(DSP_TOK), lds / 2, s, a, cnt);
-    else hipLaunchKernelGGL(k_dispatch_count<OROME_MAXK>, dim3(G), dim3(DSP_TOK), lds / 2, s, a, cnt);
-    hipLaunchKernelGGL(k_dispatch_scan, dim3(1), dim3(DSP_THREADS), 0, s, a, cnt, G, tiles_s, tiles_b, has_shared);
-    if (a.K <= 8) hipLaunchKernelGGL(k_dispatch_scatter<8>, dim3(G), dim3(DSP_TOK), lds, s, a, (const uint32_t *)cnt);
-    else hipLaunchKernelGGL(k_dispatch_scatter<OROME_MAXK>, dim3(G), dim3(DSP_TOK), lds, s, a, (const uint32_t *)cnt);
+    if (a.K <= 8) KLAUNCH(k_dispatch_count<8>, dim3(G), dim3(DSP_TOK), lds / 2, s, a, cnt);
+    else KLAUNCH(k_dispatch_count<OROME_MAXK>, dim3(G), dim3(DSP_TOK), lds / 2, s, a, cnt);
+    KLAUNCH(k_dispatch_scan, dim3(1), dim3(DSP_THREADS), 0, s, a, cnt, G, tiles_s, tiles_b, has_shared);
+    if (a.K <= 8) KLAUNCH(k_dispatch_scatter<8>, dim3(G), dim3(DSP_TOK), lds, s, a, (const uint32_t *)cnt);
+    else KLAUNCH(k_dispatch_scatter<OROME_MAXK>, dim3(G), dim3(DSP_TOK), lds, s, a, (const uint32_t *)cnt);
     return hipGetLastError() == hipSuccess ? 0 : -3;
 }
 
 int launch_rmsnorm(const float *h, const float *w, int T, int H, float eps, float *x, hipStream_t s) {
     if (H % 256 || H > 256 * CANON_NI) return -2;
-    if (H <= 256 * 8) hipLaunchKernelGGL(k_rmsnorm<8>, dim3(T), dim3(64), 0, s, h, w, H, eps, x);
-    else hipLaunchKernelGGL(k_rmsnorm<CANON_NI>, dim3(T), dim3(64), 0, s, h, w, H, eps, x);
+    if (H <= 256 * 8) KLAUNCH(k_rmsnorm<8>, dim3(T), dim3(64), 0, s, h, w, H, eps, x);
+    else KLAUNCH(k_rmsnorm<CANON_NI>, dim3(T), dim3(64), 0, s, h, w, H, eps, x);
     return hipGetLastError() == hipSuccess ? 0 : -3;
 }
