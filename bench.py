@@ -49,6 +49,10 @@ CONFIGS = {
               steps=200),
     "3": dict(T=512, name="moe_prefill_512_zipf_q6k", mode="layer", layers=4,
               spec=dict(down=Q6K, zipf=True), xbank=4, steps=200),
+    # the layout of common Q4_K_M MoE files: Q5_K routed down, Q8_0 shared
+    # expert (not a BASELINE config; a parity-tested variant)
+    "2r": dict(T=512, name="moe_prefill_512_q5k_down_q8_shared", mode="layer", layers=4,
+               spec=dict(down=13, shared=8), xbank=4, steps=200),
     "4d": dict(T=1, name="moe_stack40_decode_b1", mode="stack", layers=40,
                spec=dict(q6k_every=4, centered=True), xbank=16, steps=100),
     "4p": dict(T=2048, name="moe_stack40_prefill_2048", mode="stack", layers=40,
@@ -63,6 +67,12 @@ def q4k_bytes(rows, cols):
 
 def q6k_bytes(rows, cols):
     return rows * (cols // 256) * 210
+
+
+def mat_bytes(ggml_type, rows, cols):
+    """Bytes of a [rows x cols] matrix in a ggml block format (Q4_K, Q5_K, Q6_K, Q8_0)."""
+    per = {12: (256, 144), 13: (256, 176), 14: (256, 210), 8: (32, 34)}[ggml_type]
+    return rows * (cols // per[0]) * per[1]
 
 
 def log(msg):
@@ -210,12 +220,14 @@ def run_config(key, steps, warmup, path, cpu_seconds, no_cpu):
     # algorithmic work per gate/up launch and per MoE layer
     nl = L if stack else 1
     n_q6 = sum(1 for l in range(L) if cf["spec"].get("q6k_every") and l % 4 == 3) if stack else 0
-    down_e = q6k_bytes(H, M) if cf["spec"].get("down") == Q6K else q4k_bytes(H, M)
+    down_e = mat_bytes(cf["spec"].get("down", Q4K), H, M)
+    sh_t = cf["spec"].get("shared", Q4K)
     rows = T * K + T  # routed pairs plus shared-expert rows
-    gu_bytes = (u_mean + 1) * 2 * q4k_bytes(M, H) + T * H * (4 if kpath == "gemv" else 2) + rows * M * 2
+    gu_bytes = (u_mean * 2 * q4k_bytes(M, H) + 2 * mat_bytes(sh_t, S, H) + T * H * (4 if kpath == "gemv" else 2)
+                + rows * M * 2)
     gu_flops = 2.0 * 2 * rows * M * H
-    layer_bytes = (u_mean * (2 * q4k_bytes(M, H) + down_e) + 3 * q4k_bytes(S, H) + E * H * 4 + H * 4
-                   + T * H * 4 * 3)
+    layer_bytes = (u_mean * (2 * q4k_bytes(M, H) + down_e) + 2 * mat_bytes(sh_t, S, H) + mat_bytes(sh_t, H, S)
+                   + E * H * 4 + H * 4 + T * H * 4 * 3)
     if stack:
         layer_bytes += (q6k_bytes(H, M) - q4k_bytes(H, M)) * u_mean * n_q6 / L
     step_bytes = layer_bytes * nl

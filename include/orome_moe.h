@@ -208,11 +208,11 @@ int orome_hip_set_path(orome_hip_ctx *ctx, int path);
  * counterpart in the reference (its kernels read the GGUF blocks in place):
  * registering a layer declares its weights immutable while registered and
  * repacks, into one allocation on the context's device (the same bytes as the
- * originals), the routed gate/up (Q4_K), each down projection that is Q4_K or
- * Q6_K, and the shared gate/up when Q4_K; a Q8_0 shared expert (the
- * reference's 35B layout) stays row-major and the grouped GEMMs read it in
- * place beside the copies.  orome_moe_forward then feeds the grouped GEMMs
- * from the copies, so each wave's weight load is one contiguous 1 KB.
+ * originals), the routed gate/up (Q4_K), the routed down when Q4_K, Q5_K or
+ * Q6_K, the shared gate/up when Q4_K or Q8_0 (the reference's 35B layout has
+ * a Q8_0 shared expert), and, beside a repacked routed down, the shared down
+ * (Q4_K, Q5_K, Q6_K or Q8_0).  orome_moe_forward then feeds the grouped GEMMs
+ * from the copies, so each wave's weight loads are contiguous 1-2 KB runs.
  * Outputs are bit-identical with and without.  Layers are keyed by the routed
  * gate and shared gate addresses; registering again replaces the copy.  With
  * an F32 router (any shared-expert format) the copy also holds the router as
@@ -377,7 +377,7 @@ int orome_dequant_rows_f16(orome_hip_ctx *ctx, OromeHipQuantFormat fmt, const vo
  * of `fmt` (Q4_K, Q5_K, Q6_K, Q8_0) is multiplied by in_dim one-hot fp16
  * activation rows, so out_dev[j][r] = the fp16 weight (r, j) the matrix cores
  * used, exactly (products with 1, sums of zeros).  tiled: repack it first
- * (Q4_K, Q6_K) as orome_hip_pack_layer does and read the tile-major copy.
+ * (any of the four) as orome_hip_pack_layer does and read the tile-major copy.
  * out_dev: fp32 [in_dim x rows].  For tests; not thread-safe with forward
  * calls on the context (it uses the context's scratch).  No counterpart in
  * the reference. */

@@ -76,7 +76,8 @@ struct Pack {
     void *mem;
     const uint8_t *gate, *up, *down, *sgate, *sup, *sdown;
     size_t gate_stride, down_stride;
-    int down_fmt, sdown_fmt; /* GEMM_FMT_Q4K_TILED or GEMM_FMT_Q6K_TILED */
+    int sgate_fmt;           /* GEMM_FMT_Q4K_TILED or GEMM_FMT_Q8_TILED */
+    int down_fmt, sdown_fmt; /* GEMM_FMT_Q{4,5,6}K_TILED (or, shared, GEMM_FMT_Q8_TILED) */
     /* router copy for the two-pass large-batch router (r16 NULL: none) */
     const float *rkey;
     _Float16 *r16;
@@ -281,8 +282,7 @@ static int kfmt(OromeHipQuantFormat f) {
 /* ------------------------------------------------- tile-major repacking */
 
 /* The grouped GEMMs' view of a layer: registered layers read their
- * tile-major copies (each matrix that was repacked; a Q8_0 shared expert
- * stays row-major). */
+ * tile-major copies (each matrix that was repacked). */
 static const Pack *find_pack(const orome_hip_ctx *c, const uint8_t *gate, const uint8_t *sh_gate);
 static void apply_pack(const orome_hip_ctx *c, int S, ExpertSide &exm, SharedSide &shm) {
     const Pack *pk = find_pack(c, exm.gate, shm.gate);
@@ -294,7 +294,7 @@ static void apply_pack(const orome_hip_ctx *c, int S, ExpertSide &exm, SharedSid
     if (S && pk->sgate) {
         shm.gate = pk->sgate;
         shm.up = pk->sup;
-        shm.gate_fmt = GEMM_FMT_Q4K_TILED;
+        shm.gate_fmt = pk->sgate_fmt;
     }
     if (pk->down) {
         exm.down = pk->down;
@@ -331,17 +331,41 @@ extern "C" int orome_hip_pack_layer(orome_hip_ctx *c, const OromeHipModelConfig 
     const int S = lt->shared_gate.buffer ? (int)lt->shared_gate.out_dim : 0;
     if (S % 256) return orome_fail(OROME_EUNSUPPORTED, "orome_hip_pack_layer: shared intermediate %d not a multiple of 256", S);
     /* Every matrix the tile-major spans can hold is repacked: routed gate/up
-     * (Q4_K), the shared gate/up when Q4_K, each down projection when Q4_K or
-     * Q6_K.  A Q8_0 shared expert (the reference's 35B layout) stays
-     * row-major; the grouped GEMMs read it in place beside the copies. */
-    auto tileable = [](OromeHipQuantFormat f) { return f == OROME_QFMT_GGUF_Q4_K || f == OROME_QFMT_GGUF_Q6_K; };
-    const bool sh_gu = S && lt->shared_gate.format == OROME_QFMT_GGUF_Q4_K && lt->shared_up.format == OROME_QFMT_GGUF_Q4_K;
-    const bool dn = tileable(elr->down.format), sdn_t = S && dn && tileable(lt->shared_down.format);
-    const bool rq6 = elr->down.format == OROME_QFMT_GGUF_Q6_K, sq6 = S && lt->shared_down.format == OROME_QFMT_GGUF_Q6_K;
+     * (Q4_K), the shared gate/up when Q4_K or Q8_0 (the reference's 35B
+     * layout has a Q8_0 shared expert), the routed down when Q4_K, Q5_K or
+     * Q6_K, and then the shared down when Q4_K, Q5_K, Q6_K or Q8_0. */
+    auto tileable = [](OromeHipQuantFormat f) {
+        return f == OROME_QFMT_GGUF_Q4_K || f == OROME_QFMT_GGUF_Q5_K || f == OROME_QFMT_GGUF_Q6_K;
+    };
+    /* bytes, packer and tile-major format id of a down projection */
+    auto dn_bytes = [](OromeHipQuantFormat f, int R, int K, int n) {
+        return f == OROME_QFMT_GGUF_Q6_K ? packed_q6k_bytes(R, K, n)
+               : f == OROME_QFMT_GGUF_Q5_K ? packed_q5k_bytes(R, K, n)
+               : f == OROME_QFMT_GGUF_Q8_0 ? packed_q8_bytes(R, K, n)
+                                           : packed_q4k_bytes(R, K, n);
+    };
+    auto dn_pack = [](OromeHipQuantFormat f) {
+        return f == OROME_QFMT_GGUF_Q6_K ? launch_pack_q6k
+               : f == OROME_QFMT_GGUF_Q5_K ? launch_pack_q5k
+               : f == OROME_QFMT_GGUF_Q8_0 ? launch_pack_q8
+                                           : launch_pack_q4k;
+    };
+    auto dn_fmt = [](OromeHipQuantFormat f) {
+        return f == OROME_QFMT_GGUF_Q6_K ? (int)GEMM_FMT_Q6K_TILED
+               : f == OROME_QFMT_GGUF_Q5_K ? (int)GEMM_FMT_Q5K_TILED
+               : f == OROME_QFMT_GGUF_Q8_0 ? (int)GEMM_FMT_Q8_TILED
+                                           : (int)GEMM_FMT_Q4K_TILED;
+    };
+    const OromeHipQuantFormat sgf = S ? lt->shared_gate.format : OROME_QFMT_F32;
+    const bool sh_q8 = S && sgf == OROME_QFMT_GGUF_Q8_0 && lt->shared_up.format == OROME_QFMT_GGUF_Q8_0;
+    const bool sh_gu = sh_q8 || (S && sgf == OROME_QFMT_GGUF_Q4_K && lt->shared_up.format == OROME_QFMT_GGUF_Q4_K);
+    const bool dn = tileable(elr->down.format);
+    const bool sdn_q8 = S && lt->shared_down.format == OROME_QFMT_GGUF_Q8_0;
+    const bool sdn_t = S && dn && (tileable(lt->shared_down.format) || sdn_q8);
     const size_t gu = packed_q4k_bytes(M, H, E),
-                 dnb = !dn ? 0 : rq6 ? packed_q6k_bytes(H, M, E) : packed_q4k_bytes(H, M, E),
-                 sgu = sh_gu ? packed_q4k_bytes(S, H, 1) : 0,
-                 sdn = !sdn_t ? 0 : sq6 ? packed_q6k_bytes(H, S, 1) : packed_q4k_bytes(H, S, 1);
+                 dnb = !dn ? 0 : dn_bytes(elr->down.format, H, M, E),
+                 sgu = !sh_gu ? 0 : sh_q8 ? packed_q8_bytes(S, H, 1) : packed_q4k_bytes(S, H, 1),
+                 sdn = !sdn_t ? 0 : dn_bytes(lt->shared_down.format, H, S, 1);
     if (set_dev(c)) return OROME_EHIP;
     const uint8_t *gate = dev_addr(elr->buffer, elr->gate.offset), *sh_gate = S ? dev_addr(lt->shared_gate.buffer, lt->shared_gate.offset) : NULL;
     if (c->npacks == c->pcap) {
@@ -378,25 +402,27 @@ extern "C" int orome_hip_pack_layer(orome_hip_ctx *c, const OromeHipModelConfig 
     pk.gate_stride = gu / E;
     if (dn) {
         pk.down = m;
-        pk.down_fmt = rq6 ? GEMM_FMT_Q6K_TILED : GEMM_FMT_Q4K_TILED;
-        rc |= (rq6 ? launch_pack_q6k : launch_pack_q4k)(dev_addr(elr->buffer, elr->down.offset), m, H, M, E,
-                                                         elr->down.expert_stride, c->stream);
+        pk.down_fmt = dn_fmt(elr->down.format);
+        rc |= dn_pack(elr->down.format)(dev_addr(elr->buffer, elr->down.offset), m, H, M, E, elr->down.expert_stride,
+                                        c->stream);
         m += dnb;
         pk.down_stride = dnb / E;
     }
     if (sh_gu) {
+        auto packf = sh_q8 ? launch_pack_q8 : launch_pack_q4k;
+        pk.sgate_fmt = sh_q8 ? GEMM_FMT_Q8_TILED : GEMM_FMT_Q4K_TILED;
         pk.sgate = m;
-        rc |= launch_pack_q4k(sh_gate, m, S, H, 1, 0, c->stream);
+        rc |= packf(sh_gate, m, S, H, 1, 0, c->stream);
         m += sgu;
         pk.sup = m;
-        rc |= launch_pack_q4k(dev_addr(lt->shared_up.buffer, lt->shared_up.offset), m, S, H, 1, 0, c->stream);
+        rc |= packf(dev_addr(lt->shared_up.buffer, lt->shared_up.offset), m, S, H, 1, 0, c->stream);
         m += sgu;
     }
     if (sdn_t) {
         pk.sdown = m;
-        pk.sdown_fmt = sq6 ? GEMM_FMT_Q6K_TILED : GEMM_FMT_Q4K_TILED;
-        rc |= (sq6 ? launch_pack_q6k : launch_pack_q4k)(dev_addr(lt->shared_down.buffer, lt->shared_down.offset), m,
-                                                         H, S, 1, 0, c->stream);
+        pk.sdown_fmt = dn_fmt(lt->shared_down.format);
+        rc |= dn_pack(lt->shared_down.format)(dev_addr(lt->shared_down.buffer, lt->shared_down.offset), m, H, S, 1, 0,
+                                              c->stream);
     }
     if (rc || hipStreamSynchronize(c->stream) != hipSuccess) {
         (void)hipFree(pk.mem);
@@ -792,7 +818,7 @@ extern "C" int orome_debug_mfma_weights(orome_hip_ctx *c, OromeHipQuantFormat fm
     if (!c || !w || !out) return orome_fail(OROME_EINVAL, "orome_debug_mfma_weights: NULL argument");
     const int H = c->cfg.hidden_dim, M = c->cfg.moe_intermediate;
     const int f = kfmt(fmt);
-    if ((int)rows != H || (int)in_dim != M || f < 0 || (tiled && f != 0 && f != 2))
+    if ((int)rows != H || (int)in_dim != M || f < 0 || (tiled && f != 0 && f != 1 && f != 2 && f != 3))
         return orome_fail(OROME_EINVAL, "orome_debug_mfma_weights: a %ux%u %s matrix does not fit", rows, in_dim,
                           tiled ? "tile-major" : "row-major");
     if ((size_t)M > (size_t)c->tmax * c->kmax)
@@ -805,15 +831,17 @@ extern "C" int orome_debug_mfma_weights(orome_hip_ctx *c, OromeHipQuantFormat fm
     ex.down_fmt = f;
     ex.gate_fmt = 0;
     if (tiled) {
-        const size_t nb = f == 0 ? packed_q4k_bytes(H, M, 1) : packed_q6k_bytes(H, M, 1);
+        const size_t nb = f == 0 ? packed_q4k_bytes(H, M, 1) : f == 1 ? packed_q5k_bytes(H, M, 1)
+                          : f == 2 ? packed_q6k_bytes(H, M, 1) : packed_q8_bytes(H, M, 1);
         HIP_OK(hipMalloc(&packed, nb), OROME_ENOMEM);
-        const int rc = (f == 0 ? launch_pack_q4k : launch_pack_q6k)((const uint8_t *)w, (uint8_t *)packed, H, M, 1, 0, s);
+        const int rc = (f == 0 ? launch_pack_q4k : f == 1 ? launch_pack_q5k : f == 2 ? launch_pack_q6k : launch_pack_q8)(
+            (const uint8_t *)w, (uint8_t *)packed, H, M, 1, 0, s);
         if (rc) {
             (void)hipFree(packed);
             return launch_rc(rc, "orome_debug_mfma_weights: repack");
         }
         ex.down = (const uint8_t *)packed;
-        ex.down_fmt = f == 0 ? GEMM_FMT_Q4K_TILED : GEMM_FMT_Q6K_TILED;
+        ex.down_fmt = f == 0 ? GEMM_FMT_Q4K_TILED : f == 1 ? GEMM_FMT_Q5K_TILED : f == 2 ? GEMM_FMT_Q6K_TILED : GEMM_FMT_Q8_TILED;
     }
     SharedSide sh = {NULL, NULL, NULL, 0, 0, 0};
     /* M one-hot rows as the pairs of expert 0, in 32-row tiles */

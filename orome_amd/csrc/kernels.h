@@ -129,11 +129,15 @@ int launch_gemm_down(const ExpertSide &ex, const SharedSide &sh, const _Float16 
                      hipStream_t s);
 /* tile-major repack of Q4_K expert matrices for the grouped GEMMs (format
  * id 4 in ExpertSide / SharedSide) */
-enum { GEMM_FMT_Q4K_TILED = 4, GEMM_FMT_Q6K_TILED = 5 };
+enum { GEMM_FMT_Q4K_TILED = 4, GEMM_FMT_Q6K_TILED = 5, GEMM_FMT_Q8_TILED = 6, GEMM_FMT_Q5K_TILED = 7 };
 size_t packed_q4k_bytes(int R, int K, int E);
 int launch_pack_q4k(const uint8_t *src, uint8_t *dst, int R, int K, int E, size_t src_stride, hipStream_t s);
 size_t packed_q6k_bytes(int R, int K, int E);
 int launch_pack_q6k(const uint8_t *src, uint8_t *dst, int R, int K, int E, size_t src_stride, hipStream_t s);
+size_t packed_q8_bytes(int R, int K, int E);
+size_t packed_q5k_bytes(int R, int K, int E);
+int launch_pack_q5k(const uint8_t *src, uint8_t *dst, int R, int K, int E, size_t src_stride, hipStream_t s);
+int launch_pack_q8(const uint8_t *src, uint8_t *dst, int R, int K, int E, size_t src_stride, hipStream_t s);
 /* prefill combine of one token per wave that also writes the next layer's
  * RMSNorm of h_out into xnorm (nw: its weight, or NULL for ones) */
 int launch_combine_norm(const float *y, const float *ysh, const uint32_t *pos, const float *w, const float *sgl,

@@ -33,9 +33,10 @@
 #include "dev_common.h"
 #include "kernels.h"
 
-/* FQ4KT, FQ6KT: Q4_K / Q6_K repacked tile-major (launch_pack_q4k,
- * launch_pack_q6k), same values */
-enum { FQ4K = 0, FQ5K = 1, FQ6K = 2, FQ8 = 3, FQ4KT = GEMM_FMT_Q4K_TILED, FQ6KT = GEMM_FMT_Q6K_TILED };
+/* FQ4KT, FQ5KT, FQ6KT, FQ8T: Q4_K / Q5_K / Q6_K / Q8_0 repacked tile-major
+ * (launch_pack_q4k, _q5k, _q6k, _q8), same values */
+enum { FQ4K = 0, FQ5K = 1, FQ6K = 2, FQ8 = 3, FQ4KT = GEMM_FMT_Q4K_TILED, FQ6KT = GEMM_FMT_Q6K_TILED, FQ8T = GEMM_FMT_Q8_TILED,
+       FQ5KT = GEMM_FMT_Q5K_TILED };
 
 typedef float f4v __attribute__((ext_vector_type(4)));
 
@@ -43,11 +44,21 @@ typedef float f4v __attribute__((ext_vector_type(4)));
  * regime) run 4-wave blocks with a 2-deep weight ring, so four waves share
  * a SIMD; big tiles run 8-wave blocks with a 4-deep ring (their LDS tile
  * allows one block per CU). */
+#ifndef GEMM_BIG_W
+#define GEMM_BIG_W 8
+#endif
+#ifndef GEMM_BIG_DEPTH
+#define GEMM_BIG_DEPTH 4
+#endif
 template <int TBM>
 struct Shape {
-    static constexpr int W = TBM <= 2 ? 4 : 8;     /* waves per block */
-    static constexpr int DEPTH = TBM <= 2 ? 2 : 4; /* weight stages in flight per wave */
-    static constexpr int CHV = 8 / W;              /* chunk vectors per token block and thread */
+    static constexpr int W = TBM <= 2 ? 4 : GEMM_BIG_W;         /* waves per block */
+    static constexpr int DEPTH = TBM <= 2 ? 2 : GEMM_BIG_DEPTH; /* weight stages in flight per wave */
+    /* activation chunk: TBM*16 rows of 32 16-byte vectors, NV per thread;
+     * when the last pass runs past the tile its rows land in one spare LDS
+     * row (XR = rows per chunk buffer) */
+    static constexpr int NV = (TBM * 16 * 32 + W * 64 - 1) / (W * 64);
+    static constexpr int XR = NV * W * 2 > TBM * 16 ? TBM * 16 + 1 : TBM * 16;
 };
 #define KC 128                          /* k per stage (one A fragment set) */
 #define KCH 256                         /* k per LDS activation chunk */
@@ -55,7 +66,7 @@ struct Shape {
 
 DEV size_t gemm_row_bytes(int fmt, int n) {
     return fmt == FQ4K || fmt == FQ4KT ? (size_t)(n / 256) * 144
-           : fmt == FQ5K               ? (size_t)(n / 256) * 176
+           : fmt == FQ5K || fmt == FQ5KT ? (size_t)(n / 256) * 176
            : fmt == FQ6K || fmt == FQ6KT ? (size_t)(n / 256) * 210
                                          : (size_t)(n / 32) * 34;
 }
@@ -63,7 +74,9 @@ DEV size_t gemm_row_bytes(int fmt, int n) {
  * own, or (tile-major Q4_K) the block base plus the lane's 16-byte column */
 template <int FMT>
 DEV size_t lane_row(int row0, int i, size_t rbytes) {
-    return FMT == FQ4KT || FMT == FQ6KT ? (size_t)row0 * rbytes + (size_t)i * 16 : (size_t)(row0 + i) * rbytes;
+    return FMT == FQ4KT || FMT == FQ5KT || FMT == FQ6KT ? (size_t)row0 * rbytes + (size_t)i * 16
+           : FMT == FQ8T                 ? (size_t)row0 * rbytes
+                                         : (size_t)(row0 + i) * rbytes;
 }
 DEV uint32_t u4_at(u4 v, int i) { return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w; }
 DEV h2 splat(_Float16 v) { return h2{v, v}; }
@@ -94,7 +107,7 @@ DEV void q8_h2_0213(uint32_t w, h2 &p02, h2 &p13) {
  * copied into LDS unchanged. */
 template <int FMT>
 DEV int frag_pos(int c) {
-    if (FMT == FQ4K || FMT == FQ4KT || FMT == FQ5K) { /* lane kg, step s: k = 64(kg>>1) + 16(kg&1) + 4s (+32 high nibbles) */
+    if (FMT == FQ4K || FMT == FQ4KT || FMT == FQ5K || FMT == FQ5KT) { /* lane kg, step s: k = 64(kg>>1) + 16(kg&1) + 4s (+32 high nibbles) */
         const int g = c >> 4, r = c & 15, hi = r >> 3, rr = r & 7;
         return (((rr & 3) * 4 + 2 * g + (rr >> 2)) * 8) + 4 * hi;
     } else if (FMT == FQ6K || FMT == FQ6KT) { /* k = 32(kg&1) + 16(kg>>1) + 4s (+64 high nibbles) */
@@ -230,6 +243,20 @@ struct Span<FQ5K> {
     }
 };
 
+/* Tile-major Q5_K: per 16-row block and super-block, 2816 bytes = the 16
+ * rows' 16-byte headers, the 64 lanes' 16 quant bytes per 128-k half in lane
+ * order (as Q4_K), then the qh bytes: for g = kg & 1, the 16 rows' bytes
+ * 16g .. 16g+15 of qh.  `p` is the block base plus 16 i. */
+template <>
+struct Span<FQ5KT> : Span<FQ5K> {
+    MDEV void load(const uint8_t *p, int j, int kg) {
+        const uint8_t *b = p + (size_t)(j >> 1) * 2816;
+        hdr = ld_u4(b);
+        q = ld_u4(b + 256 + (j & 1) * 1024 + kg * 256);
+        qh = ld_u4(b + 2304 + (kg & 1) * 256);
+    }
+};
+
 template <>
 struct Span<FQ6K> {
     u4 ql, qh;
@@ -302,6 +329,37 @@ struct Span<FQ8> {
     }
 };
 
+/* Tile-major Q8_0: per 16-row block and 128-k stage, 2176 bytes = the 64
+ * lanes' 32 quant bytes in lane order (lane kg * 16 + i: row i, blocks 4j..4j+3,
+ * bytes 8kg..8kg+7 of each), then the 16 rows' four fp16 scales.  Aligned
+ * 16-byte loads (row-major Q8_0 blocks are 34 bytes, 2-byte aligned) and
+ * half the registers per stage.  `p` is the 16-row block base. */
+template <>
+struct Span<FQ8T> {
+    u4 q0, q1;
+    u2 dd;
+    MDEV void init(int) {}
+    MDEV void load(const uint8_t *p, int j, int) {
+        const int ln = threadIdx.x & 63;
+        const uint8_t *b = p + (size_t)j * 2176;
+        q0 = ld_u4(b + 32 * ln);
+        q1 = ld_u4(b + 32 * ln + 16);
+        typedef const __attribute__((address_space(1))) u2 *gp2;
+        dd = *(gp2)(uintptr_t)(b + 2048 + 8 * (ln & 15));
+    }
+    MDEV void prepare(int, int) {}
+    MDEV h8 frag(int s) const {
+        const uint32_t dw = s < 2 ? dd.x : dd.y;
+        const h2 d = splat(__builtin_bit_cast(_Float16, (uint16_t)((s & 1) ? dw >> 16 : dw & 0xFFFFu)));
+        const uint32_t w0 = s == 0 ? q0.x : s == 1 ? q0.z : s == 2 ? q1.x : q1.z;
+        const uint32_t w1 = s == 0 ? q0.y : s == 1 ? q0.w : s == 2 ? q1.y : q1.w;
+        h2 p02, p13, p46, p57; /* k order l, l+2, l+1, l+3, l+4, l+6, l+5, l+7 */
+        q8_h2_0213(w0, p02, p13);
+        q8_h2_0213(w1, p46, p57);
+        return cat4(p02 * d, p13 * d, p46 * d, p57 * d);
+    }
+};
+
 DEV f4v mfma(h8 a, h8 b, f4v c) { return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0); }
 
 /* ------------------------------------------------------- B chunks */
@@ -315,21 +373,27 @@ DEV f4v mfma(h8 a, h8 b, f4v c) { return __builtin_amdgcn_mfma_f32_16x16x32_f16(
  * select. */
 template <int TBM>
 struct Chunk {
-    static constexpr int W = Shape<TBM>::W, CHV = Shape<TBM>::CHV;
-    u4 v[TBM * CHV];
+    static constexpr int W = Shape<TBM>::W, NV = Shape<TBM>::NV, TR = TBM * 16;
+    u4 v[NV];
+    /* chunk row of this thread's vector n, clamped to `lim` only where the
+     * last pass runs past the tile */
+    MDEV int row(int n, int lim) const {
+        const int r = (W * 2) * n + (int)(threadIdx.x >> 5);
+        return NV * W * 2 > TR ? min(r, lim) : r;
+    }
     MDEV void fetch(const _Float16 *src, const int *rowoff, int ld, int k0) {
         const int cc = (threadIdx.x & 31) * 8;
 #pragma unroll
-        for (int n = 0; n < TBM * CHV; n++)
-            v[n] = ld_u4((const uint8_t *)(src + (size_t)rowoff[(W * 2) * n + (threadIdx.x >> 5)] * ld + k0 + cc));
+        for (int n = 0; n < NV; n++)
+            v[n] = ld_u4((const uint8_t *)(src + (size_t)rowoff[row(n, TR - 1)] * ld + k0 + cc));
     }
     template <int FMT>
     MDEV void store(_Float16 *xs) const {
         const int col = threadIdx.x & 31, half = col >> 4, c0 = (col & 15) * 2;
         const int p0 = half * KC + frag_pos<FMT>(c0), p1 = half * KC + frag_pos<FMT>(c0 + 1);
 #pragma unroll
-        for (int n = 0; n < TBM * CHV; n++) {
-            _Float16 *row = xs + ((W * 2) * n + (threadIdx.x >> 5)) * BLD;
+        for (int n = 0; n < NV; n++) {
+            _Float16 *row = xs + this->row(n, TR) * BLD;
             *(u2 *)(row + p0) = u2{v[n].x, v[n].y};
             *(u2 *)(row + p1) = u2{v[n].z, v[n].w};
         }
@@ -377,7 +441,7 @@ DEV void tile_run(const uint8_t *w0, const uint8_t *w1, int in_dim, const _Float
     ch.template store<FMT>(xs);
     if (nch > 1) {
         ch.fetch(src, rowoff, ld, KCH);
-        ch.template store<FMT>(xs + TBM * 16 * BLD);
+        ch.template store<FMT>(xs + Shape<TBM>::XR * BLD);
     }
     if (nch > 2) ch.fetch(src, rowoff, ld, 2 * KCH);
     __syncthreads();
@@ -410,7 +474,7 @@ DEV void tile_run(const uint8_t *w0, const uint8_t *w1, int in_dim, const _Float
 #pragma unroll
                 for (int m = 0; m < NMAT; m++) ring[d][m].load((m ? rw1 : rw0) + (size_t)rb2 * 16 * rbytes, j2, kg);
             }
-            const _Float16 *bp = xs + ((j >> 1) & 1) * (TBM * 16 * BLD) + (j & 1) * KC + i * BLD + kg * 8;
+            const _Float16 *bp = xs + ((j >> 1) & 1) * (Shape<TBM>::XR * BLD) + (j & 1) * KC + i * BLD + kg * 8;
 #pragma unroll
             for (int s = 0; s < 4; s++) {
                 h8 a[NMAT];
@@ -444,7 +508,7 @@ DEV void tile_run(const uint8_t *w0, const uint8_t *w1, int in_dim, const _Float
             }
             if (nch > 2 && (j & 1) && (j >> 1) + 2 < nch) {
                 __syncthreads();
-                ch.template store<FMT>(xs + ((j >> 1) & 1) * (TBM * 16 * BLD));
+                ch.template store<FMT>(xs + ((j >> 1) & 1) * (Shape<TBM>::XR * BLD));
                 if ((j >> 1) + 3 < nch) ch.fetch(src, rowoff, ld, ((j >> 1) + 3) * KCH);
             } else if (nch > 2 && (j & 1) && (j >> 1) + 1 < nch) {
                 __syncthreads(); /* chunk c+1 was stored before the previous barrier */
@@ -573,7 +637,7 @@ DEV UnitDesc unit_desc(const uint32_t *tiles, int nyb, int E, int n, int uwin) {
  * epilogue. */
 template <int FMT, int NMAT, int RPW, int DEPTH, int NST, int TBM, typename P>
 DEV void tile_stream(const P &pol, _Float16 *xs, int *rowoff) {
-    constexpr int W = Shape<TBM>::W, TR = TBM * 16, nst = NST, nch = NST / 2, U = RPW * NST, CB = TR * BLD;
+    constexpr int W = Shape<TBM>::W, TR = TBM * 16, nst = NST, nch = NST / 2, U = RPW * NST, CB = Shape<TBM>::XR * BLD;
     static_assert(NST % 4 == 0 && U % DEPTH == 0 && (RPW == 1 || nch == 2), "stream shape");
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int kg = lane >> 4, i = lane & 15;
@@ -766,7 +830,7 @@ struct DnPol {
  * expert's (the same, or Q8_0 row-major) */
 template <int RF, int SF, int NST, int TBM>
 DEV void k_gemm_gate_up_body(GemmArgs a) {
-    __shared__ __attribute__((aligned(16))) _Float16 xs[2 * TBM * 16 * BLD];
+    __shared__ __attribute__((aligned(16))) _Float16 xs[2 * Shape<TBM>::XR * BLD];
     __shared__ int rowoff[TBM * 16];
     int ti, yb;
     block_tile(a.nyb, ti, yb);
@@ -782,7 +846,7 @@ DEV void k_gemm_gate_up_body(GemmArgs a) {
     __syncthreads();
     if (sh) {
         const GuEpi epi{a.act_sh, a.S, (int)first, (int)rows};
-        tile_run<SF, 2, GU_RPW, (SF == FQ8 ? 2 : Shape<TBM>::DEPTH), NST, TBM>(a.sh_a, a.sh_b, a.H, a.src, a.H, rowoff, (int)rows, yb, xs, epi);
+        tile_run<SF, 2, GU_RPW, (SF == FQ8 || SF == FQ8T ? 2 : Shape<TBM>::DEPTH), NST, TBM>(a.sh_a, a.sh_b, a.H, a.src, a.H, rowoff, (int)rows, yb, xs, epi);
     } else {
         const GuEpi epi{a.act, a.M, (int)first, (int)rows};
         tile_run<RF, 2, GU_RPW, Shape<TBM>::DEPTH, NST, TBM>(a.wa + (size_t)e * a.stride_a, a.wb + (size_t)e * a.stride_b, a.H, a.src,
@@ -799,7 +863,7 @@ __global__ __launch_bounds__(Shape<TBM>::W * 64) void k_gemm_gate_up(GemmArgs a)
 
 template <int EFMT, int SFMT, int NST, int TBM>
 __global__ __launch_bounds__(Shape<TBM>::W * 64) void k_gemm_down(GemmArgs a) {
-    __shared__ __attribute__((aligned(16))) _Float16 xs[2 * TBM * 16 * BLD];
+    __shared__ __attribute__((aligned(16))) _Float16 xs[2 * Shape<TBM>::XR * BLD];
     __shared__ int rowoff[TBM * 16];
     int ti, yb;
     block_tile(a.nyb, ti, yb);
@@ -834,9 +898,9 @@ __global__ __launch_bounds__(Shape<TBM>::W * 64) void k_gemm_down(GemmArgs a) {
 #endif
 template <int TBM, int GF>
 DEV void k_gemm_gate_up_p_body(GemmArgs a) {
-    __shared__ __attribute__((aligned(16))) _Float16 xs[3 * TBM * 16 * BLD];
+    __shared__ __attribute__((aligned(16))) _Float16 xs[3 * Shape<TBM>::XR * BLD];
     __shared__ int rowoff[3 * TBM * 16];
-    tile_stream<GF, 2, GU_RPW, (GF == FQ8 ? 2 : Shape<TBM>::DEPTH), 16, TBM>(GuPol{a}, xs, rowoff);
+    tile_stream<GF, 2, GU_RPW, (GF == FQ8 || GF == FQ8T ? 2 : Shape<TBM>::DEPTH), 16, TBM>(GuPol{a}, xs, rowoff);
 }
 
 template <int TBM, int GF>
@@ -848,7 +912,7 @@ __global__ __launch_bounds__(Shape<TBM>::W * 64) void k_gemm_gate_up_p(GemmArgs 
 
 template <int EFMT, int TBM>
 __global__ __launch_bounds__(Shape<TBM>::W * 64) void k_gemm_down_p(GemmArgs a) {
-    __shared__ __attribute__((aligned(16))) _Float16 xs[3 * TBM * 16 * BLD];
+    __shared__ __attribute__((aligned(16))) _Float16 xs[3 * Shape<TBM>::XR * BLD];
     __shared__ int rowoff[3 * TBM * 16];
     tile_stream<EFMT, 1, DN_RPW, Shape<TBM>::DEPTH, 4, TBM>(DnPol{a}, xs, rowoff);
 }
@@ -885,8 +949,10 @@ static int gate_up_shape(const ExpertSide &ex, const SharedSide &sh, int H, int 
     const int NB = W * 16 * GU_RPW;
     if ((H / KC * GU_RPW) % 4) return -2; /* every ring depth used divides the unit count */
     if (H % KCH || M % NB || (sh.gate && sh.S % NB) || (ex.gate_fmt != FQ4K && ex.gate_fmt != FQ4KT)) return -2;
-    /* shared expert: the routed format, or Q8_0 (row-major) */
-    if (sh.gate && sh.gate_fmt != ex.gate_fmt && sh.gate_fmt != FQ8) return -2;
+    /* shared expert: the routed format, or Q8_0 (row-major, or tile-major
+     * beside tile-major routed matrices) */
+    if (sh.gate && sh.gate_fmt != ex.gate_fmt && sh.gate_fmt != FQ8 && !(sh.gate_fmt == FQ8T && ex.gate_fmt == FQ4KT))
+        return -2;
     return 0;
 }
 static int down_shape(const ExpertSide &ex, const SharedSide &sh, int H, int M, int tile_m) {
@@ -895,14 +961,14 @@ static int down_shape(const ExpertSide &ex, const SharedSide &sh, int H, int M, 
     if ((M / KC * DN_RPW) % 4 || (sh.gate && (sh.S / KC * DN_RPW) % 4)) return -2;
     /* all of a tile's activations stay resident: in_dim <= 2 chunks */
     if (H % NB || M % KCH || M > 2 * KCH || (sh.gate && (sh.S % KCH || sh.S > 2 * KCH))) return -2;
-    const bool dtiled = ex.down_fmt == FQ4KT || ex.down_fmt == FQ6KT;
+    const bool dtiled = ex.down_fmt == FQ4KT || ex.down_fmt == FQ5KT || ex.down_fmt == FQ6KT || ex.down_fmt == FQ8T;
     /* (a Q8_0 routed down only reaches here from the weight read-back debug
      * entry; the forward rejects it) */
     if (ex.down_fmt != FQ4K && ex.down_fmt != FQ5K && ex.down_fmt != FQ6K && ex.down_fmt != FQ8 && !dtiled) return -2;
-    /* shared down: any supported format; with a tile-major routed down a
-     * Q4_K/Q6_K shared down must be tile-major too (the packer makes both) */
+    /* shared down: any supported format, tile-major beside a tile-major
+     * routed down (the packer makes both) */
     const int sf = sh.gate ? sh.down_fmt : ex.down_fmt;
-    if (dtiled ? sf != FQ4KT && sf != FQ6KT && sf != FQ5K && sf != FQ8
+    if (dtiled ? sf != FQ4KT && sf != FQ5KT && sf != FQ6KT && sf != FQ8T
                : sf != FQ4K && sf != FQ5K && sf != FQ6K && sf != FQ8)
         return -2;
     return 0;
@@ -937,7 +1003,7 @@ int launch_gemm_gate_up(const ExpertSide &ex, const SharedSide &sh, const _Float
     a.tiles = tiles; a.pairs = pairs; a.act = act; a.act_sh = act_sh;
     a.nyb = (M > a.S ? M : a.S) / NB;
     const dim3 grid((unsigned)((n_tiles_max + 7) / 8 * 8 * a.nyb)), block(W * 64);
-    const bool q8 = sh.gate && sh.gate_fmt == FQ8;
+    const bool q8 = sh.gate && (sh.gate_fmt == FQ8 || sh.gate_fmt == FQ8T);
     const unsigned pb = !GEMM_PERSIST || tile_m == GEMM_TILE_MIN ? 0u
                         : tile_m == GEMM_TILE_BIG ? persist_blocks() : GEMM_PERSIST_SMALL * persist_blocks();
     a.kt = kt && (long)grid.x <= kt_cap ? kt : nullptr;
@@ -956,7 +1022,8 @@ int launch_gemm_gate_up(const ExpertSide &ex, const SharedSide &sh, const _Float
             as.kt = nullptr;
             if (tiled) GP_LAUNCH(FQ4KT, ar);
             else GP_LAUNCH(FQ4K, ar);
-            GP_LAUNCH(FQ8, as);
+            if (sh.gate_fmt == FQ8T) GP_LAUNCH(FQ8T, as);
+            else GP_LAUNCH(FQ8, as);
         } else if (tiled) {
             GP_LAUNCH(FQ4KT, a);
         } else {
@@ -974,7 +1041,10 @@ int launch_gemm_gate_up(const ExpertSide &ex, const SharedSide &sh, const _Float
         else KLAUNCH((k_gemm_gate_up<RF, SF, NS, GEMM_TILE_BIG / 16>), grid, block, 0, s, a);              \
     } while (0)
     if (tiled) {
-        if (q8) GU_LAUNCH(FQ4KT, FQ8, 0);
+        if (sh.gate && sh.gate_fmt == FQ8T) {
+            if (H == 2048) GU_LAUNCH(FQ4KT, FQ8T, 16);
+            else GU_LAUNCH(FQ4KT, FQ8T, 0);
+        } else if (q8) GU_LAUNCH(FQ4KT, FQ8, 0);
         else if (H == 2048) GU_LAUNCH(FQ4KT, FQ4KT, 16);
         else GU_LAUNCH(FQ4KT, FQ4KT, 0);
     } else if (q8) GU_LAUNCH(FQ4K, FQ8, 0);
@@ -1011,6 +1081,8 @@ int launch_gemm_down(const ExpertSide &ex, const SharedSide &sh, const _Float16 
         else if ((F) == FQ4KT) KLAUNCH((k_gemm_down_p<FQ4KT, TB>), dim3(pb), block, 0, s, ARGS);             \
         else if ((F) == FQ6KT) KLAUNCH((k_gemm_down_p<FQ6KT, TB>), dim3(pb), block, 0, s, ARGS);             \
         else if ((F) == FQ8) KLAUNCH((k_gemm_down_p<FQ8, TB>), dim3(pb), block, 0, s, ARGS);                 \
+        else if ((F) == FQ8T) KLAUNCH((k_gemm_down_p<FQ8T, TB>), dim3(pb), block, 0, s, ARGS);               \
+        else if ((F) == FQ5KT) KLAUNCH((k_gemm_down_p<FQ5KT, TB>), dim3(pb), block, 0, s, ARGS);             \
         else if ((F) == FQ5K) KLAUNCH((k_gemm_down_p<FQ5K, TB>), dim3(pb), block, 0, s, ARGS);               \
         else KLAUNCH((k_gemm_down_p<FQ6K, TB>), dim3(pb), block, 0, s, ARGS);                                \
     } while (0)
@@ -1032,7 +1104,7 @@ int launch_gemm_down(const ExpertSide &ex, const SharedSide &sh, const _Float16 
 #undef DP_LAUNCH
         return hipGetLastError() == hipSuccess ? 0 : -3;
     }
-    if (ex.down_fmt == FQ8) return -2; /* persistent kernels only */
+    if (ex.down_fmt == FQ8 || ex.down_fmt == FQ8T) return -2; /* persistent kernels only */
     /* generic unit loop (a compile-time stage count spills here) */
 #define DN_LAUNCH(EF, SF)                                                                    \
     do {                                                                                     \
@@ -1040,16 +1112,19 @@ int launch_gemm_down(const ExpertSide &ex, const SharedSide &sh, const _Float16 
         else if (tile_m == GEMM_TILE_MIN) KLAUNCH((k_gemm_down<EF, SF, 0, GEMM_TILE_MIN / 16>), grid, block, 0, s, a); \
         else KLAUNCH((k_gemm_down<EF, SF, 0, GEMM_TILE_BIG / 16>), grid, block, 0, s, a);              \
     } while (0)
+#define DN_TILED(EF)                                \
+    do {                                            \
+        if (sf == FQ4KT) DN_LAUNCH(EF, FQ4KT);      \
+        else if (sf == FQ5KT) DN_LAUNCH(EF, FQ5KT); \
+        else if (sf == FQ6KT) DN_LAUNCH(EF, FQ6KT); \
+        else DN_LAUNCH(EF, FQ8T);                   \
+    } while (0)
     if (ex.down_fmt == FQ4KT) {
-        if (sf == FQ4KT) DN_LAUNCH(FQ4KT, FQ4KT);
-        else if (sf == FQ6KT) DN_LAUNCH(FQ4KT, FQ6KT);
-        else if (sf == FQ5K) DN_LAUNCH(FQ4KT, FQ5K);
-        else DN_LAUNCH(FQ4KT, FQ8);
+        DN_TILED(FQ4KT);
+    } else if (ex.down_fmt == FQ5KT) {
+        DN_TILED(FQ5KT);
     } else if (ex.down_fmt == FQ6KT) {
-        if (sf == FQ4KT) DN_LAUNCH(FQ6KT, FQ4KT);
-        else if (sf == FQ6KT) DN_LAUNCH(FQ6KT, FQ6KT);
-        else if (sf == FQ5K) DN_LAUNCH(FQ6KT, FQ5K);
-        else DN_LAUNCH(FQ6KT, FQ8);
+        DN_TILED(FQ6KT);
     } else if (ex.down_fmt == FQ4K) {
         if (sf == FQ4K) DN_LAUNCH(FQ4K, FQ4K);
         else if (sf == FQ5K) DN_LAUNCH(FQ4K, FQ5K);
@@ -1066,6 +1141,7 @@ int launch_gemm_down(const ExpertSide &ex, const SharedSide &sh, const _Float16 
         else if (sf == FQ6K) DN_LAUNCH(FQ6K, FQ6K);
         else DN_LAUNCH(FQ6K, FQ8);
     }
+#undef DN_TILED
 #undef DN_LAUNCH
     return hipGetLastError() == hipSuccess ? 0 : -3;
 }
@@ -1101,6 +1177,41 @@ int launch_pack_q4k(const uint8_t *src, uint8_t *dst, int R, int K, int E, size_
     if (R % 16 || K % 256 || E < 1 || ((uintptr_t)src & 15) || ((uintptr_t)dst & 15) || (src_stride & 15)) return -2;
     const int nsb = K / 256;
     KLAUNCH(k_pack_q4k, dim3((unsigned)(R / 16 * nsb), (unsigned)E), dim3(144), 0, s, src, dst, R, nsb, src_stride);
+    return hipGetLastError() == hipSuccess ? 0 : -3;
+}
+
+/* Q5_K matrices [R rows][K/256 super-blocks of 176 B] into the tile-major
+ * layout of Span<FQ5KT>: tile (rb, sb) at (rb * nsb + sb) * 2816, whose
+ * 16-byte piece o holds row o's header (o < 16), for o = 16 + 64 jj + 16 kg +
+ * i bytes 48 + 16 (kg + 4 jj) .. +15 of row i, and for o = 144 + 16 g + i
+ * bytes 16 + 16 g .. +15 (qh) of row i.  A byte permutation. */
+__global__ __launch_bounds__(176) void k_pack_q5k(const uint8_t *src, uint8_t *dst, int R, int nsb, size_t src_stride) {
+    const int tile = blockIdx.x, e = blockIdx.y, rb = tile / nsb, sb = tile - rb * nsb, o = threadIdx.x;
+    const size_t rbytes = (size_t)nsb * 176;
+    const uint8_t *t0 = src + (size_t)e * src_stride + (size_t)rb * 16 * rbytes + (size_t)sb * 176;
+    int row, off;
+    if (o < 16) {
+        row = o;
+        off = 0;
+    } else if (o < 144) {
+        const int qo = o - 16, jj = qo >> 6, ln = qo & 63;
+        row = ln & 15;
+        off = 48 + 16 * ((ln >> 4) + 4 * jj);
+    } else {
+        const int x = o - 144;
+        row = x & 15;
+        off = 16 + 16 * (x >> 4);
+    }
+    const u4 v = ld_u4(t0 + (size_t)row * rbytes + off);
+    *(u4 *)(dst + (size_t)e * R * rbytes + (size_t)tile * 2816 + (size_t)o * 16) = v;
+}
+
+size_t packed_q5k_bytes(int R, int K, int E) { return (size_t)E * R * (K / 256) * 176; }
+
+int launch_pack_q5k(const uint8_t *src, uint8_t *dst, int R, int K, int E, size_t src_stride, hipStream_t s) {
+    if (R % 16 || K % 256 || E < 1 || ((uintptr_t)src & 15) || ((uintptr_t)dst & 15) || (src_stride & 15)) return -2;
+    const int nsb = K / 256;
+    KLAUNCH(k_pack_q5k, dim3((unsigned)(R / 16 * nsb), (unsigned)E), dim3(176), 0, s, src, dst, R, nsb, src_stride);
     return hipGetLastError() == hipSuccess ? 0 : -3;
 }
 
@@ -1141,6 +1252,43 @@ __global__ __launch_bounds__(256) void k_pack_q6k(const uint8_t *src, uint8_t *d
 }
 
 size_t packed_q6k_bytes(int R, int K, int E) { return (size_t)E * R * (K / 256) * 210; }
+
+/* Q8_0 matrices [R rows][K/32 blocks of 34 B] into the tile-major layout of
+ * Span<FQ8T> (a byte permutation, moved in 16-bit words: source blocks are
+ * 2-byte aligned).  Output byte ob of tile (rb, stage j):
+ *   ob < 2048: lane ln = ob / 32 (kg = ln / 16, row i = ln % 16), step s = ob % 32 / 8:
+ *              byte 2 + 8 kg + ob % 8 of row i's block 4j + s
+ *   else:      row i = (ob - 2048) / 8, block 4j + (ob % 8) / 2: byte ob % 2 (the scale) */
+__global__ __launch_bounds__(256) void k_pack_q8(const uint8_t *src, uint8_t *dst, int R, int nst, size_t src_stride) {
+    const int tile = blockIdx.x, e = blockIdx.y, rb = tile / nst, j = tile - rb * nst;
+    const size_t rbytes = (size_t)nst * 4 * 34;
+    const uint8_t *t0 = src + (size_t)e * src_stride + (size_t)rb * 16 * rbytes + (size_t)j * 4 * 34;
+    uint8_t *d0 = dst + (size_t)e * R * rbytes + (size_t)tile * 2176;
+    for (int w = threadIdx.x; w < 1088; w += 256) {
+        const int ob = 2 * w;
+        int row, byte;
+        if (ob < 2048) {
+            const int ln = ob >> 5, st = (ob & 31) >> 3;
+            row = ln & 15;
+            byte = st * 34 + 2 + 8 * (ln >> 4) + (ob & 7);
+        } else {
+            const int x = ob - 2048;
+            row = x >> 3;
+            byte = ((x & 7) >> 1) * 34;
+        }
+        *(uint16_t *)(d0 + ob) = *(const uint16_t *)(t0 + (size_t)row * rbytes + byte);
+    }
+}
+
+size_t packed_q8_bytes(int R, int K, int E) { return (size_t)E * R * (K / 32) * 34; }
+
+int launch_pack_q8(const uint8_t *src, uint8_t *dst, int R, int K, int E, size_t src_stride, hipStream_t s) {
+    if (R % 16 || K % 128 || E < 1 || ((uintptr_t)src & 1) || ((uintptr_t)dst & 15) || (src_stride & 1)) return -2;
+    const int nst = K / 128;
+    KLAUNCH(k_pack_q8, dim3((unsigned)(R / 16 * nst), (unsigned)E), dim3(256), 0, s, src, dst, R, nst, src_stride);
+    return hipGetLastError() == hipSuccess ? 0 : -3;
+}
+
 
 int launch_pack_q6k(const uint8_t *src, uint8_t *dst, int R, int K, int E, size_t src_stride, hipStream_t s) {
     if (R % 16 || K % 256 || E < 1 || ((uintptr_t)src & 1) || ((uintptr_t)dst & 15) || (src_stride & 1)) return -2;

@@ -177,12 +177,14 @@ def test_tile_major_copies_bit_identical(base):
 
 
 def test_tile_major_q6k_down_and_q8_shared():
-    """Q6_K down projections get tile-major Q6_K copies (routed only, and
-    routed + shared); layers with a Q8_0 shared expert are left row-major.
-    Each matches the oracle and its unpacked run bit for bit."""
-    banner("tile-major copies: Q6_K down / Q8_0 shared")
+    """Q6_K and Q5_K down projections get tile-major copies (routed only, and
+    routed + shared); a Q8_0 shared expert gets tile-major Q8_0 copies of its
+    gate, up and down.  Each matches the oracle and its unpacked run bit for
+    bit."""
+    banner("tile-major copies: Q6_K / Q5_K down, Q8_0 shared")
     for kw, T in ((dict(down=14, seed=36), 300), (dict(down=14, shared_down=14, seed=38), 96),
-                  (dict(shared=8, seed=37), 64)):
+                  (dict(shared=8, seed=37), 64), (dict(down=13, shared_down=13, seed=39), 200),
+                  (dict(down=13, shared=8, E=32, seed=40), 300)):
         p = Pair(max_tokens=T, **kw)
         out, _ = run_and_check(p, T, seed=1700 + T, path=_lib.OROME_PATH_MFMA)
         p.gm.unpack()
@@ -299,10 +301,10 @@ def test_small_batch_path_edges(kw, T, K):
 @pytest.mark.parametrize("T", [12, 512, 2048])
 def test_q8_shared_expert_registered(T):
     """The reference's 35B layout: a Q8_0 shared expert (gate, up and down).
-    Registration now repacks the routed matrices and the router even so, and
-    the grouped GEMMs read the Q8_0 shared expert row-major beside the
-    tile-major routed copies (T=2048: persistent kernels, one walk over the
-    routed tiles and one over the shared).  Routing bit-exact, output within
+    Registration repacks the routed matrices, the router and the Q8_0 shared
+    matrices (tile-major Q8_0), and the grouped GEMMs read them (T=2048:
+    persistent kernels, one walk over the routed tiles and one over the
+    shared).  Routing bit-exact, output within
     tolerance of the oracle and bit-identical to the unregistered layer; at
     T=512 the two-pass router runs (some non-winning logits are its
     approximations, not the canonical values)."""
@@ -379,8 +381,8 @@ def mfma_weights_model(fmt_blocks):
     return f16(q * d[:, None]).reshape(rows, cols)
 
 
-@pytest.mark.parametrize("fmt,tiled", [("Q4_K", 0), ("Q4_K", 1), ("Q5_K", 0), ("Q6_K", 0), ("Q6_K", 1),
-                                       ("Q8_0", 0)])
+@pytest.mark.parametrize("fmt,tiled", [("Q4_K", 0), ("Q4_K", 1), ("Q5_K", 0), ("Q5_K", 1), ("Q6_K", 0), ("Q6_K", 1),
+                                       ("Q8_0", 0), ("Q8_0", 1)])
 def test_mfma_fp16_weights_bit_exact(fmt, tiled):
     """The fp16 weights the matrix cores multiply (read back through the real
     grouped down GEMM with one-hot activations, orome_debug_mfma_weights)
