@@ -898,6 +898,7 @@ __global__ __launch_bounds__(Shape<TBM>::W * 64) void k_gemm_down(GemmArgs a) {
 #endif
 template <int TBM, int GF>
 DEV void k_gemm_gate_up_p_body(GemmArgs a) {
+    static_assert(TBM >= 2, "persistent kernels take 32- and 80-row tiles");
     __shared__ __attribute__((aligned(16))) _Float16 xs[3 * Shape<TBM>::XR * BLD];
     __shared__ int rowoff[3 * TBM * 16];
     tile_stream<GF, 2, GU_RPW, (GF == FQ8 || GF == FQ8T ? 2 : Shape<TBM>::DEPTH), 16, TBM>(GuPol{a}, xs, rowoff);
@@ -912,6 +913,8 @@ __global__ __launch_bounds__(Shape<TBM>::W * 64) void k_gemm_gate_up_p(GemmArgs 
 
 template <int EFMT, int TBM>
 __global__ __launch_bounds__(Shape<TBM>::W * 64) void k_gemm_down_p(GemmArgs a) {
+    /* the launchers send 16-row tile lists (T <= 16) to the per-tile kernels */
+    static_assert(TBM >= 2, "persistent kernels take 32- and 80-row tiles");
     __shared__ __attribute__((aligned(16))) _Float16 xs[3 * Shape<TBM>::XR * BLD];
     __shared__ int rowoff[3 * TBM * 16];
     tile_stream<EFMT, 1, DN_RPW, Shape<TBM>::DEPTH, 4, TBM>(DnPol{a}, xs, rowoff);
