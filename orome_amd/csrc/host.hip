@@ -591,11 +591,13 @@ static int forward_impl(orome_hip_ctx *c, const OromeHipModelConfig *cfg, const 
             a.tiles_s = c->tiles;
             a.has_shared = S ? 1 : 0;
         }
-        TLAUNCH(c, ST_ROUTE, launch_route_small(a, s), "router logits");
         /* one or two tokens: every gate/up block selects the experts itself
-         * (saves a launch); larger batches route once in a separate kernel */
-        const int fold = T <= 2;
-        if (!fold) TLAUNCH(c, ST_TOPK, launch_topk_dispatch_small(a, s), "top-k + dispatch");
+         * (saves a launch); larger batches route once, in the router
+         * kernel's last block where the shapes allow, else in a kernel of
+         * its own */
+        const int fold = T <= 2, rfold = !fold && route_small_folds(a);
+        TLAUNCH(c, ST_ROUTE, launch_route_small(a, s, rfold), rfold ? "router logits + top-k + dispatch" : "router logits");
+        if (!fold && !rfold) TLAUNCH(c, ST_TOPK, launch_topk_dispatch_small(a, s), "top-k + dispatch");
         if (hybrid) {
             /* every expert holds at most 16 rows: the grouped GEMMs alone
              * (gate/up on 16-row tiles; down keeps the persistent 32-row

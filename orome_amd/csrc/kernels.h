@@ -81,7 +81,10 @@ struct SharedSide {
     int S;
 };
 
-int launch_route_small(const RouteArgs &a, hipStream_t s);
+/* fold_topk: the router's last block also runs the top-k and dispatch of
+ * launch_topk_dispatch_small (when route_small_folds(a)) */
+int launch_route_small(const RouteArgs &a, hipStream_t s, int fold_topk = 0);
+int route_small_folds(const RouteArgs &a);
 int launch_route_logits(const RouteArgs &a, hipStream_t s);
 int launch_topk(const RouteArgs &a, hipStream_t s);
 int launch_route_approx(const RouteArgs &a, hipStream_t s);

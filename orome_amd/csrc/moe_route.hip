@@ -27,19 +27,42 @@
 /* RS waves per row: wave h of a row takes tokens h TMAX .. h TMAX + TMAX - 1
  * (5..8 tokens: two waves of 4, 9..16: four, instead of one wave with
  * dependent 4-token chunks). */
-template <bool NORM, int TMAX, int NIM, int RS>
-__global__ __launch_bounds__(256) void k_route_small(RouteArgs a) {
+/* FOLD (> 0: the EPL of the selection): the block that finishes last also
+ * runs the top-k and the dispatch for every token (topk_dispatch_block),
+ * which saves a launch.  The logits cross blocks with device-coherent stores
+ * and loads: each wave drains its stores before the block counts itself on
+ * a.counter, and the last block reads them back coherently and returns the
+ * counter to zero for the next launch. */
+template <bool NORM, int TMAX, int NIM, int RS, int FOLD>
+__global__ __launch_bounds__(FOLD ? 512 : 256) void k_route_small(RouteArgs a) {
+    constexpr int W = FOLD ? 8 : 4; /* waves: the folding block selects with 8 */
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-    const int row = blockIdx.x * (4 / RS) + wv / RS, tb = (wv % RS) * TMAX;
+    const int row = blockIdx.x * (W / RS) + wv / RS, tb = (wv % RS) * TMAX;
     const int E = a.E, H = a.H, T = a.T;
-    if (row > E || tb >= T) return;
-    const float *wr = row < E ? a.W + (size_t)row * H : a.wsg;
-    float acc[TMAX];
-    canon_dots<TMAX, NIM, NORM>(wr, a, lane, (NORM || a.x16) && row == 0, acc, tb);
-    if (lane == 0) {
+    if (row <= E && tb < T) {
+        const float *wr = row < E ? a.W + (size_t)row * H : a.wsg;
+        float acc[TMAX];
+        canon_dots<TMAX, NIM, NORM>(wr, a, lane, (NORM || a.x16) && row == 0, acc, tb);
+        if (lane == 0) {
 #pragma unroll
-        for (int t = 0; t < TMAX; t++)
-            if (tb + t < T) a.logits[(size_t)(tb + t) * (E + 1) + row] = acc[t];
+            for (int t = 0; t < TMAX; t++)
+                if (tb + t < T) {
+                    float *o = a.logits + (size_t)(tb + t) * (E + 1) + row;
+                    if (FOLD) st_coh(o, acc[t]);
+                    else *o = acc[t];
+                }
+        }
+    }
+    if constexpr (FOLD > 0) {
+        __shared__ int last;
+        drain_mem();
+        __syncthreads();
+        if (threadIdx.x == 0)
+            last = __hip_atomic_fetch_add(a.counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == gridDim.x - 1;
+        __syncthreads();
+        if (!last) return;
+        topk_dispatch_block<FOLD, true>(a);
+        if (threadIdx.x == 0) __hip_atomic_store(a.counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 }
 
@@ -749,13 +772,22 @@ static int epl_for(int E) {
         default: return -2;                                               \
     }
 
-int launch_route_small(const RouteArgs &a, hipStream_t s) {
+int route_small_folds(const RouteArgs &a) {
+    return a.T >= 1 && a.T <= 16 && a.T * a.K <= 256 && a.H % 256 == 0 && a.H <= 256 * 8 && epl_for(a.E) == 4;
+}
+
+int launch_route_small(const RouteArgs &a, hipStream_t s, int fold_topk) {
     if (a.T < 1 || a.T > 16 || a.T * a.K > 256 || a.H % 256 || a.H > 4096) return -2;
+    if (fold_topk && !route_small_folds(a)) return -2;
     const dim3 g((a.E + 1 + 3) / 4), g2((a.E + 1 + 1) / 2), g4((unsigned)(a.E + 1));
 #define RS_LAUNCH(TM, NIMV, RSV, G)                                                                      \
     do {                                                                                                 \
-        if (a.norm_h) KLAUNCH((k_route_small<true, TM, NIMV, RSV>), G, dim3(256), 0, s, a);  \
-        else KLAUNCH((k_route_small<false, TM, NIMV, RSV>), G, dim3(256), 0, s, a);          \
+        if (fold_topk && NIMV == 8) {                                                                    \
+            const dim3 gf((unsigned)((a.E + 1 + 8 / (RSV) - 1) / (8 / (RSV))));                          \
+            if (a.norm_h) KLAUNCH((k_route_small<true, TM, 8, RSV, 4>), gf, dim3(512), 0, s, a);         \
+            else KLAUNCH((k_route_small<false, TM, 8, RSV, 4>), gf, dim3(512), 0, s, a);                 \
+        } else if (a.norm_h) KLAUNCH((k_route_small<true, TM, NIMV, RSV, 0>), G, dim3(256), 0, s, a);    \
+        else KLAUNCH((k_route_small<false, TM, NIMV, RSV, 0>), G, dim3(256), 0, s, a);                   \
     } while (0)
 #define RS_T(NIMV)                                \
     do {                                          \

@@ -140,30 +140,32 @@ DEV uint32_t block_excl_scan256(uint32_t v, uint32_t *wsum /* LDS [4] */, uint32
         const uint32_t o = (uint32_t)__shfl_up((int)inc, off, 64);
         if (lane >= off) inc += o;
     }
-    if (lane == 63) wsum[wv] = inc;
+    if (lane == 63 && wv < 4) wsum[wv] = inc;
     __syncthreads();
     uint32_t base = 0;
-    for (int w = 0; w < wv; w++) base += wsum[w];
+    for (int w = 0; w < min(wv, 4); w++) base += wsum[w];
     *total = wsum[0] + wsum[1] + wsum[2] + wsum[3];
     return base + inc - v;
 }
 
-/* Small-batch selection and dispatch (T*K <= 256) by one block of 256
- * threads: a wave per token for the top-k, then the stable counting sort of
+/* Small-batch selection and dispatch (T*K <= 256) by one block of 256 or
+ * more threads (the first 256 count and scan; threads past them only take
+ * part in the selection): a wave per token for the top-k, then the stable
+ * counting sort of
  * the T*K pairs by expert.  Each expert keeps an LDS membership mask over
  * the pairs (8 words); its popcount is the expert's count, a block scan of
  * the counts gives the offsets and the active-expert ranks, and a pair's
  * rank inside its expert is the popcount of the mask below it. */
 template <int EPL, bool COH>
 DEV void topk_dispatch_block(const RouteArgs &a) {
-    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, tid = threadIdx.x;
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, tid = threadIdx.x, nw = (int)(blockDim.x >> 6);
     const int E = a.E, T = a.T, K = a.K, NP = T * K;
     __shared__ int s_e[256];
     __shared__ uint32_t mask[64 * EPL * 8]; /* experts (< 64 EPL) x 8 words of pair bits */
     __shared__ uint32_t eoff[64 * EPL];
     __shared__ uint32_t wsum[4];
-    for (int i = tid; i < 64 * EPL * 8; i += 256) mask[i] = 0;
-    for (int t = wv; t < T; t += 4)
+    for (int i = tid; i < 64 * EPL * 8; i += (int)blockDim.x) mask[i] = 0;
+    for (int t = wv; t < T; t += nw)
         wave_topk<EPL, COH>(a.logits + (size_t)t * (E + 1), a.bias, E, K, lane, a.idx + t * K,
                             a.w + t * K, a.sgl + t, s_e + t * K);
     __syncthreads();
