@@ -92,7 +92,7 @@ static size_t scratch_layout(orome_hip_ctx *c, uint8_t *base) {
     const size_t T = (size_t)c->tmax, E = (size_t)cfg->num_experts, K = (size_t)c->kmax,
                  H = (size_t)cfg->hidden_dim, M = (size_t)cfg->moe_intermediate,
                  S = (size_t)(cfg->shared_intermediate > 0 ? cfg->shared_intermediate : 0);
-    const size_t ntile_s = E + T / GEMM_TILE_SMALL + 2, ntile_b = (T * K) / GEMM_TILE_BIG + E + T / GEMM_TILE_BIG + 2;
+    const size_t ntile_s = 2 * E + T / GEMM_TILE_SMALL + 2, ntile_b = (T * K) / GEMM_TILE_BIG + E + T / GEMM_TILE_BIG + 2;
     struct { void **p; size_t bytes; } parts[] = {
         {(void **)&c->logits, T * (E + 1) * 4}, {(void **)&c->idx, T * K * 4},
         {(void **)&c->w, T * K * 4},           {(void **)&c->sgl, T * 4},
@@ -652,8 +652,11 @@ static int forward_impl(orome_hip_ctx *c, const OromeHipModelConfig *cfg, const 
         }
         TLAUNCH(c, ST_DISPATCH, launch_dispatch(a, c->tiles, c->tiles_b, S ? 1 : 0, c->dcount, s), "dispatch");
         /* one launch per tile list (grid sized for the most tiles it can hold) */
+        /* small batches (T K <= 32 E): every expert in 32-row tiles, the
+         * shared expert too, and no big-tile list */
         const bool sh_small = (long)T * K <= (long)GEMM_TILE_SMALL * E;
-        const int ns_max = E + (S && sh_small ? (T + GEMM_TILE_SMALL - 1) / GEMM_TILE_SMALL : 0),
+        const int ns_max = E + (sh_small ? (T * K) / GEMM_TILE_SMALL : 0) +
+                           (S && sh_small ? (T + GEMM_TILE_SMALL - 1) / GEMM_TILE_SMALL : 0),
                   nb_max = (T * K) / GEMM_TILE_BIG + E + (S && !sh_small ? (T + GEMM_TILE_BIG - 1) / GEMM_TILE_BIG : 0);
         /* registered layers: the grouped GEMMs read the tile-major copies */
         ExpertSide exm = ex;
@@ -673,7 +676,10 @@ static int forward_impl(orome_hip_ctx *c, const OromeHipModelConfig *cfg, const 
                        : launch_gemm_down(exm, shm, c->act, c->act_sh, c->tmax * c->kmax, c->tmax, T, H, M, K, E, tm, c->tiles_b, nb_max, c->y,
                                           c->ysh, st);
         };
-        if (c->timing || !c->side) { /* per-stage timing (or no side stream): both lists in order on one stream */
+        if (sh_small) { /* one list */
+            TLAUNCH(c, ST_GATE_UP, gate_up(GEMM_TILE_SMALL, s), "grouped gate/up");
+            TLAUNCH(c, ST_DOWN, down(GEMM_TILE_SMALL, s), "grouped down");
+        } else if (c->timing || !c->side) { /* per-stage timing (or no side stream): both lists in order on one stream */
             TLAUNCH(c, ST_GATE_UP, (gate_up(GEMM_TILE_SMALL, s) ? -3 : gate_up(GEMM_TILE_BIG, s)), "grouped gate/up");
             TLAUNCH(c, ST_DOWN, (down(GEMM_TILE_SMALL, s) ? -3 : down(GEMM_TILE_BIG, s)), "grouped down");
         } else {

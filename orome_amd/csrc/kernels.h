@@ -161,9 +161,10 @@ int launch_zero(void *p, size_t bytes, hipStream_t s);
 /* tile list for the grouped GEMM: tiles[0] = count, then (expert, first, rows)
  * triples; expert == E denotes the shared expert over all T tokens */
 /* two tile lists per call: experts with <= GEMM_TILE_SMALL rows (one small
- * tile each) and the rest in tiles of GEMM_TILE_BIG rows; the shared expert
- * joins the small list when T*K <= GEMM_TILE_SMALL*E.  Capacities: small
- * E + T/SMALL + 1, big T*K/BIG + E + T/BIG + 1. */
+ * tile each) and the rest in tiles of GEMM_TILE_BIG rows; while T*K <=
+ * GEMM_TILE_SMALL*E every expert is cut into small tiles and the shared
+ * expert joins the small list (the big list is empty).  Capacities: small
+ * 2E + T/SMALL + 1, big T*K/BIG + E + T/BIG + 1. */
 #define GEMM_TILE_SMALL 32
 /* 16-row tiles for lists whose experts hold at most 16 rows (the small-batch
  * path: T <= 16); per-tile kernels only */

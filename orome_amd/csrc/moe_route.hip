@@ -544,9 +544,18 @@ DEV void block_scan4(uint32_t *a, uint32_t *b, uint32_t *c, uint32_t *d, int n) 
 }
 
 /* Tiles of one expert: rows <= GEMM_TILE_SMALL -> one small tile, else
- * ceil(rows / GEMM_TILE_BIG) big tiles. */
-DEV uint32_t n_small_tiles(uint32_t c) { return c != 0 && c <= GEMM_TILE_SMALL; }
-DEV uint32_t n_big_tiles(uint32_t c) { return c > GEMM_TILE_SMALL ? (c + GEMM_TILE_BIG - 1) / GEMM_TILE_BIG : 0; }
+ * ceil(rows / GEMM_TILE_BIG) big tiles.  While the batch is small (T K <=
+ * GEMM_TILE_SMALL E, tile_small_only) every expert is cut into small tiles:
+ * the few big experts of a skewed routing would otherwise leave most CUs
+ * idle in a big-tile launch of their own, and the shared expert is in the
+ * small list then anyway (the host launches only that list). */
+DEV bool tile_small_only(const RouteArgs &a) { return (size_t)a.T * a.K <= (size_t)GEMM_TILE_SMALL * a.E; }
+DEV uint32_t n_small_tiles(uint32_t c, bool so) {
+    return so ? (c + GEMM_TILE_SMALL - 1) / GEMM_TILE_SMALL : c != 0 && c <= GEMM_TILE_SMALL;
+}
+DEV uint32_t n_big_tiles(uint32_t c, bool so) {
+    return !so && c > GEMM_TILE_SMALL ? (c + GEMM_TILE_BIG - 1) / GEMM_TILE_BIG : 0;
+}
 DEV void put_tiles(uint32_t *list, uint32_t t0, uint32_t e, uint32_t first, uint32_t c, uint32_t tm) {
     for (uint32_t j = 0; j * tm < c; j++) {
         list[1 + 3 * (t0 + j)] = e;
@@ -572,8 +581,10 @@ DEV void dispatch_lists(const RouteArgs &a, const uint32_t *hist, uint32_t *offs
             const uint32_t r = arank[tid] - 1;
             ACT_E(a.list, r) = (uint32_t)tid;
             ACT_OFF(a.list, E, r) = o;
-            if (c <= GEMM_TILE_SMALL) put_tiles(tiles_s, ts[tid] - 1, (uint32_t)tid, o, c, GEMM_TILE_SMALL);
-            else put_tiles(tiles_b, tbg[tid] - n_big_tiles(c), (uint32_t)tid, o, c, GEMM_TILE_BIG);
+            const bool so = tile_small_only(a);
+            if (c <= GEMM_TILE_SMALL || so)
+                put_tiles(tiles_s, ts[tid] - n_small_tiles(c, so), (uint32_t)tid, o, c, GEMM_TILE_SMALL);
+            else put_tiles(tiles_b, tbg[tid] - n_big_tiles(c, so), (uint32_t)tid, o, c, GEMM_TILE_BIG);
         }
     }
     if (tid == 0) {
@@ -584,7 +595,7 @@ DEV void dispatch_lists(const RouteArgs &a, const uint32_t *hist, uint32_t *offs
         /* the shared expert (id E) over tokens 0..T-1, in the list that holds
          * most of the routed work (a lone list of shared tiles would run as
          * a tail after the other launch) */
-        const bool sm = (size_t)T * a.K <= (size_t)GEMM_TILE_SMALL * E;
+        const bool sm = tile_small_only(a);
         const uint32_t tm = sm ? GEMM_TILE_SMALL : GEMM_TILE_BIG, nsh = has_shared ? (Tu + tm - 1) / tm : 0;
         if (has_shared) put_tiles(sm ? tiles_s : tiles_b, sm ? ns : nb, (uint32_t)E, 0, Tu, tm);
         tiles_s[0] = ns + (sm ? nsh : 0);
@@ -616,8 +627,8 @@ __global__ __launch_bounds__(DSP_THREADS) void k_dispatch_scan(RouteArgs a, uint
         hist[tid] = run;
         offs[tid] = run;
         arank[tid] = run != 0;
-        ts[tid] = n_small_tiles(run);
-        tbg[tid] = n_big_tiles(run);
+        ts[tid] = n_small_tiles(run, tile_small_only(a));
+        tbg[tid] = n_big_tiles(run, tile_small_only(a));
     }
     __syncthreads();
     dispatch_lists(a, hist, offs, arank, ts, tbg, tiles_s, tiles_b, has_shared);
@@ -692,8 +703,8 @@ __global__ __launch_bounds__(DSP_THREADS) void k_dispatch_one(RouteArgs a, uint3
         hist[tid] = run;
         offs[tid] = run;
         arank[tid] = run != 0;
-        ts[tid] = n_small_tiles(run);
-        tbg[tid] = n_big_tiles(run);
+        ts[tid] = n_small_tiles(run, tile_small_only(a));
+        tbg[tid] = n_big_tiles(run, tile_small_only(a));
     }
     __syncthreads();
     dispatch_lists(a, hist, offs, arank, ts, tbg, tiles_s, tiles_b, has_shared);
