@@ -267,5 +267,15 @@ DEV void st_coh(float *p, float v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, 
 DEV float ld_coh(const float *p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
 DEV void drain_mem() { __builtin_amdgcn_s_waitcnt(0); }
 
+/* Workgroup barrier ordering LDS only.  __syncthreads also makes the block's
+ * global stores visible to the block, so it first waits for every store in
+ * flight (a full memory round trip); blocks that exchange data through LDS
+ * alone and whose global stores are read only by later kernels use this. */
+DEV void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 /* ------------------------------------------------------------ dots */
 DEV float dot2(h2 a, h2 b, float c) { return __builtin_amdgcn_fdot2(a, b, c, false); }

@@ -510,11 +510,11 @@ DEV void dispatch_masks(const RouteArgs &a, uint32_t *mask, int (&ek)[KM]) {
 #pragma unroll
     for (int k = 0; k < KM; k++)
         if (k >= K || t >= a.T) ek[k] = -1;
-    __syncthreads();
+    lds_barrier();
 #pragma unroll
     for (int k = 0; k < KM; k++)
         if (ek[k] >= 0) atomicOr(&mask[ek[k] * DSP_WORDS + (tid >> 5)], 1u << (tid & 31));
-    __syncthreads();
+    lds_barrier();
 }
 
 template <int KM>
@@ -530,17 +530,40 @@ __global__ __launch_bounds__(DSP_TOK) void k_dispatch_count(RouteArgs a, uint32_
     }
 }
 
-/* Block-wide inclusive scan of four counters per expert (one thread per
- * expert, E <= DSP_THREADS), Hillis-Steele over LDS. */
-DEV void block_scan4(uint32_t *a, uint32_t *b, uint32_t *c, uint32_t *d, int n) {
-    const int tid = threadIdx.x;
-    for (int off = 1; off < n; off <<= 1) {
-        uint32_t va = 0, vb = 0, vc = 0, vd = 0;
-        if (tid < n && tid >= off) { va = a[tid - off]; vb = b[tid - off]; vc = c[tid - off]; vd = d[tid - off]; }
-        __syncthreads();
-        if (tid < n && tid >= off) { a[tid] += va; b[tid] += vb; c[tid] += vc; d[tid] += vd; }
-        __syncthreads();
+/* Inclusive scan of two words over threads 0..255 (the others pass zeros
+ * and read nothing back), with both totals: wave shuffles, then one
+ * barrier for the four wave sums (wsum: LDS, 8 words).  Every thread of the
+ * block calls it. */
+DEV void scan2_256(uint32_t &x, uint32_t &y, uint32_t *wsum, uint32_t &tx, uint32_t &ty) {
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    /* wave inclusive scan with DPP: shifts by 1, 2, 4, 8 inside each row of
+     * 16 lanes (lanes shifted in from outside the row add 0), then lane 15
+     * of each row into the next row, lane 31 into rows 2 and 3 */
+#define SCAN_STEP(CTRL, ROWS)                                                            \
+    do {                                                                                 \
+        x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, CTRL, ROWS, 0xF, false);   \
+        y += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)y, CTRL, ROWS, 0xF, false);   \
+    } while (0)
+    SCAN_STEP(0x111, 0xF);
+    SCAN_STEP(0x112, 0xF);
+    SCAN_STEP(0x114, 0xF);
+    SCAN_STEP(0x118, 0xF);
+    SCAN_STEP(0x142, 0xA);
+    SCAN_STEP(0x143, 0xC);
+#undef SCAN_STEP
+    if (lane == 63 && wv < 4) {
+        wsum[wv] = x;
+        wsum[4 + wv] = y;
     }
+    lds_barrier();
+    tx = wsum[0] + wsum[1] + wsum[2] + wsum[3];
+    ty = wsum[4] + wsum[5] + wsum[6] + wsum[7];
+#pragma unroll
+    for (int w = 0; w < 3; w++)
+        if (w < wv) {
+            x += wsum[w];
+            y += wsum[4 + w];
+        }
 }
 
 /* Tiles of one expert: rows <= GEMM_TILE_SMALL -> one small tile, else
@@ -564,55 +587,56 @@ DEV void put_tiles(uint32_t *list, uint32_t t0, uint32_t e, uint32_t first, uint
     }
 }
 
-/* Given per-expert counts (hist, copied into offs), and offs/arank/ts/tbg
- * filled with the counts, active flags and tile counts: scans them and
- * writes offsets, the active list and the two GEMM tile lists (E <=
- * blockDim.x; every thread of the block calls it). */
-DEV void dispatch_lists(const RouteArgs &a, const uint32_t *hist, uint32_t *offs, uint32_t *arank, uint32_t *ts,
-                        uint32_t *tbg, uint32_t *tiles_s, uint32_t *tiles_b, int has_shared) {
+/* Given the count c of expert tid (threads tid < E; others pass anything):
+ * scans counts, active flags and tile counts (two 16-bit fields per word:
+ * T K <= 32768, E <= 256) and writes offsets, the active list and the two
+ * GEMM tile lists, and the expert's exclusive offset to xo[tid] (LDS, when
+ * given).  Every thread of the block calls it; wsum: LDS, 8 words. */
+DEV void dispatch_lists(const RouteArgs &a, uint32_t c, uint32_t *xo, uint32_t *wsum, uint32_t *tiles_s,
+                        uint32_t *tiles_b, int has_shared) {
     const int E = a.E, T = a.T, tid = threadIdx.x;
-    block_scan4(offs, arank, ts, tbg, E);
-    /* inclusive -> exclusive views: ex(x)[e] = x[e] - own */
-    if (tid < E) {
-        const uint32_t c = hist[tid];
-        const uint32_t o = offs[tid] - c;
+    const bool so = tile_small_only(a), mine = tid < E;
+    if (!mine) c = 0;
+    const uint32_t ns_own = n_small_tiles(c, so), nb_own = n_big_tiles(c, so);
+    uint32_t x = c | ((uint32_t)(c != 0) << 16), y = ns_own | (nb_own << 16), tx, ty;
+    scan2_256(x, y, wsum, tx, ty);
+    if (mine) {
+        const uint32_t o = (x & 0xFFFFu) - c;
         a.offsets[tid] = o;
+        if (xo) xo[tid] = o;
         if (c) {
-            const uint32_t r = arank[tid] - 1;
+            const uint32_t r = (x >> 16) - 1;
             ACT_E(a.list, r) = (uint32_t)tid;
             ACT_OFF(a.list, E, r) = o;
-            const bool so = tile_small_only(a);
             if (c <= GEMM_TILE_SMALL || so)
-                put_tiles(tiles_s, ts[tid] - n_small_tiles(c, so), (uint32_t)tid, o, c, GEMM_TILE_SMALL);
-            else put_tiles(tiles_b, tbg[tid] - n_big_tiles(c, so), (uint32_t)tid, o, c, GEMM_TILE_BIG);
+                put_tiles(tiles_s, (y & 0xFFFFu) - ns_own, (uint32_t)tid, o, c, GEMM_TILE_SMALL);
+            else put_tiles(tiles_b, (y >> 16) - nb_own, (uint32_t)tid, o, c, GEMM_TILE_BIG);
         }
     }
     if (tid == 0) {
-        const uint32_t n_act = arank[E - 1], ns = ts[E - 1], nb = tbg[E - 1], Tu = (uint32_t)T;
-        a.offsets[E] = offs[E - 1];
+        const uint32_t n_act = tx >> 16, ns = ty & 0xFFFFu, nb = ty >> 16, Tu = (uint32_t)T, total = tx & 0xFFFFu;
+        a.offsets[E] = total;
         ACT_N(a.list) = n_act;
-        ACT_OFF(a.list, E, n_act) = offs[E - 1];
+        ACT_OFF(a.list, E, n_act) = total;
         /* the shared expert (id E) over tokens 0..T-1, in the list that holds
          * most of the routed work (a lone list of shared tiles would run as
          * a tail after the other launch) */
-        const bool sm = tile_small_only(a);
-        const uint32_t tm = sm ? GEMM_TILE_SMALL : GEMM_TILE_BIG, nsh = has_shared ? (Tu + tm - 1) / tm : 0;
-        if (has_shared) put_tiles(sm ? tiles_s : tiles_b, sm ? ns : nb, (uint32_t)E, 0, Tu, tm);
-        tiles_s[0] = ns + (sm ? nsh : 0);
-        tiles_b[0] = nb + (sm ? 0 : nsh);
+        const uint32_t tm = so ? GEMM_TILE_SMALL : GEMM_TILE_BIG, nsh = has_shared ? (Tu + tm - 1) / tm : 0;
+        if (has_shared) put_tiles(so ? tiles_s : tiles_b, so ? ns : nb, (uint32_t)E, 0, Tu, tm);
+        tiles_s[0] = ns + (so ? nsh : 0);
+        tiles_b[0] = nb + (so ? 0 : nsh);
     }
 }
 
 __global__ __launch_bounds__(DSP_THREADS) void k_dispatch_scan(RouteArgs a, uint32_t *cnt, int G,
                                                                uint32_t *tiles_s, uint32_t *tiles_b,
                                                                int has_shared) {
-    __shared__ uint32_t hist[DSP_THREADS], offs[DSP_THREADS], arank[DSP_THREADS], ts[DSP_THREADS],
-        tbg[DSP_THREADS];
-    const int E = a.E, T = a.T, tid = threadIdx.x;
+    __shared__ uint32_t wsum[8];
+    const int E = a.E, tid = threadIdx.x;
+    uint32_t run = 0;
     if (tid < E) {
         /* counts 16 blocks at a time, all loaded before the prefixes are
          * stored (a load behind a store waits for it) */
-        uint32_t run = 0;
         for (int g0 = 0; g0 < G; g0 += 16) {
             uint32_t c[16];
 #pragma unroll
@@ -624,14 +648,8 @@ __global__ __launch_bounds__(DSP_THREADS) void k_dispatch_scan(RouteArgs a, uint
                     run += c[j];
                 }
         }
-        hist[tid] = run;
-        offs[tid] = run;
-        arank[tid] = run != 0;
-        ts[tid] = n_small_tiles(run, tile_small_only(a));
-        tbg[tid] = n_big_tiles(run, tile_small_only(a));
     }
-    __syncthreads();
-    dispatch_lists(a, hist, offs, arank, ts, tbg, tiles_s, tiles_b, has_shared);
+    dispatch_lists(a, run, nullptr, wsum, tiles_s, tiles_b, has_shared);
 }
 
 template <int KM>
@@ -649,7 +667,7 @@ __global__ __launch_bounds__(DSP_TOK) void k_dispatch_scatter(RouteArgs a, const
             run += __popc(mask[e * DSP_WORDS + w]);
         }
     }
-    __syncthreads();
+    lds_barrier();
     const uint32_t below = (1u << (tid & 31)) - 1u;
 #pragma unroll
     for (int k = 0; k < KM; k++)
@@ -673,52 +691,62 @@ __global__ __launch_bounds__(DSP_TOK) void k_dispatch_scatter(RouteArgs a, const
 template <int KM>
 __global__ __launch_bounds__(DSP_THREADS) void k_dispatch_one(RouteArgs a, uint32_t *tiles_s, uint32_t *tiles_b,
                                                               int has_shared) {
-    __shared__ uint32_t hist[DSP_THREADS], offs[DSP_THREADS], arank[DSP_THREADS], ts[DSP_THREADS],
-        tbg[DSP_THREADS];
+    __shared__ uint32_t xo[256], wsum[8];
     __shared__ uint32_t mask[DSP1_SUB * 256 * DSP_WORDS], wpre[DSP1_SUB * 256 * DSP_WORDS];
     const int E = a.E, K = a.K, T = a.T, tid = threadIdx.x;
     const int sub = tid / DSP_TOK, tl = tid % DSP_TOK;
-    for (int i = tid; i < DSP1_SUB * E * DSP_WORDS; i += DSP_THREADS) mask[i] = 0;
-    __syncthreads();
     /* the token's K expert ids, loaded together (indices clamped; a load
-     * under a branch is waited for alone), then marked */
+     * under a branch is waited for alone) while the masks are cleared, then
+     * marked */
     int ek[KM];
 #pragma unroll
     for (int k = 0; k < KM; k++) ek[k] = a.idx[min(tid, T - 1) * K + min(k, K - 1)];
+    for (int i = tid; i < DSP1_SUB * E * DSP_WORDS; i += DSP_THREADS) mask[i] = 0;
+    lds_barrier();
 #pragma unroll
     for (int k = 0; k < KM; k++) {
         if (k >= K || tid >= T) ek[k] = -1;
         if (ek[k] >= 0) atomicOr(&mask[(sub * E + ek[k]) * DSP_WORDS + (tl >> 5)], 1u << (tl & 31));
     }
-    __syncthreads();
+    lds_barrier();
+    uint32_t run = 0;
     if (tid < E) { /* word prefixes from 0, and the expert's count */
-        uint32_t run = 0;
+        uint32_t m[DSP1_SUB * DSP_WORDS];
+#pragma unroll
+        for (int sc = 0; sc < DSP1_SUB; sc++)
+#pragma unroll
+            for (int w = 0; w < DSP_WORDS; w++) m[sc * DSP_WORDS + w] = mask[(sc * E + tid) * DSP_WORDS + w];
+#pragma unroll
         for (int sc = 0; sc < DSP1_SUB; sc++)
 #pragma unroll
             for (int w = 0; w < DSP_WORDS; w++) {
-                const int i = (sc * E + tid) * DSP_WORDS + w;
-                wpre[i] = run;
-                run += __popc(mask[i]);
+                wpre[(sc * E + tid) * DSP_WORDS + w] = run;
+                run += __popc(m[sc * DSP_WORDS + w]);
             }
-        hist[tid] = run;
-        offs[tid] = run;
-        arank[tid] = run != 0;
-        ts[tid] = n_small_tiles(run, tile_small_only(a));
-        tbg[tid] = n_big_tiles(run, tile_small_only(a));
     }
-    __syncthreads();
-    dispatch_lists(a, hist, offs, arank, ts, tbg, tiles_s, tiles_b, has_shared);
-    __syncthreads();
+    dispatch_lists(a, run, xo, wsum, tiles_s, tiles_b, has_shared);
+    lds_barrier();
     const uint32_t below = (1u << (tl & 31)) - 1u;
+    uint32_t pk[KM];
 #pragma unroll
     for (int k = 0; k < KM; k++)
         if (ek[k] >= 0) {
             const int e = ek[k], i = (sub * E + e) * DSP_WORDS + (tl >> 5);
-            const uint32_t pos = offs[e] - hist[e] + wpre[i] + __popc(mask[i] & below);
-            const uint32_t p = (uint32_t)(tid * K + k);
-            a.pairs[pos] = p;
-            a.pos[p] = pos;
+            pk[k] = xo[e] + wpre[i] + __popc(mask[i] & below);
+            a.pairs[pk[k]] = (uint32_t)(tid * K + k);
         }
+    /* the token's K inverse positions: contiguous, written as 16-byte runs
+     * when K = 8 */
+    if (KM == 8 && K == 8) {
+        if (tid < T) {
+            *(u4 *)(a.pos + tid * 8) = u4{pk[0], pk[1], pk[2], pk[3]};
+            *(u4 *)(a.pos + tid * 8 + 4) = u4{pk[4], pk[5], pk[6], pk[7]};
+        }
+    } else {
+#pragma unroll
+        for (int k = 0; k < KM; k++)
+            if (ek[k] >= 0) a.pos[tid * K + k] = pk[k];
+    }
 }
 
 /* RMSNorm (inference/src/shaders.metal:128-149) with the canonical sum of
@@ -896,7 +924,8 @@ int dispatch_blocks(int T) { return (T + DSP_TOK - 1) / DSP_TOK; }
 int launch_dispatch(const RouteArgs &a, uint32_t *tiles_s, uint32_t *tiles_b, int has_shared, uint32_t *cnt,
                     hipStream_t s) {
     const size_t lds = sizeof(uint32_t) * (size_t)a.E * DSP_WORDS * 2;
-    if (lds > 64 * 1024 || a.E > DSP_THREADS || a.K > OROME_MAXK) return -2;
+    /* one scan lane per expert; 16-bit fields for the pair counts */
+    if (lds > 64 * 1024 || a.E > 256 || a.K > OROME_MAXK || (long)a.T * a.K > 32768) return -2;
 #ifndef DISPATCH_ONE
 #define DISPATCH_ONE 1
 #endif

@@ -141,7 +141,7 @@ DEV uint32_t block_excl_scan256(uint32_t v, uint32_t *wsum /* LDS [4] */, uint32
         if (lane >= off) inc += o;
     }
     if (lane == 63 && wv < 4) wsum[wv] = inc;
-    __syncthreads();
+    lds_barrier();
     uint32_t base = 0;
     for (int w = 0; w < min(wv, 4); w++) base += wsum[w];
     *total = wsum[0] + wsum[1] + wsum[2] + wsum[3];
@@ -168,9 +168,9 @@ DEV void topk_dispatch_block(const RouteArgs &a) {
     for (int t = wv; t < T; t += nw)
         wave_topk<EPL, COH>(a.logits + (size_t)t * (E + 1), a.bias, E, K, lane, a.idx + t * K,
                             a.w + t * K, a.sgl + t, s_e + t * K);
-    __syncthreads();
+    lds_barrier();
     if (tid < NP) atomicOr(&mask[s_e[tid] * 8 + (tid >> 5)], 1u << (tid & 31));
-    __syncthreads();
+    lds_barrier();
     /* thread tid owns experts [tid*EPT, tid*EPT + EPT), EPT = EPL/4 (E <= 64 EPL) */
     constexpr int EPT = EPL >= 4 ? EPL / 4 : 1;
     uint32_t cnt[EPT], packed = 0;
@@ -220,7 +220,7 @@ DEV void topk_dispatch_block(const RouteArgs &a) {
             a.tiles_s[0] = n + (a.has_shared ? 1u : 0u);
         }
     }
-    __syncthreads();
+    lds_barrier();
     if (tid < NP) {
         const int e = s_e[tid], wd = tid >> 5;
         uint32_t r = __popc(mask[e * 8 + wd] & ((1u << (tid & 31)) - 1u));
