@@ -530,11 +530,10 @@ __global__ __launch_bounds__(DSP_TOK) void k_dispatch_count(RouteArgs a, uint32_
     }
 }
 
-/* Inclusive scan of two words over threads 0..255 (the others pass zeros
- * and read nothing back), with both totals: wave shuffles, then one
- * barrier for the four wave sums (wsum: LDS, 8 words).  Every thread of the
- * block calls it. */
-DEV void scan2_256(uint32_t &x, uint32_t &y, uint32_t *wsum, uint32_t &tx, uint32_t &ty) {
+/* Inclusive scan of two words over the block (up to 16 waves), with both
+ * totals: a DPP scan per wave, then one barrier for the wave sums (wsum:
+ * LDS, 32 words).  Every thread of the block calls it. */
+DEV void scan2_block(uint32_t &x, uint32_t &y, uint32_t *wsum, uint32_t &tx, uint32_t &ty) {
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     /* wave inclusive scan with DPP: shifts by 1, 2, 4, 8 inside each row of
      * 16 lanes (lanes shifted in from outside the row add 0), then lane 15
@@ -551,19 +550,23 @@ DEV void scan2_256(uint32_t &x, uint32_t &y, uint32_t *wsum, uint32_t &tx, uint3
     SCAN_STEP(0x142, 0xA);
     SCAN_STEP(0x143, 0xC);
 #undef SCAN_STEP
-    if (lane == 63 && wv < 4) {
+    const int nw = (int)(blockDim.x >> 6);
+    if (lane == 63) {
         wsum[wv] = x;
-        wsum[4 + wv] = y;
+        wsum[16 + wv] = y;
     }
     lds_barrier();
-    tx = wsum[0] + wsum[1] + wsum[2] + wsum[3];
-    ty = wsum[4] + wsum[5] + wsum[6] + wsum[7];
-#pragma unroll
-    for (int w = 0; w < 3; w++)
+    tx = 0;
+    ty = 0;
+    for (int w = 0; w < nw; w++) {
+        const uint32_t sx = wsum[w], sy = wsum[16 + w];
         if (w < wv) {
-            x += wsum[w];
-            y += wsum[4 + w];
+            x += sx;
+            y += sy;
         }
+        tx += sx;
+        ty += sy;
+    }
 }
 
 /* Tiles of one expert: rows <= GEMM_TILE_SMALL -> one small tile, else
@@ -587,11 +590,12 @@ DEV void put_tiles(uint32_t *list, uint32_t t0, uint32_t e, uint32_t first, uint
     }
 }
 
-/* Given the count c of expert tid (threads tid < E; others pass anything):
- * scans counts, active flags and tile counts (two 16-bit fields per word:
- * T K <= 32768, E <= 256) and writes offsets, the active list and the two
- * GEMM tile lists, and the expert's exclusive offset to xo[tid] (LDS, when
- * given).  Every thread of the block calls it; wsum: LDS, 8 words. */
+/* Given the count c of expert tid (threads tid < E <= blockDim.x; others
+ * pass anything): scans counts, active flags and tile counts (two 16-bit
+ * fields per word: T K <= 32768, E <= 1024) and writes offsets, the active
+ * list and the two GEMM tile lists, and the expert's exclusive offset to
+ * xo[tid] (LDS, when given).  Every thread of the block calls it; wsum:
+ * LDS, 32 words. */
 DEV void dispatch_lists(const RouteArgs &a, uint32_t c, uint32_t *xo, uint32_t *wsum, uint32_t *tiles_s,
                         uint32_t *tiles_b, int has_shared) {
     const int E = a.E, T = a.T, tid = threadIdx.x;
@@ -599,7 +603,7 @@ DEV void dispatch_lists(const RouteArgs &a, uint32_t c, uint32_t *xo, uint32_t *
     if (!mine) c = 0;
     const uint32_t ns_own = n_small_tiles(c, so), nb_own = n_big_tiles(c, so);
     uint32_t x = c | ((uint32_t)(c != 0) << 16), y = ns_own | (nb_own << 16), tx, ty;
-    scan2_256(x, y, wsum, tx, ty);
+    scan2_block(x, y, wsum, tx, ty);
     if (mine) {
         const uint32_t o = (x & 0xFFFFu) - c;
         a.offsets[tid] = o;
@@ -631,7 +635,7 @@ DEV void dispatch_lists(const RouteArgs &a, uint32_t c, uint32_t *xo, uint32_t *
 __global__ __launch_bounds__(DSP_THREADS) void k_dispatch_scan(RouteArgs a, uint32_t *cnt, int G,
                                                                uint32_t *tiles_s, uint32_t *tiles_b,
                                                                int has_shared) {
-    __shared__ uint32_t wsum[8];
+    __shared__ uint32_t wsum[32];
     const int E = a.E, tid = threadIdx.x;
     uint32_t run = 0;
     if (tid < E) {
@@ -691,7 +695,7 @@ __global__ __launch_bounds__(DSP_TOK) void k_dispatch_scatter(RouteArgs a, const
 template <int KM>
 __global__ __launch_bounds__(DSP_THREADS) void k_dispatch_one(RouteArgs a, uint32_t *tiles_s, uint32_t *tiles_b,
                                                               int has_shared) {
-    __shared__ uint32_t xo[256], wsum[8];
+    __shared__ uint32_t xo[256], wsum[32];
     __shared__ uint32_t mask[DSP1_SUB * 256 * DSP_WORDS], wpre[DSP1_SUB * 256 * DSP_WORDS];
     const int E = a.E, K = a.K, T = a.T, tid = threadIdx.x;
     const int sub = tid / DSP_TOK, tl = tid % DSP_TOK;
@@ -925,7 +929,7 @@ int launch_dispatch(const RouteArgs &a, uint32_t *tiles_s, uint32_t *tiles_b, in
                     hipStream_t s) {
     const size_t lds = sizeof(uint32_t) * (size_t)a.E * DSP_WORDS * 2;
     /* one scan lane per expert; 16-bit fields for the pair counts */
-    if (lds > 64 * 1024 || a.E > 256 || a.K > OROME_MAXK || (long)a.T * a.K > 32768) return -2;
+    if (lds > 64 * 1024 || a.E > DSP_THREADS || a.K > OROME_MAXK || (long)a.T * a.K > 32768) return -2;
 #ifndef DISPATCH_ONE
 #define DISPATCH_ONE 1
 #endif

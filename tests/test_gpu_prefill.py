@@ -413,3 +413,15 @@ def test_mfma_fp16_weights_bit_exact(fmt, tiled):
     else:  # fp16(dmin m) can carry an error larger than w itself where they cancel
         assert rel_l2(got, exact) < 1e-3
     p.gm.close()
+
+
+@pytest.mark.parametrize("T", [200, 1100])
+def test_more_than_256_experts(T):
+    """E = 384 (above the one-block dispatch's 256): the three-launch dispatch
+    with its block-wide scan over 6 waves of experts, the 8-expert-per-lane
+    top-k, and the grouped GEMMs at H = 512, M = S = 256.  Routing bit-exact,
+    output within tolerance of the oracle."""
+    banner("E=384 H=512 M=256, T=%d" % T)
+    p = Pair(max_tokens=T, E=384, H=512, M=256, S=256, seed=91)
+    run_and_check(p, T, seed=3300 + T, path=_lib.OROME_PATH_MFMA)
+    p.gm.close()
