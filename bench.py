@@ -235,8 +235,11 @@ def run_config(key, steps, warmup, path, cpu_seconds, no_cpu):
     gu_us = stage_us["gate_up"]
     gu_gbs = gu_bytes / (gu_us * 1e-6) / 1e9
     gu_tflops = gu_flops / (gu_us * 1e-6) / 1e12
+    # up to T K = 32 E every expert is in 32-row tiles (one list); above, the
+    # 32-row and 80-row tile lists
     kname = {"gemv": "gemv_gate_up", "small_batch_gemm": "gemm_gate_up (16-row tiles)",
-             "mfma": "gemm_gate_up (small + big tile lists)"}[kpath]
+             "mfma": ("gemm_gate_up (32-row tile list)" if T * K <= 32 * E
+                      else "gemm_gate_up (32-row + 80-row tile lists)")}[kpath]
     if T >= 2048:
         roof = {"bound": "mfma", "kernel": kname, "achieved": round(gu_tflops, 2),
                 "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(gu_tflops / MFMA_F16_PEAK_TFLOPS, 4)}
