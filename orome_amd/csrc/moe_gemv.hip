@@ -372,118 +372,168 @@ DEV void k_gemv_gate_up1_body(GUArgs a, RouteArgs ra) {
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int rows_blk = 4 * GU_RPW, b = blockIdx.x;
     const int E = a.E, K = a.K;
-    /* x, then the logits (and bias), issued in every block and held here:
-     * one round trip for both (the compiler would otherwise load the logits
-     * inside the routed branch, after converting x) */
     int klo;
     q4_pos(lane, klo);
-    f4 xr[8];
-#pragma unroll
-    for (int q = 0; q < 4; q++) {
-        xr[q] = *(const f4 *)(a.x + klo + 4 * q);
-        xr[4 + q] = *(const f4 *)(a.x + klo + 32 + 4 * q);
-    }
-    const float *l = ra.logits, *bias = ra.bias ? ra.bias : ra.logits;
-    float v[EPL], bv[EPL];
-#pragma unroll
-    for (int j = 0; j < EPL; j++) {
-        v[j] = l[min(lane * EPL + j, E - 1)];
-        bv[j] = bias[min(lane * EPL + j, E - 1)];
-    }
-    const float sg = l[E];
-#pragma unroll
-    for (int j = 0; j < EPL; j++) asm volatile("" : : "v"(v[j]), "v"(bv[j]));
-    h2 xl[8], xh[8];
-    const float Xl = cvt_x16_f32(xr, xl), Xh = cvt_x16_f32(xr + 4, xh);
     if (b >= a.routed_blocks) { /* shared expert (Q4_K): needs no routing */
+        f4 xr[8];
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            xr[q] = *(const f4 *)(a.x + klo + 4 * q);
+            xr[4 + q] = *(const f4 *)(a.x + klo + 32 + 4 * q);
+        }
+        h2 xl[8], xh[8];
+        const float Xl = cvt_x16_f32(xr, xl), Xh = cvt_x16_f32(xr + 4, xh);
         const int r0 = (b - a.routed_blocks) * rows_blk + wv * GU_RPW;
         gu_body1<GU_RPW>(a, a.sh_gate, a.sh_up, r0, xl, xh, Xl, Xh, a.act_sh, lane);
         return;
     }
+    /* x reaches the block once: wave w converts a quarter of it to fp16 into
+     * LDS (each wave loading all of x made 576 blocks x 4 waves x 8 KB of L2
+     * reads that held back the logits); the selecting wave also loads the
+     * logits (and bias), in the same round trip */
+    __shared__ __attribute__((aligned(16))) _Float16 s_x16[2048];
+    const int sel = (b >> 8) & 3;
+    const int xq = (wv * 64 + lane) * 8; /* this thread's 8 elements of x (H = 2048) */
+    const f4 xa = *(const f4 *)(a.x + xq), xb = *(const f4 *)(a.x + xq + 4);
+    const float *l = ra.logits, *bias = ra.bias ? ra.bias : ra.logits;
+    float v[EPL], bv[EPL], sg = 0.0f;
+    if (wv == sel) {
+#pragma unroll
+        for (int j = 0; j < EPL; j++) {
+            v[j] = l[min(lane * EPL + j, E - 1)];
+            bv[j] = bias[min(lane * EPL + j, E - 1)];
+        }
+        sg = l[E];
+    }
+    *(h8 *)(s_x16 + xq) = h8{(_Float16)xa.x, (_Float16)xa.y, (_Float16)xa.z, (_Float16)xa.w,
+                             (_Float16)xb.x, (_Float16)xb.y, (_Float16)xb.z, (_Float16)xb.w};
     const int bpe = a.M / rows_blk, u = b / bpe, r0 = (b % bpe) * rows_blk + wv * GU_RPW;
     const size_t rb = row_bytes(FQ4K, a.H);
-
-    uint32_t key[EPL];
-    int kj[EPL];
-#pragma unroll
-    for (int j = 0; j < EPL; j++) {
-        key[j] = lane * EPL + j < E ? route_ord(ra.bias ? v[j] + bv[j] : v[j]) : 0u;
-        kj[j] = j;
-    }
-#pragma unroll
-    for (int pass = 0; pass < EPL; pass++)
-#pragma unroll
-        for (int j = pass & 1; j + 1 < EPL; j += 2)
-            if (key[j + 1] > key[j]) {
-                const uint32_t tk = key[j]; key[j] = key[j + 1]; key[j + 1] = tk;
-                const int tj = kj[j]; kj[j] = kj[j + 1]; kj[j + 1] = tj;
-            }
-    /* lane k keeps the k-th winner */
-    int myid = 0, eu = 0;
-    float myval = 0.0f, v0 = 0.0f;
+    /* one wave of the block selects; the others wait at a barrier that it
+     * passes right after round u has named the block's expert (and by which
+     * every wave has stored its quarter of x).  The selecting wave is wave
+     * (b / 256) % 4, so the blocks that share a CU (b, b + 256, b + 512 with
+     * one block per CU and round) select on different SIMDs. */
+    __shared__ int s_eu, s_rank;
     Q4Raw g[GU_RPW], w2[GU_RPW];
-    /* a rolled loop: each wave runs these rounds once */
-#pragma unroll 1
-    for (int k = 0; k < K; k++) {
-        const uint32_t m = wave_max_u32(key[0]);
-        const int wl = (int)__builtin_ctzll(__ballot(key[0] == m));
-        const int id = wl * EPL + __builtin_amdgcn_readlane(kj[0], wl);
-        const float val = ord_value(m);
-        if (lane == k) { myid = id; myval = val; }
-        if (k == 0) v0 = val;
-        if (lane == wl) {
+    auto issue = [&](int e) {
+        const uint8_t *gb = a.gate + (size_t)e * a.gate_stride, *ub = a.up + (size_t)e * a.up_stride;
 #pragma unroll
-            for (int j = 0; j + 1 < EPL; j++) { key[j] = key[j + 1]; kj[j] = kj[j + 1]; }
-            key[EPL - 1] = 0u;
+        for (int i = 0; i < GU_RPW; i++) {
+            g[i] = q4_load(gb + (size_t)(r0 + i) * rb, lane);
+            w2[i] = q4_load(ub + (size_t)(r0 + i) * rb, lane);
         }
-        if (k == u) {
-            eu = id;
-            const uint8_t *gb = a.gate + (size_t)eu * a.gate_stride, *ub = a.up + (size_t)eu * a.up_stride;
+    };
+    int rank = 0;
+    if (wv == sel) {
+        uint32_t key[EPL];
+        int kj[EPL];
 #pragma unroll
-            for (int i = 0; i < GU_RPW; i++) {
-                g[i] = q4_load(gb + (size_t)(r0 + i) * rb, lane);
-                w2[i] = q4_load(ub + (size_t)(r0 + i) * rb, lane);
+        for (int j = 0; j < EPL; j++) {
+            key[j] = lane * EPL + j < E ? route_ord(ra.bias ? v[j] + bv[j] : v[j]) : 0u;
+            kj[j] = j;
+        }
+#pragma unroll
+        for (int pass = 0; pass < EPL; pass++)
+#pragma unroll
+            for (int j = pass & 1; j + 1 < EPL; j += 2)
+                if (key[j + 1] > key[j]) {
+                    const uint32_t tk = key[j]; key[j] = key[j + 1]; key[j + 1] = tk;
+                    const int tj = kj[j]; kj[j] = kj[j + 1]; kj[j + 1] = tj;
+                }
+        /* lane k keeps the k-th winner */
+        int myid = 0, eu = 0;
+        float myval = 0.0f, v0 = 0.0f;
+        /* a rolled loop: each wave runs these rounds once */
+#pragma unroll 1
+        for (int k = 0; k < K; k++) {
+            const uint32_t m = wave_max_u32(key[0]);
+            const int wl = (int)__builtin_ctzll(__ballot(key[0] == m));
+            const int id = wl * EPL + __builtin_amdgcn_readlane(kj[0], wl);
+            const float val = ord_value(m);
+            if (lane == k) { myid = id; myval = val; }
+            if (k == 0) v0 = val;
+            if (lane == wl) {
+#pragma unroll
+                for (int j = 0; j + 1 < EPL; j++) { key[j] = key[j + 1]; kj[j] = kj[j + 1]; }
+                key[EPL - 1] = 0u;
+            }
+            if (k == u) {
+                eu = id;
+                if (lane == 0) s_eu = id;
+                lds_barrier();
+                issue(eu);
             }
         }
+        rank = __popcll(__ballot(lane < K && myid < eu));
+        if (lane == 0) s_rank = rank;
+        if (b == 0) { /* publish the call's routing for the down kernel */
+            const float tw = lane < K ? expf(myval - v0) : 0.0f;
+            float sum = 0.0f;
+#pragma unroll 1
+            for (int k = 0; k < K; k++)
+                sum += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, tw), k));
+            const float inv = sum > 0.0f ? 1.0f / sum : 0.0f;
+            int rkk = 0;
+#pragma unroll 1
+            for (int k = 0; k < K; k++) rkk += __builtin_amdgcn_readlane(myid, k) < myid;
+            if (lane < K) {
+                ra.idx[lane] = myid;
+                ra.w[lane] = tw * inv;
+                ra.pairs[rkk] = (uint32_t)lane;
+                ra.pos[lane] = (uint32_t)rkk;
+                ACT_E(ra.list, rkk) = (uint32_t)myid;
+                ACT_OFF(ra.list, E, rkk) = (uint32_t)rkk;
+            }
+            if (lane == 0) {
+                ra.sgl[0] = sg;
+                ACT_N(ra.list) = (uint32_t)K;
+                ACT_OFF(ra.list, E, K) = (uint32_t)K;
+            }
+            for (int ee = lane; ee <= E; ee += 64) {
+                int c = 0;
+#pragma unroll 1
+                for (int k = 0; k < K; k++) c += __builtin_amdgcn_readlane(myid, k) < ee;
+                ra.offsets[ee] = (uint32_t)c;
+            }
+        }
+    } else {
+        lds_barrier();
+        issue(s_eu);
     }
-    const int rank = __popcll(__ballot(lane < K && myid < eu));
-    if (b == 0 && wv == 0) { /* publish the call's routing for the down kernel */
-        const float tw = lane < K ? expf(myval - v0) : 0.0f;
-        float sum = 0.0f;
-#pragma unroll 1
-        for (int k = 0; k < K; k++)
-            sum += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, tw), k));
-        const float inv = sum > 0.0f ? 1.0f / sum : 0.0f;
-        int rkk = 0;
-#pragma unroll 1
-        for (int k = 0; k < K; k++) rkk += __builtin_amdgcn_readlane(myid, k) < myid;
-        if (lane < K) {
-            ra.idx[lane] = myid;
-            ra.w[lane] = tw * inv;
-            ra.pairs[rkk] = (uint32_t)lane;
-            ra.pos[lane] = (uint32_t)rkk;
-            ACT_E(ra.list, rkk) = (uint32_t)myid;
-            ACT_OFF(ra.list, E, rkk) = (uint32_t)rkk;
+    /* this lane's 32 values of x (k = klo .. klo + 15, klo + 32 .. + 47) */
+    h2 xl[8], xh[8];
+    float Xl = 0.0f, Xh = 0.0f;
+    {
+        const h2 one = {(_Float16)1.0f, (_Float16)1.0f};
+        const u4 q0 = *(const u4 *)(s_x16 + klo), q1 = *(const u4 *)(s_x16 + klo + 8);
+        const u4 q2 = *(const u4 *)(s_x16 + klo + 32), q3 = *(const u4 *)(s_x16 + klo + 40);
+        const uint32_t wl[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+        const uint32_t wh[8] = {q2.x, q2.y, q2.z, q2.w, q3.x, q3.y, q3.z, q3.w};
+#pragma unroll
+        for (int v2 = 0; v2 < 8; v2++) {
+            xl[v2] = as_h2(wl[v2]);
+            xh[v2] = as_h2(wh[v2]);
         }
-        if (lane == 0) {
-            ra.sgl[0] = sg;
-            ACT_N(ra.list) = (uint32_t)K;
-            ACT_OFF(ra.list, E, K) = (uint32_t)K;
-        }
-        for (int ee = lane; ee <= E; ee += 64) {
-            int c = 0;
-#pragma unroll 1
-            for (int k = 0; k < K; k++) c += __builtin_amdgcn_readlane(myid, k) < ee;
-            ra.offsets[ee] = (uint32_t)c;
-        }
+#pragma unroll
+        for (int v2 = 0; v2 < 8; v2++) Xl = dot2(xl[v2], one, Xl);
+#pragma unroll
+        for (int v2 = 0; v2 < 8; v2++) Xh = dot2(xh[v2], one, Xh);
     }
-    _Float16 *out = a.act + (size_t)rank * a.M;
+    float pg[GU_RPW], pu[GU_RPW];
 #pragma unroll
     for (int i = 0; i < GU_RPW; i++) {
-        const float pg = wave_sum_fast(q4_dot(g[i], lane, xl, xh, Xl, Xh));
-        const float pu = wave_sum_fast(q4_dot(w2[i], lane, xl, xh, Xl, Xh));
-        if (lane == 0) out[r0 + i] = glu_f16(pg, pu);
+        pg[i] = wave_sum_fast(q4_dot(g[i], lane, xl, xh, Xl, Xh));
+        pu[i] = wave_sum_fast(q4_dot(w2[i], lane, xl, xh, Xl, Xh));
     }
+    /* the act row is the expert's rank among the selected ids, which the
+     * selecting wave knows once its rounds are done */
+    lds_barrier();
+    if (wv != sel) rank = s_rank;
+    _Float16 *out = a.act + (size_t)rank * a.M;
+    if (lane == 0)
+#pragma unroll
+        for (int i = 0; i < GU_RPW; i++) out[r0 + i] = glu_f16(pg[i], pu[i]);
 }
 
 template <int EPL>
