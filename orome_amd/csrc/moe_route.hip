@@ -39,6 +39,19 @@ __global__ __launch_bounds__(FOLD ? 512 : 256) void k_route_small(RouteArgs a) {
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int row = blockIdx.x * (W / RS) + wv / RS, tb = (wv % RS) * TMAX;
     const int E = a.E, H = a.H, T = a.T;
+    if (TMAX == 1 && !FOLD && H <= 2048) {
+        /* one token: the block stages x once in LDS for its four rows */
+        __shared__ f4 xl[512];
+        const float *src = NORM ? a.norm_h : a.x;
+        const int q = threadIdx.x;
+        const f4 xp[2] = {*(const f4 *)(src + 4 * min(q, H / 4 - 1)), *(const f4 *)(src + 4 * min(q + 256, H / 4 - 1))};
+        const bool live = row <= E;
+        const float *wr = !live ? nullptr : row < E ? a.W + (size_t)row * H : a.wsg;
+        float acc[TMAX];
+        canon_dots<TMAX, NIM, NORM>(wr, a, lane, (NORM || a.x16) && row == 0, acc, 0, xl, xp);
+        if (live && lane == 0) a.logits[row] = acc[0];
+        return;
+    }
     if (row <= E && tb < T) {
         const float *wr = row < E ? a.W + (size_t)row * H : a.wsg;
         float acc[TMAX];

@@ -309,7 +309,8 @@ DEV void route_block_lds(const RouteArgs &a, RouteLds &r, bool publish) {
  * unconditional (indices clamped, values past T or H unused), since a load
  * under a branch is waited for alone.  A NULL wrow gives zeros. */
 template <int TMAX, int NIM, bool NORM>
-DEV void canon_dots(const float *wrow, const RouteArgs &a, int lane, bool write_x, float *acc, int tb = 0) {
+DEV void canon_dots(const float *wrow, const RouteArgs &a, int lane, bool write_x, float *acc, int tb = 0,
+                    f4 *xlds = nullptr, const f4 *xpart = nullptr) {
     /* tokens tb .. tb + TMAX - 1 (acc[t - tb]) */
     /* write_x also stages fp16(x) into a.x16 when set (round to nearest
      * even, each 4-group stored (0,2,1,3), the grouped GEMMs' layout) */
@@ -323,6 +324,16 @@ DEV void canon_dots(const float *wrow, const RouteArgs &a, int lane, bool write_
         wv[i] = *(const f4 *)((wrow ? wrow : xs) + ic);
         if (NORM) nw[i] = *(const f4 *)((a.norm_w ? a.norm_w : xs) + ic);
     }
+    /* xlds (one token, H <= 2048, every wave of the block calls this): the
+     * block's threads hold x (or the norm input) in xpart, two 16-byte
+     * pieces each; it is stored into LDS once and read back from there
+     * (the waves would otherwise each fetch the whole row) */
+    if (xlds) {
+        const int q = threadIdx.x;
+        xlds[q] = xpart[0];
+        xlds[q + 256] = xpart[1];
+        lds_barrier();
+    }
 #pragma unroll
     for (int t0 = 0; t0 < TMAX; t0 += TC) {
         if (t0 >= T) break;
@@ -331,7 +342,8 @@ DEV void canon_dots(const float *wrow, const RouteArgs &a, int lane, bool write_
         for (int c = 0; c < TC; c++)
 #pragma unroll
             for (int i = 0; i < NIM; i++)
-                hv[c][i] = *(const f4 *)(xs + (size_t)min(t0 + c, T - 1) * H + 256 * min(i, NI - 1) + 4 * lane);
+                hv[c][i] = xlds ? xlds[(256 * min(i, NI - 1) + 4 * lane) >> 2]
+                                : *(const f4 *)(xs + (size_t)min(t0 + c, T - 1) * H + 256 * min(i, NI - 1) + 4 * lane);
         if (t0 == 0) {
 #pragma unroll
             for (int i = 0; i < NIM; i++) {
