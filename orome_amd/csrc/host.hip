@@ -488,6 +488,7 @@ thread_local LaunchEvents g_launch_ev = {nullptr, nullptr};
  * may be NULL). */
 struct FwdOut {
     float *res, *ssq;
+    const float *next_router = nullptr; /* the next layer's router rows (a stack forward), touched early */
 };
 
 static int forward_impl(orome_hip_ctx *c, const OromeHipModelConfig *cfg, const OromeHipExpertLayerRef *elr,
@@ -622,7 +623,7 @@ static int forward_impl(orome_hip_ctx *c, const OromeHipModelConfig *cfg, const 
         /* one token: down and combine in one kernel when the shape allows */
         const bool dc1 = T == 1 && K <= 8 && M == 512 && (!S || S == 512);
         if (dc1) {
-            TLAUNCH(c, ST_DOWN, launch_gemv_down_combine1(ex, sh, a, c->act, c->act_sh, H, M, K, h_in, h_out, fo.res, s),
+            TLAUNCH(c, ST_DOWN, launch_gemv_down_combine1(ex, sh, a, c->act, c->act_sh, H, M, K, h_in, h_out, fo.res, s, fo.next_router),
                     "gemv down + combine");
             if (fo.ssq) TLAUNCH(c, ST_COMBINE, launch_sumsq_parts(h_out, T, H, fo.ssq, s), "sum-of-squares parts");
         } else {
@@ -754,7 +755,10 @@ extern "C" int orome_moe_stack_forward(orome_hip_ctx *c, const OromeHipModelConf
     for (int l = 0; l < n_layers; l++) {
         if (!lts[l].routing_gate.buffer) return orome_fail(OROME_EINVAL, "orome_moe_stack_forward: layer %d", l);
         const bool next = fuse && l + 1 < n_layers;
-        int rc = forward_impl(c, cfg, &elrs[l], &lts[l], NULL, h, h, T, K, h, norm_w(l), s, FwdOut{NULL, NULL},
+        FwdOut fo{NULL, NULL};
+        if (l + 1 < n_layers && lts[l + 1].routing_gate.buffer)
+            fo.next_router = (const float *)dev_addr(lts[l + 1].routing_gate.buffer, lts[l + 1].routing_gate.offset);
+        int rc = forward_impl(c, cfg, &elrs[l], &lts[l], NULL, h, h, T, K, h, norm_w(l), s, fo,
                               next ? norm_w(l + 1) : NULL, next ? 1 : 0, fuse && l > 0 ? 1 : 0);
         if (rc) return rc;
     }

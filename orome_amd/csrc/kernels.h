@@ -113,7 +113,8 @@ int launch_gemv_down(const ExpertSide &ex, const SharedSide &sh, const _Float16 
  * (K <= 8, M = S = 512); returns -2 when the shape is not covered */
 int launch_gemv_down_combine1(const ExpertSide &ex, const SharedSide &sh, const RouteArgs &ra,
                               const _Float16 *act, const _Float16 *act_sh, int H, int M, int K,
-                              const float *h_in, float *h_out, float *res, hipStream_t s);
+                              const float *h_in, float *h_out, float *res, hipStream_t s,
+                              const float *next_router = nullptr);
 int launch_delay(uint32_t usec, hipStream_t s);
 int launch_rmsnorm(const float *h, const float *w, int T, int H, float eps, float *x, hipStream_t s);
 int launch_dequant(int fmt, const uint8_t *src, uint32_t rows, uint32_t n, float *out32,

@@ -30,7 +30,7 @@
 
 enum { FQ4K = 0, FQ5K = 1, FQ6K = 2, FQ8 = 3 };
 
-DEV size_t row_bytes(int fmt, int n) {
+static __host__ __device__ __forceinline__ size_t row_bytes(int fmt, int n) {
     return fmt == FQ4K ? (size_t)(n / 256) * 144 : fmt == FQ5K ? (size_t)(n / 256) * 176
            : fmt == FQ6K ? (size_t)(n / 256) * 210 : (size_t)(n / 32) * 34;
 }
@@ -208,7 +208,24 @@ struct GUArgs {
     _Float16 *act, *act_sh;
     int routed_blocks;
     unsigned long long *kt; /* per-block launch stamps (KT_BEGIN / KT_END) or NULL */
+    /* T = 1: the down matrices the next kernel reads (row-major, pf_rb bytes
+     * a row, H rows), touched one 4-byte load per 128-byte line so that they
+     * are on their way to the caches while this kernel waits; NULL: none */
+    const uint8_t *pf_down, *pf_sh_down;
+    size_t pf_down_stride;
+    int pf_rb, pf_sh_rb;
 };
+
+/* One 4-byte load per 128-byte line of the 8-row groups g = i, i + step, ...
+ * (< H / 8) of a row-major matrix: the rows that the T = 1 down kernel's
+ * blocks g read, from a block on the same XCD as they are (g = i mod 8).
+ * The value lands in `sink`, which the caller keeps until a wait for it. */
+DEV void touch_rows8(const uint8_t *m, int rb, int H, int i, int step, int lane, uint32_t &sink) {
+    const int nl = (8 * rb + 127) / 128, g = i + step * (lane / nl);
+    if (lane / nl >= 2 || g >= H / 8) return;
+    const uint8_t *p = m + (size_t)g * 8 * rb + min((lane % nl) * 128, 8 * rb - 4);
+    asm volatile("global_load_dword %0, %1, off" : "=v"(sink) : "v"(p) : "memory");
+}
 
 /* One wave: RPW gate rows and RPW up rows for the n tokens of a slot.  Raw
  * weight chunks of all rows are loaded first; the token loop is a runtime
@@ -384,7 +401,10 @@ DEV void k_gemv_gate_up1_body(GUArgs a, RouteArgs ra) {
         h2 xl[8], xh[8];
         const float Xl = cvt_x16_f32(xr, xl), Xh = cvt_x16_f32(xr + 4, xh);
         const int r0 = (b - a.routed_blocks) * rows_blk + wv * GU_RPW;
+        uint32_t sink = 0;
+        if (wv == 1 && a.pf_sh_down) touch_rows8(a.pf_sh_down, a.pf_sh_rb, a.H, b - a.routed_blocks, a.S / rows_blk, lane, sink);
         gu_body1<GU_RPW>(a, a.sh_gate, a.sh_up, r0, xl, xh, Xl, Xh, a.act_sh, lane);
+        asm volatile("s_waitcnt vmcnt(0)" : : "v"(sink));
         return;
     }
     /* x reaches the block once: wave w converts a quarter of it to fp16 into
@@ -501,6 +521,11 @@ DEV void k_gemv_gate_up1_body(GUArgs a, RouteArgs ra) {
         lds_barrier();
         issue(s_eu);
     }
+    /* the next wave after the selecting one touches the selected expert's
+     * down rows that this block's XCD will read */
+    uint32_t sink = 0;
+    if (wv == ((sel + 1) & 3) && a.pf_down)
+        touch_rows8(a.pf_down + (size_t)s_eu * a.pf_down_stride, a.pf_rb, a.H, b % bpe, bpe, lane, sink);
     /* this lane's 32 values of x (k = klo .. klo + 15, klo + 32 .. + 47) */
     h2 xl[8], xh[8];
     float Xl = 0.0f, Xh = 0.0f;
@@ -528,6 +553,7 @@ DEV void k_gemv_gate_up1_body(GUArgs a, RouteArgs ra) {
     }
     /* the act row is the expert's rank among the selected ids, which the
      * selecting wave knows once its rounds are done */
+    asm volatile("s_waitcnt vmcnt(0)" : : "v"(sink));
     lds_barrier();
     if (wv != sel) rank = s_rank;
     _Float16 *out = a.act + (size_t)rank * a.M;
@@ -782,6 +808,7 @@ struct DownArgs {
     int T, H, M, K, E;
     const uint32_t *list;
     float *y, *ysh;
+    const float *pf_router; /* T = 1, H = 2048: rows E x H to touch (the next layer's router) or NULL */
 };
 
 template <int NT, int FMT>
@@ -1084,6 +1111,20 @@ __global__ __launch_bounds__(128) void k_gemv_down_combine1(DownArgs a, RouteArg
     for (int j = 0; j < 4; j++) sq[j] = ld_u4((const uint8_t *)(xs + osh[j]));
     const float hb = (h_in ? h_in : h_out)[r];
     const float sgv = ra.sgl[0];
+    /* the next layer's router (one wave per 4-row block of 2048 fp32, the
+     * T = 1 router's blocks): block j touches row 4 (x + 8 (s / 4)) + s % 4,
+     * x = j % 8, s = j / 8, so the rows reach the XCD whose router block
+     * reads them; one 4-byte load per 128-byte line */
+    uint32_t sink = 0;
+#ifndef NO_RPF
+    if (a.pf_router && wv == 1) {
+        const int x8 = blockIdx.x & 7, sl = blockIdx.x >> 3, row = 4 * (x8 + 8 * (sl >> 2)) + (sl & 3);
+        if (row < a.E) {
+            const float *p = a.pf_router + (size_t)row * 2048 + lane * 32;
+            asm volatile("global_load_dword %0, %1, off" : "=v"(sink) : "v"(p) : "memory");
+        }
+    }
+#endif
     float y[DC_K];
 #pragma unroll
     for (int k = 0; k < DC_K; k++) {
@@ -1107,6 +1148,7 @@ __global__ __launch_bounds__(128) void k_gemv_down_combine1(DownArgs a, RouteArg
         h_out[r] = o;
         if (res) res[r] = o;
     }
+    asm volatile("s_waitcnt vmcnt(0)" : : "v"(sink));
 }
 
 /* Batched down (T <= 8, in_dim = 512): a block = 4 waves = 64 output rows of
@@ -1169,6 +1211,11 @@ int launch_gemv_gate_up(const ExpertSide &ex, const SharedSide &sh, const RouteA
     a.sh_gate = sh.gate; a.sh_up = sh.up; a.sh_fmt = sh.gate_fmt; a.S = sh.gate ? sh.S : 0;
     a.x = x; a.T = T; a.H = H; a.M = M; a.K = K; a.E = E; a.list = ra.list; a.pairs = ra.pairs;
     a.act = act; a.act_sh = act_sh;
+    a.pf_down = a.pf_sh_down = nullptr; a.pf_down_stride = 0; a.pf_rb = a.pf_sh_rb = 0;
+    if (T == 1) {
+        a.pf_down = ex.down; a.pf_down_stride = ex.down_stride; a.pf_rb = (int)row_bytes(ex.down_fmt, M);
+        if (sh.gate) { a.pf_sh_down = sh.down; a.pf_sh_rb = (int)row_bytes(sh.down_fmt, sh.S); }
+    }
     const int umax = T * K < E ? T * K : E;
     a.routed_blocks = umax * (M / rows_blk);
     const int blocks = a.routed_blocks + (sh.gate ? sh.S / rows_blk : 0);
@@ -1251,7 +1298,7 @@ int launch_gemv_down(const ExpertSide &ex, const SharedSide &sh, const _Float16 
     if (!NT || H % 8 || M % 512 || (sh.gate && sh.S % 512)) return -2;
     if (ex.down_fmt != FQ4K && ex.down_fmt != FQ5K && ex.down_fmt != FQ6K) return -2;
     if (sh.gate && sh.down_fmt != FQ4K && sh.down_fmt != FQ5K && sh.down_fmt != FQ6K && sh.down_fmt != FQ8) return -2;
-    DownArgs a;
+    DownArgs a = {};
     a.down = ex.down; a.down_stride = ex.down_stride; a.fmt = ex.down_fmt;
     a.sh_down = sh.gate ? sh.down : nullptr; a.sh_fmt = sh.down_fmt; a.S = sh.S;
     a.act = act; a.act_sh = act_sh; a.T = T; a.H = H; a.M = M; a.K = K; a.E = E;
@@ -1277,7 +1324,8 @@ int launch_gemv_down(const ExpertSide &ex, const SharedSide &sh, const _Float16 
 
 int launch_gemv_down_combine1(const ExpertSide &ex, const SharedSide &sh, const RouteArgs &ra,
                               const _Float16 *act, const _Float16 *act_sh, int H, int M, int K,
-                              const float *h_in, float *h_out, float *res, hipStream_t s) {
+                              const float *h_in, float *h_out, float *res, hipStream_t s,
+                              const float *next_router) {
     if (K < 1 || K > DC_K || H % 8 || M != 512 || (sh.gate && sh.S != 512)) return -2;
     if (ex.down_fmt != FQ4K && ex.down_fmt != FQ5K && ex.down_fmt != FQ6K) return -2;
     const int sf = sh.gate ? sh.down_fmt : FQ4K;
@@ -1285,7 +1333,8 @@ int launch_gemv_down_combine1(const ExpertSide &ex, const SharedSide &sh, const 
     DownArgs a = {};
     a.down = ex.down; a.down_stride = ex.down_stride; a.fmt = ex.down_fmt;
     a.sh_down = sh.gate ? sh.down : nullptr; a.sh_fmt = sf; a.S = sh.gate ? sh.S : 0;
-    a.act = act; a.act_sh = act_sh; a.T = 1; a.H = H; a.M = M; a.K = K;
+    a.act = act; a.act_sh = act_sh; a.T = 1; a.H = H; a.M = M; a.K = K; a.E = ra.E;
+    a.pf_router = H == 2048 ? next_router : nullptr;
 #define DC_LAUNCH(EF, SF) KLAUNCH((k_gemv_down_combine1<EF, SF>), dim3(H / 8), dim3(128), 0, s, a, ra, h_in, h_out, res)
     DOWN_FMT_SWITCH(ex.down_fmt, sf, DC_LAUNCH);
 #undef DC_LAUNCH
