@@ -238,8 +238,8 @@ __global__ __launch_bounds__(256) void k_pack_router(const float *W, int H, _Flo
  * (v_mfma_f32_16x16x32_f16, tokens as A rows, experts as B columns).  Wave w
  * covers k in [w H/NW, (w+1) H/NW) in chunks of S steps of 32; a chunk's
  * loads are all issued before its first MFMA.  The NW partial tiles are
- * summed through LDS in wave order.  The blocks of the first expert tile also
- * stage x as fp16 for the grouped GEMMs (round to nearest even, each 4-group
+ * summed through LDS in wave order.  The blocks of a token tile also stage
+ * its x as fp16 for the grouped GEMMs (round to nearest even, each 4-group
  * stored (0,2,1,3)). */
 template <int TTS, int TES, int NW, int S>
 __global__ __launch_bounds__(64 * NW) void k_route_approx(RouteArgs a) {
@@ -260,7 +260,7 @@ __global__ __launch_bounds__(64 * NW) void k_route_approx(RouteArgs a) {
     for (int ts = 0; ts < TTS; ts++) {
         const int t = t0 + ts * 16 + r;
         xr[ts] = a.x + (size_t)min(t, T - 1) * H + kq;
-        stage[ts] = a.x16 && ex == 0 && t < T;
+        stage[ts] = a.x16 && t < T;
     }
     const _Float16 *wr[TES];
 #pragma unroll
@@ -306,13 +306,19 @@ __global__ __launch_bounds__(64 * NW) void k_route_approx(RouteArgs a) {
             }
         }
         /* staging stores after the chunk's last load is consumed: stores
-         * share the load counter, so earlier ones would hold up the waits */
+         * share the load counter, so earlier ones would hold up the waits.
+         * With one 16-token tile per block (T <= 1024) the token tile's nex
+         * expert-tile blocks split the steps (step i of a wave's k range goes
+         * to block i % nex), so no block carries all of the tile's stores
+         * (T = 512: 12.2 -> 11.0 us); the larger tiles of bigger batches
+         * stage from the first expert tile's blocks (splitting them measured
+         * 0.8 us slower at T = 2048). */
 #pragma unroll
         for (int st = 0; st < S; st++) {
             const int k = k0 + 32 * st;
 #pragma unroll
             for (int ts = 0; ts < TTS; ts++)
-                if (stage[ts] && k < ke) {
+                if (stage[ts] && k < ke && (TTS == 1 ? ((k - kb) >> 5) % nex == ex : ex == 0)) {
                     const h8 v = A[st][ts];
                     _Float16 *d = a.x16 + (xr[ts] - a.x) + k;
                     *(h4 *)d = h4{v[0], v[2], v[1], v[3]};
