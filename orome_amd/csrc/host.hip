@@ -550,7 +550,7 @@ static int forward_impl(orome_hip_ctx *c, const OromeHipModelConfig *cfg, const 
     a.offsets = c->offsets; a.pairs = c->pairs; a.pos = c->pos; a.list = c->list;
     a.counter = c->counter;
     a.norm_h = NULL; a.norm_w = NULL; a.norm_eps = cfg->rms_norm_eps; a.xnorm = c->xnorm;
-    a.x16 = NULL;
+    a.x16 = NULL; a.x16in = NULL;
     a.W16 = NULL; a.wscale = NULL; a.wnorm = NULL; a.eps_c1 = a.eps_c2 = 0.0f;
     a.tiles_s = NULL; a.has_shared = 0;
 
@@ -634,12 +634,15 @@ static int forward_impl(orome_hip_ctx *c, const OromeHipModelConfig *cfg, const 
                     "combine");
         }
     } else {
-        a.x16 = c->x16; /* the router writes the fp16 copy of x the GEMMs read */
+        /* the router writes the fp16 copy of x the GEMMs read, unless the
+         * previous layer's combine + RMSNorm already wrote it (a stack) */
+        a.x16 = pre_normed ? NULL : c->x16;
         const Pack *rpk = find_pack(c, ex.gate, sh.gate);
         if (rpk && rpk->r16 && rpk->rkey == a.W && H <= 4096 && K <= 64 && !route_exact_only()) {
             /* registered layer: approximate logits on the matrix cores, then
              * the canonical logits of the experts that can win */
             a.W16 = rpk->r16;
+            if (pre_normed) a.x16in = c->x16;
             a.wscale = rpk->rscale;
             a.wnorm = rpk->rnorm;
             route_eps_coeffs(H, &a.eps_c1, &a.eps_c2);
@@ -698,7 +701,7 @@ static int forward_impl(orome_hip_ctx *c, const OromeHipModelConfig *cfg, const 
         if (fuse_next_norm) /* also the next layer's RMSNorm of h_out into xnorm */
             TLAUNCH(c, ST_COMBINE,
                     launch_combine_norm(c->y, c->ysh, c->pos, c->w, c->sgl, S ? 1 : 0, h_in, h_out, fo.res, fo.ssq, T, H, K, next_norm_w,
-                                        cfg->rms_norm_eps, c->xnorm, s),
+                                        cfg->rms_norm_eps, c->xnorm, c->x16, s),
                     "combine + next RMSNorm");
         else
             TLAUNCH(c, ST_COMBINE, launch_combine(c->y, c->ysh, c->pos, c->w, c->sgl, S ? 1 : 0, h_in, h_out, fo.res, fo.ssq, T, H, K, s),

@@ -43,6 +43,8 @@ struct RouteArgs {
     int T, E, H, K;
     float *logits;       /* [T][E+1] */
     _Float16 *x16;       /* large-batch router: also writes x as fp16, (0,2,1,3) per 4-group (or NULL) */
+    const _Float16 *x16in; /* two-pass router: x already staged so (the previous layer's combine), read
+                              in place of x by the approximation pass; NULL: x */
     int32_t *idx;        /* [T][K] */
     float *w;            /* [T][K] */
     float *sgl;          /* [T] shared-gate logit */
@@ -146,7 +148,7 @@ int launch_pack_q8(const uint8_t *src, uint8_t *dst, int R, int K, int E, size_t
  * RMSNorm of h_out into xnorm (nw: its weight, or NULL for ones) */
 int launch_combine_norm(const float *y, const float *ysh, const uint32_t *pos, const float *w, const float *sgl,
                         int has_shared, const float *h_in, float *h_out, float *res, float *ssq, int T, int H, int K,
-                        const float *nw, float eps, float *xnorm, hipStream_t s);
+                        const float *nw, float eps, float *xnorm, _Float16 *x16, hipStream_t s);
 /* combine; res (a copy of h_out) and ssq (the [T][H/256] canonical Sigma h^2
  * parts) may be NULL */
 int launch_combine(const float *y, const float *ysh, const uint32_t *pos, const float *w,

@@ -213,7 +213,7 @@ __global__ __launch_bounds__(64 * CN_W) void k_combine_norm(const float *y, cons
                                                              const float *w, const float *sgl, int has_sh,
                                                              const float *h_in, float *h_out, float *res, float *ssq,
                                                              int T, int H, int K, const float *nw, float eps,
-                                                             float *xnorm) {
+                                                             float *xnorm, _Float16 *x16) {
     __shared__ f4 ro[CANON_NI][64];
     __shared__ float sc;
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, t = blockIdx.x;
@@ -277,23 +277,25 @@ __global__ __launch_bounds__(64 * CN_W) void k_combine_norm(const float *y, cons
             r.z = (o.z * scale) * __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, wn.z) & 0xFFFF0000u);
             r.w = (o.w * scale) * __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, wn.w) & 0xFFFF0000u);
             *(f4 *)(xnorm + (size_t)t * H + j) = r;
+            if (x16) /* the GEMMs' fp16 copy, (0,2,1,3) within the 4-group */
+                *(h4 *)(x16 + (size_t)t * H + j) = h4{(_Float16)r.x, (_Float16)r.z, (_Float16)r.y, (_Float16)r.w};
         }
     }
 }
 
 int launch_combine_norm(const float *y, const float *ysh, const uint32_t *pos, const float *w, const float *sgl,
                         int has_shared, const float *h_in, float *h_out, float *res, float *ssq, int T, int H, int K,
-                        const float *nw, float eps, float *xnorm, hipStream_t s) {
+                        const float *nw, float eps, float *xnorm, _Float16 *x16, hipStream_t s) {
     const int NI = H / 256;
     if (H % 512 || NI > 2 * 8 || NI > CANON_NI || K < 1 || K > OROME_MAXK) return -2;
 #define CN_LAUNCH(CW)                                                                                            \
     do {                                                                                                         \
         if (K <= 8)                                                                                              \
             KLAUNCH((k_combine_norm<CW, 8>), dim3((unsigned)T), dim3(64 * CW), 0, s, y, ysh, pos, w,   \
-                               sgl, has_shared, h_in, h_out, res, ssq, T, H, K, nw, eps, xnorm);               \
+                               sgl, has_shared, h_in, h_out, res, ssq, T, H, K, nw, eps, xnorm, x16);               \
         else                                                                                                     \
             KLAUNCH((k_combine_norm<CW, OROME_MAXK>), dim3((unsigned)T), dim3(64 * CW), 0, s, y, ysh, \
-                               pos, w, sgl, has_shared, h_in, h_out, res, ssq, T, H, K, nw, eps, xnorm);         \
+                               pos, w, sgl, has_shared, h_in, h_out, res, ssq, T, H, K, nw, eps, xnorm, x16);         \
     } while (0)
     switch (NI / 2) {
         case 1: CN_LAUNCH(1); break;

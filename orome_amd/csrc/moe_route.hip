@@ -187,7 +187,10 @@ __global__ __launch_bounds__(256) void k_topk(RouteArgs a) {
  * rounded up at pack time and |x| is rounded up in pass 2; a non-finite
  * approximation or bound makes the expert a candidate. */
 
-/* W16/wscale/wnorm for one router matrix: a block per row. */
+/* W16/wscale/wnorm for one router matrix: a block per row.  W16 rows hold
+ * each 4-group of k in the order (0,2,1,3), the order of the fp16 copy of x
+ * that the grouped GEMMs read, so the approximation pass can take either
+ * that copy or x itself (permuted as it converts) as its other operand. */
 __global__ __launch_bounds__(256) void k_pack_router(const float *W, int H, _Float16 *W16, float *wscale,
                                                       float *wnorm) {
     const int e = blockIdx.x;
@@ -224,7 +227,8 @@ __global__ __launch_bounds__(256) void k_pack_router(const float *W, int H, _Flo
         }
     }
     const float sc = ldexpf(1.0f, sh);
-    for (int i = threadIdx.x; i < H; i += 256) W16[(size_t)e * H + i] = (_Float16)(row[i] * sc);
+    for (int i = threadIdx.x; i < H; i += 256)
+        W16[(size_t)e * H + ((i & ~3) | ((i & 1) << 1) | ((i >> 1) & 1))] = (_Float16)(row[i] * sc);
     if (threadIdx.x == 0) {
         wscale[e] = ldexpf(1.0f, -sh);
         /* sqrt in double, then one float step up: an upper bound of |w| */
@@ -241,7 +245,7 @@ __global__ __launch_bounds__(256) void k_pack_router(const float *W, int H, _Flo
  * summed through LDS in wave order.  The blocks of a token tile also stage
  * its x as fp16 for the grouped GEMMs (round to nearest even, each 4-group
  * stored (0,2,1,3)). */
-template <int TTS, int TES, int NW, int S>
+template <int TTS, int TES, int NW, int S, bool XH>
 __global__ __launch_bounds__(64 * NW) void k_route_approx(RouteArgs a) {
     /* the wave index is uniform: say so, or the k loop is compiled divergent */
     const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -254,13 +258,16 @@ __global__ __launch_bounds__(64 * NW) void k_route_approx(RouteArgs a) {
     if (ty * 16 * TTS >= T) return;
     const int e0 = ex * (16 * TES), t0 = ty * (16 * TTS);
     const int r = lane & 15, kq = (lane >> 4) * 8;
+    /* XH: x comes as the staged fp16 copy (a.x16in), else as fp32 */
     const float *xr[TTS];
+    const _Float16 *xhr[TTS];
     bool stage[TTS];
 #pragma unroll
     for (int ts = 0; ts < TTS; ts++) {
         const int t = t0 + ts * 16 + r;
         xr[ts] = a.x + (size_t)min(t, T - 1) * H + kq;
-        stage[ts] = a.x16 && t < T;
+        xhr[ts] = XH ? a.x16in + (size_t)min(t, T - 1) * H + kq : nullptr;
+        stage[ts] = !XH && a.x16 && t < T;
     }
     const _Float16 *wr[TES];
 #pragma unroll
@@ -272,6 +279,7 @@ __global__ __launch_bounds__(64 * NW) void k_route_approx(RouteArgs a) {
         for (int es = 0; es < TES; es++) acc[ts][es] = f4{0, 0, 0, 0};
     const int kw = H / NW, kb = wv * kw, ke = kb + kw;
     f4 xa[S][TTS][2];
+    h8 xh[S][TTS];
     h8 B[S][TES];
     /* loads unconditional (k clamped into the range; a clamped step is not
      * used): a load under a branch makes the compiler wait for it */
@@ -281,8 +289,12 @@ __global__ __launch_bounds__(64 * NW) void k_route_approx(RouteArgs a) {
             const int k = min(k0 + 32 * st, ke - 32);
 #pragma unroll
             for (int ts = 0; ts < TTS; ts++) {
-                xa[st][ts][0] = *(const f4 *)(xr[ts] + k);
-                xa[st][ts][1] = *(const f4 *)(xr[ts] + k + 4);
+                if (XH) {
+                    xh[st][ts] = *(const h8 *)(xhr[ts] + k);
+                } else {
+                    xa[st][ts][0] = *(const f4 *)(xr[ts] + k);
+                    xa[st][ts][1] = *(const f4 *)(xr[ts] + k + 4);
+                }
             }
 #pragma unroll
             for (int es = 0; es < TES; es++) B[st][es] = *(const h8 *)(wr[es] + k);
@@ -296,9 +308,11 @@ __global__ __launch_bounds__(64 * NW) void k_route_approx(RouteArgs a) {
             if (k < ke) {
 #pragma unroll
                 for (int ts = 0; ts < TTS; ts++) {
+                    /* each 4-group in W16's (0,2,1,3) order */
                     const f4 lo = xa[st][ts][0], hi = xa[st][ts][1];
-                    A[st][ts] = h8{(_Float16)lo.x, (_Float16)lo.y, (_Float16)lo.z, (_Float16)lo.w,
-                                   (_Float16)hi.x, (_Float16)hi.y, (_Float16)hi.z, (_Float16)hi.w};
+                    A[st][ts] = XH ? xh[st][ts]
+                                   : h8{(_Float16)lo.x, (_Float16)lo.z, (_Float16)lo.y, (_Float16)lo.w,
+                                        (_Float16)hi.x, (_Float16)hi.z, (_Float16)hi.y, (_Float16)hi.w};
 #pragma unroll
                     for (int es = 0; es < TES; es++)
                         acc[ts][es] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[st][ts], B[st][es], acc[ts][es], 0, 0, 0);
@@ -319,10 +333,7 @@ __global__ __launch_bounds__(64 * NW) void k_route_approx(RouteArgs a) {
 #pragma unroll
             for (int ts = 0; ts < TTS; ts++)
                 if (stage[ts] && k < ke && (TTS == 1 ? ((k - kb) >> 5) % nex == ex : ex == 0)) {
-                    const h8 v = A[st][ts];
-                    _Float16 *d = a.x16 + (xr[ts] - a.x) + k;
-                    *(h4 *)d = h4{v[0], v[2], v[1], v[3]};
-                    *(h4 *)(d + 4) = h4{v[4], v[6], v[5], v[7]};
+                    *(h8 *)(a.x16 + (xr[ts] - a.x) + k) = A[st][ts];
                 }
         }
     };
@@ -905,10 +916,13 @@ int launch_route_approx(const RouteArgs &a, hipStream_t s) {
     if (!a.W16 || !a.wscale || a.H % 256 || a.T < 1) return -2;
     /* 1-D grid: expert tiles x token tiles rounded up to 8 (see the kernel) */
     auto grid = [&](int te, int tt) { return dim3((unsigned)((a.E + te - 1) / te * (((a.T + tt - 1) / tt + 7) / 8 * 8))); };
-    if (a.T <= 1024)
-        KLAUNCH((k_route_approx<1, 2, 8, 8>), grid(32, 16), dim3(512), 0, s, a);
-    else
-        KLAUNCH((k_route_approx<2, 4, 4, 4>), grid(64, 32), dim3(256), 0, s, a);
+    if (a.T <= 1024) {
+        if (a.x16in) KLAUNCH((k_route_approx<1, 2, 8, 8, true>), grid(32, 16), dim3(512), 0, s, a);
+        else KLAUNCH((k_route_approx<1, 2, 8, 8, false>), grid(32, 16), dim3(512), 0, s, a);
+    } else {
+        if (a.x16in) KLAUNCH((k_route_approx<2, 4, 4, 4, true>), grid(64, 32), dim3(256), 0, s, a);
+        else KLAUNCH((k_route_approx<2, 4, 4, 4, false>), grid(64, 32), dim3(256), 0, s, a);
+    }
     return hipGetLastError() == hipSuccess ? 0 : -3;
 }
 
