@@ -759,7 +759,11 @@ extern "C" int orome_moe_stack_forward(orome_hip_ctx *c, const OromeHipModelConf
         if (!lts[l].routing_gate.buffer) return orome_fail(OROME_EINVAL, "orome_moe_stack_forward: layer %d", l);
         const bool next = fuse && l + 1 < n_layers;
         FwdOut fo{NULL, NULL};
-        if (l + 1 < n_layers && lts[l + 1].routing_gate.buffer)
+        /* (only a router the next layer's forward will accept: F32, and
+         * [E][H] where the reference gives its shape) */
+        const OromeHipTensorRef *nr = l + 1 < n_layers ? &lts[l + 1].routing_gate : NULL;
+        if (nr && nr->buffer && nr->format == OROME_QFMT_F32 && (!nr->out_dim || (int)nr->out_dim >= cfg->num_experts) &&
+            (!nr->in_dim || (int)nr->in_dim == cfg->hidden_dim))
             fo.next_router = (const float *)dev_addr(lts[l + 1].routing_gate.buffer, lts[l + 1].routing_gate.offset);
         int rc = forward_impl(c, cfg, &elrs[l], &lts[l], NULL, h, h, T, K, h, norm_w(l), s, fo,
                               next ? norm_w(l + 1) : NULL, next ? 1 : 0, fuse && l > 0 ? 1 : 0);
