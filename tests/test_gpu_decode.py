@@ -202,6 +202,35 @@ def test_topk_teacher_forced(base):
             assert np.allclose(w[ok], rw[ok], rtol=2e-6, atol=1e-7)
 
 
+def _tie_group(img, om):
+    """Ten identical router rows scaled by 10: for about a quarter of the
+    tokens their logit is among the K = 8 largest, and the winners then take
+    some of the ten exact ties (the lowest ids must win)."""
+    W = om.array("blk.0.ffn_gate_inp.weight", np.float32).reshape(om.E, om.H)
+    W[16:26] = W[16] * 10
+
+
+@pytest.mark.parametrize("T", [1, 2, 8])
+def test_decode_planted_ties(T):
+    """Decode with exact ties at the top-K boundary: the one-token gate/up
+    (selection folded in), the two-token GEMV routing and the small-batch
+    routing select what the oracle selects, bit for bit, and the outputs
+    match."""
+    banner("decode with a planted tie group, T=%d" % T)
+    p = Pair(mutate=_tie_group, seed=71)
+    split = 0
+    for i in range(48 // T):
+        x, h = p.inputs(T, seed=700 + i)
+        out, dbg = p.run(0, x, h)
+        rdbg = check_routing(p, x, dbg, 8)
+        split += int(np.sum(np.isin(rdbg["idx"], np.arange(16, 26)).sum(axis=1) >= 1))
+        ref = p.om.forward(0, x, h)
+        assert rel_l2(out - h, ref - h) < TOL
+    print("tokens whose winners take part of the tie group: %d" % split)
+    assert split >= 4  # the planted case is exercised
+    p.gm.close()
+
+
 @pytest.mark.parametrize("fmt_name,kw", [("Q4_K", {}), ("Q5_K", dict(down=13)), ("Q6_K", dict(down=14)),
                                          ("Q8_0", dict(shared=8))])
 def test_dequant_bit_exact(fmt_name, kw):
