@@ -552,7 +552,7 @@ static int forward_impl(orome_hip_ctx *c, const OromeHipModelConfig *cfg, const 
     a.norm_h = NULL; a.norm_w = NULL; a.norm_eps = cfg->rms_norm_eps; a.xnorm = c->xnorm;
     a.x16 = NULL; a.x16in = NULL;
     a.W16 = NULL; a.wscale = NULL; a.wnorm = NULL; a.eps_c1 = a.eps_c2 = 0.0f;
-    a.tiles_s = NULL; a.has_shared = 0;
+    a.tiles_s = NULL; a.has_shared = 0; a.dcnt = NULL;
 
     int path = c->path;
     /* AUTO: GEMV kernels up to 2 tokens (routing folded into gate/up), the
@@ -648,13 +648,15 @@ static int forward_impl(orome_hip_ctx *c, const OromeHipModelConfig *cfg, const 
             route_eps_coeffs(H, &a.eps_c1, &a.eps_c2);
             TLAUNCH(c, ST_ROUTE, launch_route_approx(a, s), "router logits (matrix cores) + fp16 staging");
             a.x16 = NULL;
+            /* where the dispatch takes three launches, the top-k counts for it */
+            if (dispatch_three_launches(a)) a.dcnt = c->dcount;
             TLAUNCH(c, ST_TOPK, launch_topk_exact(a, s), "top-k with canonical recomputation");
         } else {
             TLAUNCH(c, ST_ROUTE, launch_route_logits(a, s), "router logits + fp16 staging");
             a.x16 = NULL;
             TLAUNCH(c, ST_TOPK, launch_topk(a, s), "top-k");
         }
-        TLAUNCH(c, ST_DISPATCH, launch_dispatch(a, c->tiles, c->tiles_b, S ? 1 : 0, c->dcount, s), "dispatch");
+        TLAUNCH(c, ST_DISPATCH, launch_dispatch(a, c->tiles, c->tiles_b, S ? 1 : 0, c->dcount, s, a.dcnt ? 1 : 0), "dispatch");
         /* one launch per tile list (grid sized for the most tiles it can hold) */
         /* small batches (T K <= 32 E): every expert in 32-row tiles, the
          * shared expert too, and no big-tile list */

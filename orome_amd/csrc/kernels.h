@@ -69,6 +69,11 @@ struct RouteArgs {
      * tile list (one tile per active expert, then the shared expert's) */
     uint32_t *tiles_s;
     int has_shared;
+    /* exact top-k above the one-block dispatch's size: also adds each
+     * selected (token, expert) to dcnt[token / 256][expert], the counts the
+     * three-launch dispatch would otherwise count (launch_dispatch(counted));
+     * the dispatch's scatter returns them to zero.  NULL: not counted */
+    uint32_t *dcnt;
 };
 
 struct ExpertSide {
@@ -97,7 +102,10 @@ int launch_pack_router(const float *W, int E, int H, _Float16 *W16, float *wscal
 void route_eps_coeffs(int H, float *c1, float *c2);
 int dispatch_blocks(int T); /* rows of the dispatch count scratch ([rows][E] words) */
 int launch_dispatch(const RouteArgs &a, uint32_t *tiles_s, uint32_t *tiles_b, int has_shared, uint32_t *cnt,
-                    hipStream_t s);
+                    hipStream_t s, int counted = 0);
+/* the dispatch runs in three launches (count, scan, scatter) for these
+ * shapes, one block otherwise */
+bool dispatch_three_launches(const RouteArgs &a);
 
 /* decode gate/up; with route_in_block the top-k + dispatch of the call is
  * folded in (every block selects; block 0 publishes the routing outputs in

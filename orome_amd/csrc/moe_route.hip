@@ -505,7 +505,9 @@ __global__ __launch_bounds__(256) void k_topk_exact(RouteArgs a) {
         if (lane * EPL + j < E) lrow[lane * EPL + j] = v[j];
     }
     if (lane == 0) lrow[E] = sg;
-    wave_topk_keys<EPL>(key, sg, K, lane, a.idx + t * K, a.w + t * K, a.sgl + t, nullptr);
+    const TopkLane r = wave_topk_keys<EPL>(key, sg, K, lane, a.idx + t * K, a.w + t * K, a.sgl + t, nullptr);
+    /* the three-launch dispatch's per-block expert counts (order-free) */
+    if (a.dcnt && lane < K) atomicAdd(a.dcnt + (size_t)(t / 256) * E + r.id, 1u);
 }
 
 /* Dispatch for any T, in three launches over blocks of DSP_TOK tokens.  A
@@ -687,7 +689,7 @@ __global__ __launch_bounds__(DSP_THREADS) void k_dispatch_scan(RouteArgs a, uint
 }
 
 template <int KM>
-__global__ __launch_bounds__(DSP_TOK) void k_dispatch_scatter(RouteArgs a, const uint32_t *base) {
+__global__ __launch_bounds__(DSP_TOK) void k_dispatch_scatter(RouteArgs a, uint32_t *base) {
     extern __shared__ uint32_t mask[]; /* E * DSP_WORDS, then E * DSP_WORDS word prefixes */
     uint32_t *wpre = mask + a.E * DSP_WORDS;
     int ek[KM];
@@ -695,6 +697,8 @@ __global__ __launch_bounds__(DSP_TOK) void k_dispatch_scatter(RouteArgs a, const
     const int E = a.E, K = a.K, tid = threadIdx.x, t = blockIdx.x * DSP_TOK + tid;
     for (int e = tid; e < E; e += DSP_TOK) {
         uint32_t run = a.offsets[e] + base[(size_t)blockIdx.x * E + e];
+        /* back to zero: the exact top-k of the next forward may count into it */
+        base[(size_t)blockIdx.x * E + e] = 0u;
 #pragma unroll
         for (int w = 0; w < DSP_WORDS; w++) {
             wpre[e * DSP_WORDS + w] = run;
@@ -958,25 +962,30 @@ int launch_topk_exact(const RouteArgs &a, hipStream_t s) {
 
 int dispatch_blocks(int T) { return (T + DSP_TOK - 1) / DSP_TOK; }
 
-int launch_dispatch(const RouteArgs &a, uint32_t *tiles_s, uint32_t *tiles_b, int has_shared, uint32_t *cnt,
-                    hipStream_t s) {
-    const size_t lds = sizeof(uint32_t) * (size_t)a.E * DSP_WORDS * 2;
-    /* one scan lane per expert; 16-bit fields for the pair counts */
-    if (lds > 64 * 1024 || a.E > DSP_THREADS || a.K > OROME_MAXK || (long)a.T * a.K > 32768) return -2;
 #ifndef DISPATCH_ONE
 #define DISPATCH_ONE 1
 #endif
-    if (DISPATCH_ONE && a.E <= 256 && a.T <= DSP_THREADS) {
+bool dispatch_three_launches(const RouteArgs &a) { return !(DISPATCH_ONE && a.E <= 256 && a.T <= DSP_THREADS); }
+
+/* counted: cnt already holds the per-block expert counts (the exact top-k
+ * added them), so the count launch is skipped */
+int launch_dispatch(const RouteArgs &a, uint32_t *tiles_s, uint32_t *tiles_b, int has_shared, uint32_t *cnt,
+                    hipStream_t s, int counted) {
+    const size_t lds = sizeof(uint32_t) * (size_t)a.E * DSP_WORDS * 2;
+    /* one scan lane per expert; 16-bit fields for the pair counts */
+    if (lds > 64 * 1024 || a.E > DSP_THREADS || a.K > OROME_MAXK || (long)a.T * a.K > 32768) return -2;
+    if (!dispatch_three_launches(a)) {
         if (a.K <= 8) KLAUNCH(k_dispatch_one<8>, dim3(1), dim3(DSP_THREADS), 0, s, a, tiles_s, tiles_b, has_shared);
         else KLAUNCH(k_dispatch_one<OROME_MAXK>, dim3(1), dim3(DSP_THREADS), 0, s, a, tiles_s, tiles_b, has_shared);
         return hipGetLastError() == hipSuccess ? 0 : -3;
     }
     const int G = dispatch_blocks(a.T);
-    if (a.K <= 8) KLAUNCH(k_dispatch_count<8>, dim3(G), dim3(DSP_TOK), lds / 2, s, a, cnt);
+    if (counted) {
+    } else if (a.K <= 8) KLAUNCH(k_dispatch_count<8>, dim3(G), dim3(DSP_TOK), lds / 2, s, a, cnt);
     else KLAUNCH(k_dispatch_count<OROME_MAXK>, dim3(G), dim3(DSP_TOK), lds / 2, s, a, cnt);
     KLAUNCH(k_dispatch_scan, dim3(1), dim3(DSP_THREADS), 0, s, a, cnt, G, tiles_s, tiles_b, has_shared);
-    if (a.K <= 8) KLAUNCH(k_dispatch_scatter<8>, dim3(G), dim3(DSP_TOK), lds, s, a, (const uint32_t *)cnt);
-    else KLAUNCH(k_dispatch_scatter<OROME_MAXK>, dim3(G), dim3(DSP_TOK), lds, s, a, (const uint32_t *)cnt);
+    if (a.K <= 8) KLAUNCH(k_dispatch_scatter<8>, dim3(G), dim3(DSP_TOK), lds, s, a, cnt);
+    else KLAUNCH(k_dispatch_scatter<OROME_MAXK>, dim3(G), dim3(DSP_TOK), lds, s, a, cnt);
     return hipGetLastError() == hipSuccess ? 0 : -3;
 }
 
