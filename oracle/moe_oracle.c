@@ -308,7 +308,7 @@ ORC_API void orc_router_logits(const float *W, const float *wsg, const float *x,
 /* inference/src/shaders.metal:1141-1234 (softmax_topk_route):
  *  - K rounds of argmax over the raw logits (plus the optional per-expert bias
  *    of the skewed-routing config); slot order = descending logit;
- *  - exact ties go to the lower expert index.  That is the rule BASELINE's
+ *  - exact ties go to the lower expert index.  That is the rule the task's
  *    contract states; the reference's own kernel resolves an exact tie by the
  *    position in its shuffle-down tree (1166-1200: lane L keeps its value
  *    against L + offset on a tie, so a tie between experts 1 and 2 selects 2,

@@ -1,4 +1,4 @@
-"""BASELINE config 4 on the GPU at its workload: the 40-layer stack of MoE
+"""Benchmark config 4 on the GPU at its workload: the 40-layer stack of MoE
 blocks (256 experts top-8 + shared, hidden 2048, expert intermediate 512,
 Q6_K down on every 4th layer, independent seeded weights per layer; about
 17.6 GB of GGUF weights resident in HBM), h_{l+1} = h_l + MoE_l(RMSNorm(h_l)).
@@ -13,7 +13,7 @@ permutation grouped by expert, offsets are the histogram, weights sum to 1,
 outputs finite), a 64-token oracle sample of the last layer's input->output,
 and the stack entry point bit-identical to the 40 layer calls.
 
-The synthetic weights use the centred Q4_K option (the literal BASELINE
+The synthetic weights use the centred Q4_K option (the config's literal
 distribution makes every Q4_K row's mean large, and 40 residual layers then
 overflow the fp16 activation staging in the oracle as on the GPU)."""
 import numpy as np
