@@ -646,10 +646,11 @@ static int forward_impl(orome_hip_ctx *c, const OromeHipModelConfig *cfg, const 
             a.wscale = rpk->rscale;
             a.wnorm = rpk->rnorm;
             route_eps_coeffs(H, &a.eps_c1, &a.eps_c2);
+            /* where the dispatch takes more than one launch, the top-k counts
+             * for it (into counts the approximation pass clears) */
+            if (dispatch_three_launches(a)) a.dcnt = c->dcount;
             TLAUNCH(c, ST_ROUTE, launch_route_approx(a, s), "router logits (matrix cores) + fp16 staging");
             a.x16 = NULL;
-            /* where the dispatch takes three launches, the top-k counts for it */
-            if (dispatch_three_launches(a)) a.dcnt = c->dcount;
             TLAUNCH(c, ST_TOPK, launch_topk_exact(a, s), "top-k with canonical recomputation");
         } else {
             TLAUNCH(c, ST_ROUTE, launch_route_logits(a, s), "router logits + fp16 staging");

@@ -72,7 +72,7 @@ struct RouteArgs {
     /* exact top-k above the one-block dispatch's size: also adds each
      * selected (token, expert) to dcnt[token / 256][expert], the counts the
      * three-launch dispatch would otherwise count (launch_dispatch(counted));
-     * the dispatch's scatter returns them to zero.  NULL: not counted */
+     * the approximation pass clears them first.  NULL: not counted */
     uint32_t *dcnt;
 };
 

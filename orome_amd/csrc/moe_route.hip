@@ -257,6 +257,10 @@ __global__ __launch_bounds__(64 * NW) void k_route_approx(RouteArgs a) {
     const int ex = q % nex, ty = (q / nex) * 8 + (blockIdx.x & 7);
     if (ty * 16 * TTS >= T) return;
     const int e0 = ex * (16 * TES), t0 = ty * (16 * TTS);
+    /* the exact top-k that follows counts into dcnt: clear it ((T / 256
+     * rounded up) E words) */
+    if (a.dcnt && blockIdx.x == 0)
+        for (int i = threadIdx.x; i < (T + 255) / 256 * E; i += 64 * NW) a.dcnt[i] = 0u;
     const int r = lane & 15, kq = (lane >> 4) * 8;
     /* XH: x comes as the staged fp16 copy (a.x16in), else as fp32 */
     const float *xr[TTS];
@@ -629,7 +633,9 @@ DEV void put_tiles(uint32_t *list, uint32_t t0, uint32_t e, uint32_t first, uint
  * xo[tid] (LDS, when given).  Every thread of the block calls it; wsum:
  * LDS, 32 words. */
 DEV void dispatch_lists(const RouteArgs &a, uint32_t c, uint32_t *xo, uint32_t *wsum, uint32_t *tiles_s,
-                        uint32_t *tiles_b, int has_shared) {
+                        uint32_t *tiles_b, int has_shared, bool glob = true) {
+    /* glob false: the exclusive offsets into xo only (the blocks of a
+     * dispatch that one other block writes the lists for) */
     const int E = a.E, T = a.T, tid = threadIdx.x;
     const bool so = tile_small_only(a), mine = tid < E;
     if (!mine) c = 0;
@@ -638,8 +644,12 @@ DEV void dispatch_lists(const RouteArgs &a, uint32_t c, uint32_t *xo, uint32_t *
     scan2_block(x, y, wsum, tx, ty);
     if (mine) {
         const uint32_t o = (x & 0xFFFFu) - c;
-        a.offsets[tid] = o;
         if (xo) xo[tid] = o;
+    }
+    if (!glob) return;
+    if (mine) {
+        const uint32_t o = (x & 0xFFFFu) - c;
+        a.offsets[tid] = o;
         if (c) {
             const uint32_t r = (x >> 16) - 1;
             ACT_E(a.list, r) = (uint32_t)tid;
@@ -689,7 +699,7 @@ __global__ __launch_bounds__(DSP_THREADS) void k_dispatch_scan(RouteArgs a, uint
 }
 
 template <int KM>
-__global__ __launch_bounds__(DSP_TOK) void k_dispatch_scatter(RouteArgs a, uint32_t *base) {
+__global__ __launch_bounds__(DSP_TOK) void k_dispatch_scatter(RouteArgs a, const uint32_t *base) {
     extern __shared__ uint32_t mask[]; /* E * DSP_WORDS, then E * DSP_WORDS word prefixes */
     uint32_t *wpre = mask + a.E * DSP_WORDS;
     int ek[KM];
@@ -697,12 +707,63 @@ __global__ __launch_bounds__(DSP_TOK) void k_dispatch_scatter(RouteArgs a, uint3
     const int E = a.E, K = a.K, tid = threadIdx.x, t = blockIdx.x * DSP_TOK + tid;
     for (int e = tid; e < E; e += DSP_TOK) {
         uint32_t run = a.offsets[e] + base[(size_t)blockIdx.x * E + e];
-        /* back to zero: the exact top-k of the next forward may count into it */
-        base[(size_t)blockIdx.x * E + e] = 0u;
 #pragma unroll
         for (int w = 0; w < DSP_WORDS; w++) {
             wpre[e * DSP_WORDS + w] = run;
             run += __popc(mask[e * DSP_WORDS + w]);
+        }
+    }
+    lds_barrier();
+    const uint32_t below = (1u << (tid & 31)) - 1u;
+#pragma unroll
+    for (int k = 0; k < KM; k++)
+        if (ek[k] >= 0) {
+            const int i = ek[k] * DSP_WORDS + (tid >> 5);
+            const uint32_t pos = wpre[i] + __popc(mask[i] & below);
+            const uint32_t p = (uint32_t)(t * K + k);
+            a.pairs[pos] = p;
+            a.pos[p] = pos;
+        }
+}
+
+/* Scan and scatter in one launch, for counts the exact top-k made (E <=
+ * DSP_TOK): every block forms every expert's total and its own prefix over
+ * the earlier blocks from the counts (G E words), scans the totals, and
+ * block 0 writes the offsets and lists; then each scatters its tokens as
+ * k_dispatch_scatter does.  The counts are left as they are (the
+ * approximation pass of the next forward clears them). */
+template <int KM>
+__global__ __launch_bounds__(DSP_TOK) void k_dispatch_scan_scatter(RouteArgs a, const uint32_t *cnt, int G,
+                                                                   uint32_t *tiles_s, uint32_t *tiles_b,
+                                                                   int has_shared) {
+    extern __shared__ uint32_t mask[]; /* E * DSP_WORDS, then E * DSP_WORDS word prefixes */
+    __shared__ uint32_t xo[DSP_TOK], wsum[32];
+    uint32_t *wpre = mask + a.E * DSP_WORDS;
+    const int E = a.E, K = a.K, tid = threadIdx.x, t = blockIdx.x * DSP_TOK + tid, gb = blockIdx.x;
+    uint32_t tot = 0, pre = 0;
+    if (tid < E) {
+        /* 8 blocks' counts at a time, all loaded before any is used */
+        for (int g0 = 0; g0 < G; g0 += 8) {
+            uint32_t c[8];
+#pragma unroll
+            for (int j = 0; j < 8; j++) c[j] = cnt[(size_t)min(g0 + j, G - 1) * E + tid];
+#pragma unroll
+            for (int j = 0; j < 8; j++)
+                if (g0 + j < G) {
+                    tot += c[j];
+                    if (g0 + j < gb) pre += c[j];
+                }
+        }
+    }
+    int ek[KM];
+    dispatch_masks<KM>(a, mask, ek);
+    dispatch_lists(a, tot, xo, wsum, tiles_s, tiles_b, has_shared, gb == 0);
+    if (tid < E) {
+        uint32_t run = xo[tid] + pre;
+#pragma unroll
+        for (int w = 0; w < DSP_WORDS; w++) {
+            wpre[tid * DSP_WORDS + w] = run;
+            run += __popc(mask[tid * DSP_WORDS + w]);
         }
     }
     lds_barrier();
@@ -980,12 +1041,17 @@ int launch_dispatch(const RouteArgs &a, uint32_t *tiles_s, uint32_t *tiles_b, in
         return hipGetLastError() == hipSuccess ? 0 : -3;
     }
     const int G = dispatch_blocks(a.T);
+    if (counted && a.E <= DSP_TOK) { /* scan and scatter together */
+        if (a.K <= 8) KLAUNCH(k_dispatch_scan_scatter<8>, dim3(G), dim3(DSP_TOK), lds, s, a, cnt, G, tiles_s, tiles_b, has_shared);
+        else KLAUNCH(k_dispatch_scan_scatter<OROME_MAXK>, dim3(G), dim3(DSP_TOK), lds, s, a, cnt, G, tiles_s, tiles_b, has_shared);
+        return hipGetLastError() == hipSuccess ? 0 : -3;
+    }
     if (counted) {
     } else if (a.K <= 8) KLAUNCH(k_dispatch_count<8>, dim3(G), dim3(DSP_TOK), lds / 2, s, a, cnt);
     else KLAUNCH(k_dispatch_count<OROME_MAXK>, dim3(G), dim3(DSP_TOK), lds / 2, s, a, cnt);
     KLAUNCH(k_dispatch_scan, dim3(1), dim3(DSP_THREADS), 0, s, a, cnt, G, tiles_s, tiles_b, has_shared);
-    if (a.K <= 8) KLAUNCH(k_dispatch_scatter<8>, dim3(G), dim3(DSP_TOK), lds, s, a, cnt);
-    else KLAUNCH(k_dispatch_scatter<OROME_MAXK>, dim3(G), dim3(DSP_TOK), lds, s, a, cnt);
+    if (a.K <= 8) KLAUNCH(k_dispatch_scatter<8>, dim3(G), dim3(DSP_TOK), lds, s, a, (const uint32_t *)cnt);
+    else KLAUNCH(k_dispatch_scatter<OROME_MAXK>, dim3(G), dim3(DSP_TOK), lds, s, a, (const uint32_t *)cnt);
     return hipGetLastError() == hipSuccess ? 0 : -3;
 }
 
