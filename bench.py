@@ -12,8 +12,10 @@ is.
 
 Default (no --config): BASELINE's metric is quoted on two workloads, B=1
 decode and B=512 prefill; the line is config 0 (B=1 decode) and carries
-config 2 (T=512 prefill, balanced) as "secondary", each with its own roofline
-and CPU baseline, both timed for --steps steps.  --config C runs one config.
+config 2 (T=512 prefill, balanced) as "secondary", both timed for --steps
+steps, and config 4p (the 40-layer stack over a 2048-token prefill, the
+MFMA-bound workload) as "prefill_stack" at its own step count, each with its
+own roofline and CPU baseline.  --config C runs one config.
 
 Per config the line holds the roofline of the dominant kernel: algorithmic
 bytes (or flops) per launch over that kernel's average duration, measured with
@@ -89,7 +91,7 @@ def cpu_model():
     return "unknown"
 
 
-def run_config(key, steps, warmup, path, cpu_seconds, no_cpu):
+def run_config(key, steps, warmup, path, cpu_seconds, no_cpu, graph=True):
     import orome_amd
     from orome_amd import _lib
     from orome_amd._lib import check, lib
@@ -162,21 +164,48 @@ def run_config(key, steps, warmup, path, cpu_seconds, no_cpu):
         check(lib.orome_hip_capture_end(ctx.handle, C.byref(ex)), "capture_end")
         return ex
 
-    g_main = capture(step, G)
     rem = steps % G
-    g_rem = capture(step, rem) if rem else None
-    g_warm = capture(warm_step, max(1, min(warmup, G)))
     reps = steps // G
+    nwarm = max(1, min(warmup, G))
+    if graph:
+        g_main = capture(step, G)
+        g_rem = capture(step, rem) if rem else None
+        g_warm = capture(warm_step, nwarm)
+    else:
+        g_main = g_rem = g_warm = None
+
+    def warm():
+        if g_warm:
+            check(lib.orome_hip_graph_launch(ctx.handle, g_warm))
+        else:
+            for i in range(nwarm):
+                warm_step(i)
+
     for _ in range(max(1, math.ceil(warmup / G))):
-        check(lib.orome_hip_graph_launch(ctx.handle, g_warm))
+        warm()
     ctx.sync()
-    t0 = time.perf_counter()
-    for _ in range(reps):
-        check(lib.orome_hip_graph_launch(ctx.handle, g_main))
-    if g_rem:
-        check(lib.orome_hip_graph_launch(ctx.handle, g_rem))
-    ctx.sync()
-    elapsed = time.perf_counter() - t0
+    # zero-length k_delay dispatches mark the regions for a kernel trace:
+    # the 1st and 2nd bracket the timed steps, the 3rd (the stage timing's
+    # spin) and 4th the per-stage event pass
+    mark = lambda: check(lib.orome_hip_stream_delay(ctx.handle, 0))
+    mark()
+    if graph:
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            check(lib.orome_hip_graph_launch(ctx.handle, g_main))
+        if g_rem:
+            check(lib.orome_hip_graph_launch(ctx.handle, g_rem))
+        ctx.sync()
+        elapsed = time.perf_counter() - t0
+    else:
+        # --no-graph: the timed steps launched eagerly, so the wall clock
+        # holds the host's launch cost too (a profiling mode, not the figure)
+        t0 = time.perf_counter()
+        for i in range(steps):
+            step(i)
+        ctx.sync()
+        elapsed = time.perf_counter() - t0
+    mark()
     restore()
 
     # per-kernel durations: the timed steps launched again, eagerly, on the
@@ -184,13 +213,14 @@ def run_config(key, steps, warmup, path, cpu_seconds, no_cpu):
     # (orome_hip_stage_timing), all queued behind a GPU-side delay so that
     # they run back to back as in the graph; after a warm-up replay
     n_prof = min(steps, G)
-    check(lib.orome_hip_graph_launch(ctx.handle, g_warm))
+    warm()
     check(lib.orome_hip_stage_timing(ctx.handle, n_prof * (L if stack else 1)))
     check(lib.orome_hip_stream_delay(ctx.handle, 200000))
     for i in range(n_prof):
         step(i)
     tot = (C.c_float * 8)()
     cnt = (C.c_int * 8)()
+    mark()
     check(lib.orome_hip_stage_times(ctx.handle, tot, cnt, 8))
     check(lib.orome_hip_stage_timing(ctx.handle, 0))
     stage_us = {_lib.STAGES[i]: (round(tot[i] / cnt[i] * 1000.0, 3) if cnt[i] else None) for i in range(8)}
@@ -246,17 +276,35 @@ def run_config(key, steps, warmup, path, cpu_seconds, no_cpu):
     else:
         roof = {"bound": "hbm", "kernel": kname, "achieved": round(gu_gbs, 1), "peak": HBM_PEAK_GBS,
                 "unit": "GB/s", "frac": round(gu_gbs / HBM_PEAK_GBS, 4)}
-    traffic = None
+    # the committed profile of this workload: HBM traffic per launch (two
+    # rocprofv3 --pmc passes) and the kernel-trace average of the gate/up
+    # stage over the timed steps (a kernel trace cut at the region marks)
+    traffic, rp = None, {}
     tf = os.path.join(ROOT, "profiles", "traffic_%s.json" % cf["name"])
     if os.path.exists(tf):
-        traffic = json.load(open(tf)).get("gate_up_hbm_bytes_per_launch")
+        rp = json.load(open(tf))
+        traffic = rp.get("gate_up_hbm_bytes_per_launch")
+    serial = kpath == "mfma" and T * K > 32 * E
     roof.update({"traffic": traffic, "algorithmic_bytes_per_launch": int(gu_bytes),
                  "algorithmic_flops_per_launch": gu_flops, "avg_launch_us": gu_us,
                  "timing": "HIP events recorded by the gate/up launches themselves (hipExtLaunchKernel "
                            "start/stop, on the launch's stream), the timed steps relaunched back to back "
-                           "(%d launches)" % (n_prof * nl),
+                           "(%d launches)%s" % (n_prof * nl,
+                                                "; under stage timing the two tile lists run one after the "
+                                                "other on one stream, where the timed steps overlap them on two"
+                                                if serial else ""),
                  "in_kernel_us": round(float(np.mean(spans)), 3),
                  "gbs": round(gu_gbs, 1), "tflops": round(gu_tflops, 2)})
+    if rp.get("rocprof_gate_up_avg_us"):
+        ra = rp["rocprof_gate_up_avg_us"]
+        roof["rocprof"] = {"avg_launch_us": ra, "source": rp.get("rocprof_source"),
+                           "frac": round((gu_flops / (ra * 1e-6) / 1e12 / MFMA_F16_PEAK_TFLOPS) if T >= 2048
+                                         else (gu_bytes / (ra * 1e-6) / 1e9 / HBM_PEAK_GBS), 4),
+                           "events_over_rocprof": round(gu_us / ra, 4)}
+    fmts = {12: "q4_k", 13: "q5_k", 14: "q6_k", 8: "q8_0"}
+    dn = fmts[cf["spec"].get("down", Q4K)] + ("/q6_k (every 4th layer)" if stack else "")
+    dtype = ("routed gate/up q4_k, routed down %s, shared %s weights; fp16 activations, fp32 accumulate"
+             % (dn, fmts[sh_t]))
 
     cpu = None if no_cpu else cpu_baseline(img, xs_h, hs_h, T, L, NX, nl, stack, cpu_seconds)
 
@@ -272,11 +320,11 @@ def run_config(key, steps, warmup, path, cpu_seconds, no_cpu):
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "q4_k/q6_k weights, fp16 activations, fp32 accumulate",
+        "dtype": dtype,
         "data": "synthetic seeded GGUF per BASELINE config %s (%d timed layers, %d input batches; warm-up on "
                 "%d layers and inputs of its own)" % (key, L, NX, LW),
         "config": {"workload": cf["name"], "baseline_config": key, "tokens_per_step": T,
-                   "kernel_path": kpath,
+                   "kernel_path": kpath, "launch": "hip graph" if graph else "eager (--no-graph)",
                    "layers_per_step": nl, "hidden": H, "experts": E, "top_k": K,
                    "expert_intermediate": M, "shared_intermediate": S, "parallelism": "single GPU"},
         "roofline": roof,
@@ -345,6 +393,8 @@ def main():
                          "grouped GEMMs for 3..16, large-batch routing and grouped GEMMs above)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-graph", action="store_true",
+                    help="launch the timed steps eagerly instead of replaying a HIP graph (a profiling mode)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="run only a plain device-to-device copy of MIB MiB (5 times), the known-size "
                          "kernel that scales rocprofv3 FETCH_SIZE / WRITE_SIZE to bytes")
@@ -365,14 +415,19 @@ def main():
         print(json.dumps({"copy_bytes_per_launch": n, "launches": 5}))
         return
 
+    kw = dict(graph=not args.no_graph)
     if args.config is not None:
-        out = run_config(args.config, args.steps, args.warmup, args.path, args.cpu_seconds, args.no_cpu)
+        out = run_config(args.config, args.steps, args.warmup, args.path, args.cpu_seconds, args.no_cpu, **kw)
     else:
-        out = run_config("0", args.steps, args.warmup, args.path, args.cpu_seconds, args.no_cpu)
-        sec = run_config("2", args.steps, args.warmup, args.path, args.cpu_seconds / 2, args.no_cpu)
-        out["secondary"] = {k: sec[k] for k in ("metric", "value", "unit", "steps", "warmup", "ms_per_step",
-                                                 "config", "roofline", "step", "stage_us", "cpu_baseline",
-                                                 "data")}
+        out = run_config("0", args.steps, args.warmup, args.path, args.cpu_seconds, args.no_cpu, **kw)
+        keys = ("metric", "value", "unit", "steps", "warmup", "ms_per_step", "dtype", "config", "roofline", "step",
+                "stage_us", "cpu_baseline", "data")
+        sec = run_config("2", args.steps, args.warmup, args.path, args.cpu_seconds / 2, args.no_cpu, **kw)
+        out["secondary"] = {k: sec[k] for k in keys}
+        # the 40-layer T=2048 prefill stack: the MFMA-bound workload (its own
+        # default step count; --steps applies to the two above)
+        pre = run_config("4p", None, None, args.path, args.cpu_seconds / 2, args.no_cpu, **kw)
+        out["prefill_stack"] = {k: pre[k] for k in keys}
     print(json.dumps(out), flush=True)
 
 

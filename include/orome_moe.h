@@ -334,7 +334,12 @@ int orome_moe_stack_forward(orome_hip_ctx *ctx, const OromeHipModelConfig *cfg,
  * exceeds the array, and larger T, are rejected with OROME_EINVAL.  All calls
  * on one GPU share that GPU's array and it keeps the last call's contents:
  * calls that overlap on one GPU (two streams, two threads) race and must be
- * serialised by the caller. */
+ * serialised by the caller.  The array is cleared (by a fill kernel on
+ * `stream`) on the first call, whenever the shapes (H, E, M, S) differ from
+ * the previous call's, and after a call that failed; its zero rows sit at
+ * shape-dependent offsets.  So a HIP graph that captured a call stays valid
+ * only while no call with other shapes runs on that GPU between its
+ * replays. */
 #define OROME_NOALLOC_MAX_TOKENS 16
 #define OROME_NOALLOC_SCRATCH_BYTES (8u << 20)
 int orome_moe_forward_noalloc(const OromeHipModelConfig *cfg, const OromeHipExpertLayerRef *elr,
@@ -384,6 +389,15 @@ int orome_dequant_rows_f16(orome_hip_ctx *ctx, OromeHipQuantFormat fmt, const vo
 int orome_debug_mfma_weights(orome_hip_ctx *ctx, OromeHipQuantFormat fmt, int tiled, const void *w_dev,
                              uint32_t rows, uint32_t in_dim, float *out_dev);
 
+/* Test hook for the error path: the next forward call on the context that
+ * takes the small-batch routing (1..16 tokens) fails right after its router
+ * launch, having first set the router's arrival counter to a torn value (as
+ * a forward interrupted between launches could leave it).  Every forward
+ * entry point that fails returns the kernel-carried state to its initial
+ * value before it returns, so the following call computes normally.  No
+ * counterpart in the reference. */
+int orome_hip_debug_inject_failure(orome_hip_ctx *ctx);
+
 /* ------------------------------------------------- graphs and timing */
 
 /* Capture the work queued on the context stream into a HIP graph and replay
@@ -391,7 +405,9 @@ int orome_debug_mfma_weights(orome_hip_ctx *ctx, OromeHipQuantFormat fmt, int ti
  * once and committed (inference/src/engine.m:453-454, 1048-1050); a graph
  * removes per-kernel launch cost from decode.  Forward calls made between
  * begin and end are recorded, not executed.  No memset nodes are recorded:
- * the forward path clears nothing with hipMemset. */
+ * the forward path clears nothing with hipMemset.  capture_begin first
+ * resets the scratch state kernels carry between forwards (a fill kernel
+ * queued before the capture starts). */
 int orome_hip_capture_begin(orome_hip_ctx *ctx);
 int orome_hip_capture_end(orome_hip_ctx *ctx, void **graph_exec);
 int orome_hip_graph_launch(orome_hip_ctx *ctx, void *graph_exec);

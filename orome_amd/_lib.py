@@ -126,6 +126,7 @@ SIGNATURES = {
     "orome_dequant_rows": (I, [VP, I, VP, U32, U32, VP]),
     "orome_dequant_rows_f16": (I, [VP, I, VP, U32, U32, VP]),
     "orome_debug_mfma_weights": (I, [VP, I, I, VP, U32, U32, VP]),
+    "orome_hip_debug_inject_failure": (I, [VP]),
     "orome_version": (C.c_char_p, []),
     "orome_hip_capture_begin": (I, [VP]),
     "orome_hip_capture_end": (I, [VP, P(VP)]),

@@ -259,13 +259,12 @@ DEV u4 ld_u4(const uint8_t *p) {
     return *(gp4)(uintptr_t)p;
 }
 
-/* Cross-block hand-off inside one kernel without cache maintenance: data is
- * stored and loaded with device-coherent (sc1) accesses, the writer drains
- * its memory counter before signalling on an atomic counter, and the block
- * that observes the last arrival reads the data back coherently. */
+/* Cross-block hand-off inside one kernel: data stored and loaded as
+ * agent-scope atomics, published by an agent-scope release (the counter
+ * increment that follows a workgroup barrier) and read after the matching
+ * agent-scope acquire. */
 DEV void st_coh(float *p, float v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
 DEV float ld_coh(const float *p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
-DEV void drain_mem() { __builtin_amdgcn_s_waitcnt(0); }
 
 /* Workgroup barrier ordering LDS only.  __syncthreads also makes the block's
  * global stores visible to the block, so it first waits for every store in

@@ -67,6 +67,7 @@ struct orome_hip_ctx {
     /* per-block stamps of the gate/up launches (orome_hip_kernel_timing) */
     unsigned long long *kt;
     int kt_blocks;
+    int inject; /* orome_hip_debug_inject_failure: fail the next forward after its router launch */
 };
 
 /* One registered layer: keyed by the routed gate and shared gate device
@@ -481,6 +482,16 @@ thread_local LaunchEvents g_launch_ev = {nullptr, nullptr};
         if (ev_) (c)->tcount[st]++;                                                        \
     } while (0)
 
+/* State that kernels carry from one forward to the next: the folded small-
+ * batch router's arrival counter, which its last block returns to zero.  A
+ * forward that stops between launches (an error on the host) may leave it
+ * torn; this fill kernel (no memset node, so graph capture may record it)
+ * puts it back.  The top-k counts are cleared by every forward that uses
+ * them, before use. */
+static int reset_state(orome_hip_ctx *c, hipStream_t s) {
+    return launch_rc(launch_zero(c->counter, 256, s), "scratch state reset");
+}
+
 /* The MoE block on x (or, with norm_h, on RMSNorm(norm_h) * bf16(norm_w),
  * which the small-batch router computes itself and the large-batch path
  * computes in a separate kernel first). */
@@ -598,6 +609,11 @@ static int forward_impl(orome_hip_ctx *c, const OromeHipModelConfig *cfg, const 
          * its own */
         const int fold = T <= 2, rfold = !fold && route_small_folds(a);
         TLAUNCH(c, ST_ROUTE, launch_route_small(a, s, rfold), rfold ? "router logits + top-k + dispatch" : "router logits");
+        if (c->inject) { /* test hook: a torn hand-off counter, then an error */
+            c->inject = 0;
+            LAUNCH(launch_fill_u32(c->counter, 1u, 1, s), "injected failure");
+            return orome_fail(OROME_EHIP, "orome_moe_forward: injected failure after the router launch");
+        }
         if (!fold && !rfold) TLAUNCH(c, ST_TOPK, launch_topk_dispatch_small(a, s), "top-k + dispatch");
         if (hybrid) {
             /* every expert holds at most 16 rows: the grouped GEMMs alone
@@ -723,8 +739,10 @@ extern "C" int orome_moe_forward(orome_hip_ctx *c, const OromeHipModelConfig *cf
                                  const OromeHipLayerTensorCache *lt, const float *x, const float *h_in, float *h_out,
                                  float *residual_out, float *sumsq_parts, int T, int K, void *stream) {
     if (!c || !x) return orome_fail(OROME_EINVAL, "orome_moe_forward: NULL argument");
-    return forward_impl(c, cfg, elr, lt, x, h_in, h_out, T, K, NULL, NULL, call_stream(c, stream),
-                        FwdOut{residual_out, sumsq_parts});
+    const int rc = forward_impl(c, cfg, elr, lt, x, h_in, h_out, T, K, NULL, NULL, call_stream(c, stream),
+                                FwdOut{residual_out, sumsq_parts});
+    if (rc) (void)reset_state(c, call_stream(c, stream));
+    return rc;
 }
 
 extern "C" int orome_moe_layer_forward(orome_hip_ctx *c, const OromeHipModelConfig *cfg,
@@ -736,7 +754,9 @@ extern "C" int orome_moe_layer_forward(orome_hip_ctx *c, const OromeHipModelConf
     const float *nw = lt->post_norm.buffer && lt->post_norm.format == OROME_QFMT_F32
                           ? (const float *)dev_addr(lt->post_norm.buffer, lt->post_norm.offset)
                           : NULL;
-    return forward_impl(c, cfg, elr, lt, NULL, h, h, T, K, h, nw, call_stream(c, stream), FwdOut{NULL, NULL});
+    const int rc = forward_impl(c, cfg, elr, lt, NULL, h, h, T, K, h, nw, call_stream(c, stream), FwdOut{NULL, NULL});
+    if (rc) (void)reset_state(c, call_stream(c, stream));
+    return rc;
 }
 
 extern "C" int orome_moe_stack_forward(orome_hip_ctx *c, const OromeHipModelConfig *cfg,
@@ -770,7 +790,10 @@ extern "C" int orome_moe_stack_forward(orome_hip_ctx *c, const OromeHipModelConf
             fo.next_router = (const float *)dev_addr(lts[l + 1].routing_gate.buffer, lts[l + 1].routing_gate.offset);
         int rc = forward_impl(c, cfg, &elrs[l], &lts[l], NULL, h, h, T, K, h, norm_w(l), s, fo,
                               next ? norm_w(l + 1) : NULL, next ? 1 : 0, fuse && l > 0 ? 1 : 0);
-        if (rc) return rc;
+        if (rc) {
+            (void)reset_state(c, s);
+            return rc;
+        }
     }
     return OROME_OK;
 }
@@ -891,12 +914,20 @@ extern "C" int orome_debug_mfma_weights(orome_hip_ctx *c, OromeHipQuantFormat fm
     return OROME_OK;
 }
 
+extern "C" int orome_hip_debug_inject_failure(orome_hip_ctx *c) {
+    if (!c) return orome_fail(OROME_EINVAL, "orome_hip_debug_inject_failure: NULL ctx");
+    c->inject = 1;
+    return OROME_OK;
+}
+
 /* ------------------------------------------------------- graphs, timing */
 
 extern "C" int orome_hip_capture_begin(orome_hip_ctx *c) {
     if (!c) return orome_fail(OROME_EINVAL, "orome_hip_capture_begin: NULL ctx");
     if (c->timing) return orome_fail(OROME_EINVAL, "stage timing must be off while capturing");
     if (set_dev(c)) return OROME_EHIP;
+    /* the graph starts from a clean counter whatever ran before */
+    if (reset_state(c, c->stream)) return OROME_EHIP;
     HIP_OK(hipStreamBeginCapture(c->stream, hipStreamCaptureModeRelaxed), OROME_EHIP);
     return OROME_OK;
 }
@@ -1016,12 +1047,26 @@ extern "C" int orome_moe_forward_noalloc(const OromeHipModelConfig *cfg, const O
         base = g_na_ptr[dev];
         /* the zero rows of the layout sit at shape-dependent offsets: clear
          * the scratch whenever the shapes change (and on the first call) */
-        if (memcmp(g_na_key[dev], key, sizeof key)) {
-            memcpy(g_na_key[dev], key, sizeof key);
-            clear = true;
-        }
+        clear = memcmp(g_na_key[dev], key, sizeof key) != 0;
     }
-    if (clear) LAUNCH(launch_zero(base, need, c.stream), "orome_moe_forward_noalloc: scratch clear");
+    /* the key is recorded only once the clear is queued, and forgotten when
+     * a call fails, so the next call clears the array (zero rows and the
+     * router's arrival counter) again */
+    auto forget = [&]() {
+        std::lock_guard<std::mutex> g(g_na_lock);
+        memset(g_na_key[dev], 0, sizeof g_na_key[dev]);
+    };
+    if (clear) {
+        const int rc = launch_rc(launch_zero(base, need, c.stream), "orome_moe_forward_noalloc: scratch clear");
+        if (rc) {
+            forget();
+            return rc;
+        }
+        std::lock_guard<std::mutex> g(g_na_lock);
+        memcpy(g_na_key[dev], key, sizeof key);
+    }
     scratch_layout(&c, base);
-    return forward_impl(&c, cfg, elr, lt, x, h_in, h_out, T, K, NULL, NULL, c.stream, FwdOut{residual_out, sumsq_parts});
+    const int rc = forward_impl(&c, cfg, elr, lt, x, h_in, h_out, T, K, NULL, NULL, c.stream, FwdOut{residual_out, sumsq_parts});
+    if (rc) forget();
+    return rc;
 }

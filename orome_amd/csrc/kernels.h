@@ -168,6 +168,7 @@ int launch_sumsq_parts(const float *h, int T, int H, float *ssq, hipStream_t s);
 int launch_q4k_ggml_to_ref(uint8_t *blocks, size_t n, hipStream_t s);
 /* zero fill by a kernel (bytes a multiple of 4) */
 int launch_zero(void *p, size_t bytes, hipStream_t s);
+int launch_fill_u32(void *p, uint32_t v, size_t words, hipStream_t s);
 
 /* tile list for the grouped GEMM: tiles[0] = count, then (expert, first, rows)
  * triples; expert == E denotes the shared expert over all T tokens */

@@ -369,18 +369,21 @@ int launch_q4k_ggml_to_ref(uint8_t *blocks, size_t n, hipStream_t s) {
     return hipGetLastError() == hipSuccess ? 0 : -3;
 }
 
-/* Zero fill of `words` 32-bit words (a kernel, not a memset node, so that
- * callers may capture it in a graph). */
-__global__ void k_zero(uint32_t *p, size_t words) {
+/* Fill of `words` 32-bit words with `v` (a kernel, not a memset node, so
+ * that callers may capture it in a graph). */
+__global__ void k_fill_u32(uint32_t *p, uint32_t v, size_t words) {
     for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < words; i += (size_t)gridDim.x * blockDim.x)
-        p[i] = 0u;
+        p[i] = v;
+}
+
+int launch_fill_u32(void *p, uint32_t v, size_t words, hipStream_t s) {
+    const unsigned blocks = (unsigned)((words + 255) / 256 < 1024 ? (words + 255) / 256 : 1024);
+    if (!blocks) return 0;
+    KLAUNCH(k_fill_u32, dim3(blocks), dim3(256), 0, s, (uint32_t *)p, v, words);
+    return hipGetLastError() == hipSuccess ? 0 : -3;
 }
 
 int launch_zero(void *p, size_t bytes, hipStream_t s) {
     if (bytes % 4) return -1;
-    const size_t words = bytes / 4;
-    const unsigned blocks = (unsigned)((words + 255) / 256 < 1024 ? (words + 255) / 256 : 1024);
-    if (!blocks) return 0;
-    KLAUNCH(k_zero, dim3(blocks), dim3(256), 0, s, (uint32_t *)p, words);
-    return hipGetLastError() == hipSuccess ? 0 : -3;
+    return launch_fill_u32(p, 0u, bytes / 4, s);
 }

@@ -29,10 +29,9 @@
  * dependent 4-token chunks). */
 /* FOLD (> 0: the EPL of the selection): the block that finishes last also
  * runs the top-k and the dispatch for every token (topk_dispatch_block),
- * which saves a launch.  The logits cross blocks with device-coherent stores
- * and loads: each wave drains its stores before the block counts itself on
- * a.counter, and the last block reads them back coherently and returns the
- * counter to zero for the next launch. */
+ * which saves a launch.  The logits cross blocks through a release/acquire
+ * pair on a.counter (agent scope), stored and loaded as agent-scope atomics;
+ * the last block returns the counter to zero for the next launch. */
 template <bool NORM, int TMAX, int NIM, int RS, int FOLD>
 __global__ __launch_bounds__(FOLD ? 512 : 256) void k_route_small(RouteArgs a) {
     constexpr int W = FOLD ? 8 : 4; /* waves: the folding block selects with 8 */
@@ -67,15 +66,24 @@ __global__ __launch_bounds__(FOLD ? 512 : 256) void k_route_small(RouteArgs a) {
         }
     }
     if constexpr (FOLD > 0) {
+        /* Ordering (HIP's scoped memory model): the workgroup barrier orders
+         * every wave's logit stores before thread 0's counter increment,
+         * which is an agent-scope release; the block that reads the final
+         * count acquires at agent scope (the increment is acq_rel, and every
+         * wave of that block fences acquire after the broadcast barrier), so
+         * the logits of all blocks happen-before its loads, whichever XCD
+         * wrote them. */
         __shared__ int last;
-        drain_mem();
         __syncthreads();
         if (threadIdx.x == 0)
-            last = __hip_atomic_fetch_add(a.counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == gridDim.x - 1;
+            last = __hip_atomic_fetch_add(a.counter, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) == gridDim.x - 1;
         __syncthreads();
         if (!last) return;
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
         topk_dispatch_block<FOLD, true>(a);
-        if (threadIdx.x == 0) __hip_atomic_store(a.counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        /* back to zero for the next launch (the kernel boundary orders it
+         * before that launch's increments) */
+        if (threadIdx.x == 0) __hip_atomic_store(a.counter, 0u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
     }
 }
 

@@ -105,6 +105,27 @@ def test_decode_forward_parity(base, T):
     assert err < TOL
 
 
+@pytest.mark.parametrize("T", [8, 3])
+def test_forward_after_injected_failure(base, T):
+    """A forward that fails between launches (test hook: the router's arrival
+    counter is left torn, then the call returns an error) is followed by a
+    forward whose routing is bit-exact and whose output is within tolerance
+    of the oracle: the failing entry point returned the kernel-carried state
+    to its initial value."""
+    banner("forward after an injected failure T=%d" % T)
+    x, h = base.inputs(T, seed=900 + T)
+    base.ctx.set_path(_lib.OROME_PATH_AUTO)
+    dx, dh, dout = DeviceBuffer.from_array(base.ctx, x), DeviceBuffer.from_array(base.ctx, h), DeviceBuffer(base.ctx, h.nbytes)
+    check(lib.orome_hip_debug_inject_failure(base.ctx.handle), "inject")
+    with pytest.raises(_lib.OromeError, match="injected failure"):
+        base.gm.forward(0, dx, dh, dout, T)
+    base.ctx.sync()
+    out, dbg = base.run(0, x, h)
+    check_routing(base, x, dbg, 8)
+    ref = base.om.forward(0, x, h)
+    assert rel_l2(out - h, ref - h) < TOL
+
+
 @pytest.mark.parametrize("T,path", [(1, _lib.OROME_PATH_AUTO), (4, _lib.OROME_PATH_AUTO),
                                     (3, _lib.OROME_PATH_GEMV), (40, _lib.OROME_PATH_AUTO)])
 def test_combine_residual_copy_and_sumsq_parts(base, T, path):
@@ -256,6 +277,28 @@ def test_dequant_bit_exact(fmt_name, kw):
     got16 = out16.download(np.uint16, (rows, n))
     assert np.array_equal(got16, ref.astype(np.float16).view(np.uint16))
     p.gm.close()
+
+
+def test_dequant_q4k_one_hot_fields(base):
+    """The one-hot Q4_K scale and min fields of the CPU pins (decoded values
+    written out by hand from format.m:41-64, sub-blocks 4..7 included)
+    through the GPU dequant: fp32 bit for bit."""
+    banner("dequant Q4_K one-hot scale/min fields")
+    from test_oracle import MIN_ONE_HOT, SCALE_ONE_HOT, _q4k_block
+    blocks, expect = [], []
+    for table, nib, sign in ((MIN_ONE_HOT, 9, -1), (SCALE_ONE_HOT, 3, 3)):
+        for byte, val, e in table:
+            sc = [0] * 12
+            sc[byte] = val
+            blocks.append(_q4k_block(1.0, 1.0, sc, nib))
+            expect.append(sign * np.repeat(np.float32(e), 32))
+    rows = len(blocks)
+    src = DeviceBuffer.from_array(base.ctx, np.frombuffer(b"".join(blocks), np.uint8).copy())
+    out = DeviceBuffer(base.ctx, rows * 256 * 4)
+    check(lib.orome_dequant_rows(base.ctx.handle, O.Q4_K, src.ptr, rows, 256, out.ptr))
+    base.ctx.sync()
+    got = out.download(np.float32, (rows, 256))
+    assert np.array_equal(got, np.array(expect, np.float32))
 
 
 @pytest.mark.parametrize("T", [1, 2, 5, 12, 16])

@@ -385,6 +385,39 @@ def mfma_weights_model(fmt_blocks):
     return f16(q * d[:, None]).reshape(rows, cols)
 
 
+def f16_ulp(v):
+    """Spacing of fp16 numbers at |v| (2^-24 below the normal range)."""
+    a = np.abs(np.asarray(v, np.float64))
+    e = np.floor(np.log2(np.maximum(a, 2.0 ** -14)))
+    return np.exp2(e - 10)
+
+
+def q4k_q5k_exact_and_min(fmt, blocks, rows, cols):
+    """Per weight of a Q4_K / Q5_K matrix: the exact value d sc q - dmin m
+    (float64) and fp16(dmin m), the min term as the GEMMs round it."""
+    bb = 144 if fmt == "Q4_K" else 176
+    b = blocks.reshape(-1, bb)
+    d = b[:, 0:2].copy().view(np.float16).astype(np.float64)[:, 0]
+    dmin = b[:, 2:4].copy().view(np.float16).astype(np.float64)[:, 0]
+    from test_oracle import layout_table_np
+    sc, mn = layout_table_np(b[:, 4:16])
+    ex = np.empty((len(b), 256))
+    mb = np.empty((len(b), 256))
+    for j in range(4):
+        for h in range(2):
+            s_ = 2 * j + h
+            if fmt == "Q4_K":
+                q = (b[:, 16 + 32 * j:16 + 32 * j + 32].astype(np.int64) >> (4 * h)) & 0xF
+            else:
+                qh = b[:, 16:48].astype(np.int64)
+                q = ((b[:, 48 + 32 * j:48 + 32 * j + 32].astype(np.int64) >> (4 * h)) & 0xF) + \
+                    16 * ((qh >> (2 * j + h)) & 1)
+            cols_ = slice(64 * j + 32 * h, 64 * j + 32 * h + 32)
+            ex[:, cols_] = d[:, None] * sc[:, s_][:, None] * q - (dmin * mn[:, s_])[:, None]
+            mb[:, cols_] = f16(dmin * mn[:, s_]).astype(np.float64)[:, None]
+    return ex.reshape(rows, cols), mb.reshape(rows, cols)
+
+
 @pytest.mark.parametrize("fmt,tiled", [("Q4_K", 0), ("Q4_K", 1), ("Q5_K", 0), ("Q5_K", 1), ("Q6_K", 0), ("Q6_K", 1),
                                        ("Q8_0", 0), ("Q8_0", 1)])
 def test_mfma_fp16_weights_bit_exact(fmt, tiled):
@@ -414,8 +447,16 @@ def test_mfma_fp16_weights_bit_exact(fmt, tiled):
     if fmt in ("Q6_K", "Q8_0"):  # one or two roundings of the exact value
         ulp = np.abs(exact) * 2.0 ** -10 + 2.0 ** -24
         assert np.all(np.abs(got.astype(np.float64) - exact) <= 2 * ulp)
-    else:  # fp16(dmin m) can carry an error larger than w itself where they cancel
-        assert rel_l2(got, exact) < 1e-3
+    else:
+        # two roundings, bounded per weight: w = fp16(q sc d - fp16(dmin m)),
+        # so |w - exact| <= ulp(w)/2 + ulp(fp16(dmin m))/2, with exact the
+        # real value d sc q - dmin m (float64, from the block fields)
+        ex64, mb = q4k_q5k_exact_and_min(fmt, blocks, H, M)
+        bound = 0.5 * f16_ulp(got) + 0.5 * f16_ulp(mb)
+        err = np.abs(got.astype(np.float64) - ex64)
+        assert np.all(err <= bound), float((err / bound).max())
+        # and the oracle's fp32 value is the float32 rounding of that exact value
+        assert np.array_equal(exact, ex64.astype(np.float32))
     p.gm.close()
 
 

@@ -140,6 +140,64 @@ def test_q4k_layout_differs_from_ggml():
     assert ggml_sc[2:] == [0, 0]
 
 
+def _q4k_block(d, dmin, scales, nib):
+    """One 144-byte Q4_K super-block: fp16 d, dmin, the 12 scale bytes as
+    given, every quant nibble = nib."""
+    b = bytearray(144)
+    b[0:2] = np.float16(d).tobytes()
+    b[2:4] = np.float16(dmin).tobytes()
+    b[4:16] = bytes(scales)
+    b[16:144] = bytes([nib | (nib << 4)]) * 128
+    return bytes(b)
+
+
+# (scale byte index, value) -> the 8 sub-block mins (or scales) that
+# inference/src/format.m:41-64 decodes from it, written out by hand:
+#   bytes 0..3  -> scales of sub-blocks 0..3 (low 6 bits); bits 6..7 are the
+#                  high bits of the scales of sub-blocks 4..7
+#   bytes 4..7  -> mins of sub-blocks 0..3; bits 6..7 the high bits of the
+#                  mins of sub-blocks 4..7
+#   byte 8 / 9  -> low nibble: scale of sub-block 4 / 6, high nibble: 5 / 7
+#   byte 10 / 11 -> the same for the mins
+MIN_ONE_HOT = [
+    (4, 0x01, [1, 0, 0, 0, 0, 0, 0, 0]), (7, 0x3F, [0, 0, 0, 63, 0, 0, 0, 0]),
+    (10, 0x01, [0, 0, 0, 0, 1, 0, 0, 0]), (10, 0x10, [0, 0, 0, 0, 0, 1, 0, 0]),
+    (11, 0x01, [0, 0, 0, 0, 0, 0, 1, 0]), (11, 0x10, [0, 0, 0, 0, 0, 0, 0, 1]),
+    (10, 0x0F, [0, 0, 0, 0, 15, 0, 0, 0]), (11, 0xF0, [0, 0, 0, 0, 0, 0, 0, 15]),
+    (4, 0x40, [0, 0, 0, 0, 16, 0, 0, 0]), (5, 0x40, [0, 0, 0, 0, 0, 16, 0, 0]),
+    (6, 0x40, [0, 0, 0, 0, 0, 0, 16, 0]), (7, 0x80, [0, 0, 0, 0, 0, 0, 0, 32]),
+]
+SCALE_ONE_HOT = [
+    (0, 0x01, [1, 0, 0, 0, 0, 0, 0, 0]), (3, 0x3F, [0, 0, 0, 63, 0, 0, 0, 0]),
+    (8, 0x01, [0, 0, 0, 0, 1, 0, 0, 0]), (8, 0x10, [0, 0, 0, 0, 0, 1, 0, 0]),
+    (9, 0x01, [0, 0, 0, 0, 0, 0, 1, 0]), (9, 0x10, [0, 0, 0, 0, 0, 0, 0, 1]),
+    (0, 0x40, [0, 0, 0, 0, 16, 0, 0, 0]), (1, 0x40, [0, 0, 0, 0, 0, 16, 0, 0]),
+    (2, 0x40, [0, 0, 0, 0, 0, 0, 16, 0]), (3, 0x80, [0, 0, 0, 0, 0, 0, 0, 32]),
+]
+
+
+@pytest.mark.parametrize("byte,val,expect", MIN_ONE_HOT)
+def test_q4k_min_fields_one_hot(byte, val, expect):
+    """A single min field set (scales zero, d = dmin = 1): every weight of
+    sub-block j (elements 32j .. 32j+31) decodes to -min_j, with the mins
+    read off format.m:57-63 by hand (MIN_ONE_HOT).  Swapping the min bytes
+    10/11, or reading them as ggml's packing does, fails these cases."""
+    sc = [0] * 12
+    sc[byte] = val
+    w = O.decode_rows(O.Q4_K, np.frombuffer(_q4k_block(1.0, 1.0, sc, 9), np.uint8), 1, 256)[0]
+    assert np.array_equal(w, -np.repeat(np.float32(expect), 32))
+
+
+@pytest.mark.parametrize("byte,val,expect", SCALE_ONE_HOT)
+def test_q4k_scale_fields_one_hot(byte, val, expect):
+    """A single scale field set (mins zero, d = 1, every nibble 3): sub-block j
+    decodes to 3 sc_j."""
+    sc = [0] * 12
+    sc[byte] = val
+    w = O.decode_rows(O.Q4_K, np.frombuffer(_q4k_block(1.0, 1.0, sc, 3), np.uint8), 1, 256)[0]
+    assert np.array_equal(w, 3 * np.repeat(np.float32(expect), 32))
+
+
 # ------------------------------------------------------------------ A3-A5
 def test_q4k_kat_reference():
     """tests/test_q4k.m:18-66: 4 rows x 256, scale 1, min 0, all nibbles 5, x=0.01."""

@@ -1,9 +1,14 @@
 """GPU check of orome_moe_forward_noalloc (the entry point that allocates
 nothing, with its scratch in a static per-GPU device array) against
-orome_moe_forward on the same inputs, through the C ABI: two calls in a row,
-the second with fewer tokens, outputs bit-identical (the same kernels run on
-the same data; only the scratch addresses differ), routing bit-exact against
-the oracle."""
+orome_moe_forward on the same inputs, through the C ABI: calls in a row with
+fewer tokens each time (8, 3, 2, 1: the folded small-batch router with its
+arrival counter in the static array, the two-token GEMV path, and the
+one-token path with routing folded into gate/up and the fused down +
+combine), outputs, residual copy and sum-of-squares parts bit-identical to
+orome_moe_forward (the same kernels on the same data; only the scratch
+addresses differ), and within 1e-3 relative L2 of the oracle.  Routing is
+not read back here (the array has no debug copy-out); the context path's
+routing is pinned bit-exact by the other GPU tests."""
 import ctypes as C
 
 import numpy as np
@@ -28,13 +33,13 @@ def _noalloc(gm, layer, dx, dh, dout, dres, dparts, T, K=8):
 
 
 def test_noalloc_matches_context_forward():
-    banner("no-alloc forward: T=8 then T=3 against orome_moe_forward")
+    banner("no-alloc forward: T=8, 3, 2, 1 against orome_moe_forward")
     img = orome_amd.synth_gguf(orome_amd.make_spec(layers=1, H=2048, E=256, K=8, M=512, S=512, seed=11))
     gm = orome_amd.MoEModel(image=img, max_tokens=16, pack=False)
     om = O.OracleModel(img)
     H = gm.H
     try:
-        for T in (8, 3):
+        for T in (8, 3, 2, 1):
             x = orome_amd.synth_normal(70 + T, 1, T * H).reshape(T, H)
             h = orome_amd.synth_normal(70 + T, 2, T * H).reshape(T, H)
             dx, dh = DeviceBuffer.from_array(gm.ctx, x), DeviceBuffer.from_array(gm.ctx, h)
