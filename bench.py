@@ -55,6 +55,10 @@ CONFIGS = {
     # expert (not a BASELINE config; a parity-tested variant)
     "2r": dict(T=512, name="moe_prefill_512_q5k_down_q8_shared", mode="layer", layers=4,
                spec=dict(down=13, shared=8), xbank=4, steps=200),
+    # one layer over a 2048-token prefill, its routing fixed by the inputs
+    # (not a BASELINE config: the layer of config 4p without the stack, for
+    # kernel studies whose outputs feed nothing)
+    "p2048": dict(T=2048, name="moe_prefill_2048_layer", mode="layer", layers=4, spec={}, xbank=2, steps=40),
     "4d": dict(T=1, name="moe_stack40_decode_b1", mode="stack", layers=40,
                spec=dict(q6k_every=4, centered=True), xbank=16, steps=100),
     "4p": dict(T=2048, name="moe_stack40_prefill_2048", mode="stack", layers=40,
