@@ -68,18 +68,20 @@ __global__ __launch_bounds__(FOLD ? 512 : 256) void k_route_small(RouteArgs a) {
     if constexpr (FOLD > 0) {
         /* Ordering (HIP's scoped memory model): the workgroup barrier orders
          * every wave's logit stores before thread 0's counter increment,
-         * which is an agent-scope release; the block that reads the final
-         * count acquires at agent scope (the increment is acq_rel, and every
-         * wave of that block fences acquire after the broadcast barrier), so
-         * the logits of all blocks happen-before its loads, whichever XCD
-         * wrote them. */
+         * which is an agent-scope release.  In the block that reads the
+         * final count, thread 0 fences acquire at agent scope after that
+         * read, before the barrier that broadcasts it, so the logits of all
+         * blocks (through the counter's release sequence) happen-before every
+         * wave's loads, whichever XCD wrote them.  The other blocks only
+         * release. */
         __shared__ int last;
         __syncthreads();
-        if (threadIdx.x == 0)
-            last = __hip_atomic_fetch_add(a.counter, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) == gridDim.x - 1;
+        if (threadIdx.x == 0) {
+            last = __hip_atomic_fetch_add(a.counter, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT) == gridDim.x - 1;
+            if (last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+        }
         __syncthreads();
         if (!last) return;
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
         topk_dispatch_block<FOLD, true>(a);
         /* back to zero for the next launch (the kernel boundary orders it
          * before that launch's increments) */
