@@ -634,12 +634,17 @@ static int forward_impl(orome_hip_ctx *c, const OromeHipModelConfig *cfg, const 
             c->last_K = K;
             return OROME_OK;
         }
-        TLAUNCH(c, ST_GATE_UP, launch_gemv_gate_up(ex, sh, a, fold, x, T, H, M, K, E, c->act, c->act_sh, s, c->kt, c->kt_blocks),
-                "gemv gate/up");
-        /* one token: down and combine in one kernel when the shape allows */
+        /* one token: down and combine in one kernel when the shape allows;
+         * after the one-token gate/up the act rows are in slot order, so
+         * that kernel requests them without waiting for the routing */
         const bool dc1 = T == 1 && K <= 8 && M == 512 && (!S || S == 512);
+        const int by_slot = dc1 && gemv_gate_up1_path(fold, T, H, sh) ? 1 : 0;
+        TLAUNCH(c, ST_GATE_UP,
+                launch_gemv_gate_up(ex, sh, a, fold, x, T, H, M, K, E, c->act, c->act_sh, s, c->kt, c->kt_blocks, by_slot),
+                "gemv gate/up");
         if (dc1) {
-            TLAUNCH(c, ST_DOWN, launch_gemv_down_combine1(ex, sh, a, c->act, c->act_sh, H, M, K, h_in, h_out, fo.res, s, fo.next_router),
+            TLAUNCH(c, ST_DOWN,
+                    launch_gemv_down_combine1(ex, sh, a, c->act, c->act_sh, H, M, K, h_in, h_out, fo.res, s, fo.next_router, by_slot),
                     "gemv down + combine");
             if (fo.ssq) TLAUNCH(c, ST_COMBINE, launch_sumsq_parts(h_out, T, H, fo.ssq, s), "sum-of-squares parts");
         } else {

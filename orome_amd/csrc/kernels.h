@@ -110,9 +110,14 @@ bool dispatch_three_launches(const RouteArgs &a);
 /* decode gate/up; with route_in_block the top-k + dispatch of the call is
  * folded in (every block selects; block 0 publishes the routing outputs in
  * `ra`), otherwise it reads the routing written by launch_topk_dispatch_small */
+/* act_by_slot (only where the one-token kernel runs, gemv_gate_up1_path):
+ * act row k holds the expert of selection slot k instead of its sorted
+ * position, for launch_gemv_down_combine1 with the same flag */
 int launch_gemv_gate_up(const ExpertSide &ex, const SharedSide &sh, const RouteArgs &ra, int route_in_block,
                         const float *x, int T, int H, int M, int K, int E, _Float16 *act, _Float16 *act_sh,
-                        hipStream_t s, unsigned long long *kt = nullptr, int kt_cap = 0);
+                        hipStream_t s, unsigned long long *kt = nullptr, int kt_cap = 0, int act_by_slot = 0);
+/* the decode gate/up takes its one-token kernel (routing folded in) */
+bool gemv_gate_up1_path(int route_in_block, int T, int H, const SharedSide &sh);
 int launch_topk_dispatch_small(const RouteArgs &a, hipStream_t s);
 
 int launch_gemv_down(const ExpertSide &ex, const SharedSide &sh, const _Float16 *act,
@@ -124,7 +129,7 @@ int launch_gemv_down(const ExpertSide &ex, const SharedSide &sh, const _Float16 
 int launch_gemv_down_combine1(const ExpertSide &ex, const SharedSide &sh, const RouteArgs &ra,
                               const _Float16 *act, const _Float16 *act_sh, int H, int M, int K,
                               const float *h_in, float *h_out, float *res, hipStream_t s,
-                              const float *next_router = nullptr);
+                              const float *next_router = nullptr, int act_by_slot = 0);
 int launch_delay(uint32_t usec, hipStream_t s);
 int launch_rmsnorm(const float *h, const float *w, int T, int H, float eps, float *x, hipStream_t s);
 int launch_dequant(int fmt, const uint8_t *src, uint32_t rows, uint32_t n, float *out32,

@@ -214,6 +214,10 @@ struct GUArgs {
     const uint8_t *pf_down, *pf_sh_down;
     size_t pf_down_stride;
     int pf_rb, pf_sh_rb;
+    /* T = 1: act row k holds the expert of selection round k (slot order)
+     * instead of its sorted position, so the down + combine kernel can load
+     * the act rows without waiting for the routing */
+    int act_by_slot;
 };
 
 /* One 4-byte load per 128-byte line of the 8-row groups g = i, i + step, ...
@@ -554,8 +558,12 @@ DEV void k_gemv_gate_up1_body(GUArgs a, RouteArgs ra) {
     /* the act row is the expert's rank among the selected ids, which the
      * selecting wave knows once its rounds are done */
     asm volatile("s_waitcnt vmcnt(0)" : : "v"(sink));
-    lds_barrier();
-    if (wv != sel) rank = s_rank;
+    if (a.act_by_slot) {
+        rank = u; /* block u's expert was named by round u */
+    } else {
+        lds_barrier();
+        if (wv != sel) rank = s_rank;
+    }
     _Float16 *out = a.act + (size_t)rank * a.M;
     if (lane == 0)
 #pragma unroll
@@ -811,6 +819,7 @@ struct DownArgs {
     const float *pf_router; /* T = 1, H = 2048: rows E x H to touch (the next layer's router) or NULL */
 };
 
+
 template <int NT, int FMT>
 DEV void down_slot(const uint8_t *row, int in_dim, int cl, int n, const _Float16 *const *xrow,
                    float *acc) {
@@ -1064,7 +1073,10 @@ struct DnX<FQ8> {
     MDEV float dot(const DnRaw<FQ8> &r, int) const { return q8_dot(r.r, x); }
 };
 
-template <int EFMT, int SFMT>
+/* SLOT: act row k belongs to slot k (the gate/up wrote them in selection
+ * order), so the activation loads go out with the routing loads instead of
+ * after them. */
+template <int EFMT, int SFMT, bool SLOT>
 __global__ __launch_bounds__(128) void k_gemv_down_combine1(DownArgs a, RouteArgs ra, const float *h_in,
                                                             float *h_out, float *res) {
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
@@ -1084,6 +1096,19 @@ __global__ __launch_bounds__(128) void k_gemv_down_combine1(DownArgs a, RouteArg
     const i4v e0 = *(const i4v *)ra.idx, e1 = *(const i4v *)(ra.idx + 4);
     const u4 p0 = *(const u4 *)ra.pos, p1 = *(const u4 *)(ra.pos + 4);
     const f4 w0 = *(const f4 *)ra.w, w1 = *(const f4 *)(ra.w + 4);
+    int o[4], osh[4];
+    DnX<EFMT>::offs(cl, o);
+    DnX<SFMT>::offs(cl, osh);
+    u4 xq[DC_K][4], sq[4];
+    const _Float16 *xs = has_sh ? a.act_sh : a.act;
+    if constexpr (SLOT) {
+#pragma unroll
+        for (int k = 0; k < DC_K; k++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) xq[k][j] = ld_u4((const uint8_t *)(a.act + (size_t)(k < K ? k : 0) * a.M + o[j]));
+#pragma unroll
+        for (int j = 0; j < 4; j++) sq[j] = ld_u4((const uint8_t *)(xs + osh[j]));
+    }
     const int ev[DC_K] = {e0.x, e0.y, e0.z, e0.w, e1.x, e1.y, e1.z, e1.w};
     const int pv[DC_K] = {(int)p0.x, (int)p0.y, (int)p0.z, (int)p0.w, (int)p1.x, (int)p1.y, (int)p1.z, (int)p1.w};
     const float wk[DC_K] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
@@ -1098,17 +1123,14 @@ __global__ __launch_bounds__(128) void k_gemv_down_combine1(DownArgs a, RouteArg
     for (int k = 0; k < DC_K; k++) raw[k].load(a.down + (size_t)e[k] * a.down_stride + (size_t)r * rb, cl);
     DnRaw<SFMT> rsh;
     rsh.load(has_sh ? a.sh_down + (size_t)r * row_bytes(SFMT, a.S) : a.down + (size_t)r * rb, cl);
-    int o[4], osh[4];
-    DnX<EFMT>::offs(cl, o);
-    DnX<SFMT>::offs(cl, osh);
-    u4 xq[DC_K][4], sq[4];
+    if constexpr (!SLOT) {
 #pragma unroll
-    for (int k = 0; k < DC_K; k++)
+        for (int k = 0; k < DC_K; k++)
 #pragma unroll
-        for (int j = 0; j < 4; j++) xq[k][j] = ld_u4((const uint8_t *)(a.act + (size_t)ps[k] * a.M + o[j]));
-    const _Float16 *xs = has_sh ? a.act_sh : a.act;
+            for (int j = 0; j < 4; j++) xq[k][j] = ld_u4((const uint8_t *)(a.act + (size_t)ps[k] * a.M + o[j]));
 #pragma unroll
-    for (int j = 0; j < 4; j++) sq[j] = ld_u4((const uint8_t *)(xs + osh[j]));
+        for (int j = 0; j < 4; j++) sq[j] = ld_u4((const uint8_t *)(xs + osh[j]));
+    }
     const float hb = (h_in ? h_in : h_out)[r];
     const float sgv = ra.sgl[0];
     /* the next layer's router (one wave per 4-row block of 2048 fp32, the
@@ -1199,9 +1221,13 @@ __global__ __launch_bounds__(256) void k_gemv_down_b(DownArgs a) {
 
 static int epl_of(int E) { return E <= 64 ? 1 : E <= 128 ? 2 : E <= 256 ? 4 : E <= 512 ? 8 : E <= 1024 ? 16 : 0; }
 
+bool gemv_gate_up1_path(int route_in_block, int T, int H, const SharedSide &sh) {
+    return route_in_block && T == 1 && H == 2048 && (!sh.gate || sh.gate_fmt == FQ4K);
+}
+
 int launch_gemv_gate_up(const ExpertSide &ex, const SharedSide &sh, const RouteArgs &ra, int route_in_block,
                         const float *x, int T, int H, int M, int K, int E, _Float16 *act, _Float16 *act_sh,
-                        hipStream_t s, unsigned long long *kt, int kt_cap) {
+                        hipStream_t s, unsigned long long *kt, int kt_cap, int act_by_slot) {
     const int rows_blk = 4 * GU_RPW;
     if (T < 1 || T > 16 || T * K > 256 || H % 256 || ex.gate_fmt != FQ4K || !epl_of(E)) return -2;
     if (M % rows_blk || (sh.gate && sh.S % rows_blk)) return -2;
@@ -1212,6 +1238,7 @@ int launch_gemv_gate_up(const ExpertSide &ex, const SharedSide &sh, const RouteA
     a.x = x; a.T = T; a.H = H; a.M = M; a.K = K; a.E = E; a.list = ra.list; a.pairs = ra.pairs;
     a.act = act; a.act_sh = act_sh;
     a.pf_down = a.pf_sh_down = nullptr; a.pf_down_stride = 0; a.pf_rb = a.pf_sh_rb = 0;
+    a.act_by_slot = 0;
     if (T == 1) {
         a.pf_down = ex.down; a.pf_down_stride = ex.down_stride; a.pf_rb = (int)row_bytes(ex.down_fmt, M);
         if (sh.gate) { a.pf_sh_down = sh.down; a.pf_sh_rb = (int)row_bytes(sh.down_fmt, sh.S); }
@@ -1243,7 +1270,9 @@ int launch_gemv_gate_up(const ExpertSide &ex, const SharedSide &sh, const RouteA
 #undef GB_LAUNCH
         return hipGetLastError() == hipSuccess ? 0 : -3;
     }
-    if (route_in_block && T == 1 && H == 2048 && (!sh.gate || sh.gate_fmt == FQ4K)) {
+    if (act_by_slot && !gemv_gate_up1_path(route_in_block, T, H, sh)) return -1;
+    if (gemv_gate_up1_path(route_in_block, T, H, sh)) {
+        a.act_by_slot = act_by_slot;
 #define GU1_LAUNCH(EPLV) KLAUNCH((k_gemv_gate_up1<EPLV>), dim3(blocks), dim3(256), 0, s, a, ra)
         switch (epl_of(E)) {
             case 1: GU1_LAUNCH(1); break;
@@ -1325,7 +1354,7 @@ int launch_gemv_down(const ExpertSide &ex, const SharedSide &sh, const _Float16 
 int launch_gemv_down_combine1(const ExpertSide &ex, const SharedSide &sh, const RouteArgs &ra,
                               const _Float16 *act, const _Float16 *act_sh, int H, int M, int K,
                               const float *h_in, float *h_out, float *res, hipStream_t s,
-                              const float *next_router) {
+                              const float *next_router, int act_by_slot) {
     if (K < 1 || K > DC_K || H % 8 || M != 512 || (sh.gate && sh.S != 512)) return -2;
     if (ex.down_fmt != FQ4K && ex.down_fmt != FQ5K && ex.down_fmt != FQ6K) return -2;
     const int sf = sh.gate ? sh.down_fmt : FQ4K;
@@ -1335,7 +1364,11 @@ int launch_gemv_down_combine1(const ExpertSide &ex, const SharedSide &sh, const 
     a.sh_down = sh.gate ? sh.down : nullptr; a.sh_fmt = sf; a.S = sh.gate ? sh.S : 0;
     a.act = act; a.act_sh = act_sh; a.T = 1; a.H = H; a.M = M; a.K = K; a.E = ra.E;
     a.pf_router = H == 2048 ? next_router : nullptr;
-#define DC_LAUNCH(EF, SF) KLAUNCH((k_gemv_down_combine1<EF, SF>), dim3(H / 8), dim3(128), 0, s, a, ra, h_in, h_out, res)
+#define DC_LAUNCH(EF, SF)                                                                                                     \
+    do {                                                                                                                      \
+        if (act_by_slot) KLAUNCH((k_gemv_down_combine1<EF, SF, true>), dim3(H / 8), dim3(128), 0, s, a, ra, h_in, h_out, res); \
+        else KLAUNCH((k_gemv_down_combine1<EF, SF, false>), dim3(H / 8), dim3(128), 0, s, a, ra, h_in, h_out, res);           \
+    } while (0)
     DOWN_FMT_SWITCH(ex.down_fmt, sf, DC_LAUNCH);
 #undef DC_LAUNCH
     return hipGetLastError() == hipSuccess ? 0 : -3;
