@@ -220,12 +220,13 @@ struct GUArgs {
     int act_by_slot;
 };
 
-/* One 4-byte load per 128-byte line of the 8-row groups g = i, i + step, ...
- * (< H / 8) of a row-major matrix: the rows that the T = 1 down kernel's
- * blocks g read, from a block on the same XCD as they are (g = i mod 8).
- * The value lands in `sink`, which the caller keeps until a wait for it. */
-DEV void touch_rows8(const uint8_t *m, int rb, int H, int i, int step, int lane, uint32_t &sink) {
-    const int nl = (8 * rb + 127) / 128, g = i + step * (lane / nl);
+/* One 4-byte load per 128-byte line of two of the 8-row groups g = i,
+ * i + step, i + 2 step, ... (< H / 8) of a row-major matrix, the pair
+ * starting at group slot s0: the rows that the T = 1 down kernel's blocks g
+ * read, from a block on the same XCD as they are (g = i mod 8).  The value
+ * lands in `sink`, which the caller keeps until a wait for it. */
+DEV void touch_rows8(const uint8_t *m, int rb, int H, int i, int step, int s0, int lane, uint32_t &sink) {
+    const int nl = (8 * rb + 127) / 128, g = i + step * (s0 + lane / nl);
     if (lane / nl >= 2 || g >= H / 8) return;
     const uint8_t *p = m + (size_t)g * 8 * rb + min((lane % nl) * 128, 8 * rb - 4);
     asm volatile("global_load_dword %0, %1, off" : "=v"(sink) : "v"(p) : "memory");
@@ -406,7 +407,11 @@ DEV void k_gemv_gate_up1_body(GUArgs a, RouteArgs ra) {
         const float Xl = cvt_x16_f32(xr, xl), Xh = cvt_x16_f32(xr + 4, xh);
         const int r0 = (b - a.routed_blocks) * rows_blk + wv * GU_RPW;
         uint32_t sink = 0;
-        if (wv == 1 && a.pf_sh_down) touch_rows8(a.pf_sh_down, a.pf_sh_rb, a.H, b - a.routed_blocks, a.S / rows_blk, lane, sink);
+        /* waves 1 and 2 touch the group slots 0..3 of this block's rows (the
+         * H / 8 groups of 8 rows over S / (4 GU_RPW) blocks: 4 each at
+         * H = 2048, S = 512) */
+        if ((wv == 1 || wv == 2) && a.pf_sh_down)
+            touch_rows8(a.pf_sh_down, a.pf_sh_rb, a.H, b - a.routed_blocks, a.S / rows_blk, 2 * (wv - 1), lane, sink);
         gu_body1<GU_RPW>(a, a.sh_gate, a.sh_up, r0, xl, xh, Xl, Xh, a.act_sh, lane);
         asm volatile("s_waitcnt vmcnt(0)" : : "v"(sink));
         return;
@@ -525,11 +530,12 @@ DEV void k_gemv_gate_up1_body(GUArgs a, RouteArgs ra) {
         lds_barrier();
         issue(s_eu);
     }
-    /* the next wave after the selecting one touches the selected expert's
-     * down rows that this block's XCD will read */
+    /* the two waves after the selecting one touch the selected expert's
+     * down rows that this block's XCD will read (group slots 0..3) */
     uint32_t sink = 0;
-    if (wv == ((sel + 1) & 3) && a.pf_down)
-        touch_rows8(a.pf_down + (size_t)s_eu * a.pf_down_stride, a.pf_rb, a.H, b % bpe, bpe, lane, sink);
+    const int tw = (wv - sel) & 3;
+    if ((tw == 1 || tw == 2) && a.pf_down)
+        touch_rows8(a.pf_down + (size_t)s_eu * a.pf_down_stride, a.pf_rb, a.H, b % bpe, bpe, 2 * (tw - 1), lane, sink);
     /* this lane's 32 values of x (k = klo .. klo + 15, klo + 32 .. + 47) */
     h2 xl[8], xh[8];
     float Xl = 0.0f, Xh = 0.0f;
