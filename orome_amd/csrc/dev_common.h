@@ -258,6 +258,13 @@ DEV u4 ld_u4(const uint8_t *p) {
     typedef const __attribute__((address_space(1))) u4 *gp4;
     return *(gp4)(uintptr_t)p;
 }
+/* Streaming load (`nt`): for expert weights, which a forward reads once, so
+ * that they do not push the activations and expert outputs the next kernels
+ * read back out of the last-level cache */
+DEV u4 ld_u4_nt(const uint8_t *p) {
+    typedef __attribute__((address_space(1))) u4 *gp4;
+    return __builtin_nontemporal_load((gp4)(uintptr_t)p);
+}
 
 /* Cross-block hand-off inside one kernel: data stored and loaded as
  * agent-scope atomics, published by an agent-scope release (the counter

@@ -130,8 +130,8 @@ struct Span<FQ4K> {
     MDEV void init(int) {}
     MDEV void load(const uint8_t *row, int j, int kg) {
         const uint8_t *p = row + (size_t)(j >> 1) * 144;
-        hdr = ld_u4(p);
-        q = ld_u4(p + 16 + 16 * (kg + 4 * (j & 1)));
+        hdr = ld_u4_nt(p);
+        q = ld_u4_nt(p + 16 + 16 * (kg + 4 * (j & 1)));
     }
     h2 d, sc, nc, mb; /* (lo, hi) sub-block pairs: sc = (sl, sh/16), nc = (-1024 sl, -64 sh), mb = -(dmin m) */
     MDEV void prepare(int j, int kg) {
@@ -186,8 +186,8 @@ template <>
 struct Span<FQ4KT> : Span<FQ4K> {
     MDEV void load(const uint8_t *p, int j, int kg) {
         const uint8_t *b = p + (size_t)(j >> 1) * 2304;
-        hdr = ld_u4(b);
-        q = ld_u4(b + 256 + (j & 1) * 1024 + kg * 256);
+        hdr = ld_u4_nt(b);
+        q = ld_u4_nt(b + 256 + (j & 1) * 1024 + kg * 256);
     }
 };
 
@@ -202,9 +202,9 @@ struct Span<FQ5K> {
     MDEV void init(int) {}
     MDEV void load(const uint8_t *row, int j, int kg) {
         const uint8_t *p = row + (size_t)(j >> 1) * 176;
-        hdr = ld_u4(p);
-        q = ld_u4(p + 48 + 16 * (kg + 4 * (j & 1)));
-        qh = ld_u4(p + 16 + 16 * (kg & 1));
+        hdr = ld_u4_nt(p);
+        q = ld_u4_nt(p + 48 + 16 * (kg + 4 * (j & 1)));
+        qh = ld_u4_nt(p + 16 + 16 * (kg & 1));
     }
     h2 d, sc, nc, mb;
     int sh_lo; /* qh bit of the low values: 2g, g = 2(j&1) + kg/2 */
@@ -251,9 +251,9 @@ template <>
 struct Span<FQ5KT> : Span<FQ5K> {
     MDEV void load(const uint8_t *p, int j, int kg) {
         const uint8_t *b = p + (size_t)(j >> 1) * 2816;
-        hdr = ld_u4(b);
-        q = ld_u4(b + 256 + (j & 1) * 1024 + kg * 256);
-        qh = ld_u4(b + 2304 + (kg & 1) * 256);
+        hdr = ld_u4_nt(b);
+        q = ld_u4_nt(b + 256 + (j & 1) * 1024 + kg * 256);
+        qh = ld_u4_nt(b + 2304 + (kg & 1) * 256);
     }
 };
 
@@ -299,8 +299,8 @@ struct Span<FQ6KT> : Span<FQ6K> {
     MDEV void load(const uint8_t *p, int j, int kg) {
         const uint8_t *b = p + (size_t)(j >> 1) * 3360;
         const int h = j & 1, i = (int)(threadIdx.x & 15);
-        ql = ld_u4(b + h * 1024 + kg * 256);
-        qh = ld_u4(b + 2048 + h * 512 + (kg >> 1) * 256);
+        ql = ld_u4_nt(b + h * 1024 + kg * 256);
+        qh = ld_u4_nt(b + 2048 + h * 512 + (kg >> 1) * 256);
         sc8 = *(const u2 *)(b + 3072 + h * 8);
         dw = *(const uint16_t *)(b + 3328 - 14 * i);
     }
@@ -342,8 +342,8 @@ struct Span<FQ8T> {
     MDEV void load(const uint8_t *p, int j, int) {
         const int ln = threadIdx.x & 63;
         const uint8_t *b = p + (size_t)j * 2176;
-        q0 = ld_u4(b + 32 * ln);
-        q1 = ld_u4(b + 32 * ln + 16);
+        q0 = ld_u4_nt(b + 32 * ln);
+        q1 = ld_u4_nt(b + 32 * ln + 16);
         typedef const __attribute__((address_space(1))) u2 *gp2;
         dd = *(gp2)(uintptr_t)(b + 2048 + 8 * (ln & 15));
     }
