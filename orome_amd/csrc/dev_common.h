@@ -258,7 +258,7 @@ DEV u4 ld_u4(const uint8_t *p) {
     typedef const __attribute__((address_space(1))) u4 *gp4;
     return *(gp4)(uintptr_t)p;
 }
-/* Streaming load (`nt`): for expert weights, which a forward reads once, so
+/* Streaming load (`nt`): for expert weights that a forward reads once, so
  * that they do not push the activations and expert outputs the next kernels
  * read back out of the last-level cache */
 DEV u4 ld_u4_nt(const uint8_t *p) {

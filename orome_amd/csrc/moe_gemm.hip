@@ -78,6 +78,11 @@ DEV size_t lane_row(int row0, int i, size_t rbytes) {
            : FMT == FQ8T                 ? (size_t)row0 * rbytes
                                          : (size_t)(row0 + i) * rbytes;
 }
+/* weight loads: streaming (`nt`) in the big-tile kernels, where each
+ * weight is read by one unit, and cached elsewhere, where the tiles of a
+ * popular expert (and of the shared expert) read the same weights again */
+template <bool NT>
+DEV u4 ld_w(const uint8_t *p) { return NT ? ld_u4_nt(p) : ld_u4(p); }
 DEV uint32_t u4_at(u4 v, int i) { return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w; }
 DEV h2 splat(_Float16 v) { return h2{v, v}; }
 DEV h2 hfma(h2 a, h2 b, h2 c) { return __builtin_elementwise_fma(a, b, c); }
@@ -128,10 +133,11 @@ template <>
 struct Span<FQ4K> {
     u4 hdr, q;
     MDEV void init(int) {}
+    template <bool NT = false>
     MDEV void load(const uint8_t *row, int j, int kg) {
         const uint8_t *p = row + (size_t)(j >> 1) * 144;
-        hdr = ld_u4_nt(p);
-        q = ld_u4_nt(p + 16 + 16 * (kg + 4 * (j & 1)));
+        hdr = ld_w<NT>(p);
+        q = ld_w<NT>(p + 16 + 16 * (kg + 4 * (j & 1)));
     }
     h2 d, sc, nc, mb; /* (lo, hi) sub-block pairs: sc = (sl, sh/16), nc = (-1024 sl, -64 sh), mb = -(dmin m) */
     MDEV void prepare(int j, int kg) {
@@ -184,10 +190,11 @@ struct Span<FQ4K> {
  * layout touches 16 rows 1152 B apart.  `p` is the block base plus 16 i. */
 template <>
 struct Span<FQ4KT> : Span<FQ4K> {
+    template <bool NT = false>
     MDEV void load(const uint8_t *p, int j, int kg) {
         const uint8_t *b = p + (size_t)(j >> 1) * 2304;
-        hdr = ld_u4_nt(b);
-        q = ld_u4_nt(b + 256 + (j & 1) * 1024 + kg * 256);
+        hdr = ld_w<NT>(b);
+        q = ld_w<NT>(b + 256 + (j & 1) * 1024 + kg * 256);
     }
 };
 
@@ -200,11 +207,12 @@ template <>
 struct Span<FQ5K> {
     u4 hdr, q, qh;
     MDEV void init(int) {}
+    template <bool NT = false>
     MDEV void load(const uint8_t *row, int j, int kg) {
         const uint8_t *p = row + (size_t)(j >> 1) * 176;
-        hdr = ld_u4_nt(p);
-        q = ld_u4_nt(p + 48 + 16 * (kg + 4 * (j & 1)));
-        qh = ld_u4_nt(p + 16 + 16 * (kg & 1));
+        hdr = ld_w<NT>(p);
+        q = ld_w<NT>(p + 48 + 16 * (kg + 4 * (j & 1)));
+        qh = ld_w<NT>(p + 16 + 16 * (kg & 1));
     }
     h2 d, sc, nc, mb;
     int sh_lo; /* qh bit of the low values: 2g, g = 2(j&1) + kg/2 */
@@ -249,11 +257,12 @@ struct Span<FQ5K> {
  * 16g .. 16g+15 of qh.  `p` is the block base plus 16 i. */
 template <>
 struct Span<FQ5KT> : Span<FQ5K> {
+    template <bool NT = false>
     MDEV void load(const uint8_t *p, int j, int kg) {
         const uint8_t *b = p + (size_t)(j >> 1) * 2816;
-        hdr = ld_u4_nt(b);
-        q = ld_u4_nt(b + 256 + (j & 1) * 1024 + kg * 256);
-        qh = ld_u4_nt(b + 2304 + (kg & 1) * 256);
+        hdr = ld_w<NT>(b);
+        q = ld_w<NT>(b + 256 + (j & 1) * 1024 + kg * 256);
+        qh = ld_w<NT>(b + 2304 + (kg & 1) * 256);
     }
 };
 
@@ -264,6 +273,7 @@ struct Span<FQ6K> {
     uint32_t dw;
     int odd2;
     MDEV void init(int kg) { odd2 = 2 * (kg & 1); }
+    template <bool NT = false>
     MDEV void load(const uint8_t *row, int j, int kg) {
         const uint8_t *p = row + (size_t)(j >> 1) * 210;
         const int h = j & 1, lq = 16 * (kg >> 1);
@@ -296,11 +306,12 @@ struct Span<FQ6K> {
  * but d are aligned 16-, 8-byte loads.  `p` is the block base plus 16 i. */
 template <>
 struct Span<FQ6KT> : Span<FQ6K> {
+    template <bool NT = false>
     MDEV void load(const uint8_t *p, int j, int kg) {
         const uint8_t *b = p + (size_t)(j >> 1) * 3360;
         const int h = j & 1, i = (int)(threadIdx.x & 15);
-        ql = ld_u4_nt(b + h * 1024 + kg * 256);
-        qh = ld_u4_nt(b + 2048 + h * 512 + (kg >> 1) * 256);
+        ql = ld_w<NT>(b + h * 1024 + kg * 256);
+        qh = ld_w<NT>(b + 2048 + h * 512 + (kg >> 1) * 256);
         sc8 = *(const u2 *)(b + 3072 + h * 8);
         dw = *(const uint16_t *)(b + 3328 - 14 * i);
     }
@@ -311,6 +322,7 @@ struct Span<FQ8> {
     u2 qv[4];
     uint32_t dd[4];
     MDEV void init(int) {}
+    template <bool NT = false>
     MDEV void load(const uint8_t *row, int j, int kg) {
         const uint8_t *p = row + (size_t)(4 * j) * 34;
 #pragma unroll
@@ -339,11 +351,12 @@ struct Span<FQ8T> {
     u4 q0, q1;
     u2 dd;
     MDEV void init(int) {}
+    template <bool NT = false>
     MDEV void load(const uint8_t *p, int j, int) {
         const int ln = threadIdx.x & 63;
         const uint8_t *b = p + (size_t)j * 2176;
-        q0 = ld_u4_nt(b + 32 * ln);
-        q1 = ld_u4_nt(b + 32 * ln + 16);
+        q0 = ld_w<NT>(b + 32 * ln);
+        q1 = ld_w<NT>(b + 32 * ln + 16);
         typedef const __attribute__((address_space(1))) u2 *gp2;
         dd = *(gp2)(uintptr_t)(b + 2048 + 8 * (ln & 15));
     }
@@ -432,7 +445,7 @@ DEV void tile_run(const uint8_t *w0, const uint8_t *w1, int in_dim, const _Float
 #pragma unroll
         for (int m = 0; m < NMAT; m++) {
             ring[d][m].init(kg);
-            ring[d][m].load((m ? rw1 : rw0) + (size_t)rb * 16 * rbytes, j, kg);
+            ring[d][m].template load<(TBM >= 5)>((m ? rw1 : rw0) + (size_t)rb * 16 * rbytes, j, kg);
         }
     }
 
@@ -472,7 +485,7 @@ DEV void tile_run(const uint8_t *w0, const uint8_t *w1, int in_dim, const _Float
             {
                 const int u2 = min(u + DEPTH, U - 1), rb2 = u2 / nst, j2 = u2 - rb2 * nst;
 #pragma unroll
-                for (int m = 0; m < NMAT; m++) ring[d][m].load((m ? rw1 : rw0) + (size_t)rb2 * 16 * rbytes, j2, kg);
+                for (int m = 0; m < NMAT; m++) ring[d][m].template load<(TBM >= 5)>((m ? rw1 : rw0) + (size_t)rb2 * 16 * rbytes, j2, kg);
             }
             const _Float16 *bp = xs + ((j >> 1) & 1) * (Shape<TBM>::XR * BLD) + (j & 1) * KC + i * BLD + kg * 8;
 #pragma unroll
@@ -668,7 +681,7 @@ DEV void tile_stream(const P &pol, _Float16 *xs, int *rowoff) {
 #pragma unroll
         for (int m = 0; m < NMAT; m++) {
             ring[d][m].init(kg);
-            ring[d][m].load(cw[m] + (size_t)rb * 16 * rbytes, j, kg);
+            ring[d][m].template load<(TBM >= 5)>(cw[m] + (size_t)rb * 16 * rbytes, j, kg);
         }
     }
     /* chunks 0, 1 of the stream into buffers 0, 1, chunk 2 (unit 0's when
@@ -727,7 +740,7 @@ DEV void tile_stream(const P &pol, _Float16 *xs, int *rowoff) {
                     const int u2 = here ? u + DEPTH : u + DEPTH - U;
                     const int rb2 = u2 / nst, j2 = u2 - rb2 * nst;
 #pragma unroll
-                    for (int m = 0; m < NMAT; m++) ring[d][m].load((here ? cw[m] : nw[m]) + (size_t)rb2 * 16 * rbytes, j2, kg);
+                    for (int m = 0; m < NMAT; m++) ring[d][m].template load<(TBM >= 5)>((here ? cw[m] : nw[m]) + (size_t)rb2 * 16 * rbytes, j2, kg);
                 }
                 /* the stage after this one: next row block or next unit
                  * restart at stage 0, whose chunk 0 is this unit's (row
