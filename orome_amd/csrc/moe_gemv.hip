@@ -85,6 +85,13 @@ DEV Q4Raw q4_load(const uint8_t *row, int c) {
     const uint8_t *sb = row + (c >> 3) * 144;
     return Q4Raw{ld_u4(sb + 16 + (c & 7) * 16), ld_u4(sb)};
 }
+/* the same with streaming loads (`nt`), for the routed experts of the
+ * one-token gate/up: read once, they would push the shared expert, the
+ * touched down rows and the router out of the last-level cache */
+DEV Q4Raw q4_load_nt(const uint8_t *row, int c) {
+    const uint8_t *sb = row + (c >> 3) * 144;
+    return Q4Raw{ld_u4_nt(sb + 16 + (c & 7) * 16), ld_u4_nt(sb)};
+}
 DEV void q4_pos(int c, int &klo) { klo = (c >> 3) * 256 + ((c & 7) >> 1) * 64 + (c & 1) * 16; }
 DEV float q4_dot(const Q4Raw &r, int c, const h2 *xl, const h2 *xh, float Xl, float Xh) {
     Q4Affine af = q4k_affine(r.hdr, (c & 7) >> 1);
@@ -449,8 +456,8 @@ DEV void k_gemv_gate_up1_body(GUArgs a, RouteArgs ra) {
         const uint8_t *gb = a.gate + (size_t)e * a.gate_stride, *ub = a.up + (size_t)e * a.up_stride;
 #pragma unroll
         for (int i = 0; i < GU_RPW; i++) {
-            g[i] = q4_load(gb + (size_t)(r0 + i) * rb, lane);
-            w2[i] = q4_load(ub + (size_t)(r0 + i) * rb, lane);
+            g[i] = q4_load_nt(gb + (size_t)(r0 + i) * rb, lane);
+            w2[i] = q4_load_nt(ub + (size_t)(r0 + i) * rb, lane);
         }
     };
     int rank = 0;
