@@ -78,9 +78,10 @@ DEV size_t lane_row(int row0, int i, size_t rbytes) {
            : FMT == FQ8T                 ? (size_t)row0 * rbytes
                                          : (size_t)(row0 + i) * rbytes;
 }
-/* weight loads: streaming (`nt`) in the big-tile kernels, where each
- * weight is read by one unit, and cached elsewhere, where the tiles of a
- * popular expert (and of the shared expert) read the same weights again */
+/* weight loads: streaming (`nt`) in the big-tile kernels and the 16-row
+ * tiles of small batches, where each weight is read by one unit, and cached
+ * in the 32-row tiles, where the tiles of a popular expert (and of the
+ * shared expert) read the same weights again */
 template <bool NT>
 DEV u4 ld_w(const uint8_t *p) { return NT ? ld_u4_nt(p) : ld_u4(p); }
 DEV uint32_t u4_at(u4 v, int i) { return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w; }
@@ -445,7 +446,7 @@ DEV void tile_run(const uint8_t *w0, const uint8_t *w1, int in_dim, const _Float
 #pragma unroll
         for (int m = 0; m < NMAT; m++) {
             ring[d][m].init(kg);
-            ring[d][m].template load<(TBM >= 5)>((m ? rw1 : rw0) + (size_t)rb * 16 * rbytes, j, kg);
+            ring[d][m].template load<(TBM >= 5 || TBM == 1)>((m ? rw1 : rw0) + (size_t)rb * 16 * rbytes, j, kg);
         }
     }
 
@@ -485,7 +486,7 @@ DEV void tile_run(const uint8_t *w0, const uint8_t *w1, int in_dim, const _Float
             {
                 const int u2 = min(u + DEPTH, U - 1), rb2 = u2 / nst, j2 = u2 - rb2 * nst;
 #pragma unroll
-                for (int m = 0; m < NMAT; m++) ring[d][m].template load<(TBM >= 5)>((m ? rw1 : rw0) + (size_t)rb2 * 16 * rbytes, j2, kg);
+                for (int m = 0; m < NMAT; m++) ring[d][m].template load<(TBM >= 5 || TBM == 1)>((m ? rw1 : rw0) + (size_t)rb2 * 16 * rbytes, j2, kg);
             }
             const _Float16 *bp = xs + ((j >> 1) & 1) * (Shape<TBM>::XR * BLD) + (j & 1) * KC + i * BLD + kg * 8;
 #pragma unroll
