@@ -568,8 +568,9 @@ DEV void k_gemv_gate_up1_body(GUArgs a, RouteArgs ra) {
         pg[i] = wave_sum_fast(q4_dot(g[i], lane, xl, xh, Xl, Xh));
         pu[i] = wave_sum_fast(q4_dot(w2[i], lane, xl, xh, Xl, Xh));
     }
-    /* the act row is the expert's rank among the selected ids, which the
-     * selecting wave knows once its rounds are done */
+    /* the act row: the block's selection round (act_by_slot), else the
+     * expert's rank among the selected ids, which the selecting wave knows
+     * once its rounds are done */
     asm volatile("s_waitcnt vmcnt(0)" : : "v"(sink));
     if (a.act_by_slot) {
         rank = u; /* block u's expert was named by round u */
@@ -831,7 +832,6 @@ struct DownArgs {
     float *y, *ysh;
     const float *pf_router; /* T = 1, H = 2048: rows E x H to touch (the next layer's router) or NULL */
 };
-
 
 template <int NT, int FMT>
 DEV void down_slot(const uint8_t *row, int in_dim, int cl, int n, const _Float16 *const *xrow,
