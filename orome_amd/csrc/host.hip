@@ -550,6 +550,7 @@ static int forward_impl(orome_hip_ctx *c, const OromeHipModelConfig *cfg, const 
     if (set_dev(c)) return OROME_EHIP;
 
     RouteArgs a;
+    memset(&a, 0, sizeof a);
     a.W = (const float *)dev_addr(lt->routing_gate.buffer, lt->routing_gate.offset);
     a.wsg = lt->shared_expert_gate.buffer && lt->shared_expert_gate.format == OROME_QFMT_F32
                 ? (const float *)dev_addr(lt->shared_expert_gate.buffer, lt->shared_expert_gate.offset)
@@ -659,13 +660,18 @@ static int forward_impl(orome_hip_ctx *c, const OromeHipModelConfig *cfg, const 
          * previous layer's combine + RMSNorm already wrote it (a stack) */
         a.x16 = pre_normed ? NULL : c->x16;
         const Pack *rpk = find_pack(c, ex.gate, sh.gate);
-        if (rpk && rpk->r16 && rpk->rkey == a.W && H <= 4096 && K <= 64 && !route_exact_only()) {
+        /* the two-pass router's partial sums (8 T E floats) borrow the down
+         * projection's output rows, which are written only after the top-k
+         * has read them */
+        if (rpk && rpk->r16 && rpk->rkey == a.W && H <= 4096 && K <= 64 && (size_t)8 * E <= (size_t)c->kmax * H &&
+            !route_exact_only()) {
             /* registered layer: approximate logits on the matrix cores, then
              * the canonical logits of the experts that can win */
             a.W16 = rpk->r16;
             if (pre_normed) a.x16in = c->x16;
             a.wscale = rpk->rscale;
             a.wnorm = rpk->rnorm;
+            a.part = c->y;
             route_eps_coeffs(H, &a.eps_c1, &a.eps_c2);
             /* where the dispatch takes more than one launch, the top-k counts
              * for it (into counts the approximation pass clears) */

@@ -65,6 +65,10 @@ struct RouteArgs {
     const _Float16 *W16;
     const float *wscale, *wnorm;
     float eps_c1, eps_c2;
+    /* the approximation pass writes unscaled partial sums part[q][t][e]
+     * over 8 k-slices q ([8][T][E]); the exact top-k sums them, q
+     * ascending, and applies wscale */
+    float *part;
     /* small-batch dispatch feeding the grouped GEMMs: also write the small
      * tile list (one tile per active expert, then the shared expert's) */
     uint32_t *tiles_s;

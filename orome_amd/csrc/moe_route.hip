@@ -248,148 +248,113 @@ __global__ __launch_bounds__(256) void k_pack_router(const float *W, int H, _Flo
 }
 
 
-/* Pass 1: a block of NW waves computes 16*TTS tokens x 16*TES experts
- * (v_mfma_f32_16x16x32_f16, tokens as A rows, experts as B columns).  Wave w
- * covers k in [w H/NW, (w+1) H/NW) in chunks of S steps of 32; a chunk's
- * loads are all issued before its first MFMA.  The NW partial tiles are
- * summed through LDS in wave order.  The blocks of a token tile also stage
- * its x as fp16 for the grouped GEMMs (round to nearest even, each 4-group
- * stored (0,2,1,3)). */
-template <int TTS, int TES, int NW, int S, bool XH>
+/* Pass 1: approximate logits on the matrix cores (v_mfma_f32_16x16x32_f16,
+ * tokens as A rows, experts as B columns), split over k.  Block (tile, q)
+ * sums k in [q H/8, (q+1) H/8) for 16*TTS tokens and every expert into
+ * part[q][t][e], unscaled (the top-k adds the 8 slices and applies wscale).
+ * The slices go to linear ids with the same id % 8, so each slice's blocks
+ * run on one XCD: that XCD reads its eighth of x and of W16 from HBM once,
+ * and a block moves 16*TTS rows of x plus E rows of W16 of one slice to its
+ * CU (at T = 512, 36 MB over all blocks, against 64 MB for 16 x 32 tiles
+ * over all of k).  The block's x slice is converted once into LDS as fp16
+ * A fragments (round to nearest even, each 4-group stored (0,2,1,3), the
+ * order of W16's rows), and into x16 for the grouped GEMMs; in a prefill
+ * stack, where the previous layer's combine + RMSNorm has written x16, the
+ * pass reads it instead (XH) and stages nothing.  Wave w takes the expert
+ * groups w, w + NW, ... (16*TES experts each), issues a group's W16 loads
+ * for the slice, then runs its MFMAs. */
+template <int TTS, int TES, int NW, bool XH, int KS_MAX>
 __global__ __launch_bounds__(64 * NW) void k_route_approx(RouteArgs a) {
-    /* the wave index is uniform: say so, or the k loop is compiled divergent */
+    /* KS_MAX: the largest slice (H / 8) the launch allows */
+    __shared__ __attribute__((aligned(16))) _Float16 xs[16 * TTS][KS_MAX + 16];
     const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int E = a.E, H = a.H, T = a.T;
-    /* XCD-aware tiles: work-groups are dealt to the 8 XCDs round-robin by
-     * linear id, so the expert tiles of one token tile take ids that share
-     * id % 8 and read the token rows through one L2 (HBM reads x once) */
-    const int nex = (E + 16 * TES - 1) / (16 * TES), q = blockIdx.x >> 3;
-    const int ex = q % nex, ty = (q / nex) * 8 + (blockIdx.x & 7);
-    if (ty * 16 * TTS >= T) return;
-    const int e0 = ex * (16 * TES), t0 = ty * (16 * TTS);
-    /* the exact top-k that follows counts into dcnt: clear it ((T / 256
-     * rounded up) E words) */
+    const int E = a.E, H = a.H, T = a.T, KS = H / 8, nst = KS / 32;
+    const int q = blockIdx.x & 7, t0 = (blockIdx.x >> 3) * (16 * TTS), k0 = q * KS;
+    const int r = lane & 15, kq = (lane >> 4) * 8;
+    const int ngr = (E + 16 * TES - 1) / (16 * TES);
+    /* 8 steps (256 k) of a group's W16 loads at a time, all issued before
+     * the chunk's MFMAs (the whole slice at H = 2048); steps past the slice
+     * are clamped and unused */
+    h8 B[8][TES];
+    auto load_b = [&](int g, int c0) {
+#pragma unroll
+        for (int st = 0; st < 8; st++)
+#pragma unroll
+            for (int es = 0; es < TES; es++)
+                B[st][es] = *(const h8 *)(a.W16 + (size_t)min(g * 16 * TES + es * 16 + r, E - 1) * H + k0 + kq +
+                                          32 * min(c0 + st, nst - 1));
+    };
     if (a.dcnt && blockIdx.x == 0)
         for (int i = threadIdx.x; i < (T + 255) / 256 * E; i += 64 * NW) a.dcnt[i] = 0u;
-    const int r = lane & 15, kq = (lane >> 4) * 8;
-    /* XH: x comes as the staged fp16 copy (a.x16in), else as fp32 */
-    const float *xr[TTS];
-    const _Float16 *xhr[TTS];
-    bool stage[TTS];
+    /* stage the slice, 8 k values (two 4-groups) per item: the x loads go
+     * out first, then the first chunk's W16 loads, so the conversion waits
+     * only for x (loads complete in order) */
+    constexpr int NIT = (16 * TTS * (KS_MAX / 8) + 64 * NW - 1) / (64 * NW);
+    const int ipr = KS / 8, items = 16 * TTS * ipr;
+    f4 xl[NIT][2];
+    h8 xh[NIT];
 #pragma unroll
-    for (int ts = 0; ts < TTS; ts++) {
-        const int t = t0 + ts * 16 + r;
-        xr[ts] = a.x + (size_t)min(t, T - 1) * H + kq;
-        xhr[ts] = XH ? a.x16in + (size_t)min(t, T - 1) * H + kq : nullptr;
-        stage[ts] = !XH && a.x16 && t < T;
-    }
-    const _Float16 *wr[TES];
-#pragma unroll
-    for (int es = 0; es < TES; es++) wr[es] = a.W16 + (size_t)min(e0 + es * 16 + r, E - 1) * H + kq;
-    f4 acc[TTS][TES];
-#pragma unroll
-    for (int ts = 0; ts < TTS; ts++)
-#pragma unroll
-        for (int es = 0; es < TES; es++) acc[ts][es] = f4{0, 0, 0, 0};
-    const int kw = H / NW, kb = wv * kw, ke = kb + kw;
-    f4 xa[S][TTS][2];
-    h8 xh[S][TTS];
-    h8 B[S][TES];
-    /* loads unconditional (k clamped into the range; a clamped step is not
-     * used): a load under a branch makes the compiler wait for it */
-    auto load = [&](int k0) {
-#pragma unroll
-        for (int st = 0; st < S; st++) {
-            const int k = min(k0 + 32 * st, ke - 32);
-#pragma unroll
-            for (int ts = 0; ts < TTS; ts++) {
-                if (XH) {
-                    xh[st][ts] = *(const h8 *)(xhr[ts] + k);
-                } else {
-                    xa[st][ts][0] = *(const f4 *)(xr[ts] + k);
-                    xa[st][ts][1] = *(const f4 *)(xr[ts] + k + 4);
-                }
-            }
-#pragma unroll
-            for (int es = 0; es < TES; es++) B[st][es] = *(const h8 *)(wr[es] + k);
+    for (int j = 0; j < NIT; j++) {
+        const int it = min((int)threadIdx.x + 64 * NW * j, items - 1), rr = it / ipr, c = (it % ipr) * 8;
+        const int t = min(t0 + rr, T - 1);
+        if (XH) {
+            xh[j] = *(const h8 *)(a.x16in + (size_t)t * H + k0 + c);
+        } else {
+            xl[j][0] = *(const f4 *)(a.x + (size_t)t * H + k0 + c);
+            xl[j][1] = *(const f4 *)(a.x + (size_t)t * H + k0 + c + 4);
         }
-    };
-    auto compute = [&](int k0) {
-        h8 A[S][TTS];
-#pragma unroll
-        for (int st = 0; st < S; st++) {
-            const int k = k0 + 32 * st;
-            if (k < ke) {
-#pragma unroll
-                for (int ts = 0; ts < TTS; ts++) {
-                    /* each 4-group in W16's (0,2,1,3) order */
-                    const f4 lo = xa[st][ts][0], hi = xa[st][ts][1];
-                    A[st][ts] = XH ? xh[st][ts]
-                                   : h8{(_Float16)lo.x, (_Float16)lo.z, (_Float16)lo.y, (_Float16)lo.w,
-                                        (_Float16)hi.x, (_Float16)hi.z, (_Float16)hi.y, (_Float16)hi.w};
-#pragma unroll
-                    for (int es = 0; es < TES; es++)
-                        acc[ts][es] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[st][ts], B[st][es], acc[ts][es], 0, 0, 0);
-                }
-            }
-        }
-        /* staging stores after the chunk's last load is consumed: stores
-         * share the load counter, so earlier ones would hold up the waits.
-         * With one 16-token tile per block (T <= 1024) the token tile's nex
-         * expert-tile blocks split the steps (step i of a wave's k range goes
-         * to block i % nex), so no block carries all of the tile's stores
-         * (T = 512: 12.2 -> 11.0 us); the larger tiles of bigger batches
-         * stage from the first expert tile's blocks (splitting them measured
-         * 0.8 us slower at T = 2048). */
-#pragma unroll
-        for (int st = 0; st < S; st++) {
-            const int k = k0 + 32 * st;
-#pragma unroll
-            for (int ts = 0; ts < TTS; ts++)
-                if (stage[ts] && k < ke && (TTS == 1 ? ((k - kb) >> 5) % nex == ex : ex == 0)) {
-                    *(h8 *)(a.x16 + (xr[ts] - a.x) + k) = A[st][ts];
-                }
-        }
-    };
-    load(kb);
-    /* the output scales of this thread's slots o = threadIdx.x + 64 NW j,
-     * issued behind the first chunk's loads */
-    constexpr int NO = (TTS * TES * 4 * 64 + 64 * NW - 1) / (64 * NW);
-    float osc[NO];
-#pragma unroll
-    for (int j = 0; j < NO; j++) {
-        const int o = threadIdx.x + 64 * NW * j, slot = o >> 6;
-        osc[j] = a.wscale[min(e0 + ((slot >> 2) % TES) * 16 + (o & 15), E - 1)];
     }
-    compute(kb);
-    for (int k0 = kb + 32 * S; k0 < ke; k0 += 32 * S) {
-        load(k0);
-        compute(k0);
+    if (wv < ngr) load_b(wv, 0);
+#pragma unroll
+    for (int j = 0; j < NIT; j++) {
+        const int it = (int)threadIdx.x + 64 * NW * j, rr = it / ipr, c = (it % ipr) * 8;
+        if (it < items) {
+            const f4 lo = xl[j][0], hi = xl[j][1];
+            const h8 v = XH ? xh[j]
+                            : h8{(_Float16)lo.x, (_Float16)lo.z, (_Float16)lo.y, (_Float16)lo.w,
+                                 (_Float16)hi.x, (_Float16)hi.z, (_Float16)hi.y, (_Float16)hi.w};
+            if (!XH && a.x16 && t0 + rr < T) *(h8 *)(a.x16 + (size_t)(t0 + rr) * H + k0 + c) = v;
+            *(h8 *)&xs[rr][c] = v;
+        }
     }
-    __shared__ float red[NW][TTS * TES * 4][64];
-#pragma unroll
-    for (int ts = 0; ts < TTS; ts++)
-#pragma unroll
-        for (int es = 0; es < TES; es++)
-#pragma unroll
-            for (int v = 0; v < 4; v++) red[wv][(ts * TES + es) * 4 + v][lane] = acc[ts][es][v];
     __syncthreads();
+    for (int g = wv; g < ngr; g += NW) {
+        const int e0 = g * 16 * TES;
+        f4 acc[TTS][TES];
 #pragma unroll
-    for (int j = 0; j < NO; j++) {
-        const int o = threadIdx.x + 64 * NW * j;
-        if (o >= TTS * TES * 4 * 64) break;
-        const int slot = o >> 6, ln = o & 63;
-        float sum = red[0][slot][ln];
+        for (int ts = 0; ts < TTS; ts++)
 #pragma unroll
-        for (int w = 1; w < NW; w++) sum += red[w][slot][ln];
-        const int ts = slot / (TES * 4), es = (slot >> 2) % TES, v = slot & 3;
-        const int t = t0 + ts * 16 + 4 * (ln >> 4) + v, e = e0 + es * 16 + (ln & 15);
-        if (t < T && e < E) a.logits[(size_t)t * (E + 1) + e] = sum * osc[j];
+            for (int es = 0; es < TES; es++) acc[ts][es] = f4{0, 0, 0, 0};
+        for (int c0 = 0; c0 < nst; c0 += 8) {
+            if (c0 || g != wv) load_b(g, c0);
+#pragma unroll
+            for (int st = 0; st < 8; st++) {
+                const int step = c0 + st;
+                if (step < nst) {
+#pragma unroll
+                    for (int ts = 0; ts < TTS; ts++) {
+                        const h8 A = *(const h8 *)&xs[ts * 16 + r][32 * step + kq];
+#pragma unroll
+                        for (int es = 0; es < TES; es++)
+                            acc[ts][es] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, B[st][es], acc[ts][es], 0, 0, 0);
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int ts = 0; ts < TTS; ts++)
+#pragma unroll
+            for (int es = 0; es < TES; es++)
+#pragma unroll
+                for (int v = 0; v < 4; v++) {
+                    const int t = t0 + ts * 16 + 4 * (lane >> 4) + v, e = e0 + es * 16 + (lane & 15);
+                    if (t < T && e < E) a.part[((size_t)q * T + t) * E + e] = acc[ts][es][v];
+                }
     }
 }
 
 /* Pass 2: WPT waves per token (the lane layout of wave_topk).  Every wave of
- * a token computes the bounds, the K-th largest lower bound and the candidate
+ * a token adds up the approximation's partial sums, computes the bounds, the K-th largest lower bound and the candidate
  * list; the candidates (the shared-gate row first) are recomputed NB = 32/NI
  * rows at a time, batch i by wave i % WPT, with all loads of a batch in
  * flight together; the exact values meet in LDS and the token's first wave
@@ -419,9 +384,32 @@ __global__ __launch_bounds__(256) void k_topk_exact(RouteArgs a) {
 #pragma unroll
     for (int j = 0; j < EPL; j++) {
         const int e = min(lane * EPL + j, E - 1);
-        v[j] = lrow[e];
         rn[j] = a.wnorm[e];
         bv[j] = bias[e];
+    }
+    { /* the approximate logit: the pass's partial sums, slices ascending, then the row scale */
+        const int tt = min(t, a.T - 1);
+        float pq[8][EPL];
+        if (EPL == 4 && E % 4 == 0) { /* one 16-byte load per slice (lanes past E clamped) */
+            const int e4 = min(lane * 4, E - 4);
+#pragma unroll
+            for (int qq = 0; qq < 8; qq++) {
+                const f4 v4 = *(const f4 *)(a.part + ((size_t)qq * a.T + tt) * E + e4);
+                pq[qq][0] = v4.x; pq[qq][EPL > 1 ? 1 : 0] = v4.y; pq[qq][EPL > 2 ? 2 : 0] = v4.z; pq[qq][EPL > 3 ? 3 : 0] = v4.w;
+            }
+        } else {
+#pragma unroll
+            for (int qq = 0; qq < 8; qq++)
+#pragma unroll
+                for (int j = 0; j < EPL; j++) pq[qq][j] = a.part[((size_t)qq * a.T + tt) * E + min(lane * EPL + j, E - 1)];
+        }
+#pragma unroll
+        for (int j = 0; j < EPL; j++) {
+            float sum = pq[0][j];
+#pragma unroll
+            for (int qq = 1; qq < 8; qq++) sum += pq[qq][j];
+            v[j] = sum * a.wscale[min(lane * EPL + j, E - 1)];
+        }
     }
     float ss = 0.0f;
 #pragma unroll
@@ -984,25 +972,30 @@ int launch_pack_router(const float *W, int E, int H, _Float16 *W16, float *wscal
     return hipGetLastError() == hipSuccess ? 0 : -3;
 }
 
-/* Tile shapes (measured): up to 1024 tokens, 16 tokens x 32 experts and 8
- * waves per block (blocks for every CU); beyond, 32 x 64 and 4 waves (the
- * fewest bytes moved per logit). */
+/* the approximation pass: 16 tokens a block up to 1024 tokens, 32 beyond;
+ * 8 waves */
 int launch_route_approx(const RouteArgs &a, hipStream_t s) {
-    if (!a.W16 || !a.wscale || a.H % 256 || a.T < 1) return -2;
-    /* 1-D grid: expert tiles x token tiles rounded up to 8 (see the kernel) */
-    auto grid = [&](int te, int tt) { return dim3((unsigned)((a.E + te - 1) / te * (((a.T + tt - 1) / tt + 7) / 8 * 8))); };
+    if (!a.W16 || !a.wscale || !a.part || a.H % 256 || a.H > 4096 || a.T < 1) return -2;
+    const int tt = a.T <= 1024 ? 16 : 32;
+    const dim3 grid((unsigned)((a.T + tt - 1) / tt * 8));
+#define SK_LAUNCH(TTS, KSM)                                                                          \
+    do {                                                                                            \
+        if (a.x16in) KLAUNCH((k_route_approx<TTS, 2, 8, true, KSM>), grid, dim3(512), 0, s, a);  \
+        else KLAUNCH((k_route_approx<TTS, 2, 8, false, KSM>), grid, dim3(512), 0, s, a);         \
+    } while (0)
     if (a.T <= 1024) {
-        if (a.x16in) KLAUNCH((k_route_approx<1, 2, 8, 8, true>), grid(32, 16), dim3(512), 0, s, a);
-        else KLAUNCH((k_route_approx<1, 2, 8, 8, false>), grid(32, 16), dim3(512), 0, s, a);
+        if (a.H <= 2048) SK_LAUNCH(1, 256);
+        else SK_LAUNCH(1, 512);
     } else {
-        if (a.x16in) KLAUNCH((k_route_approx<2, 4, 4, 4, true>), grid(64, 32), dim3(256), 0, s, a);
-        else KLAUNCH((k_route_approx<2, 4, 4, 4, false>), grid(64, 32), dim3(256), 0, s, a);
+        if (a.H <= 2048) SK_LAUNCH(2, 256);
+        else SK_LAUNCH(2, 512);
     }
+#undef SK_LAUNCH
     return hipGetLastError() == hipSuccess ? 0 : -3;
 }
 
 int launch_topk_exact(const RouteArgs &a, hipStream_t s) {
-    if (!a.wnorm || a.H % 256 || a.H > 4096 || a.K > 64 || a.K > a.E) return -2;
+    if (!a.wnorm || !a.part || !a.wscale || a.H % 256 || a.H > 4096 || a.K > 64 || a.K > a.E) return -2;
     const int ni = a.H / 256;
     /* up to 1024 tokens a token's candidates spread over 4 waves (more waves
      * in flight); beyond, one wave per token already fills the chip */
