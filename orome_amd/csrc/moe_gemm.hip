@@ -422,7 +422,7 @@ struct Chunk {
  * chunks (256 k) sit in two LDS buffers: with <= 2 chunks both stay resident
  * (one barrier in all); with more, chunk c+2 is written into c's buffer
  * after the barrier that ends chunk c (RPW must be 1 then). */
-template <int FMT, int NMAT, int RPW, int DEPTH, int NST, int TBM, typename Epi>
+template <int FMT, int NMAT, int RPW, int DEPTH, int NST, int TBM, bool NT, typename Epi>
 DEV void tile_run(const uint8_t *w0, const uint8_t *w1, int in_dim, const _Float16 *src, int ld,
                   const int *rowoff, int rows, int yb, _Float16 *xs, const Epi &epi) {
     const int tb = (rows + 15) >> 4;
@@ -446,7 +446,7 @@ DEV void tile_run(const uint8_t *w0, const uint8_t *w1, int in_dim, const _Float
 #pragma unroll
         for (int m = 0; m < NMAT; m++) {
             ring[d][m].init(kg);
-            ring[d][m].template load<(TBM >= 5 || TBM == 1)>((m ? rw1 : rw0) + (size_t)rb * 16 * rbytes, j, kg);
+            ring[d][m].template load<NT>((m ? rw1 : rw0) + (size_t)rb * 16 * rbytes, j, kg);
         }
     }
 
@@ -486,7 +486,7 @@ DEV void tile_run(const uint8_t *w0, const uint8_t *w1, int in_dim, const _Float
             {
                 const int u2 = min(u + DEPTH, U - 1), rb2 = u2 / nst, j2 = u2 - rb2 * nst;
 #pragma unroll
-                for (int m = 0; m < NMAT; m++) ring[d][m].template load<(TBM >= 5 || TBM == 1)>((m ? rw1 : rw0) + (size_t)rb2 * 16 * rbytes, j2, kg);
+                for (int m = 0; m < NMAT; m++) ring[d][m].template load<NT>((m ? rw1 : rw0) + (size_t)rb2 * 16 * rbytes, j2, kg);
             }
             const _Float16 *bp = xs + ((j >> 1) & 1) * (Shape<TBM>::XR * BLD) + (j & 1) * KC + i * BLD + kg * 8;
 #pragma unroll
@@ -858,13 +858,21 @@ DEV void k_gemm_gate_up_body(GemmArgs a) {
         rowoff[threadIdx.x] = q >= rows ? a.zrow : sh ? (int)(first + q) : (int)(a.pairs[first + q] / (uint32_t)a.K);
     }
     __syncthreads();
+    constexpr bool NT = TBM >= 5 || TBM == 1;
+    /* a 32-row tile holding at most 16 rows runs the 16-row code: half the
+     * matrix instructions and B-fragment reads, the same weight stream */
     if (sh) {
         const GuEpi epi{a.act_sh, a.S, (int)first, (int)rows};
-        tile_run<SF, 2, GU_RPW, (SF == FQ8 || SF == FQ8T ? 2 : Shape<TBM>::DEPTH), NST, TBM>(a.sh_a, a.sh_b, a.H, a.src, a.H, rowoff, (int)rows, yb, xs, epi);
+        constexpr int D = SF == FQ8 || SF == FQ8T ? 2 : Shape<TBM>::DEPTH;
+        if (TBM == 2 && rows <= 16)
+            tile_run<SF, 2, GU_RPW, D, NST, 1, NT>(a.sh_a, a.sh_b, a.H, a.src, a.H, rowoff, (int)rows, yb, xs, epi);
+        else tile_run<SF, 2, GU_RPW, D, NST, TBM, NT>(a.sh_a, a.sh_b, a.H, a.src, a.H, rowoff, (int)rows, yb, xs, epi);
     } else {
         const GuEpi epi{a.act, a.M, (int)first, (int)rows};
-        tile_run<RF, 2, GU_RPW, Shape<TBM>::DEPTH, NST, TBM>(a.wa + (size_t)e * a.stride_a, a.wb + (size_t)e * a.stride_b, a.H, a.src,
-                                                          a.H, rowoff, (int)rows, yb, xs, epi);
+        const uint8_t *w0 = a.wa + (size_t)e * a.stride_a, *w1 = a.wb + (size_t)e * a.stride_b;
+        if (TBM == 2 && rows <= 16)
+            tile_run<RF, 2, GU_RPW, Shape<TBM>::DEPTH, NST, 1, NT>(w0, w1, a.H, a.src, a.H, rowoff, (int)rows, yb, xs, epi);
+        else tile_run<RF, 2, GU_RPW, Shape<TBM>::DEPTH, NST, TBM, NT>(w0, w1, a.H, a.src, a.H, rowoff, (int)rows, yb, xs, epi);
     }
 }
 
@@ -890,10 +898,10 @@ __global__ __launch_bounds__(Shape<TBM>::W * 64) void k_gemm_down(GemmArgs a) {
     __syncthreads();
     if (sh) {
         const DnEpi epi{a.ysh, a.H, (int)first, (int)rows};
-        tile_run<SFMT, 1, DN_RPW, Shape<TBM>::DEPTH, NST, TBM>(a.sh_a, nullptr, a.S, a.src_sh, a.S, rowoff, (int)rows, yb, xs, epi);
+        tile_run<SFMT, 1, DN_RPW, Shape<TBM>::DEPTH, NST, TBM, (TBM >= 5 || TBM == 1)>(a.sh_a, nullptr, a.S, a.src_sh, a.S, rowoff, (int)rows, yb, xs, epi);
     } else {
         const DnEpi epi{a.y, a.H, (int)first, (int)rows};
-        tile_run<EFMT, 1, DN_RPW, Shape<TBM>::DEPTH, NST, TBM>(a.wa + (size_t)e * a.stride_a, nullptr, a.M, a.src, a.M, rowoff, (int)rows, yb, xs, epi);
+        tile_run<EFMT, 1, DN_RPW, Shape<TBM>::DEPTH, NST, TBM, (TBM >= 5 || TBM == 1)>(a.wa + (size_t)e * a.stride_a, nullptr, a.M, a.src, a.M, rowoff, (int)rows, yb, xs, epi);
     }
 }
 
