@@ -470,3 +470,14 @@ def test_more_than_256_experts(T):
     p = Pair(max_tokens=T, E=384, H=512, M=256, S=256, seed=91)
     run_and_check(p, T, seed=3300 + T, path=_lib.OROME_PATH_MFMA)
     p.gm.close()
+
+
+def test_two_pass_router_h4096():
+    """H = 4096 (the largest hidden size the two-pass router takes): the
+    approximation pass walks its k-slice in two chunks of loads and the exact
+    top-k holds 16 f4 of x per lane.  Routing bit-exact, output within
+    tolerance of the oracle."""
+    banner("H=4096, T=48")
+    p = Pair(max_tokens=48, H=4096, seed=77)
+    run_and_check(p, 48, seed=4048, path=_lib.OROME_PATH_MFMA)
+    p.gm.close()
