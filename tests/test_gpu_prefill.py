@@ -481,3 +481,37 @@ def test_two_pass_router_h4096():
     p = Pair(max_tokens=48, H=4096, seed=77)
     run_and_check(p, 48, seed=4048, path=_lib.OROME_PATH_MFMA)
     p.gm.close()
+
+
+@pytest.mark.parametrize("shape", [dict(E=256, H=2048, M=512, S=512), dict(E=384, H=1024, M=256, S=256),
+                                   dict(E=128, H=3072, M=512, S=512)])
+def test_two_pass_router_sweep(shape):
+    """The two-pass router over batch sizes on both sides of its tile-size
+    switch (16 and 32 tokens a block) and three router shapes, with activations
+    at two scales: expert indices bit-exact against the oracle's router and
+    top-k, the winners' and shared-gate logits bit-exact, weights to the
+    softmax's rounding."""
+    banner("two-pass sweep E=%(E)d H=%(H)d" % shape)
+    p = Pair(max_tokens=2048, seed=5, **shape)
+    L = O.lib(omp=True)
+    lr = p.om.layer(0)
+    E, H, K = p.om.E, p.om.H, p.om.K
+    for T in (17, 129, 512, 1025, 2048):
+        for s in range(2):
+            x = orome_amd.synth_normal(700 + s, T, T * H).reshape(T, H)
+            if s:
+                x *= np.float32(37.0)
+            _, dbg = p.run(0, x, np.zeros_like(x), path=_lib.OROME_PATH_MFMA)
+            lg = np.empty((T, E + 1), np.float32)
+            L.orc_router_logits(lr.router, lr.shared_gate_vec, O.p(x), T, E, H, O.p(lg))
+            idx = np.empty((T, K), np.int32)
+            w = np.empty((T, K), np.float32)
+            sg = np.empty(T, np.float32)
+            L.orc_topk_route(O.p(lg), lr.bias, T, E, K, O.p(idx), O.p(w), O.p(sg))
+            assert np.array_equal(dbg["idx"], idx), "indices T=%d s=%d" % (T, s)
+            assert np.allclose(dbg["w"], w, rtol=2e-6, atol=1e-7)
+            win = np.take_along_axis(lg[:, :E], idx, 1)
+            gwin = np.take_along_axis(dbg["logits"][:, :E], idx, 1)
+            assert np.array_equal(win.view(np.uint32), gwin.view(np.uint32)), "winner logits"
+            assert np.array_equal(lg[:, E].view(np.uint32), dbg["logits"][:, E].view(np.uint32)), "shared-gate logit"
+    p.gm.close()
