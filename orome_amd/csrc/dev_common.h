@@ -283,5 +283,44 @@ DEV void lds_barrier() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
+/* Inclusive scan of two words over the block (up to 16 waves), with both
+ * totals: a DPP scan per wave, then one barrier for the wave sums (wsum:
+ * LDS, 32 words).  Every thread of the block calls it. */
+DEV void scan2_block(uint32_t &x, uint32_t &y, uint32_t *wsum, uint32_t &tx, uint32_t &ty) {
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    /* wave inclusive scan with DPP: shifts by 1, 2, 4, 8 inside each row of
+     * 16 lanes (lanes shifted in from outside the row add 0), then lane 15
+     * of each row into the next row, lane 31 into rows 2 and 3 */
+#define SCAN_STEP(CTRL, ROWS)                                                            \
+    do {                                                                                 \
+        x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, CTRL, ROWS, 0xF, false);   \
+        y += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)y, CTRL, ROWS, 0xF, false);   \
+    } while (0)
+    SCAN_STEP(0x111, 0xF);
+    SCAN_STEP(0x112, 0xF);
+    SCAN_STEP(0x114, 0xF);
+    SCAN_STEP(0x118, 0xF);
+    SCAN_STEP(0x142, 0xA);
+    SCAN_STEP(0x143, 0xC);
+#undef SCAN_STEP
+    const int nw = (int)(blockDim.x >> 6);
+    if (lane == 63) {
+        wsum[wv] = x;
+        wsum[16 + wv] = y;
+    }
+    lds_barrier();
+    tx = 0;
+    ty = 0;
+    for (int w = 0; w < nw; w++) {
+        const uint32_t sx = wsum[w], sy = wsum[16 + w];
+        if (w < wv) {
+            x += sx;
+            y += sy;
+        }
+        tx += sx;
+        ty += sy;
+    }
+}
+
 /* ------------------------------------------------------------ dots */
 DEV float dot2(h2 a, h2 b, float c) { return __builtin_amdgcn_fdot2(a, b, c, false); }

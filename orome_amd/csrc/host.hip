@@ -52,6 +52,7 @@ struct orome_hip_ctx {
     float *logits, *w, *sgl, *y, *ysh, *xnorm;
     int32_t *idx;
     uint32_t *offsets, *pairs, *pos, *list, *counter, *tiles, *tiles_b, *dcount;
+    uint8_t *tmask;
     _Float16 *x16, *act, *act_sh;
     void *arena;
     size_t arena_bytes;
@@ -102,6 +103,7 @@ static size_t scratch_layout(orome_hip_ctx *c, uint8_t *base) {
         {(void **)&c->counter, 256},            {(void **)&c->tiles, (1 + 3 * ntile_s) * 4},
         {(void **)&c->tiles_b, (1 + 3 * ntile_b) * 4},
         {(void **)&c->dcount, (size_t)dispatch_blocks((int)T) * E * 4},
+        {(void **)&c->tmask, (size_t)TMASK_LD(T) * E},
         /* one extra all-zero row each (index tmax, tmax*kmax, tmax) */
         {(void **)&c->x16, (T + 1) * H * 2},    {(void **)&c->act, (T * K + 1) * M * 2},
         {(void **)&c->act_sh, (T + 1) * (S ? S : 1) * 2}, {(void **)&c->y, T * K * H * 4},
@@ -660,6 +662,7 @@ static int forward_impl(orome_hip_ctx *c, const OromeHipModelConfig *cfg, const 
          * previous layer's combine + RMSNorm already wrote it (a stack) */
         a.x16 = pre_normed ? NULL : c->x16;
         const Pack *rpk = find_pack(c, ex.gate, sh.gate);
+        bool self_dispatch = false; /* the small-tile gate/up forms the dispatch itself */
         /* the two-pass router's partial sums (8 T E floats) borrow the down
          * projection's output rows, which are written only after the top-k
          * has read them */
@@ -674,8 +677,12 @@ static int forward_impl(orome_hip_ctx *c, const OromeHipModelConfig *cfg, const 
             a.part = c->y;
             route_eps_coeffs(H, &a.eps_c1, &a.eps_c2);
             /* where the dispatch takes more than one launch, the top-k counts
-             * for it (into counts the approximation pass clears) */
-            if (dispatch_three_launches(a)) a.dcnt = c->dcount;
+             * for it, and where the small-tile gate/up dispatches itself, it
+             * marks each expert's tokens (into counts or masks the
+             * approximation pass clears) */
+            self_dispatch = gemm_self_dispatch_ok(T, K, E);
+            if (dispatch_three_launches(a) || self_dispatch) a.dcnt = c->dcount;
+            if (self_dispatch) a.tmask = c->tmask;
             TLAUNCH(c, ST_ROUTE, launch_route_approx(a, s), "router logits (matrix cores) + fp16 staging");
             a.x16 = NULL;
             TLAUNCH(c, ST_TOPK, launch_topk_exact(a, s), "top-k with canonical recomputation");
@@ -684,7 +691,9 @@ static int forward_impl(orome_hip_ctx *c, const OromeHipModelConfig *cfg, const 
             a.x16 = NULL;
             TLAUNCH(c, ST_TOPK, launch_topk(a, s), "top-k");
         }
-        TLAUNCH(c, ST_DISPATCH, launch_dispatch(a, c->tiles, c->tiles_b, S ? 1 : 0, c->dcount, s, a.dcnt ? 1 : 0), "dispatch");
+        if (!self_dispatch)
+            TLAUNCH(c, ST_DISPATCH, launch_dispatch(a, c->tiles, c->tiles_b, S ? 1 : 0, c->dcount, s, a.dcnt ? 1 : 0), "dispatch");
+        const GemmSelfDispatch sdargs = {c->dcount, dispatch_blocks(T), c->tmask, c->idx, c->offsets, c->pairs, c->pos};
         /* one launch per tile list (grid sized for the most tiles it can hold) */
         /* small batches (T K <= 32 E): every expert in 32-row tiles, the
          * shared expert too, and no big-tile list */
@@ -699,7 +708,8 @@ static int forward_impl(orome_hip_ctx *c, const OromeHipModelConfig *cfg, const 
         auto gate_up = [&](int tm, hipStream_t st) {
             return tm == GEMM_TILE_SMALL
                        ? launch_gemm_gate_up(exm, shm, c->x16, c->tmax, T, H, M, K, E, tm, c->tiles, ns_max, c->pairs, c->act,
-                                             c->act_sh, st, c->kt ? c->kt + 2 * (c->kt_blocks / 2) : nullptr, c->kt_blocks / 2)
+                                             c->act_sh, st, c->kt ? c->kt + 2 * (c->kt_blocks / 2) : nullptr, c->kt_blocks / 2,
+                                             self_dispatch ? &sdargs : nullptr)
                        : launch_gemm_gate_up(exm, shm, c->x16, c->tmax, T, H, M, K, E, tm, c->tiles_b, nb_max, c->pairs, c->act,
                                              c->act_sh, st, c->kt, c->kt_blocks / 2);
         };

@@ -78,6 +78,11 @@ struct RouteArgs {
      * three-launch dispatch would otherwise count (launch_dispatch(counted));
      * the approximation pass clears them first.  NULL: not counted */
     uint32_t *dcnt;
+    /* exact top-k: sets byte tmask[e * TMASK_LD(T) + t] to 1 for each
+     * selection (t, e): the token marks the self-dispatching gate/up reads
+     * (plain byte stores; the approximation pass clears them first).  NULL:
+     * not set */
+    uint8_t *tmask;
 };
 
 struct ExpertSide {
@@ -143,9 +148,24 @@ int launch_dequant(int fmt, const uint8_t *src, uint32_t rows, uint32_t n, float
 int launch_to_f16(const float *x, int T, int H, _Float16 *x16, hipStream_t s);
 /* x16, act and act_sh rows are stored (0,2,1,3) within each 4-group; zrow /
  * zrow_sh name an all-zero row of the activation source(s) */
+/* self-dispatch of the small-tile gate/up: the exact top-k's counts, token
+ * marks and selections, and the dispatch outputs the gate/up writes in place
+ * of the dispatch kernel (offsets, pairs, pos and the tile list `tiles`) */
+/* row pitch (bytes) of the token marks: T rounded up to 64 */
+#define TMASK_LD(T) (((T) + 63) / 64 * 64)
+struct GemmSelfDispatch {
+    const uint32_t *dcnt;  /* [g][E] expert counts per 256-token block */
+    int g;
+    const uint8_t *tmask;  /* [E][TMASK_LD(T)] token marks per expert */
+    const int32_t *idx;    /* [T][K] */
+    uint32_t *offsets, *pairs, *pos;
+};
+/* whether the small-tile gate/up can dispatch itself at these shapes */
+bool gemm_self_dispatch_ok(int T, int K, int E);
 int launch_gemm_gate_up(const ExpertSide &ex, const SharedSide &sh, const _Float16 *x16, int zrow, int T,
                         int H, int M, int K, int E, int tile_m, const uint32_t *tiles, int n_tiles_max,
-                        const uint32_t *pairs, _Float16 *act, _Float16 *act_sh, hipStream_t s, unsigned long long *kt = nullptr, int kt_cap = 0);
+                        const uint32_t *pairs, _Float16 *act, _Float16 *act_sh, hipStream_t s, unsigned long long *kt = nullptr,
+                        int kt_cap = 0, const GemmSelfDispatch *sd = nullptr);
 int launch_gemm_down(const ExpertSide &ex, const SharedSide &sh, const _Float16 *act,
                      const _Float16 *act_sh, int zrow, int zrow_sh, int T, int H, int M, int K, int E, int tile_m,
                      const uint32_t *tiles, int n_tiles_max, float *y, float *ysh,

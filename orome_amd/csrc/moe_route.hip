@@ -286,6 +286,11 @@ __global__ __launch_bounds__(64 * NW) void k_route_approx(RouteArgs a) {
     };
     if (a.dcnt && blockIdx.x == 0)
         for (int i = threadIdx.x; i < (T + 255) / 256 * E; i += 64 * NW) a.dcnt[i] = 0u;
+    if (a.tmask) { /* the token marks, 16 bytes a thread over all blocks */
+        const size_t n16 = (size_t)E * TMASK_LD(T) / 16;
+        for (size_t i = (size_t)blockIdx.x * 64 * NW + threadIdx.x; i < n16; i += (size_t)gridDim.x * 64 * NW)
+            *(u4 *)(a.tmask + 16 * i) = u4{0u, 0u, 0u, 0u};
+    }
     /* stage the slice, 8 k values (two 4-groups) per item: the x loads go
      * out first, then the first chunk's W16 loads, so the conversion waits
      * only for x (loads complete in order) */
@@ -510,6 +515,7 @@ __global__ __launch_bounds__(256) void k_topk_exact(RouteArgs a) {
     const TopkLane r = wave_topk_keys<EPL>(key, sg, K, lane, a.idx + t * K, a.w + t * K, a.sgl + t, nullptr);
     /* the three-launch dispatch's per-block expert counts (order-free) */
     if (a.dcnt && lane < K) atomicAdd(a.dcnt + (size_t)(t / 256) * E + r.id, 1u);
+    if (a.tmask && lane < K) a.tmask[(size_t)r.id * TMASK_LD(a.T) + t] = 1;
 }
 
 /* Dispatch for any T, in three launches over blocks of DSP_TOK tokens.  A
@@ -561,45 +567,6 @@ __global__ __launch_bounds__(DSP_TOK) void k_dispatch_count(RouteArgs a, uint32_
 #pragma unroll
         for (int w = 0; w < DSP_WORDS; w++) c += __popc(mask[e * DSP_WORDS + w]);
         cnt[(size_t)blockIdx.x * a.E + e] = c;
-    }
-}
-
-/* Inclusive scan of two words over the block (up to 16 waves), with both
- * totals: a DPP scan per wave, then one barrier for the wave sums (wsum:
- * LDS, 32 words).  Every thread of the block calls it. */
-DEV void scan2_block(uint32_t &x, uint32_t &y, uint32_t *wsum, uint32_t &tx, uint32_t &ty) {
-    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-    /* wave inclusive scan with DPP: shifts by 1, 2, 4, 8 inside each row of
-     * 16 lanes (lanes shifted in from outside the row add 0), then lane 15
-     * of each row into the next row, lane 31 into rows 2 and 3 */
-#define SCAN_STEP(CTRL, ROWS)                                                            \
-    do {                                                                                 \
-        x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, CTRL, ROWS, 0xF, false);   \
-        y += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)y, CTRL, ROWS, 0xF, false);   \
-    } while (0)
-    SCAN_STEP(0x111, 0xF);
-    SCAN_STEP(0x112, 0xF);
-    SCAN_STEP(0x114, 0xF);
-    SCAN_STEP(0x118, 0xF);
-    SCAN_STEP(0x142, 0xA);
-    SCAN_STEP(0x143, 0xC);
-#undef SCAN_STEP
-    const int nw = (int)(blockDim.x >> 6);
-    if (lane == 63) {
-        wsum[wv] = x;
-        wsum[16 + wv] = y;
-    }
-    lds_barrier();
-    tx = 0;
-    ty = 0;
-    for (int w = 0; w < nw; w++) {
-        const uint32_t sx = wsum[w], sy = wsum[16 + w];
-        if (w < wv) {
-            x += sx;
-            y += sy;
-        }
-        tx += sx;
-        ty += sy;
     }
 }
 
