@@ -592,7 +592,9 @@ DEV bool sd_locate(const GemmArgs &a, int ti, int yb, uint32_t &e, uint32_t &fir
     const uint32_t nt = (c + 31u) >> 5;
     uint32_t x = c, y = nt, tx, ty;
     scan2_block(x, y, wsum, tx, ty);
-    const uint32_t off = x - c, t0 = y - nt, ntiles = ty + (uint32_t)a.nsh;
+    /* counts that do not add up to T K (state not cleared) give an empty
+     * list rather than tiles past the buffers */
+    const uint32_t off = x - c, t0 = y - nt, ntiles = tx == (uint32_t)(a.T * a.K) ? ty + (uint32_t)a.nsh : 0u;
     if (ti == 0 && yb == 0) {
         if (tid < E) a.offsets[tid] = off;
         if (tid == 0) {
