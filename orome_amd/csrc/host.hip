@@ -622,7 +622,8 @@ static int forward_impl(orome_hip_ctx *c, const OromeHipModelConfig *cfg, const 
             /* every expert holds at most 16 rows: the grouped GEMMs alone
              * (gate/up on 16-row tiles; down keeps the persistent 32-row
              * kernel, faster here), then the combine */
-            const int ns_max = E + (S ? 1 : 0);
+            /* tiles: the active experts (at most T K), then the shared expert's */
+            const int ns_max = (T * K < E ? T * K : E) + (S ? 1 : 0);
             TLAUNCH(c, ST_GATE_UP,
                     launch_gemm_gate_up(hx, hs, c->x16, c->tmax, T, H, M, K, E, GEMM_TILE_MIN, c->tiles, ns_max,
                                         c->pairs, c->act, c->act_sh, s, c->kt, c->kt_blocks),
