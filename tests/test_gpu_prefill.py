@@ -486,17 +486,18 @@ def test_two_pass_router_h4096():
 @pytest.mark.parametrize("shape", [dict(E=256, H=2048, M=512, S=512), dict(E=384, H=1024, M=256, S=256),
                                    dict(E=128, H=3072, M=512, S=512)])
 def test_two_pass_router_sweep(shape):
-    """The two-pass router over batch sizes on both sides of its tile-size
-    switch (16 and 32 tokens a block) and three router shapes, with activations
-    at two scales: expert indices bit-exact against the oracle's router and
-    top-k, the winners' and shared-gate logits bit-exact, weights to the
-    softmax's rounding."""
+    """The two-pass router over batch sizes covering its three tile sizes (16,
+    32 and 64 tokens a block) and both sides of the self-dispatching gate/up's
+    limit (1024 tokens), three router shapes (E = 384 takes the dispatch
+    kernel), activations at two scales: expert indices bit-exact against the
+    oracle's router and top-k, the winners' and shared-gate logits bit-exact,
+    weights to the softmax's rounding."""
     banner("two-pass sweep E=%(E)d H=%(H)d" % shape)
     p = Pair(max_tokens=2048, seed=5, **shape)
     L = O.lib(omp=True)
     lr = p.om.layer(0)
     E, H, K = p.om.E, p.om.H, p.om.K
-    for T in (17, 129, 512, 1025, 2048):
+    for T in (17, 129, 512, 1024, 1025, 2048):
         for s in range(2):
             x = orome_amd.synth_normal(700 + s, T, T * H).reshape(T, H)
             if s:
