@@ -491,7 +491,8 @@ def test_two_pass_router_sweep(shape):
     limit (1024 tokens), three router shapes (E = 384 takes the dispatch
     kernel), activations at two scales: expert indices bit-exact against the
     oracle's router and top-k, the winners' and shared-gate logits bit-exact,
-    weights to the softmax's rounding."""
+    weights to the softmax's rounding; the dispatch (offsets, pair order) bit-exact
+    against the oracle's."""
     banner("two-pass sweep E=%(E)d H=%(H)d" % shape)
     p = Pair(max_tokens=2048, seed=5, **shape)
     L = O.lib(omp=True)
@@ -515,4 +516,7 @@ def test_two_pass_router_sweep(shape):
             gwin = np.take_along_axis(dbg["logits"][:, :E], idx, 1)
             assert np.array_equal(win.view(np.uint32), gwin.view(np.uint32)), "winner logits"
             assert np.array_equal(lg[:, E].view(np.uint32), dbg["logits"][:, E].view(np.uint32)), "shared-gate logit"
+            off, pairs = O.dispatch(idx, E)
+            assert np.array_equal(dbg["offsets"], off), "dispatch offsets T=%d" % T
+            assert np.array_equal(dbg["pairs"], pairs), "dispatch order T=%d" % T
     p.gm.close()
