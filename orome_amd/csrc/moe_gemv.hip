@@ -450,7 +450,7 @@ DEV void k_gemv_gate_up1_body(GUArgs a, RouteArgs ra) {
      * every wave has stored its quarter of x).  The selecting wave is wave
      * (b / 256) % 4, so the blocks that share a CU (b, b + 256, b + 512 with
      * one block per CU and round) select on different SIMDs. */
-    __shared__ int s_eu, s_rank;
+    __shared__ int s_eu, s_rank, s_ids[64];
     Q4Raw g[GU_RPW], w2[GU_RPW];
     auto issue = [&](int e) {
         const uint8_t *gb = a.gate + (size_t)e * a.gate_stride, *ub = a.up + (size_t)e * a.up_stride;
@@ -503,35 +503,20 @@ DEV void k_gemv_gate_up1_body(GUArgs a, RouteArgs ra) {
         }
         rank = __popcll(__ballot(lane < K && myid < eu));
         if (lane == 0) s_rank = rank;
-        if (b == 0) { /* publish the call's routing for the down kernel */
+        if (b == 0) { /* the call's selections and weights; the block's
+                       * waves write the rest of the routing at the end */
             const float tw = lane < K ? expf(myval - v0) : 0.0f;
             float sum = 0.0f;
 #pragma unroll 1
             for (int k = 0; k < K; k++)
                 sum += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, tw), k));
             const float inv = sum > 0.0f ? 1.0f / sum : 0.0f;
-            int rkk = 0;
-#pragma unroll 1
-            for (int k = 0; k < K; k++) rkk += __builtin_amdgcn_readlane(myid, k) < myid;
             if (lane < K) {
                 ra.idx[lane] = myid;
                 ra.w[lane] = tw * inv;
-                ra.pairs[rkk] = (uint32_t)lane;
-                ra.pos[lane] = (uint32_t)rkk;
-                ACT_E(ra.list, rkk) = (uint32_t)myid;
-                ACT_OFF(ra.list, E, rkk) = (uint32_t)rkk;
+                s_ids[lane] = myid;
             }
-            if (lane == 0) {
-                ra.sgl[0] = sg;
-                ACT_N(ra.list) = (uint32_t)K;
-                ACT_OFF(ra.list, E, K) = (uint32_t)K;
-            }
-            for (int ee = lane; ee <= E; ee += 64) {
-                int c = 0;
-#pragma unroll 1
-                for (int k = 0; k < K; k++) c += __builtin_amdgcn_readlane(myid, k) < ee;
-                ra.offsets[ee] = (uint32_t)c;
-            }
+            if (lane == 0) ra.sgl[0] = sg;
         }
     } else {
         lds_barrier();
@@ -582,6 +567,34 @@ DEV void k_gemv_gate_up1_body(GUArgs a, RouteArgs ra) {
     if (lane == 0)
 #pragma unroll
         for (int i = 0; i < GU_RPW; i++) out[r0 + i] = glu_f16(pg[i], pu[i]);
+    if (b == 0) {
+        /* the dispatch of the call's routing for the down kernel, from the
+         * selected ids the selecting wave left in LDS before its products:
+         * sorted positions (pairs, pos), the active list and offsets[e] =
+         * the number of selected ids below e, one entry per thread.  Here,
+         * after every wave's products, it adds no time to the selecting
+         * wave (done there, it made block 0 end ~0.9 us after the rest). */
+        lds_barrier();
+        const int tid = threadIdx.x;
+        if (tid < K) {
+            const int id = s_ids[tid];
+            int rkk = 0;
+            for (int k = 0; k < K; k++) rkk += s_ids[k] < id;
+            ra.pairs[rkk] = (uint32_t)tid;
+            ra.pos[tid] = (uint32_t)rkk;
+            ACT_E(ra.list, rkk) = (uint32_t)id;
+            ACT_OFF(ra.list, E, rkk) = (uint32_t)rkk;
+        }
+        if (tid == 0) {
+            ACT_N(ra.list) = (uint32_t)K;
+            ACT_OFF(ra.list, E, K) = (uint32_t)K;
+        }
+        for (int ee = tid; ee <= E; ee += 256) {
+            int c = 0;
+            for (int k = 0; k < K; k++) c += s_ids[k] < ee;
+            ra.offsets[ee] = (uint32_t)c;
+        }
+    }
 }
 
 template <int EPL>
