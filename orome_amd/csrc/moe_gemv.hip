@@ -396,6 +396,15 @@ __global__ __launch_bounds__(256) void k_gemv_gate_up(GUArgs a, RouteArgs ra) {
  * selected ids: its act row) and, in block 0, the published routing overlap
  * those loads.  Selection and softmax restate softmax_topk_route
  * (inference/src/shaders.metal:1141-1234) exactly as wave_topk does. */
+/* a lane's EPL in-lane positions, four bits each */
+template <int EPL>
+struct PosPack {
+    typedef uint32_t type;
+};
+template <>
+struct PosPack<16> {
+    typedef uint64_t type;
+};
 template <int EPL>
 DEV void k_gemv_gate_up1_body(GUArgs a, RouteArgs ra) {
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
@@ -477,22 +486,30 @@ DEV void k_gemv_gate_up1_body(GUArgs a, RouteArgs ra) {
                     const uint32_t tk = key[j]; key[j] = key[j + 1]; key[j + 1] = tk;
                     const int tj = kj[j]; kj[j] = kj[j + 1]; kj[j + 1] = tj;
                 }
-        /* lane k keeps the k-th winner */
+        /* lane k keeps the k-th winner.  A round is a serial chain on one
+         * wave, so it carries only what the next round needs: the lanes'
+         * lists (the in-lane positions packed four bits each, popped by one
+         * shift) and the winner's key; keys become values after the
+         * rounds. */
+        typedef typename PosPack<EPL>::type PK;
+        PK kjp = 0;
+#pragma unroll
+        for (int j = 0; j < EPL; j++) kjp |= (PK)kj[j] << (4 * j);
         int myid = 0, eu = 0;
-        float myval = 0.0f, v0 = 0.0f;
+        uint32_t mykey = 0u, key0 = 0u;
         /* a rolled loop: each wave runs these rounds once */
 #pragma unroll 1
         for (int k = 0; k < K; k++) {
             const uint32_t m = wave_max_u32(key[0]);
             const int wl = (int)__builtin_ctzll(__ballot(key[0] == m));
-            const int id = wl * EPL + __builtin_amdgcn_readlane(kj[0], wl);
-            const float val = ord_value(m);
-            if (lane == k) { myid = id; myval = val; }
-            if (k == 0) v0 = val;
+            const int id = wl * EPL + (int)((uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)kjp, wl) & 0xFu);
+            if (lane == k) { myid = id; mykey = m; }
+            if (k == 0) key0 = m;
             if (lane == wl) {
 #pragma unroll
-                for (int j = 0; j + 1 < EPL; j++) { key[j] = key[j + 1]; kj[j] = kj[j + 1]; }
+                for (int j = 0; j + 1 < EPL; j++) key[j] = key[j + 1];
                 key[EPL - 1] = 0u;
+                kjp >>= 4;
             }
             if (k == u) {
                 eu = id;
@@ -501,6 +518,7 @@ DEV void k_gemv_gate_up1_body(GUArgs a, RouteArgs ra) {
                 issue(eu);
             }
         }
+        const float myval = ord_value(mykey), v0 = ord_value(key0);
         rank = __popcll(__ballot(lane < K && myid < eu));
         if (lane == 0) s_rank = rank;
         if (b == 0) { /* the call's selections and weights; the block's

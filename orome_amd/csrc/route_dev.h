@@ -37,7 +37,13 @@ DEV uint32_t wave_max_u32(uint32_t m) {
     m = max(m, dppu<DPP_MIRROR>(m));
     const uint32_t a = (uint32_t)__builtin_amdgcn_readlane((int)m, 0), b = (uint32_t)__builtin_amdgcn_readlane((int)m, 16);
     const uint32_t c = (uint32_t)__builtin_amdgcn_readlane((int)m, 32), d = (uint32_t)__builtin_amdgcn_readlane((int)m, 48);
-    return max(max(a, b), max(c, d));
+    /* on the scalar unit (left to itself the compiler copies b and d back
+     * into vector registers for one v_max3); s_max writes SCC */
+    uint32_t ab, cd, r;
+    asm("s_max_u32 %0, %1, %2" : "=s"(ab) : "s"(a), "s"(b) : "scc");
+    asm("s_max_u32 %0, %1, %2" : "=s"(cd) : "s"(c), "s"(d) : "scc");
+    asm("s_max_u32 %0, %1, %2" : "=s"(r) : "s"(ab), "s"(cd) : "scc");
+    return r;
 }
 
 /* One token's top-K on one wave.  Lane L owns the EPL consecutive experts
