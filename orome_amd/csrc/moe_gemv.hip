@@ -1119,17 +1119,33 @@ struct DnX<FQ8> {
 
 /* SLOT: act row k belongs to slot k (the gate/up wrote them in selection
  * order), so the activation loads go out with the routing loads instead of
- * after them. */
+ * after them.
+ *
+ * A block holds 8 output rows as two halves of 4 rows (a 16-lane group per
+ * row), and each half's nine dots (8 routed slots, then the shared expert)
+ * are spread over DC_SG waves: wave g of a half takes slots g, g + DC_SG,
+ * g + 2 DC_SG (slot 8 is the shared expert's).  One wave per half running
+ * all nine dots one after the other was bound by that wave's instruction
+ * chain (~1200 instructions after its loads arrived).  The dots are
+ * unchanged, and the sums go through LDS to the half's first wave, which
+ * combines them in k_combine's order: h_in + sum_k w_k y_k (k ascending),
+ * then + sigmoid(s) y_shared. */
+#define DC_SG 3
 template <int EFMT, int SFMT, bool SLOT>
-__global__ __launch_bounds__(128) void k_gemv_down_combine1(DownArgs a, RouteArgs ra, const float *h_in,
-                                                            float *h_out, float *res) {
+__global__ __launch_bounds__(128 * DC_SG) void k_gemv_down_combine1(DownArgs a, RouteArgs ra, const float *h_in,
+                                                                   float *h_out, float *res) {
+    constexpr int NS = (DC_K + 1 + DC_SG - 1) / DC_SG; /* slots per wave */
+    static_assert(NS * DC_SG == DC_K + 1, "nine slots over the waves of a half");
+    __shared__ float ys[2][DC_K + 1][4];
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-    const int cl = lane & 15, r = blockIdx.x * 8 + wv * 4 + (lane >> 4);
+    const int half = wv / DC_SG, g = wv % DC_SG;
+    const int cl = lane & 15, rq = lane >> 4, r = blockIdx.x * 8 + half * 4 + rq;
     const int K = a.K;
     const size_t rb = row_bytes(EFMT, a.M);
     const bool has_sh = a.sh_down != nullptr;
+    const bool sh_here = g == DC_SG - 1; /* this wave's last slot is the shared expert's */
     /* every load up front and unconditional, in dependence order: the slots'
-     * experts, positions and weights; then all weight chunks; then all
+     * experts, positions and weights; then the weight chunks; then the
      * activation chunks, the residual and the gate (a load under a branch,
      * or one made inside a slot's dot, is waited for alone) */
     /* the 8 slots' experts, positions and weights as three 32-byte reads
@@ -1139,42 +1155,52 @@ __global__ __launch_bounds__(128) void k_gemv_down_combine1(DownArgs a, RouteArg
     typedef int i4v __attribute__((ext_vector_type(4)));
     const i4v e0 = *(const i4v *)ra.idx, e1 = *(const i4v *)(ra.idx + 4);
     const u4 p0 = *(const u4 *)ra.pos, p1 = *(const u4 *)(ra.pos + 4);
-    const f4 w0 = *(const f4 *)ra.w, w1 = *(const f4 *)(ra.w + 4);
     int o[4], osh[4];
     DnX<EFMT>::offs(cl, o);
     DnX<SFMT>::offs(cl, osh);
-    u4 xq[DC_K][4], sq[4];
+    /* this wave's routed slots: k = g + DC_SG j (j < NS, and the shared
+     * expert's in place of k = 8); a slot past 8 reads slot 0's rows */
+    int kk[NS];
+#pragma unroll
+    for (int j = 0; j < NS; j++) kk[j] = min(g + DC_SG * j, DC_K - 1);
+    u4 xq[NS][4], sq[4];
     const _Float16 *xs = has_sh ? a.act_sh : a.act;
     if constexpr (SLOT) {
 #pragma unroll
-        for (int k = 0; k < DC_K; k++)
+        for (int j = 0; j < NS; j++)
 #pragma unroll
-            for (int j = 0; j < 4; j++) xq[k][j] = ld_u4((const uint8_t *)(a.act + (size_t)(k < K ? k : 0) * a.M + o[j]));
+            for (int q = 0; q < 4; q++) xq[j][q] = ld_u4((const uint8_t *)(a.act + (size_t)(kk[j] < K ? kk[j] : 0) * a.M + o[q]));
 #pragma unroll
-        for (int j = 0; j < 4; j++) sq[j] = ld_u4((const uint8_t *)(xs + osh[j]));
+        for (int q = 0; q < 4; q++) sq[q] = ld_u4((const uint8_t *)(xs + osh[q]));
     }
     const int ev[DC_K] = {e0.x, e0.y, e0.z, e0.w, e1.x, e1.y, e1.z, e1.w};
     const int pv[DC_K] = {(int)p0.x, (int)p0.y, (int)p0.z, (int)p0.w, (int)p1.x, (int)p1.y, (int)p1.z, (int)p1.w};
-    const float wk[DC_K] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
-    int e[DC_K], ps[DC_K];
+    int e[NS], ps[NS];
 #pragma unroll
-    for (int k = 0; k < DC_K; k++) {
-        e[k] = k < K ? ev[k] : ev[0];
-        ps[k] = k < K ? pv[k] : pv[0];
+    for (int j = 0; j < NS; j++) {
+        /* kk[j] is wave-uniform: a select over the eight slots */
+        int ej = ev[0], pj = pv[0];
+#pragma unroll
+        for (int k = 1; k < DC_K; k++)
+            if (kk[j] == k && k < K) { ej = ev[k]; pj = pv[k]; }
+        e[j] = ej;
+        ps[j] = pj;
     }
-    DnRaw<EFMT> raw[DC_K];
+    DnRaw<EFMT> raw[NS];
 #pragma unroll
-    for (int k = 0; k < DC_K; k++) raw[k].load(a.down + (size_t)e[k] * a.down_stride + (size_t)r * rb, cl);
+    for (int j = 0; j < NS; j++) raw[j].load(a.down + (size_t)e[j] * a.down_stride + (size_t)r * rb, cl);
     DnRaw<SFMT> rsh;
     rsh.load(has_sh ? a.sh_down + (size_t)r * row_bytes(SFMT, a.S) : a.down + (size_t)r * rb, cl);
     if constexpr (!SLOT) {
 #pragma unroll
-        for (int k = 0; k < DC_K; k++)
+        for (int j = 0; j < NS; j++)
 #pragma unroll
-            for (int j = 0; j < 4; j++) xq[k][j] = ld_u4((const uint8_t *)(a.act + (size_t)ps[k] * a.M + o[j]));
+            for (int q = 0; q < 4; q++) xq[j][q] = ld_u4((const uint8_t *)(a.act + (size_t)ps[j] * a.M + o[q]));
 #pragma unroll
-        for (int j = 0; j < 4; j++) sq[j] = ld_u4((const uint8_t *)(xs + osh[j]));
+        for (int q = 0; q < 4; q++) sq[q] = ld_u4((const uint8_t *)(xs + osh[q]));
     }
+    /* what the combine needs, loaded with the rest */
+    const f4 w0 = *(const f4 *)ra.w, w1 = *(const f4 *)(ra.w + 4);
     const float hb = (h_in ? h_in : h_out)[r];
     const float sgv = ra.sgl[0];
     /* the next layer's router (one wave per 4-row block of 2048 fp32, the
@@ -1182,7 +1208,6 @@ __global__ __launch_bounds__(128) void k_gemv_down_combine1(DownArgs a, RouteArg
      * x = j % 8, s = j / 8, so the rows reach the XCD whose router block
      * reads them; one 4-byte load per 128-byte line */
     uint32_t sink = 0;
-#ifndef NO_RPF
     if (a.pf_router && wv == 1) {
         const int x8 = blockIdx.x & 7, sl = blockIdx.x >> 3, row = 4 * (x8 + 8 * (sl >> 2)) + (sl & 3);
         if (row < a.E) {
@@ -1190,29 +1215,34 @@ __global__ __launch_bounds__(128) void k_gemv_down_combine1(DownArgs a, RouteArg
             asm volatile("global_load_dword %0, %1, off" : "=v"(sink) : "v"(p) : "memory");
         }
     }
-#endif
-    float y[DC_K];
 #pragma unroll
-    for (int k = 0; k < DC_K; k++) {
+    for (int j = 0; j < NS; j++) {
+        if (sh_here && j == NS - 1) break; /* the shared expert's slot, below */
         DnX<EFMT> xv;
-        xv.set(xq[k]);
-        y[k] = row_sum16(xv.dot(raw[k], cl));
+        xv.set(xq[j]);
+        const float y = row_sum16(xv.dot(raw[j], cl));
+        if (cl == 0) ys[half][g + DC_SG * j][rq] = y;
     }
-    float ysh = 0.0f;
-    if (has_sh) {
-        DnX<SFMT> xv;
-        xv.set(sq);
-        ysh = row_sum16(xv.dot(rsh, cl));
+    if (sh_here) {
+        float ysh = 0.0f;
+        if (has_sh) {
+            DnX<SFMT> xv;
+            xv.set(sq);
+            ysh = row_sum16(xv.dot(rsh, cl));
+        }
+        if (cl == 0) ys[half][DC_K][rq] = ysh;
     }
-    if (cl == 0) {
+    __syncthreads();
+    if (g == 0 && cl == 0) {
+        const float wk[DC_K] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
         float moe = 0.0f;
 #pragma unroll
         for (int k = 0; k < DC_K; k++)
-            if (k < K) moe += wk[k] * y[k];
-        float o = (h_in ? hb : 0.0f) + moe;
-        if (has_sh) o = o + sigmoid_f(sgv) * ysh;
-        h_out[r] = o;
-        if (res) res[r] = o;
+            if (k < K) moe += wk[k] * ys[half][k][rq];
+        float ov = (h_in ? hb : 0.0f) + moe;
+        if (has_sh) ov = ov + sigmoid_f(sgv) * ys[half][DC_K][rq];
+        h_out[r] = ov;
+        if (res) res[r] = ov;
     }
     asm volatile("s_waitcnt vmcnt(0)" : : "v"(sink));
 }
@@ -1410,8 +1440,8 @@ int launch_gemv_down_combine1(const ExpertSide &ex, const SharedSide &sh, const 
     a.pf_router = H == 2048 ? next_router : nullptr;
 #define DC_LAUNCH(EF, SF)                                                                                                     \
     do {                                                                                                                      \
-        if (act_by_slot) KLAUNCH((k_gemv_down_combine1<EF, SF, true>), dim3(H / 8), dim3(128), 0, s, a, ra, h_in, h_out, res); \
-        else KLAUNCH((k_gemv_down_combine1<EF, SF, false>), dim3(H / 8), dim3(128), 0, s, a, ra, h_in, h_out, res);           \
+        if (act_by_slot) KLAUNCH((k_gemv_down_combine1<EF, SF, true>), dim3(H / 8), dim3(128 * DC_SG), 0, s, a, ra, h_in, h_out, res); \
+        else KLAUNCH((k_gemv_down_combine1<EF, SF, false>), dim3(H / 8), dim3(128 * DC_SG), 0, s, a, ra, h_in, h_out, res);           \
     } while (0)
     DOWN_FMT_SWITCH(ex.down_fmt, sf, DC_LAUNCH);
 #undef DC_LAUNCH
