@@ -617,6 +617,12 @@ DEV void k_gemv_gate_up1_body(GUArgs a, RouteArgs ra) {
 
 template <int EPL>
 __global__ __launch_bounds__(256) void k_gemv_gate_up1(GUArgs a, RouteArgs ra) {
+    /* the arguments the first loads and branches depend on, in one round of
+     * scalar loads: left alone, the compiler fetched them in four dependent
+     * rounds (each branch on an argument waited for its own loads) ahead of
+     * the logits' load */
+    asm volatile("" ::"s"(a.kt), "s"(a.routed_blocks), "s"(a.x), "s"(a.gate), "s"(a.up), "s"(a.gate_stride),
+                 "s"(a.up_stride), "s"(a.M), "s"(a.E), "s"(a.K), "s"(ra.logits), "s"(ra.bias));
     KT_BEGIN(a.kt);
     k_gemv_gate_up1_body<EPL>(a, ra);
     KT_END(a.kt);
