@@ -965,6 +965,17 @@ struct DnPol {
 };
 
 
+/* The kernel arguments (and the grid size, an implicit argument), fetched
+ * in one round of scalar loads at a kernel's entry.  Left alone, the
+ * compiler fetches each where a branch first needs it, and every such
+ * branch waits for its own round trip (two to four rounds ahead of a
+ * block's first vector load). */
+#define GEMM_PIN_ARGS(a, ...)                                                                                  \
+    asm volatile("" ::"s"(a.wa), "s"(a.wb), "s"(a.stride_a), "s"(a.stride_b), "s"(a.sh_a), "s"(a.sh_b),      \
+                 "s"(a.src), "s"(a.src_sh), "s"(a.tiles), "s"(a.pairs), "s"(a.kt), "s"(a.T), "s"(a.H),         \
+                 "s"(a.M), "s"(a.S), "s"(a.K), "s"(a.E), "s"(a.zrow), "s"(a.zrow_sh), "s"(a.nyb), "s"(a.uwin), \
+                 "s"(gridDim.x), __VA_ARGS__)
+
 /* RF: routed gate/up format (Q4_K, row-major or tile-major); SF: the shared
  * expert's (the same, or Q8_0 row-major) */
 template <int RF, int SF, int NST, int TBM>
@@ -1019,6 +1030,8 @@ DEV void k_gemm_gate_up_body(GemmArgs a) {
 
 template <int RF, int SF, int NST, int TBM>
 __global__ __launch_bounds__(Shape<TBM>::W * 64) void k_gemm_gate_up(GemmArgs a) {
+    GEMM_PIN_ARGS(a, "s"(a.act), "s"(a.act_sh), "s"(a.sd), "s"(a.sd_g), "s"(a.nsh), "s"(a.dcnt), "s"(a.tmask),
+                  "s"(a.idx), "s"(a.offsets), "s"(a.pos), "s"(a.pairs_out), "s"(a.tiles_out));
     KT_BEGIN(a.kt);
     k_gemm_gate_up_body<RF, SF, NST, TBM>(a);
     KT_END(a.kt);
@@ -1026,6 +1039,7 @@ __global__ __launch_bounds__(Shape<TBM>::W * 64) void k_gemm_gate_up(GemmArgs a)
 
 template <int EFMT, int SFMT, int NST, int TBM>
 __global__ __launch_bounds__(Shape<TBM>::W * 64) void k_gemm_down(GemmArgs a) {
+    GEMM_PIN_ARGS(a, "s"(a.y), "s"(a.ysh));
     __shared__ __attribute__((aligned(16))) _Float16 xs[2 * Shape<TBM>::XR * BLD];
     __shared__ int rowoff[TBM * 16];
     int ti, yb;
@@ -1069,6 +1083,7 @@ DEV void k_gemm_gate_up_p_body(GemmArgs a) {
 
 template <int TBM, int GF>
 __global__ __launch_bounds__(Shape<TBM>::W * 64) void k_gemm_gate_up_p(GemmArgs a) {
+    GEMM_PIN_ARGS(a, "s"(a.act), "s"(a.act_sh));
     KT_BEGIN(a.kt);
     k_gemm_gate_up_p_body<TBM, GF>(a);
     KT_END(a.kt);
@@ -1076,6 +1091,7 @@ __global__ __launch_bounds__(Shape<TBM>::W * 64) void k_gemm_gate_up_p(GemmArgs 
 
 template <int EFMT, int TBM>
 __global__ __launch_bounds__(Shape<TBM>::W * 64) void k_gemm_down_p(GemmArgs a) {
+    GEMM_PIN_ARGS(a, "s"(a.y), "s"(a.ysh));
     /* the launchers send 16-row tile lists (T <= 16) to the per-tile kernels */
     static_assert(TBM >= 2, "persistent kernels take 32- and 80-row tiles");
     __shared__ __attribute__((aligned(16))) _Float16 xs[3 * Shape<TBM>::XR * BLD];

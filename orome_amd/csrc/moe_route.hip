@@ -34,6 +34,11 @@
  * the last block returns the counter to zero for the next launch. */
 template <bool NORM, int TMAX, int NIM, int RS, int FOLD>
 __global__ __launch_bounds__(FOLD ? 512 : 256) void k_route_small(RouteArgs a) {
+    /* the arguments in one round of scalar loads at entry (left alone, the
+     * router rows' address came two dependent rounds after the first) */
+    asm volatile("" ::"s"(a.W), "s"(a.wsg), "s"(a.bias), "s"(a.x), "s"(a.T), "s"(a.E), "s"(a.H), "s"(a.K),
+                 "s"(a.logits), "s"(a.x16), "s"(a.norm_h), "s"(a.norm_w), "s"(a.norm_eps), "s"(a.xnorm),
+                 "s"(gridDim.x));
     constexpr int W = FOLD ? 8 : 4; /* waves: the folding block selects with 8 */
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int row = blockIdx.x * (W / RS) + wv / RS, tb = (wv % RS) * TMAX;
@@ -265,6 +270,10 @@ __global__ __launch_bounds__(256) void k_pack_router(const float *W, int H, _Flo
  * for the slice, then runs its MFMAs. */
 template <int TTS, int TES, int NW, bool XH, int KS_MAX>
 __global__ __launch_bounds__(64 * NW) void k_route_approx(RouteArgs a) {
+    /* the arguments in one round of scalar loads at entry (left alone, the
+     * packed router's address came in a second round) */
+    asm volatile("" ::"s"(a.W16), "s"(a.x), "s"(a.x16), "s"(a.x16in), "s"(a.part), "s"(a.dcnt), "s"(a.tmask),
+                 "s"(a.T), "s"(a.E), "s"(a.H), "s"(gridDim.x));
     /* KS_MAX: the largest slice (H / 8) the launch allows */
     __shared__ __attribute__((aligned(16))) _Float16 xs[16 * TTS][KS_MAX + 16];
     const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -701,6 +710,8 @@ template <int KM>
 __global__ __launch_bounds__(DSP_TOK) void k_dispatch_scan_scatter(RouteArgs a, const uint32_t *cnt, int G,
                                                                    uint32_t *tiles_s, uint32_t *tiles_b,
                                                                    int has_shared) {
+    asm volatile("" ::"s"(a.idx), "s"(a.E), "s"(a.K), "s"(a.T), "s"(a.offsets), "s"(a.pairs), "s"(a.pos),
+                 "s"(cnt), "s"(G), "s"(gridDim.x));
     extern __shared__ uint32_t mask[]; /* E * DSP_WORDS, then E * DSP_WORDS word prefixes */
     __shared__ uint32_t xo[DSP_TOK], wsum[32];
     uint32_t *wpre = mask + a.E * DSP_WORDS;
