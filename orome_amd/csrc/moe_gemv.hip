@@ -388,14 +388,6 @@ __global__ __launch_bounds__(256) void k_gemv_gate_up(GUArgs a, RouteArgs ra) {
     KT_END(a.kt);
 }
 
-/* One-token gate/up with the routing folded in (H = 2048, E <= 64 EPL).
- * Every wave selects the experts itself (no separate routing kernel, no
- * barrier), and the waves of the block for selection rank u issue their
- * weight loads for expert ids[u] as soon as round u has named it; the
- * remaining rounds, the expert's sorted position (the number of smaller
- * selected ids: its act row) and, in block 0, the published routing overlap
- * those loads.  Selection and softmax restate softmax_topk_route
- * (inference/src/shaders.metal:1141-1234) exactly as wave_topk does. */
 /* a lane's EPL in-lane positions, four bits each */
 template <int EPL>
 struct PosPack {
@@ -405,6 +397,16 @@ template <>
 struct PosPack<16> {
     typedef uint64_t type;
 };
+/* One-token gate/up with the routing folded in (H = 2048, E <= 64 EPL): no
+ * separate top-k kernel.  In each block one wave runs the selection rounds
+ * on the router's logits; the block's waves, all for selection rank u, wait
+ * at a barrier that it passes as soon as round u has named the expert, and
+ * then issue their weight loads for it.  The remaining rounds, the expert's
+ * sorted position (the number of smaller selected ids: its act row, unless
+ * act rows go in slot order) and, in block 0, the call's selections and
+ * weights overlap those loads; block 0's waves write the dispatch after
+ * their products.  Selection and softmax restate softmax_topk_route
+ * (inference/src/shaders.metal:1141-1234) exactly as wave_topk does. */
 template <int EPL>
 DEV void k_gemv_gate_up1_body(GUArgs a, RouteArgs ra) {
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
