@@ -194,6 +194,23 @@ def test_decode_variants(kw, T):
     p.gm.close()
 
 
+@pytest.mark.parametrize("E", [64, 128, 512, 1024])
+def test_decode_expert_counts(E):
+    """The one-token gate/up at every width of a lane's expert list (1, 2, 8
+    and 16 experts a lane; 256 is the base model's 4): routing and dispatch
+    bit-exact, output within tolerance of the oracle, at T=1 (selection folded
+    into the gate/up, the down + combine kernel) and T=2."""
+    banner("decode E=%d" % E)
+    p = Pair(max_tokens=4, E=E, seed=70 + E % 97)
+    for T in (1, 2):
+        x, h = p.inputs(T, seed=700 + T)
+        out, dbg = p.run(0, x, h)
+        check_routing(p, x, dbg, 8)
+        ref = p.om.forward(0, x, h)
+        assert rel_l2(out - h, ref - h) < TOL, T
+    p.gm.close()
+
+
 def test_topk_teacher_forced(base):
     banner("teacher-forced top-k")
     rng = np.random.default_rng(1)
